@@ -1,0 +1,396 @@
+"""Torch-CPU restatement of the reference hot path (oracle; test infrastructure).
+
+Each function follows the cited reference lines operation by operation, in the
+same order and on the same dtypes, because the reference's results depend on
+ATen's per-op rounding (reduced-precision inputs are rounded after every op)
+and on torch's CPU ``log1p``/``expm1`` (Sleef, not correctly rounded).  Running
+the same ATen ops in the same order on the same torch build reproduces the
+reference bit for bit.  The product package never imports this module.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .bitstream import pack_codes as np_pack_codes
+from .bitstream import unpack_codes as np_unpack_codes
+
+AMAX_EPS = 1e-8  # the cache layer's metadata epsilon, muzero/cache/layer.py:45
+
+
+# ---------------------------------------------------------------------------
+# Alpha selection — muzero/quantizer.py:29-112
+# ---------------------------------------------------------------------------
+
+def _strided_sample(t: torch.Tensor, max_points: int) -> torch.Tensor:
+    """Every ``numel // max_points``-th value, at most ``max_points`` (quantizer.py:86-91)."""
+    flat = t.reshape(-1)
+    if flat.numel() <= max_points:
+        return flat
+    stride = max(1, flat.numel() // max_points)
+    return flat[::stride][:max_points]
+
+
+def _groups_for_stats(t: torch.Tensor, q_group_size: int, kind: str) -> torch.Tensor:
+    """Group view used for the zero-anchor statistic (quantizer.py:94-112)."""
+    w = t.float()
+    if w.dim() == 2:
+        n, width = w.shape
+        if width != q_group_size:
+            ng = max(1, width // q_group_size)
+            return w[:, : ng * q_group_size].reshape(n, ng, q_group_size).unsqueeze(0).unsqueeze(0)
+        return w.unsqueeze(0).unsqueeze(0).unsqueeze(0)
+    if kind == "key":
+        w = w.transpose(2, 3).contiguous()
+    b, h, s, d = w.shape
+    d_pad = ((d + q_group_size - 1) // q_group_size) * q_group_size
+    if d_pad != d:
+        w = F.pad(w, (0, d_pad - d), value=0)
+    return w.reshape(b, h, s, d_pad // q_group_size, q_group_size)
+
+
+def select_alpha(tensor: torch.Tensor, *, bits: int, q_group_size: int, kind: str,
+                 max_points: int = 65536) -> float:
+    """Compander alpha from tail/concentration/zero-anchor statistics (quantizer.py:29-83)."""
+    if bits == 4:
+        return 2.0
+    sample = _strided_sample(tensor.float(), max_points).abs().reshape(-1)
+    n = sample.numel()
+    tiny = 1e-8
+
+    def kth(frac: float) -> float:
+        return float(torch.kthvalue(sample, max(1, int(frac * n))).values.item())
+
+    p50, p95, p99 = kth(0.50), kth(0.95), kth(0.99)
+    tail = p99 / max(p95, tiny)
+    conc = p95 / max(p50, tiny)
+    g = _groups_for_stats(tensor, q_group_size, kind)
+    g_lo = g.amin(dim=-1)
+    g_hi = g.amax(dim=-1)
+    anchor = ((0.0 - g_lo) / (g_hi - g_lo).clamp_min(tiny)).clamp(0.0, 1.0)
+    offset = float((anchor - 0.5).abs().mean().item())
+    if kind == "key":
+        if bits == 1:
+            if tail > 3.0 or conc > 12.0 or offset > 0.22:
+                return 16.0
+            if tail > 2.0 or conc > 8.0 or offset > 0.16:
+                return 4.0
+            return 2.0
+        if bits == 8 and (tail > 2.6 or conc > 10.0):
+            return 4.0
+        return 2.0
+    if bits >= 8:
+        if tail > 2.0 or conc > 6.0 or offset > 0.14:
+            return 4.0
+        return 2.0
+    if bits == 3 and tail > 2.3 and offset > 0.12:
+        return 4.0
+    return 2.0
+
+
+# ---------------------------------------------------------------------------
+# Quantize / pack — muzero/quantizer.py:161-202
+# ---------------------------------------------------------------------------
+
+def quantize_codes(rows: torch.Tensor, bits: int, alpha: float, eps: float = AMAX_EPS):
+    """Codes and unrounded (mn, scale) of every ``[N, G]`` row (quantizer.py:168-184).
+
+    All arithmetic runs in ``rows.dtype`` exactly as the reference does; the
+    returned ``mn``/``scale`` are still in that dtype (the reference rounds them
+    to the metadata dtype only when storing them, :186).
+    """
+    top = float((1 << bits) - 1)
+    lo = rows.amin(dim=-1, keepdim=True)
+    hi = rows.amax(dim=-1, keepdim=True)
+    span = (hi - lo).clamp_min(eps)
+    unit = ((rows - lo) / span).clamp(0.0, 1.0)
+    anchor = ((0.0 - lo) / span).clamp(0.0, 1.0)
+    anchor_level = torch.round(anchor * top)
+    up_bins = (top - anchor_level).clamp_min(1.0)
+    down_bins = anchor_level.clamp_min(1.0)
+    up_extent = (1.0 - anchor).clamp_min(eps)
+    down_extent = anchor.clamp_min(eps)
+    log_base = torch.log1p(torch.tensor(alpha, device=rows.device, dtype=torch.float32))
+    up_frac = ((unit - anchor) / up_extent).clamp(0.0, 1.0)
+    down_frac = ((anchor - unit) / down_extent).clamp(0.0, 1.0)
+    up_code = anchor_level + torch.round(torch.log1p(alpha * up_frac) / log_base * up_bins)
+    down_code = anchor_level - torch.round(torch.log1p(alpha * down_frac) / log_base * down_bins)
+    codes = torch.where(unit >= anchor, up_code, down_code).clamp(0.0, top).to(torch.uint8)
+    return codes, lo, span
+
+
+def pack_q(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """LSB-first bitstream pack in torch (quantizer.py:189-202)."""
+    g = codes.shape[-1]
+    qb = (g * bits + 7) // 8
+    nbits = g * bits
+    pos = torch.arange(nbits, device=codes.device, dtype=torch.long)
+    stream = ((codes[..., pos // bits] >> (pos % bits)) & 1).to(torch.uint8)
+    if nbits < qb * 8:
+        stream = F.pad(stream, (0, qb * 8 - nbits), value=0)
+    stream = stream.reshape(*codes.shape[:-1], qb, 8)
+    weights = torch.arange(8, device=codes.device, dtype=torch.uint8)
+    return torch.sum(torch.bitwise_left_shift(stream, weights), dim=-1, dtype=torch.uint8).contiguous()
+
+
+def unpack_q(packed: torch.Tensor, bits: int, group_size: int) -> torch.Tensor:
+    """Inverse bitstream (quantizer.py:258-266)."""
+    nbits = group_size * bits
+    pos = torch.arange(nbits, device=packed.device, dtype=torch.long)
+    stream = ((packed[..., pos >> 3] >> (pos & 7)) & 1).to(torch.uint8)
+    stream = stream.reshape(*packed.shape[:-1], group_size, bits)
+    weights = torch.arange(bits, device=packed.device, dtype=torch.uint8)
+    return torch.sum(torch.bitwise_left_shift(stream, weights), dim=-1, dtype=torch.uint8)
+
+
+def quantize_rows(rows: torch.Tensor, bits: int, alpha: float, eps: float = AMAX_EPS,
+                  amax_dtype: torch.dtype = torch.float16):
+    """(packed ``[N, qb]`` u8, mn ``[N,1]``, scale ``[N,1]``) as the reference torch path returns them."""
+    codes, lo, span = quantize_codes(rows, bits, alpha, eps)
+    return pack_q(codes, bits), lo.to(amax_dtype), span.to(amax_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Dequantize — muzero/quantizer.py:229-255
+# ---------------------------------------------------------------------------
+
+def dequantize_rows(packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor, bits: int,
+                    alpha: float, group_size: int, out_dtype: torch.dtype,
+                    eps: float = AMAX_EPS) -> torch.Tensor:
+    """Inverse compander from the STORED metadata, fp32 math, cast to ``out_dtype``."""
+    top = float((1 << bits) - 1)
+    q = unpack_q(packed, bits, group_size).to(torch.float32)
+    lo = mn.to(torch.float32)
+    span = scale.to(torch.float32)
+    anchor = ((0.0 - lo) / span).clamp(0.0, 1.0)
+    anchor_level = torch.round(anchor * top)
+    up_bins = (top - anchor_level).clamp_min(1.0)
+    down_bins = anchor_level.clamp_min(1.0)
+    up_extent = (1.0 - anchor).clamp_min(eps)
+    down_extent = anchor.clamp_min(eps)
+    log_base = torch.log1p(torch.tensor(alpha, device=packed.device, dtype=torch.float32))
+    up_frac = ((q - anchor_level) / up_bins).clamp(0.0, 1.0)
+    down_frac = ((anchor_level - q) / down_bins).clamp(0.0, 1.0)
+    up_val = torch.expm1(up_frac * log_base) / alpha
+    down_val = torch.expm1(down_frac * log_base) / alpha
+    unit = torch.where(q >= anchor_level, anchor + up_extent * up_val,
+                       anchor - down_extent * down_val).clamp(0.0, 1.0)
+    return (unit * span + lo).to(out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# K/V grouping — muzero/cache/layer.py:271-345
+# ---------------------------------------------------------------------------
+
+def key_rows(keys: torch.Tensor, group_size: int) -> torch.Tensor:
+    """``[B,H,L,hd]`` -> rows ``[B*H*(L/G)*hd, G]``: one row per channel per G tokens (layer.py:274-278)."""
+    b, h, length, d = keys.shape
+    nsg = length // group_size
+    g = keys.reshape(b, h, nsg, group_size, d).permute(0, 1, 2, 4, 3).contiguous()
+    return g.reshape(-1, group_size)
+
+
+def value_rows(values: torch.Tensor, group_size: int) -> torch.Tensor:
+    """``[B,H,L,hd]`` -> rows ``[B*H*L*ng, G]``: one row per token per G channels (layer.py:290-294)."""
+    b, h, length, d = values.shape
+    d_pad = ((d + group_size - 1) // group_size) * group_size
+    if d_pad != d:
+        values = F.pad(values, (0, d_pad - d), value=0)
+    return values.reshape(b, h, length, d_pad // group_size, group_size).reshape(-1, group_size)
+
+
+def quantize_key_block(keys: torch.Tensor, bits: int, alpha: float, group_size: int = 64,
+                       amax_dtype: torch.dtype = torch.float16):
+    """(packed ``[B,H,nsg,hd,qb]``, mn, scale ``[B,H,nsg,hd,1]``) — layer.py:271-285."""
+    b, h, length, d = keys.shape
+    nsg = length // group_size
+    pq, mn, sc = quantize_rows(key_rows(keys, group_size), bits, alpha, AMAX_EPS, amax_dtype)
+    qb = pq.shape[-1]
+    return pq.reshape(b, h, nsg, d, qb), mn.reshape(b, h, nsg, d, 1), sc.reshape(b, h, nsg, d, 1)
+
+
+def quantize_value_block(values: torch.Tensor, bits: int, alpha: float, group_size: int = 64,
+                         amax_dtype: torch.dtype = torch.float16):
+    """(packed ``[B,H,L,ng,qb]``, mn, scale ``[B,H,L,ng,1]``) — layer.py:287-301."""
+    b, h, length, d = values.shape
+    ng = (d + group_size - 1) // group_size
+    pq, mn, sc = quantize_rows(value_rows(values, group_size), bits, alpha, AMAX_EPS, amax_dtype)
+    qb = pq.shape[-1]
+    return pq.reshape(b, h, length, ng, qb), mn.reshape(b, h, length, ng, 1), sc.reshape(b, h, length, ng, 1)
+
+
+def dequantize_key_block(pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor, bits: int,
+                         alpha: float, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """Packed keys ``[B,H,nsg,hd,qb]`` -> ``[B,H,nsg*G,hd]`` (layer.py:324-334)."""
+    b, h, nsg, d, qb = pq.shape
+    rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                          group_size, out_dtype)
+    return rec.reshape(b, h, nsg, d, group_size).permute(0, 1, 2, 4, 3).reshape(b, h, nsg * group_size, d)
+
+
+def dequantize_value_block(pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor, bits: int,
+                           alpha: float, group_size: int, head_dim: int,
+                           out_dtype: torch.dtype) -> torch.Tensor:
+    """Packed values ``[B,H,T,ng,qb]`` -> ``[B,H,T,hd]`` (layer.py:336-345)."""
+    b, h, t, ng, qb = pq.shape
+    rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                          group_size, out_dtype)
+    return rec.reshape(b, h, t, ng * group_size)[..., :head_dim]
+
+
+# ---------------------------------------------------------------------------
+# Decode attention — muzero/cache/attention.py:41-45, :179-295
+# ---------------------------------------------------------------------------
+
+def repeat_kv(t: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """GQA head expansion (attention.py:41-45)."""
+    if n_rep == 1:
+        return t
+    b, h, s, d = t.shape
+    return t[:, :, None].expand(b, h, n_rep, s, d).reshape(b, h * n_rep, s, d)
+
+
+def decode_attention_exact(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                           attention_mask: Optional[torch.Tensor], scaling: float) -> torch.Tensor:
+    """fp64 softmax attention of one query token over full (dequantized + residual) K/V.
+
+    ``query [B,Hq,1,hd]``, ``keys/values [B,Hkv,L,hd]`` in the layer dtype (the
+    dequantized prefix is held in that dtype, layer.py:263), optional additive
+    ``attention_mask [B,1,1,L]``.  Returns ``[B,1,Hq,hd]`` float64 — the oracle
+    that the HIP decode attention is held to (bf16 output within 2e-3 max-abs,
+    1e-3 mean-abs).
+    """
+    n_rep = query.shape[1] // keys.shape[1]
+    k = repeat_kv(keys.double(), n_rep)
+    v = repeat_kv(values.double(), n_rep)
+    logits = torch.matmul(query.double(), k.transpose(2, 3)) * scaling
+    if attention_mask is not None:
+        logits = logits + attention_mask[..., : k.shape[-2]].double()
+    p = torch.softmax(logits, dim=-1)
+    return torch.matmul(p, v).transpose(1, 2).contiguous()
+
+
+def decode_attention_literal(query: torch.Tensor, key_prefix: torch.Tensor, value_prefix: torch.Tensor,
+                             res_keys: torch.Tensor, res_values: torch.Tensor,
+                             attention_mask: Optional[torch.Tensor], scaling: float,
+                             key_chunk_tokens: int = 32 * 64, value_chunk_tokens: int = 256) -> torch.Tensor:
+    """The reference's CPU fallback with its bf16 roundings (attention.py:213-295).
+
+    Logits are produced per chunk in the query dtype, softmax runs in fp32 and is
+    cast back to the query dtype, and the weighted values are summed chunk by
+    chunk in the query dtype.  Only used to report the distance between the
+    fp64 oracle and what the reference itself would return on CPU.
+    """
+    n_rep = query.shape[1] // res_keys.shape[1]
+    parts = []
+    cursor = 0
+    for st in range(0, key_prefix.shape[2], key_chunk_tokens):
+        kc = repeat_kv(key_prefix[:, :, st:st + key_chunk_tokens], n_rep)
+        lg = torch.matmul(query, kc.transpose(2, 3)) * scaling
+        if attention_mask is not None:
+            lg = lg + attention_mask[..., cursor:cursor + kc.shape[-2]]
+        parts.append(lg)
+        cursor += kc.shape[-2]
+    dk = repeat_kv(res_keys, n_rep)
+    if dk.shape[-2] > 0:
+        lg = torch.matmul(query, dk.transpose(2, 3)) * scaling
+        if attention_mask is not None:
+            lg = lg + attention_mask[..., cursor:cursor + dk.shape[-2]]
+        parts.append(lg)
+    w = F.softmax(torch.cat(parts, dim=-1), dim=-1, dtype=torch.float32).to(query.dtype)
+    out = None
+    vc = 0
+    for st in range(0, value_prefix.shape[2], value_chunk_tokens):
+        vv = repeat_kv(value_prefix[:, :, st:st + value_chunk_tokens], n_rep)
+        co = torch.matmul(w[..., vc:vc + vv.shape[-2]], vv)
+        out = co if out is None else out + co
+        vc += vv.shape[-2]
+    dv = repeat_kv(res_values, n_rep)
+    if dv.shape[-2] > 0:
+        co = torch.matmul(w[..., vc:vc + dv.shape[-2]], dv)
+        out = co if out is None else out + co
+    return out.transpose(1, 2).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Cache-level convenience used by the parity tests and the CPU baseline
+# ---------------------------------------------------------------------------
+
+def split_prefix(length: int, residual: int, group_size: int) -> int:
+    """Quantized-prefix length after a prefill flush (layer.py:378-382, :396)."""
+    excess = max(length - residual, 0)
+    return (excess // group_size) * group_size
+
+
+def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tensor, *, bits: int,
+                     alpha_k: float, alpha_v: float, group_size: int, residual: int,
+                     amax_dtype: torch.dtype = torch.float16,
+                     attention_mask: Optional[torch.Tensor] = None,
+                     scaling: Optional[float] = None):
+    """Quantize a prefill KV the way the cache does, then attend the decode query.
+
+    Returns ``(out_exact_fp64 [B,1,Hq,hd], state)`` where ``state`` holds the
+    packed prefix, metadata and residual tensors, so the same bytes can be fed
+    to the HIP path.
+    """
+    b, hkv, length, d = keys.shape
+    lq = split_prefix(length, residual, group_size)
+    if scaling is None:
+        scaling = d ** -0.5
+    state = {"lq": lq, "scaling": scaling}
+    if lq > 0:
+        pk, kmn, ksc = quantize_key_block(keys[:, :, :lq].contiguous(), bits, alpha_k, group_size, amax_dtype)
+        pv, vmn, vsc = quantize_value_block(values[:, :, :lq].contiguous(), bits, alpha_v, group_size, amax_dtype)
+        kq = dequantize_key_block(pk, kmn, ksc, bits, alpha_k, group_size, keys.dtype)
+        vq = dequantize_value_block(pv, vmn, vsc, bits, alpha_v, group_size, d, values.dtype)
+        state.update(packed_k=pk, k_mn=kmn, k_scale=ksc, packed_v=pv, v_mn=vmn, v_scale=vsc,
+                     key_prefix=kq, value_prefix=vq)
+    else:
+        kq = keys[:, :, :0]
+        vq = values[:, :, :0]
+        state.update(key_prefix=kq, value_prefix=vq)
+    rk = keys[:, :, lq:]
+    rv = values[:, :, lq:]
+    state.update(res_k=rk, res_v=rv)
+    full_k = torch.cat([kq, rk], dim=2)
+    full_v = torch.cat([vq, rv], dim=2)
+    out = decode_attention_exact(query, full_k, full_v, attention_mask, scaling)
+    return out, state
+
+
+def pack_codes_np(codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """Bitstream pack through the NumPy implementation (independent of :func:`pack_q`)."""
+    return torch.from_numpy(np_pack_codes(codes.cpu().numpy(), bits))
+
+
+def unpack_codes_np(packed: torch.Tensor, bits: int, group_size: int) -> torch.Tensor:
+    return torch.from_numpy(np_unpack_codes(packed.cpu().numpy(), bits, group_size))
+
+
+def alpha2_table(n: int, k: int) -> float:
+    """Known answer for alpha=2: ``expm1(k/n * ln 3) / 2 = (3**(k/n) - 1) / 2``."""
+    return (3.0 ** (k / n) - 1.0) / 2.0
+
+
+def synthetic_kv(batch: int, kv_heads: int, length: int, head_dim: int, q_heads: int, *,
+                 seed: int = 1234, outliers: int = 4, outlier_scale: float = 10.0,
+                 dtype: torch.dtype = torch.bfloat16):
+    """The benchmark inputs: K, V, Q ~ N(0,1) drawn in that order from one seeded
+    generator, with ``outliers`` key channels (``randperm(head_dim)[:outliers]``)
+    scaled by ``outlier_scale``; everything cast to ``dtype``."""
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(batch, kv_heads, length, head_dim, generator=g)
+    v = torch.randn(batch, kv_heads, length, head_dim, generator=g)
+    q = torch.randn(batch, q_heads, 1, head_dim, generator=g)
+    idx = torch.randperm(head_dim, generator=g)[:outliers]
+    k[..., idx] *= outlier_scale
+    return k.to(dtype), v.to(dtype), q.to(dtype), idx
+
+
+__all__ = [name for name in dir() if not name.startswith("_") and name not in {"annotations", "math",
+                                                                                "np", "torch", "F", "Optional"}]

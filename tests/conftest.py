@@ -1,0 +1,48 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device); runs the HIP kernels")
+
+
+def pytest_collection_modifyitems(config, items):
+    has_gpu = torch.cuda.is_available()
+    skip = pytest.mark.skip(reason="no HIP device in this container")
+    for item in items:
+        if "gpu" in item.keywords and not has_gpu:
+            item.add_marker(skip)
+
+
+def load_golden(name: str) -> dict:
+    with np.load(os.path.join(GOLDEN, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def as_tensor(arr: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    """Rebuild a tensor from a fixture array (16-bit floats are stored as raw uint16)."""
+    if dtype in (torch.bfloat16, torch.float16):
+        return torch.from_numpy(arr.astype(np.uint16).view(np.int16).copy()).view(dtype)
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(dtype)
+
+
+def bits_of(t) -> np.ndarray:
+    """Raw bit patterns of a tensor or fixture array (floats compare bit for bit)."""
+    if isinstance(t, np.ndarray):
+        return t.view(np.uint32) if t.dtype == np.float32 else t
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float32:
+        return t.numpy().view(np.uint32)
+    return t.numpy()
