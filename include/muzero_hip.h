@@ -1,0 +1,157 @@
+/*
+ * muzero_hip.h — C ABI of the MI355X (gfx950) muZero KV-cache hot path.
+ *
+ * One shared library, libmuzero_hip.so, built by hipcc for gfx950.  Every
+ * entry point takes plain device pointers, explicit sizes and strides, dtype
+ * enums and a hipStream_t (0 = the default stream), launches asynchronously
+ * and returns an int status (0 = success, negative = argument error, or the
+ * positive hipError_t of a failed launch).  Nothing here allocates device
+ * memory; callers own every buffer.  Calls are thread-safe: the library keeps
+ * no mutable global state.
+ *
+ * Reference boundary being replaced: the pybind11 module returned by
+ * load_mu_zero_cuda_extension() (muzero/kernels/loader.py:37-94, 1862-1880),
+ * whose functions take torch tensors and launch on the current stream.
+ */
+#ifndef MUZERO_HIP_H
+#define MUZERO_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; declared here so C/FFI callers need no HIP headers. */
+typedef struct ihipStream_t* mz_stream_t;
+
+/* dtype enums */
+enum { MZ_F32 = 0, MZ_BF16 = 1, MZ_F16 = 2 };
+
+/* status codes (besides 0 and positive hipError_t values) */
+enum {
+  MZ_OK = 0,
+  MZ_EINVAL = -1,        /* bad pointer, size, stride or dtype */
+  MZ_EUNSUPPORTED = -2,  /* valid for the reference but not built here (e.g. head_dim) */
+  MZ_EWORKSPACE = -3     /* workspace too small */
+};
+
+const char* muzero_version(void);
+const char* muzero_strerror(int status);
+
+/*
+ * Quantize + bit-pack rows of 64 values (one group per row).
+ * Replaces: quantize(grouped, packed_q, mn, scale, bits, alpha, eps)
+ *   (muzero/kernels/loader.py:40-42, host :1290-1322; algorithm
+ *    muzero/quantizer.py:161-202).
+ * x[r*x_row_stride + i] (x_dtype) -> packed[r*packed_row_stride + 0..8*bits-1],
+ * mn[r*meta_stride], scale[r*meta_stride] (meta_dtype).
+ * `table`: compander table for (alpha, x_dtype) built by the host (see
+ * muzero_amd/tables.py): fp32 thresholds for MZ_F32 input, the 16-bit ratio
+ * table for MZ_BF16 / MZ_F16 input.  Codes and metadata are bit-identical to
+ * the reference torch quantizer on the same input.
+ */
+int muzero_quantize_rows(const void* x, int x_dtype, int64_t nrows, int64_t x_row_stride,
+                         uint8_t* packed, int64_t packed_row_stride,
+                         void* mn, void* scale, int meta_dtype, int64_t meta_stride,
+                         int bits, float eps, const void* table, mz_stream_t stream);
+
+/*
+ * Quantize a key block [B, H, T, D] (T a multiple of 64, last dim contiguous,
+ * strides in elements) into the reference key layout: one group per channel
+ * over 64 consecutive tokens.
+ * Replaces: MuZeroCacheLayer._quantize_key_block (muzero/cache/layer.py:271-285),
+ * including its permute+contiguous copy (done here in LDS).
+ * Output group (b, h, s, d) goes to packed[b*p_sb + h*p_sh + s*D*qb + d*qb]
+ * and mn/scale[b*m_sb + h*m_sh + s*D + d], qb = 8*bits.
+ */
+int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H, int T, int D,
+                         int64_t x_sb, int64_t x_sh, int64_t x_st,
+                         uint8_t* packed, int64_t p_sb, int64_t p_sh,
+                         void* mn, void* scale, int meta_dtype, int64_t m_sb, int64_t m_sh,
+                         int bits, float eps, const void* table, mz_stream_t stream);
+
+/*
+ * Quantize a value block [B, H, T, D] into the reference value layout: one
+ * group per token over 64 consecutive channels, D zero-padded to a multiple
+ * of 64 (ng = ceil(D/64) groups per token).
+ * Replaces: MuZeroCacheLayer._quantize_value_block (muzero/cache/layer.py:287-301).
+ * Output group (b, h, t, j) goes to packed[b*p_sb + h*p_sh + t*ng*qb + j*qb]
+ * and mn/scale[b*m_sb + h*m_sh + t*ng + j].
+ */
+int muzero_quantize_values(const void* values, int x_dtype, int B, int H, int T, int D,
+                           int64_t x_sb, int64_t x_sh, int64_t x_st,
+                           uint8_t* packed, int64_t p_sb, int64_t p_sh,
+                           void* mn, void* scale, int meta_dtype, int64_t m_sb, int64_t m_sh,
+                           int bits, float eps, const void* table, mz_stream_t stream);
+
+/*
+ * Dequantize packed rows back to 64 values each (fp32 math, no FMA
+ * contraction, expm1 from the host-built table `e_table`).
+ * Replaces: dequantize(packed_q, mn, scale, output, bits, alpha)
+ *   (muzero/kernels/loader.py:43-45, host :1324-1358; algorithm
+ *    muzero/quantizer.py:229-255).
+ * Bit-identical to the reference torch dequantizer except for groups stored
+ * with scale 0 (all-zero input): like the reference CUDA kernel
+ * (loader.py:201) the scale is clamped to 1e-8 instead of producing NaN.
+ */
+int muzero_dequantize_rows(const uint8_t* packed, int64_t nrows, int64_t packed_row_stride,
+                           const void* mn, const void* scale, int meta_dtype, int64_t meta_stride,
+                           void* out, int out_dtype, int64_t out_row_stride,
+                           int bits, const float* e_table, mz_stream_t stream);
+
+/*
+ * Decode attention of one query token per (batch, q-head) over a packed
+ * key/value prefix of 64*n_groups tokens followed by n_residual dense tokens.
+ * Replaces the decode hook's quantized path: qk + softmax + av + dense
+ * residual merge (muzero/cache/attention.py:48-295 with the kernels
+ * qk/av/prefix_decode_chunked of muzero/kernels/loader.py:46-84), as one
+ * split-over-tokens kernel plus a cross-split log-sum-exp combine.
+ * Key/value prefix layouts are the reference cache layouts
+ * (muzero/cache/layer.py:271-301): packed_K [B,Hkv,>=n_groups,D,qb],
+ * K_mn/K_scale [B,Hkv,>=n_groups,D]; packed_V [B,Hkv,>=64*n_groups,ng,qb],
+ * V_mn/V_scale [B,Hkv,>=64*n_groups,ng].  Residual K/V: [B,Hkv,R,D] strided
+ * views (last dim contiguous).  Strides are in elements, except packed
+ * tensors (bytes).  mask: optional additive fp32 [B, L] (L = 64*n_groups+R),
+ * row stride mask_sb.  Output [B, Hq, D] (out_sb, out_sh) in io_dtype.
+ */
+typedef struct mz_decode_args {
+  int batch, kv_heads, n_rep, head_dim, bits;
+  int n_groups, n_residual;
+  int meta_dtype, io_dtype;
+  float scaling;
+  const void* query; int64_t q_sb, q_sh;
+  const uint8_t* k_packed; int64_t kp_sb, kp_sh;
+  const void* k_mn; const void* k_scale; int64_t km_sb, km_sh;
+  const uint8_t* v_packed; int64_t vp_sb, vp_sh;
+  const void* v_mn; const void* v_scale; int64_t vm_sb, vm_sh;
+  const void* k_res; int64_t kr_sb, kr_sh, kr_st;
+  const void* v_res; int64_t vr_sb, vr_sh, vr_st;
+  const float* mask; int64_t mask_sb;
+  const float* e_key; const float* e_value;
+  void* out; int64_t out_sb, out_sh;
+  void* workspace; int64_t workspace_bytes;
+  int n_split;  /* 0 = let the library choose */
+} mz_decode_args;
+
+/* Bytes of workspace muzero_decode_attention needs for these arguments
+ * (and the split count it will use, written to *n_split_out if non-null). */
+int64_t muzero_decode_workspace_bytes(const mz_decode_args* args, int* n_split_out);
+int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
+
+/* The two launches of muzero_decode_attention, for callers that time or merge
+ * them separately.  muzero_decode_partials writes one (acc[D], m, l) fp32
+ * record per (batch, q-head, split) into the workspace, laid out
+ * [B][Hq][n_split][D + 2]; muzero_decode_combine merges the splits of each
+ * (batch, q-head) with a log-sum-exp reduction and writes `out`.
+ * Replaces: prefix_decode_chunked + its reduce kernel
+ *   (muzero/kernels/loader.py:66-84, kernels :1146-1285), extended to the
+ *   residual window and every bit width. */
+int muzero_decode_partials(const mz_decode_args* args, mz_stream_t stream);
+int muzero_decode_combine(const mz_decode_args* args, mz_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUZERO_HIP_H */

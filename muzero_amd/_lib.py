@@ -1,0 +1,111 @@
+"""ctypes binding of libmuzero_hip.so (the C ABI declared in include/muzero_hip.h).
+
+The library is loaded once, from the package directory only.  There is no
+fallback: if it is missing or does not load, every call raises
+:class:`MuZeroHipError`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmuzero_hip.so")
+
+MZ_F32, MZ_BF16, MZ_F16 = 0, 1, 2
+DTYPE_ENUM = {torch.float32: MZ_F32, torch.bfloat16: MZ_BF16, torch.float16: MZ_F16}
+
+c_i64 = ctypes.c_int64
+c_int = ctypes.c_int
+c_float = ctypes.c_float
+c_vp = ctypes.c_void_p
+
+
+class MuZeroHipError(RuntimeError):
+    """A HIP entry point rejected its arguments or its launch failed."""
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``mz_decode_args`` (include/muzero_hip.h)."""
+
+    _fields_ = [
+        ("batch", c_int), ("kv_heads", c_int), ("n_rep", c_int), ("head_dim", c_int), ("bits", c_int),
+        ("n_groups", c_int), ("n_residual", c_int),
+        ("meta_dtype", c_int), ("io_dtype", c_int),
+        ("scaling", c_float),
+        ("query", c_vp), ("q_sb", c_i64), ("q_sh", c_i64),
+        ("k_packed", c_vp), ("kp_sb", c_i64), ("kp_sh", c_i64),
+        ("k_mn", c_vp), ("k_scale", c_vp), ("km_sb", c_i64), ("km_sh", c_i64),
+        ("v_packed", c_vp), ("vp_sb", c_i64), ("vp_sh", c_i64),
+        ("v_mn", c_vp), ("v_scale", c_vp), ("vm_sb", c_i64), ("vm_sh", c_i64),
+        ("k_res", c_vp), ("kr_sb", c_i64), ("kr_sh", c_i64), ("kr_st", c_i64),
+        ("v_res", c_vp), ("vr_sb", c_i64), ("vr_sh", c_i64), ("vr_st", c_i64),
+        ("mask", c_vp), ("mask_sb", c_i64),
+        ("e_key", c_vp), ("e_value", c_vp),
+        ("out", c_vp), ("out_sb", c_i64), ("out_sh", c_i64),
+        ("workspace", c_vp), ("workspace_bytes", c_i64),
+        ("n_split", c_int),
+    ]
+
+
+# exported symbol -> (restype, argtypes)
+SIGNATURES = {
+    "muzero_version": (ctypes.c_char_p, []),
+    "muzero_strerror": (ctypes.c_char_p, [c_int]),
+    "muzero_quantize_rows": (c_int, [c_vp, c_int, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_int, c_i64,
+                                     c_int, c_float, c_vp, c_vp]),
+    "muzero_quantize_keys": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64,
+                                     c_vp, c_i64, c_i64, c_vp, c_vp, c_int, c_i64, c_i64,
+                                     c_int, c_float, c_vp, c_vp]),
+    "muzero_quantize_values": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64,
+                                       c_vp, c_i64, c_i64, c_vp, c_vp, c_int, c_i64, c_i64,
+                                       c_int, c_float, c_vp, c_vp]),
+    "muzero_dequantize_rows": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_i64,
+                                       c_int, c_vp, c_vp]),
+    "muzero_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(c_int)]),
+    "muzero_decode_attention": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load libmuzero_hip.so from the package directory (once)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise MuZeroHipError(
+                    f"{LIB_PATH} is missing: build it with `python -m muzero_amd.build` "
+                    "(hipcc, gfx950); the muZero HIP path has no fallback")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().muzero_strerror(status).decode()
+        raise MuZeroHipError(f"{what} failed with status {status}: {msg}")
+
+
+def stream_ptr(device: torch.device) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

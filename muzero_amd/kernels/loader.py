@@ -1,0 +1,315 @@
+"""Tensor-level entry points of the HIP hot path (drop-in for the reference loader).
+
+Reference: ``muzero/kernels/loader.py`` exposes a pybind11 extension built with
+``load_inline`` (``:1862-1880``) and thin wrappers ``mu_zero_quantize_cuda``,
+``mu_zero_dequantize_cuda``, ``mu_zero_qk_cuda``, ``mu_zero_av_cuda``
+(``:1883-1911``).  Here the same names call ``libmuzero_hip.so`` through its C
+ABI (``include/muzero_hip.h``) on torch's current HIP stream.  The separate
+qk/softmax/av launches of the reference are replaced by one fused decode
+(:func:`mu_zero_decode_attention_hip`), which the cache's attention hook uses.
+
+Every function validates shapes, dtypes, devices and strides on the host
+before launching and raises :class:`MuZeroHipError` on any problem; there is
+no torch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+
+import torch
+
+from .. import _lib
+from .. import tables
+from .._lib import DTYPE_ENUM, MuZeroHipError, check, load, ptr, stream_ptr
+
+GROUP = 64
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise MuZeroHipError(msg)
+
+
+def _on_gpu(*ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _require(t.is_cuda, "muZero HIP kernels need device tensors (no CPU path in the product)")
+        dev = t.device if dev is None else dev
+        _require(t.device == dev, "all tensors must be on the same device")
+    return dev
+
+
+def _qbytes(bits: int) -> int:
+    return (GROUP * bits + 7) // 8
+
+
+@lru_cache(maxsize=1)
+def load_mu_zero_cuda_extension():
+    """Load the HIP library (reference name kept: ``loader.py:1862``)."""
+    return load()
+
+
+# --------------------------------------------------------------------------- quantize
+
+def mu_zero_quantize_cuda(grouped: torch.Tensor, packed_q: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor,
+                          bits: int, alpha: float, eps: float) -> None:
+    """Quantize rows ``grouped[N, 64]`` into ``packed_q[N, 8*bits]``, ``mn/scale[N, 1]`` in place.
+
+    Same arguments as the reference ``quantize`` binding (``loader.py:40-42``).
+    """
+    dev = _on_gpu(grouped, packed_q, mn, scale)
+    _require(grouped.dim() == 2 and grouped.shape[1] == GROUP, "grouped must be [N, 64]")
+    n = grouped.shape[0]
+    _require(grouped.dtype in DTYPE_ENUM, f"unsupported input dtype {grouped.dtype}")
+    _require(1 <= bits <= 8, "bits must be in 1..8")
+    _require(grouped.stride(1) == 1, "rows must be contiguous")
+    _require(packed_q.dtype == torch.uint8 and packed_q.shape[0] == n and packed_q.shape[-1] == _qbytes(bits)
+             and packed_q.stride(-1) == 1, "packed_q must be uint8 [N, 8*bits]")
+    _require(mn.dtype == scale.dtype and mn.dtype in DTYPE_ENUM, "mn/scale dtype")
+    _require(mn.shape[0] == n and scale.shape[0] == n and mn.stride(0) == scale.stride(0), "mn/scale shape")
+    table = tables.quantize_table(alpha, grouped.dtype, dev)
+    lib = load()
+    st = lib.muzero_quantize_rows(ptr(grouped), DTYPE_ENUM[grouped.dtype], n, grouped.stride(0) if n else GROUP,
+                                  ptr(packed_q), packed_q.stride(0) if n else _qbytes(bits),
+                                  ptr(mn), ptr(scale), DTYPE_ENUM[mn.dtype], mn.stride(0) if n else 1,
+                                  int(bits), float(eps), ptr(table), stream_ptr(dev))
+    check(st, "muzero_quantize_rows")
+
+
+def _block_checks(x: torch.Tensor, packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor, bits: int):
+    dev = _on_gpu(x, packed, mn, scale)
+    _require(x.dim() == 4 and x.stride(3) == 1, "block must be [B, H, T, D] with contiguous D")
+    _require(x.dtype in DTYPE_ENUM, f"unsupported input dtype {x.dtype}")
+    _require(packed.dtype == torch.uint8 and packed.dim() == 5, "packed must be uint8 5-d")
+    _require(mn.dtype == scale.dtype and mn.dtype in DTYPE_ENUM, "mn/scale dtype")
+    _require(mn.stride() == scale.stride() and mn.shape == scale.shape, "mn/scale layout")
+    _require(1 <= bits <= 8, "bits must be in 1..8")
+    return dev
+
+
+def quantize_key_block_into(keys: torch.Tensor, bits: int, alpha: float, eps: float,
+                            packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor) -> None:
+    """Quantize ``keys[B,H,T,D]`` (T % 64 == 0) into the key layout views
+    ``packed[B,H,T/64,D,qb]``, ``mn/scale[B,H,T/64,D,1]`` (reference ``layer.py:271-285``)."""
+    dev = _block_checks(keys, packed, mn, scale, bits)
+    b, h, t, d = keys.shape
+    qb = _qbytes(bits)
+    _require(t % GROUP == 0, "key block length must be a multiple of 64")
+    nsg = t // GROUP
+    _require(tuple(packed.shape) == (b, h, nsg, d, qb), f"packed shape {tuple(packed.shape)}")
+    _require(packed.stride(4) == 1 and packed.stride(3) == qb and packed.stride(2) == d * qb, "packed inner layout")
+    _require(tuple(mn.shape) == (b, h, nsg, d, 1), f"meta shape {tuple(mn.shape)}")
+    _require(mn.stride(3) == 1 and mn.stride(2) == d, "meta inner layout")
+    table = tables.quantize_table(alpha, keys.dtype, dev)
+    st = load().muzero_quantize_keys(ptr(keys), DTYPE_ENUM[keys.dtype], b, h, t, d,
+                                     keys.stride(0), keys.stride(1), keys.stride(2),
+                                     ptr(packed), packed.stride(0), packed.stride(1),
+                                     ptr(mn), ptr(scale), DTYPE_ENUM[mn.dtype], mn.stride(0), mn.stride(1),
+                                     int(bits), float(eps), ptr(table), stream_ptr(dev))
+    check(st, "muzero_quantize_keys")
+
+
+def quantize_value_block_into(values: torch.Tensor, bits: int, alpha: float, eps: float,
+                              packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor) -> None:
+    """Quantize ``values[B,H,T,D]`` into the value layout views ``packed[B,H,T,ng,qb]``,
+    ``mn/scale[B,H,T,ng,1]`` (reference ``layer.py:287-301``)."""
+    dev = _block_checks(values, packed, mn, scale, bits)
+    b, h, t, d = values.shape
+    qb = _qbytes(bits)
+    ng = (d + GROUP - 1) // GROUP
+    _require(tuple(packed.shape) == (b, h, t, ng, qb), f"packed shape {tuple(packed.shape)}")
+    _require(packed.stride(4) == 1 and packed.stride(3) == qb and packed.stride(2) == ng * qb, "packed inner layout")
+    _require(tuple(mn.shape) == (b, h, t, ng, 1), f"meta shape {tuple(mn.shape)}")
+    _require(mn.stride(3) == 1 and mn.stride(2) == ng, "meta inner layout")
+    table = tables.quantize_table(alpha, values.dtype, dev)
+    st = load().muzero_quantize_values(ptr(values), DTYPE_ENUM[values.dtype], b, h, t, d,
+                                       values.stride(0), values.stride(1), values.stride(2),
+                                       ptr(packed), packed.stride(0), packed.stride(1),
+                                       ptr(mn), ptr(scale), DTYPE_ENUM[mn.dtype], mn.stride(0), mn.stride(1),
+                                       int(bits), float(eps), ptr(table), stream_ptr(dev))
+    check(st, "muzero_quantize_values")
+
+
+# --------------------------------------------------------------------------- dequantize
+
+def mu_zero_dequantize_cuda(packed_q: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor, output: torch.Tensor,
+                            bits: int, alpha: float) -> None:
+    """Dequantize ``packed_q[N, qb]`` into ``output[N, 64]`` in place (reference ``loader.py:43-45``)."""
+    dev = _on_gpu(packed_q, mn, scale, output)
+    n = packed_q.shape[0]
+    _require(packed_q.dtype == torch.uint8 and packed_q.dim() == 2 and packed_q.shape[1] == _qbytes(bits)
+             and packed_q.stride(1) == 1, "packed_q must be uint8 [N, 8*bits]")
+    _require(output.dim() == 2 and tuple(output.shape) == (n, GROUP) and output.stride(1) == 1, "output [N, 64]")
+    _require(output.dtype in DTYPE_ENUM and mn.dtype in DTYPE_ENUM and mn.dtype == scale.dtype, "dtypes")
+    _require(mn.shape[0] == n and mn.stride(0) == scale.stride(0), "mn/scale shape")
+    e = tables.device_table("expm1", alpha, dev)
+    st = load().muzero_dequantize_rows(ptr(packed_q), n, packed_q.stride(0) if n else _qbytes(bits),
+                                       ptr(mn), ptr(scale), DTYPE_ENUM[mn.dtype], mn.stride(0) if n else 1,
+                                       ptr(output), DTYPE_ENUM[output.dtype], output.stride(0) if n else GROUP,
+                                       int(bits), ptr(e), stream_ptr(dev))
+    check(st, "muzero_dequantize_rows")
+
+
+# --------------------------------------------------------------------------- decode attention
+
+def prepare_mask(attention_mask: torch.Tensor | None, batch: int, length: int) -> torch.Tensor | None:
+    """HF 4-d mask ``[B, 1, q, >=L]`` (additive float or bool keep-mask) -> additive fp32 ``[B, L]``."""
+    if attention_mask is None:
+        return None
+    m = attention_mask
+    if m.dim() == 4:
+        m = m[:, 0, -1, :length]
+    elif m.dim() == 2:
+        m = m[:, :length]
+    else:
+        raise MuZeroHipError(f"unsupported attention mask rank {attention_mask.dim()}")
+    _require(m.shape[-1] == length, f"mask covers {m.shape[-1]} positions, cache holds {length}")
+    if m.dtype == torch.bool:
+        m = torch.zeros(m.shape, dtype=torch.float32, device=m.device).masked_fill_(~m, float("-inf"))
+    m = m.to(torch.float32).expand(batch, length).contiguous()
+    return m
+
+
+class DecodePlan:
+    """Validated, ready-to-launch arguments of one fused decode-attention call.
+
+    Building the plan checks every layout on the host and allocates the output
+    and the split workspace; :meth:`run` then launches with no further Python
+    work, so a caller that repeats a call (benchmarks, a fixed-shape decode
+    loop) pays the argument marshalling once.
+    """
+
+    def __init__(self, query: torch.Tensor, *, bits: int, n_groups: int,
+                 k_packed: torch.Tensor | None, k_mn: torch.Tensor | None, k_scale: torch.Tensor | None,
+                 v_packed: torch.Tensor | None, v_mn: torch.Tensor | None, v_scale: torch.Tensor | None,
+                 k_res: torch.Tensor | None, v_res: torch.Tensor | None,
+                 alpha_key: float, alpha_value: float, scaling: float,
+                 attention_mask: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None, n_split: int = 0):
+        dev = _on_gpu(query, k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, k_res, v_res, attention_mask)
+        self.device = dev
+        _require(query.dim() == 4 and query.shape[2] == 1, "query must be [B, Hq, 1, D]")
+        _require(query.dtype in (torch.bfloat16, torch.float16), "query dtype must be bf16 or fp16")
+        b, hq, _, d = query.shape
+        q = query if (query.stride(3) == 1 and query.stride(1) % 8 == 0 and query.stride(0) % 8 == 0
+                      and query.data_ptr() % 16 == 0) else query.contiguous()
+        r = 0 if k_res is None else k_res.shape[2]
+        if k_res is not None:
+            _require(v_res is not None and v_res.shape[2] == r, "residual K/V lengths differ")
+            hkv = k_res.shape[1]
+        else:
+            _require(k_packed is not None, "no prefix and no residual")
+            hkv = k_packed.shape[1]
+        _require(hq % hkv == 0, "q heads must be a multiple of kv heads")
+        n_rep = hq // hkv
+        meta_dtype = 0
+        keep = [q]
+        a = _lib.DecodeArgs()
+        if n_groups > 0:
+            qb = _qbytes(bits)
+            ng = (d + GROUP - 1) // GROUP
+            _require(k_packed.shape[:2] == (b, hkv) and v_packed.shape[:2] == (b, hkv), "packed batch/head dims")
+            _require(k_packed.shape[2] >= n_groups and tuple(k_packed.shape[3:]) == (d, qb), "packed K layout")
+            _require(k_packed.stride(4) == 1 and k_packed.stride(3) == qb and k_packed.stride(2) == d * qb,
+                     "packed K strides")
+            _require(k_mn.shape[:3] == k_packed.shape[:3] and k_mn.shape[3] == d, "K meta shape")
+            _require(k_mn.stride(3) == 1 and k_mn.stride(2) == d and k_mn.stride() == k_scale.stride(),
+                     "K meta strides")
+            _require(v_packed.shape[2] >= GROUP * n_groups and tuple(v_packed.shape[3:]) == (ng, qb),
+                     "packed V layout")
+            _require(v_packed.stride(4) == 1 and v_packed.stride(3) == qb and v_packed.stride(2) == ng * qb,
+                     "packed V strides")
+            _require(v_mn.shape[:3] == v_packed.shape[:3] and v_mn.shape[3] == ng, "V meta shape")
+            _require(v_mn.stride(3) == 1 and v_mn.stride(2) == ng and v_mn.stride() == v_scale.stride(),
+                     "V meta strides")
+            _require(k_mn.dtype == k_scale.dtype == v_mn.dtype == v_scale.dtype and k_mn.dtype in DTYPE_ENUM,
+                     "meta dtypes")
+            meta_dtype = DTYPE_ENUM[k_mn.dtype]
+            ek = tables.device_table("expm1", alpha_key, dev)
+            ev = tables.device_table("expm1", alpha_value, dev)
+            a.k_packed, a.kp_sb, a.kp_sh = ptr(k_packed), k_packed.stride(0), k_packed.stride(1)
+            a.k_mn, a.k_scale, a.km_sb, a.km_sh = ptr(k_mn), ptr(k_scale), k_mn.stride(0), k_mn.stride(1)
+            a.v_packed, a.vp_sb, a.vp_sh = ptr(v_packed), v_packed.stride(0), v_packed.stride(1)
+            a.v_mn, a.v_scale, a.vm_sb, a.vm_sh = ptr(v_mn), ptr(v_scale), v_mn.stride(0), v_mn.stride(1)
+            a.e_key, a.e_value = ptr(ek), ptr(ev)
+            keep += [k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, ek, ev]
+
+        def _res(t):
+            _require(t.dtype == query.dtype, "residual dtype must match the query dtype")
+            _require(t.shape[0] == b and t.shape[1] == hkv and t.shape[3] == d, "residual shape")
+            if t.stride(3) != 1 or any(s_ % 8 for s_ in t.stride()[:3]) or t.data_ptr() % 16:
+                t = t.contiguous()
+            return t
+
+        if r > 0:
+            k_res, v_res = _res(k_res), _res(v_res)
+            a.k_res, a.kr_sb, a.kr_sh, a.kr_st = ptr(k_res), k_res.stride(0), k_res.stride(1), k_res.stride(2)
+            a.v_res, a.vr_sb, a.vr_sh, a.vr_st = ptr(v_res), v_res.stride(0), v_res.stride(1), v_res.stride(2)
+            keep += [k_res, v_res]
+        length = GROUP * n_groups + r
+        mask = prepare_mask(attention_mask, b, length)
+        if mask is not None:
+            a.mask, a.mask_sb = ptr(mask), mask.stride(0)
+            keep.append(mask)
+        if out is None:
+            out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=dev)
+        _require(out.dtype == query.dtype and tuple(out.shape) == (b, 1, hq, d) and out.stride(3) == 1,
+                 "out layout")
+        a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = b, hkv, n_rep, d, int(bits)
+        a.n_groups, a.n_residual = int(n_groups), int(r)
+        a.meta_dtype, a.io_dtype = meta_dtype, DTYPE_ENUM[query.dtype]
+        a.scaling = float(scaling)
+        a.query, a.q_sb, a.q_sh = ptr(q), q.stride(0), q.stride(1)
+        a.out, a.out_sb, a.out_sh = ptr(out), out.stride(0), out.stride(2)
+        a.n_split = int(n_split)
+        lib = load()
+        ns = ctypes.c_int(0)
+        need = lib.muzero_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(ns))
+        _require(need >= 0, "decode arguments rejected (head_dim must be 64 or 128, n_rep <= 16)")
+        ws = torch.empty((max(int(need), 4) + 3) // 4, dtype=torch.float32, device=dev)
+        a.workspace, a.workspace_bytes = ptr(ws), int(need)
+        self.args = a
+        self.n_split = ns.value
+        self.out = out
+        self.workspace = ws
+        self._keep = keep
+        self._lib = lib
+        self._argp = ctypes.byref(a)
+
+    def run(self) -> torch.Tensor:
+        check(self._lib.muzero_decode_attention(self._argp, stream_ptr(self.device)), "muzero_decode_attention")
+        return self.out
+
+    def partials(self) -> None:
+        check(self._lib.muzero_decode_partials(self._argp, stream_ptr(self.device)), "muzero_decode_partials")
+
+    def combine(self) -> torch.Tensor:
+        check(self._lib.muzero_decode_combine(self._argp, stream_ptr(self.device)), "muzero_decode_combine")
+        return self.out
+
+
+def mu_zero_decode_attention_hip(query: torch.Tensor, **kwargs) -> torch.Tensor:
+    """Fused decode attention; returns ``[B, 1, Hq, D]`` in the query dtype.
+
+    ``query [B, Hq, 1, D]``; packed prefix in the reference cache layouts
+    covering ``64 * n_groups`` tokens (tensors may be longer along the token
+    axis: preallocated storage); residual ``[B, Hkv, R, D]`` strided views;
+    optional HF attention mask.  Replaces reference ``attention.py:48-295``
+    (qk -> softmax -> av -> residual merge).  Keyword arguments are those of
+    :class:`DecodePlan`.
+    """
+    return DecodePlan(query, **kwargs).run()
+
+
+def mu_zero_qk_cuda(*args, **kwargs):  # pragma: no cover - documented gap
+    raise MuZeroHipError("separate qk launch is not built: the decode hook uses the fused "
+                         "mu_zero_decode_attention_hip (qk+softmax+av in one pass)")
+
+
+def mu_zero_av_cuda(*args, **kwargs):  # pragma: no cover - documented gap
+    raise MuZeroHipError("separate av launch is not built: the decode hook uses the fused "
+                         "mu_zero_decode_attention_hip (qk+softmax+av in one pass)")
