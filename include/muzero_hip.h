@@ -113,12 +113,14 @@ int muzero_dequantize_rows(const uint8_t* packed, int64_t nrows, int64_t packed_
  * V_mn/V_scale [B,Hkv,>=64*n_groups,ng].  Residual K/V: [B,Hkv,R,D] strided
  * views (last dim contiguous).  Strides are in elements, except packed
  * tensors (bytes).  mask: optional additive fp32 [B, L] (L = 64*n_groups+R),
- * row stride mask_sb.  Output [B, Hq, D] (out_sb, out_sh) in io_dtype.
+ * row stride mask_sb.  Output [B, Hq, D] (out_sb, out_sh) in out_dtype
+ * (io_dtype, i.e. the reference's output dtype, or fp32).
  */
 typedef struct mz_decode_args {
   int batch, kv_heads, n_rep, head_dim, bits;
   int n_groups, n_residual;
   int meta_dtype, io_dtype;
+  int out_dtype;  /* io_dtype, or MZ_F32 for an unrounded fp32 output */
   float scaling;
   const void* query; int64_t q_sb, q_sh;
   const uint8_t* k_packed; int64_t kp_sb, kp_sh;

@@ -35,7 +35,7 @@ class DecodeArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_int), ("kv_heads", c_int), ("n_rep", c_int), ("head_dim", c_int), ("bits", c_int),
         ("n_groups", c_int), ("n_residual", c_int),
-        ("meta_dtype", c_int), ("io_dtype", c_int),
+        ("meta_dtype", c_int), ("io_dtype", c_int), ("out_dtype", c_int),
         ("scaling", c_float),
         ("query", c_vp), ("q_sb", c_i64), ("q_sh", c_i64),
         ("k_packed", c_vp), ("kp_sb", c_i64), ("kp_sh", c_i64),

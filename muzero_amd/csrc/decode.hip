@@ -14,9 +14,13 @@
 //   K tile -> LDS [64 tokens][D] in the io dtype (dequantized exactly as the
 //   reference's _dequantize_rows_torch and rounded to the layer dtype, or
 //   copied from the residual), QK^T with MFMA (A = Q rows, B = K tile),
-//   online softmax on the MFMA accumulator layout, P -> LDS,
-//   V tile -> LDS [D][64] (transposed so an MFMA B operand is 8 consecutive
-//   tokens of one channel), acc += P V with MFMA.
+//   online softmax on the MFMA accumulator layout, P -> LDS in fp16,
+//   V tile -> LDS [D][64] in fp16 (transposed so an MFMA B operand is 8
+//   consecutive tokens of one channel), acc += P V with an fp16 MFMA.
+// P V runs in fp16 whatever the io dtype: weights keep 11 mantissa bits (bf16
+// weights cost up to 2^-9 relative each, too coarse for peaked softmax rows),
+// and every bf16 value in fp16's normal range converts to fp16 exactly.  The
+// softmax denominator sums the same rounded weights the numerator uses.
 #include "common.hpp"
 
 namespace mz {
@@ -96,9 +100,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
   const float* EK = a.e_key;
   const float* EV = a.e_value;
   if constexpr (kLdsE) {
-    for (int i = threadIdx.x; i < L::E_FLOATS; i += 256) {
-      eK[i] = a.e_key[i];
-      eV[i] = a.e_value[i];
+    // the expm1 tables exist only when there is a quantized prefix
+    if (a.n_groups > 0) {
+      for (int i = threadIdx.x; i < L::E_FLOATS; i += 256) {
+        eK[i] = a.e_key[i];
+        eV[i] = a.e_value[i];
+      }
     }
     __syncthreads();
     EK = eK;
@@ -216,8 +223,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = (s[j][i] == -INFINITY) ? 0.f : __expf(s[j][i] - m_run[i]);
-        psum[i] += p;
-        pb[(4 * g + i) * L::P_LD + 16 * j + n] = M::cvt(p);
+        const uint16_t ph = f2h(p);
+        psum[i] += h2f(ph);
+        pb[(4 * g + i) * L::P_LD + 16 * j + n] = ph;
       }
     }
 #pragma unroll
@@ -251,7 +259,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
           for (int c = 0; c < 64; ++c) {
             if (64 * vg + c < D) {
               const uint32_t q = unpack_code<BITS>(bytes, c);
-              kv[(64 * vg + c) * L::V_LD + t] = M::cvt(deq_value(r, q, EV));
+              kv[(64 * vg + c) * L::V_LD + t] = f2h(M::load(M::cvt(deq_value(r, q, EV))));
             }
           }
         }
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
           const u32x4 v = *(const u32x4*)(src + c);
           const uint16_t* hv = (const uint16_t*)&v;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kv[(c + e) * L::V_LD + t] = hv[e];
+          for (int e = 0; e < 8; ++e) kv[(c + e) * L::V_LD + t] = IO == MZ_F16 ? hv[e] : f2h(bf2f(hv[e]));
         }
       } else {
 #pragma unroll
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
 #pragma unroll
       for (int jn = 0; jn < D / 16; ++jn) {
         const u32x4 vb = *(const u32x4*)(kv + (16 * jn + n) * L::V_LD + 32 * ks + 8 * g);
-        acc[jn] = M::run(pa, vb, acc[jn]);
+        acc[jn] = Mfma<MZ_F16>::run(pa, vb, acc[jn]);
       }
     }
     wave_lds_sync();
@@ -325,9 +333,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
 }
 
 // Merge the splits of one (batch, q-head): out = sum_s e^{m_s-M} acc_s / sum_s e^{m_s-M} l_s.
-template <int D, int IO>
+template <int D>
 __global__ __launch_bounds__(D) void decode_combine_kernel(const float* __restrict__ ws, int n_split, int Hq,
-                                                           void* out, int64_t out_sb, int64_t out_sh) {
+                                                           void* out, int out_dtype, int64_t out_sb, int64_t out_sh) {
   const int bh = blockIdx.x;
   const int c = threadIdx.x;
   const float* base = ws + (int64_t)bh * n_split * (D + 2);
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(const float* __restri
   }
   const float o = den > 0.f ? num / den : 0.f;
   const int b = bh / Hq, h = bh - b * Hq;
-  ((uint16_t*)out)[b * out_sb + (int64_t)h * out_sh + c] = Mfma<IO>::cvt(o);
+  store_val(out, b * out_sb + (int64_t)h * out_sh + c, o, out_dtype);
 }
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
@@ -369,6 +377,7 @@ static int check_args(const mz_decode_args* a) {
   if (a->bits < 1 || a->bits > 8) return MZ_EINVAL;
   if (a->io_dtype != MZ_BF16 && a->io_dtype != MZ_F16) return MZ_EINVAL;
   if (a->meta_dtype != MZ_F16 && a->meta_dtype != MZ_BF16 && a->meta_dtype != MZ_F32) return MZ_EINVAL;
+  if (a->out_dtype != a->io_dtype && a->out_dtype != MZ_F32) return MZ_EINVAL;
   if (a->head_dim != 64 && a->head_dim != 128) return MZ_EUNSUPPORTED;
   if (a->n_rep > 16) return MZ_EUNSUPPORTED;
   if (a->batch == 0) return MZ_OK;
@@ -431,8 +440,8 @@ static int launch_combine(const mz_decode_args* a, hipStream_t s) {
   const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (D + 2) * (int64_t)sizeof(float);
   if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
   const int Hq = a->kv_heads * a->n_rep;
-  hipLaunchKernelGGL((decode_combine_kernel<D, IO>), dim3(a->batch * Hq), dim3(D), 0, s,
-                     (const float*)a->workspace, ns, Hq, a->out, a->out_sb, a->out_sh);
+  hipLaunchKernelGGL((decode_combine_kernel<D>), dim3(a->batch * Hq), dim3(D), 0, s,
+                     (const float*)a->workspace, ns, Hq, a->out, a->out_dtype, a->out_sb, a->out_sh);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MZ_OK : (int)e;
 }

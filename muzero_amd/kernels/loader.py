@@ -189,7 +189,7 @@ class DecodePlan:
                  k_res: torch.Tensor | None, v_res: torch.Tensor | None,
                  alpha_key: float, alpha_value: float, scaling: float,
                  attention_mask: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None, n_split: int = 0):
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, n_split: int = 0):
         dev = _on_gpu(query, k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, k_res, v_res, attention_mask)
         self.device = dev
         _require(query.dim() == 4 and query.shape[2] == 1, "query must be [B, Hq, 1, D]")
@@ -229,14 +229,16 @@ class DecodePlan:
             _require(k_mn.dtype == k_scale.dtype == v_mn.dtype == v_scale.dtype and k_mn.dtype in DTYPE_ENUM,
                      "meta dtypes")
             meta_dtype = DTYPE_ENUM[k_mn.dtype]
-            ek = tables.device_table("expm1", alpha_key, dev)
-            ev = tables.device_table("expm1", alpha_value, dev)
             a.k_packed, a.kp_sb, a.kp_sh = ptr(k_packed), k_packed.stride(0), k_packed.stride(1)
             a.k_mn, a.k_scale, a.km_sb, a.km_sh = ptr(k_mn), ptr(k_scale), k_mn.stride(0), k_mn.stride(1)
             a.v_packed, a.vp_sb, a.vp_sh = ptr(v_packed), v_packed.stride(0), v_packed.stride(1)
             a.v_mn, a.v_scale, a.vm_sb, a.vm_sh = ptr(v_mn), ptr(v_scale), v_mn.stride(0), v_mn.stride(1)
-            a.e_key, a.e_value = ptr(ek), ptr(ev)
-            keep += [k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, ek, ev]
+            keep += [k_packed, k_mn, k_scale, v_packed, v_mn, v_scale]
+        # expm1 tables are always passed (the kernel reads them only for a quantized prefix)
+        ek = tables.device_table("expm1", alpha_key, dev)
+        ev = tables.device_table("expm1", alpha_value, dev)
+        a.e_key, a.e_value = ptr(ek), ptr(ev)
+        keep += [ek, ev]
 
         def _res(t):
             _require(t.dtype == query.dtype, "residual dtype must match the query dtype")
@@ -256,12 +258,12 @@ class DecodePlan:
             a.mask, a.mask_sb = ptr(mask), mask.stride(0)
             keep.append(mask)
         if out is None:
-            out = torch.empty((b, 1, hq, d), dtype=query.dtype, device=dev)
-        _require(out.dtype == query.dtype and tuple(out.shape) == (b, 1, hq, d) and out.stride(3) == 1,
-                 "out layout")
+            out = torch.empty((b, 1, hq, d), dtype=query.dtype if out_dtype is None else out_dtype, device=dev)
+        _require(out.dtype in (query.dtype, torch.float32) and tuple(out.shape) == (b, 1, hq, d)
+                 and out.stride(3) == 1, "out must be [B, 1, Hq, D] in the query dtype or fp32")
         a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = b, hkv, n_rep, d, int(bits)
         a.n_groups, a.n_residual = int(n_groups), int(r)
-        a.meta_dtype, a.io_dtype = meta_dtype, DTYPE_ENUM[query.dtype]
+        a.meta_dtype, a.io_dtype, a.out_dtype = meta_dtype, DTYPE_ENUM[query.dtype], DTYPE_ENUM[out.dtype]
         a.scaling = float(scaling)
         a.query, a.q_sb, a.q_sh = ptr(q), q.stride(0), q.stride(1)
         a.out, a.out_sb, a.out_sh = ptr(out), out.stride(0), out.stride(2)

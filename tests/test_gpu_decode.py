@@ -1,9 +1,13 @@
 """HIP decode attention parity (GPU) against the fp64 dequantize-then-attend oracle.
 
 Inputs are quantized by the CPU oracle (bit-identical to the reference cache,
-see test_oracle.py), the same bytes are handed to the HIP kernel through the
-C ABI, and the bf16 output must be within 2e-3 max-abs / 1e-3 mean-abs of the
-oracle's fp64 attention over the dequantized (bf16) prefix + bf16 residual.
+see test_oracle.py) and the same bytes are handed to the HIP kernel through
+the C ABI.  The oracle is fp64 softmax attention over the dequantized (bf16)
+prefix + bf16 residual.  Tolerances: 2e-3 max-abs and
+1e-3 mean-abs.  They are checked on the kernel's fp32 output (the kernel's own
+error), and on its bf16 output with half a bf16 ulp of the exact value added
+to the max bound: rounding the exact fp64 answer itself to bf16 already moves
+outputs near 1.0 by up to 3.9e-3, so no bf16 result can meet 2e-3 there.
 """
 
 import math
@@ -19,8 +23,15 @@ MAX_ABS = 2e-3
 MEAN_ABS = 1e-3
 
 
+def _half_ulp_bf16(x: torch.Tensor) -> torch.Tensor:
+    """Half the bf16 spacing at |x| (8 significant bits)."""
+    e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -126)))
+    return torch.pow(2.0, e - 8)
+
+
 def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n_split=0,
               dtype=torch.bfloat16, meta=torch.float16, alpha_k=2.0, alpha_v=2.0, outliers=4):
+    """Returns (fp32-output max err, mean err, io-dtype output, fp64 oracle)."""
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=seed, outliers=outliers, dtype=dtype)
     am = None
@@ -33,15 +44,25 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
                                      residual=residual, amax_dtype=meta, attention_mask=am)
     lq = st["lq"]
     dev = lambda t: None if t is None else t.to(DEV)
-    out = L.mu_zero_decode_attention_hip(
-        dev(q), bits=bits, n_groups=lq // 64,
-        k_packed=dev(st.get("packed_k")), k_mn=dev(st.get("k_mn")), k_scale=dev(st.get("k_scale")),
-        v_packed=dev(st.get("packed_v")), v_mn=dev(st.get("v_mn")), v_scale=dev(st.get("v_scale")),
-        k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=alpha_k, alpha_value=alpha_v,
-        scaling=d ** -0.5, attention_mask=dev(am), n_split=n_split)
+    kw = dict(bits=bits, n_groups=lq // 64,
+              k_packed=dev(st.get("packed_k")), k_mn=dev(st.get("k_mn")), k_scale=dev(st.get("k_scale")),
+              v_packed=dev(st.get("packed_v")), v_mn=dev(st.get("v_mn")), v_scale=dev(st.get("v_scale")),
+              k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=alpha_k, alpha_value=alpha_v,
+              scaling=d ** -0.5, attention_mask=dev(am), n_split=n_split)
+    qd = dev(q)
+    out32 = L.DecodePlan(qd, out_dtype=torch.float32, **kw).run()
+    out = L.DecodePlan(qd, **kw).run()
     torch.cuda.synchronize()
-    err = (out.cpu().double() - exact).abs()
-    return err.max().item(), err.mean().item(), out
+    out32, out = out32.cpu(), out.cpu()
+    err = (out32.double() - exact).abs()
+    # the io-dtype output is the fp32 output rounded once
+    assert torch.equal(out, out32.to(dtype))
+    if dtype == torch.bfloat16:
+        err16 = (out.double() - exact).abs()
+        bound = MAX_ABS + _half_ulp_bf16(exact)
+        assert bool((err16 <= bound).all()), (err16 - bound).max().item()
+        assert err16.mean().item() < MEAN_ABS
+    return err.max().item(), err.mean().item(), out, exact
 
 
 CASES = [
@@ -64,35 +85,35 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_b{}_R{}".format(*c))
 def test_decode_matches_oracle(case):
-    mx, mean, _ = _run_case(*case)
+    mx, mean, _, _ = _run_case(*case)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
 def test_decode_with_mask():
-    mx, mean, _ = _run_case(2, 2, 4, 128, 900, 4, 128, mask=True)
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 4, 128, mask=True)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
 @pytest.mark.parametrize("n_split", [1, 2, 3, 7, 64])
 def test_decode_split_invariance(n_split):
     """The cross-split combine gives the same answer for any split count."""
-    mx, mean, out = _run_case(1, 2, 4, 128, 2048, 4, 128, n_split=n_split)
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, 2048, 4, 128, n_split=n_split)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
 def test_decode_fp16_and_meta_dtypes():
     for dtype, meta in ((torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
                         (torch.bfloat16, torch.float32)):
-        mx, mean, _ = _run_case(1, 2, 4, 128, 600, 4, 128, dtype=dtype, meta=meta)
+        mx, mean, _, _ = _run_case(1, 2, 4, 128, 600, 4, 128, dtype=dtype, meta=meta)
         assert mx < MAX_ABS and mean < MEAN_ABS, (dtype, meta, mx, mean)
 
 
 def test_decode_alpha_values():
-    mx, mean, _ = _run_case(1, 2, 4, 128, 600, 2, 128, alpha_k=16.0, alpha_v=4.0)
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, 600, 2, 128, alpha_k=16.0, alpha_v=4.0)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
 def test_decode_deterministic():
-    _, _, o1 = _run_case(2, 2, 4, 128, 1500, 4, 128)
-    _, _, o2 = _run_case(2, 2, 4, 128, 1500, 4, 128)
+    _, _, o1, _ = _run_case(2, 2, 4, 128, 1500, 4, 128)
+    _, _, o2, _ = _run_case(2, 2, 4, 128, 1500, 4, 128)
     assert torch.equal(o1, o2)
