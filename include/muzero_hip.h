@@ -131,10 +131,20 @@ typedef struct mz_decode_args {
   const void* v_res; int64_t vr_sb, vr_sh, vr_st;
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
+  /* 4-bit (P, N) fold tables for alpha_key / alpha_value: 16 x 16 pairs of
+   * fp16 (P, N) packed in uint32, see muzero_amd/tables.py ("fold4").  Needed
+   * by the 4-bit fast path; may be null (the generic path is used then). */
+  const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;
-  int n_split;  /* 0 = let the library choose */
+  int n_split;      /* 0 = let the library choose */
+  int kernel_path;  /* MZ_PATH_AUTO, or force MZ_PATH_EXACT / MZ_PATH_FOLD */
 } mz_decode_args;
+
+/* kernel paths of muzero_decode_attention: AUTO uses the 4-bit fold kernel
+ * when it applies (bits 4, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
+ * and the exact-dequantize kernel otherwise. */
+enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments
  * (and the split count it will use, written to *n_split_out if non-null). */

@@ -46,10 +46,14 @@ class DecodeArgs(ctypes.Structure):
         ("v_res", c_vp), ("vr_sb", c_i64), ("vr_sh", c_i64), ("vr_st", c_i64),
         ("mask", c_vp), ("mask_sb", c_i64),
         ("e_key", c_vp), ("e_value", c_vp),
+        ("fold_k", c_vp), ("fold_v", c_vp),
         ("out", c_vp), ("out_sb", c_i64), ("out_sh", c_i64),
         ("workspace", c_vp), ("workspace_bytes", c_i64),
         ("n_split", c_int),
+        ("kernel_path", c_int),
     ]
+
+MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2
 
 
 # exported symbol -> (restype, argtypes)

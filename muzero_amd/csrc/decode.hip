@@ -21,40 +21,9 @@
 // weights cost up to 2^-9 relative each, too coarse for peaked softmax rows),
 // and every bf16 value in fp16's normal range converts to fp16 exactly.  The
 // softmax denominator sums the same rounded weights the numerator uses.
-#include "common.hpp"
+#include "decode_common.hpp"
 
 namespace mz {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <int IO> struct Mfma;
-template <> struct Mfma<MZ_BF16> {
-  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                    0, 0, 0);
-  }
-  static __device__ __forceinline__ uint16_t cvt(float x) { return f2bf(x); }
-  static __device__ __forceinline__ float load(uint16_t h) { return bf2f(h); }
-};
-template <> struct Mfma<MZ_F16> {
-  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                   0, 0);
-  }
-  static __device__ __forceinline__ uint16_t cvt(float x) { return f2h(x); }
-  static __device__ __forceinline__ float load(uint16_t h) { return h2f(h); }
-};
-
-// Orders LDS writes and reads of one wave (the compiler must not move the
-// reads of other lanes' data above the writes).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 constexpr int kTile = 64;
 constexpr int kWaves = 4;
@@ -71,8 +40,6 @@ struct Lds {
   static constexpr int E_FLOATS = 528;  // expm1 table rows for bins <= 31 (bits <= 5)
   static constexpr size_t BYTES = (size_t)kWaves * WAVE_HALVES * 2 + 2 * E_FLOATS * 4;
 };
-
-__device__ __forceinline__ float meta_load(const void* p, int64_t i, int dt) { return load_any(p, i, dt); }
 
 template <int D, int BITS, int IO>
 __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args a, int tiles_per_split, int n_split) {
@@ -354,6 +321,10 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(const float* __restri
   store_val(out, b * out_sb + (int64_t)h * out_sh + c, o, out_dtype);
 }
 
+bool fold_supported(const mz_decode_args* a);
+int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
+int fold_launch_partials(const mz_decode_args* a, hipStream_t s);
+
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + kTile - 1) / kTile;
   if (n_tiles <= 0) { *tiles_per_split = 1; return 1; }
@@ -378,6 +349,7 @@ static int check_args(const mz_decode_args* a) {
   if (a->io_dtype != MZ_BF16 && a->io_dtype != MZ_F16) return MZ_EINVAL;
   if (a->meta_dtype != MZ_F16 && a->meta_dtype != MZ_BF16 && a->meta_dtype != MZ_F32) return MZ_EINVAL;
   if (a->out_dtype != a->io_dtype && a->out_dtype != MZ_F32) return MZ_EINVAL;
+  if (a->kernel_path < MZ_PATH_AUTO || a->kernel_path > MZ_PATH_FOLD) return MZ_EINVAL;
   if (a->head_dim != 64 && a->head_dim != 128) return MZ_EUNSUPPORTED;
   if (a->n_rep > 16) return MZ_EUNSUPPORTED;
   if (a->batch == 0) return MZ_OK;
@@ -397,14 +369,26 @@ static int check_args(const mz_decode_args* a) {
   return MZ_OK;
 }
 
+// Which kernel runs and with how many splits (both kernels share the
+// workspace layout and the combine kernel).
+static bool use_fold(const mz_decode_args* a) {
+  if (a->kernel_path == MZ_PATH_EXACT) return false;
+  return fold_supported(a);
+}
+
+static int plan_split(const mz_decode_args* a, int* tps) {
+  return use_fold(a) ? fold_choose_split(a, tps) : choose_split(a, tps);
+}
+
 }  // namespace mz
 
 using namespace mz;
 
 extern "C" int64_t muzero_decode_workspace_bytes(const mz_decode_args* a, int* n_split_out) {
   if (check_args(a) != MZ_OK) return -1;
+  if (a->kernel_path == MZ_PATH_FOLD && !fold_supported(a)) return -1;
   int tps;
-  const int ns = choose_split(a, &tps);
+  const int ns = plan_split(a, &tps);
   if (n_split_out) *n_split_out = ns;
   return (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
 }
@@ -413,6 +397,7 @@ template <int D, int IO>
 static int launch_partials(const mz_decode_args* a, hipStream_t s) {
   int tps;
   const int ns = choose_split(a, &tps);
+  static_assert(D == 64 || D == 128, "head_dim");
   const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (D + 2) * (int64_t)sizeof(float);
   if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
   const dim3 grid(ns, a->kv_heads, a->batch);
@@ -436,7 +421,7 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s) {
 template <int D, int IO>
 static int launch_combine(const mz_decode_args* a, hipStream_t s) {
   int tps;
-  const int ns = choose_split(a, &tps);
+  const int ns = plan_split(a, &tps);
   const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (D + 2) * (int64_t)sizeof(float);
   if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
   const int Hq = a->kv_heads * a->n_rep;
@@ -458,6 +443,14 @@ extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t strea
   const int st = decode_check_launchable(a);
   if (st) return st == 1 ? MZ_OK : st;
   hipStream_t s = (hipStream_t)stream;
+  if (a->kernel_path == MZ_PATH_FOLD && !fold_supported(a)) return MZ_EUNSUPPORTED;
+  if (use_fold(a)) {
+    int tps;
+    const int ns = fold_choose_split(a, &tps);
+    const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
+    if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
+    return fold_launch_partials(a, s);
+  }
   if (a->head_dim == 128)
     return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s) : launch_partials<128, MZ_F16>(a, s);
   return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16>(a, s) : launch_partials<64, MZ_F16>(a, s);

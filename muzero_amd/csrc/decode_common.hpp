@@ -1,0 +1,47 @@
+// Shared pieces of the decode-attention kernels (gfx950, wave64, MFMA 16x16x32).
+#pragma once
+#include "common.hpp"
+
+namespace mz {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int IO> struct Mfma;
+template <> struct Mfma<MZ_BF16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                    0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) { return f2bf(x); }
+  static __device__ __forceinline__ float load(uint16_t h) { return bf2f(h); }
+};
+template <> struct Mfma<MZ_F16> {
+  static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                   0, 0);
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) { return f2h(x); }
+  static __device__ __forceinline__ float load(uint16_t h) { return h2f(h); }
+};
+
+// Orders LDS writes and reads of one wave (the compiler must not move the
+// reads of other lanes' data above the writes).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float meta_load(const void* p, int64_t i, int dt) { return load_any(p, i, dt); }
+
+// Workspace record of one (batch, q-head, split): acc[D], m, l (fp32).
+template <int D>
+__device__ __forceinline__ float* ws_record(const mz_decode_args& a, int b, int qh, int split, int n_split) {
+  const int Hq = a.kv_heads * a.n_rep;
+  return (float*)a.workspace + (((int64_t)b * Hq + qh) * n_split + split) * (D + 2);
+}
+
+}  // namespace mz

@@ -189,7 +189,8 @@ class DecodePlan:
                  k_res: torch.Tensor | None, v_res: torch.Tensor | None,
                  alpha_key: float, alpha_value: float, scaling: float,
                  attention_mask: torch.Tensor | None = None,
-                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, n_split: int = 0):
+                 out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, n_split: int = 0,
+                 kernel_path: str = "auto"):
         dev = _on_gpu(query, k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, k_res, v_res, attention_mask)
         self.device = dev
         _require(query.dim() == 4 and query.shape[2] == 1, "query must be [B, Hq, 1, D]")
@@ -239,6 +240,14 @@ class DecodePlan:
         ev = tables.device_table("expm1", alpha_value, dev)
         a.e_key, a.e_value = ptr(ek), ptr(ev)
         keep += [ek, ev]
+        if int(bits) == 4:
+            fk = tables.device_table("fold4", alpha_key, dev)
+            fv = tables.device_table("fold4", alpha_value, dev)
+            a.fold_k, a.fold_v = ptr(fk), ptr(fv)
+            keep += [fk, fv]
+        paths = {"auto": _lib.MZ_PATH_AUTO, "exact": _lib.MZ_PATH_EXACT, "fold": _lib.MZ_PATH_FOLD}
+        _require(kernel_path in paths, f"kernel_path must be one of {sorted(paths)}")
+        a.kernel_path = paths[kernel_path]
 
         def _res(t):
             _require(t.dtype == query.dtype, "residual dtype must match the query dtype")

@@ -29,6 +29,14 @@ the reference:
     1..255, ``d`` in 0..bins (``muzero/quantizer.py:250-253``).
     Layout: ``E[(bins-1)*(bins+2)/2 + d]``.
 
+``fold_table(alpha)`` (4-bit decode attention)
+    For zero level ``zl`` and code ``q`` (16 x 16), the pair
+    ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
+    as two fp16 packed in one uint32 (P in the low half), with
+    ``pb = max(15-zl, 1)``, ``nb = max(zl, 1)``.  The decode kernel rewrites
+    the reference's dequantization as ``a + bp*P + bn*N`` per group and looks
+    these pairs up per code.
+
 These are constants of the format, the way the reference's own
 ``MU_ZERO_ALPHA2_COMPAND`` table is (``muzero/kernels/loader.py:133-150``);
 no per-element work runs on the host.
@@ -43,7 +51,7 @@ import torch
 
 MAX_BINS = 255
 _VERIFIED_MONOTONE = {2.0, 4.0, 16.0}  # exhaustively checked (tests/test_tables.py)
-_lock = threading.Lock()
+_lock = threading.RLock()  # builders call host_table recursively
 _host_cache: dict = {}
 _dev_cache: dict = {}
 
@@ -126,6 +134,27 @@ def _build_expm1(alpha: float) -> torch.Tensor:
     return (torch.expm1(pc * lb) / alpha).contiguous()
 
 
+def _expm1_row(bins: int) -> int:
+    return (bins - 1) * (bins + 2) // 2
+
+
+def _build_fold4(alpha: float) -> torch.Tensor:
+    e = host_table("expm1", alpha)
+    qmax = 15
+    p = torch.zeros(16, 16, dtype=torch.float32)
+    nq = torch.zeros(16, 16, dtype=torch.float32)
+    for zl in range(16):
+        pb, nb = max(qmax - zl, 1), max(zl, 1)
+        for q in range(16):
+            if q >= zl:
+                p[zl, q] = e[_expm1_row(pb) + q - zl]
+            else:
+                nq[zl, q] = e[_expm1_row(nb) + zl - q]
+    lo = p.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    hi = nq.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    return (lo | (hi << 16)).reshape(-1).contiguous()
+
+
 def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> torch.Tensor:
     """CPU copy of one table (built once per process and cached)."""
     alpha = float(alpha)
@@ -141,6 +170,8 @@ def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> tor
                 t = _build_ratio(alpha, dtype)
             elif kind == "expm1":
                 t = _build_expm1(alpha)
+            elif kind == "fold4":
+                t = _build_fold4(alpha)
             else:
                 raise ValueError(kind)
             _host_cache[key] = t

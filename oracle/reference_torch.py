@@ -331,12 +331,20 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
                      alpha_k: float, alpha_v: float, group_size: int, residual: int,
                      amax_dtype: torch.dtype = torch.float16,
                      attention_mask: Optional[torch.Tensor] = None,
-                     scaling: Optional[float] = None):
+                     scaling: Optional[float] = None,
+                     dequant_dtype: Optional[torch.dtype] = None):
     """Quantize a prefill KV the way the cache does, then attend the decode query.
 
     Returns ``(out_exact_fp64 [B,1,Hq,hd], state)`` where ``state`` holds the
     packed prefix, metadata and residual tensors, so the same bytes can be fed
     to the HIP path.
+
+    ``dequant_dtype`` is the dtype the prefix is dequantized to before the
+    attention.  The reference has both: its CPU/dequantize fallback stores the
+    dequantized prefix in the layer dtype (``layer.py:263``, ``attention.py:213-226``),
+    while its fused CUDA kernels keep the dequantized values in fp32 registers
+    (``dequantize_mu_zero_q``/``fill_mu_zero_codebook``, ``loader.py:197-263``).
+    Default: the layer dtype (``keys.dtype``).
     """
     b, hkv, length, d = keys.shape
     lq = split_prefix(length, residual, group_size)
@@ -346,8 +354,9 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
     if lq > 0:
         pk, kmn, ksc = quantize_key_block(keys[:, :, :lq].contiguous(), bits, alpha_k, group_size, amax_dtype)
         pv, vmn, vsc = quantize_value_block(values[:, :, :lq].contiguous(), bits, alpha_v, group_size, amax_dtype)
-        kq = dequantize_key_block(pk, kmn, ksc, bits, alpha_k, group_size, keys.dtype)
-        vq = dequantize_value_block(pv, vmn, vsc, bits, alpha_v, group_size, d, values.dtype)
+        ddt = keys.dtype if dequant_dtype is None else dequant_dtype
+        kq = dequantize_key_block(pk, kmn, ksc, bits, alpha_k, group_size, ddt)
+        vq = dequantize_value_block(pv, vmn, vsc, bits, alpha_v, group_size, d, ddt)
         state.update(packed_k=pk, k_mn=kmn, k_scale=ksc, packed_v=pv, v_mn=vmn, v_scale=vsc,
                      key_prefix=kq, value_prefix=vq)
     else:
@@ -357,8 +366,8 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
     rk = keys[:, :, lq:]
     rv = values[:, :, lq:]
     state.update(res_k=rk, res_v=rv)
-    full_k = torch.cat([kq, rk], dim=2)
-    full_v = torch.cat([vq, rv], dim=2)
+    full_k = torch.cat([kq.double(), rk.double()], dim=2)
+    full_v = torch.cat([vq.double(), rv.double()], dim=2)
     out = decode_attention_exact(query, full_k, full_v, attention_mask, scaling)
     return out, state
 
