@@ -57,14 +57,13 @@ struct Smem {
   static constexpr int TBL = 16 * 4 * 16 * 4;  // 4 KB per table
   static constexpr int TBL_K = 0;
   static constexpr int TBL_V = TBL;
-  static constexpr int Q_DUP = 2 * TBL;             // uint32 [NREP][D]  (q, q) fp16 pairs
-  static constexpr int Q16 = Q_DUP + NREP * D * 4;  // fp16 [NREP][D]
+  static constexpr int Q16 = 2 * TBL;              // fp16 [NREP][D]
   static constexpr int Q_IO = Q16 + NREP * D * 2;   // io dtype [NREP][D]
   static constexpr int WAVE0 = Q_IO + NREP * D * 2;
   // per-wave region
   static constexpr int KZL = 0;                        // uint32 [D]      zl << 8
-  static constexpr int KBP = KZL + D * 4;              // uint32 [D]      (bp, bn) fp16, scaled
-  static constexpr int KA = KBP + D * 4;               // fp16 [D]        a, scaled
+  static constexpr int KBP = KZL + D * 4;              // float2 [D]      (bp, bn), scaled
+  static constexpr int KA = KBP + D * 8;               // fp16 [D]        a, scaled
   static constexpr int VZL = KA + D * 2;               // uint32 [NG][TILE]
   static constexpr int VBP = VZL + NG * TILE * 4;      // uint32 [NG][TILE]
   static constexpr int VA = VBP + NG * TILE * 4;       // fp16 [NG][TILE]
@@ -86,6 +85,21 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t y) {
   const h2 r = __builtin_bit_cast(h2, x) * __builtin_bit_cast(h2, y);
   return __builtin_bit_cast(uint32_t, r);
+}
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+// q*b0 and q*b1 as fp16 pairs hi + lo with hi + lo = q*b to about 2^-22
+// relative: one fp16 rounding of the product would cost 2^-12 per channel,
+// which the logits of long contexts amplify past the attention tolerance.
+// (Compiles to v_fma_mix{lo,hi}_f16: the fp16 q feeds the fp32 FMA directly.)
+__device__ __forceinline__ uint2 split_product(_Float16 q, float b0, float b1) {
+  const float fq = (float)q;
+  const _Float16 h0 = (_Float16)__builtin_fmaf(fq, b0, 0.f);
+  const _Float16 h1 = (_Float16)__builtin_fmaf(fq, b1, 0.f);
+  const _Float16 l0 = (_Float16)__builtin_fmaf(fq, b0, -(float)h0);
+  const _Float16 l1 = (_Float16)__builtin_fmaf(fq, b1, -(float)h1);
+  return uint2{__builtin_bit_cast(uint32_t, h2{h0, h1}), __builtin_bit_cast(uint32_t, h2{l0, l1})};
 }
 
 // Exponent k with |v| * 2^k < 2^15 (fp16 operands and products stay finite).
@@ -156,7 +170,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint16_t raw = ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c];
     const float qf = M::load(raw);
     const uint16_t qh = f2h(qf);
-    ((uint32_t*)(smem + S::Q_DUP))[i] = (uint32_t)qh | ((uint32_t)qh << 16);
     ((uint16_t*)(smem + S::Q16))[i] = qh;
     ((uint16_t*)(smem + S::Q_IO))[i] = raw;
     qabs = fmaxf(qabs, fabsf(qf));
@@ -254,7 +267,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int cc = 0; cc < 2; ++cc) {
         const int c = lane + 64 * cc;
         ((uint32_t*)(W + S::KZL))[c] = ks[cc].zlb;
-        ((uint32_t*)(W + S::KBP))[c] = pack_h2(ldexpf(ks[cc].bp, kexp), ldexpf(ks[cc].bn, kexp));
+        ((float2*)(W + S::KBP))[c] = float2{ldexpf(ks[cc].bp, kexp), ldexpf(ks[cc].bn, kexp)};
         ((uint16_t*)(W + S::KA))[c] = f2h(ldexpf(ks[cc].a, kexp));
       }
       unscale = ldexpf(a.scaling, -kexp);
@@ -291,12 +304,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int j = 0; j < 4; ++j) s[j] = s0;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
-        const u32x4 qd = *(const u32x4*)(smem + S::Q_DUP + (hA * D + 16 * kt + 4 * g) * 4);
-        const u32x4 bq = *(const u32x4*)(W + S::KBP + (16 * kt + 4 * g) * 4);
+        const h4 q4 = *(const h4*)(smem + S::Q16 + (hA * D + 16 * kt + 4 * g) * 2);
+        const f32x4 b01 = *(const f32x4*)(W + S::KBP + (16 * kt + 4 * g) * 8);
+        const f32x4 b23 = *(const f32x4*)(W + S::KBP + (16 * kt + 4 * g) * 8 + 16);
         const u32x4 zl4 = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
-        u32x4 A;
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) A[ii] = pk_mul(qd[ii], bq[ii]);
+        const uint2 p0 = split_product(q4[0], b01[0], b01[1]);
+        const uint2 p1_ = split_product(q4[1], b01[2], b01[3]);
+        const uint2 p2_ = split_product(q4[2], b23[0], b23[1]);
+        const uint2 p3 = split_product(q4[3], b23[2], b23[3]);
+        const u32x4 Ahi = u32x4{p0.x, p1_.x, p2_.x, p3.x};
+        const u32x4 Alo = u32x4{p0.y, p1_.y, p2_.y, p3.y};
         uint32_t e[4];
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) e[ii] = expand(kc[kt][ii], grep);
@@ -308,7 +325,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             B[jt][ii] = *(const uint32_t*)(smem + S::TBL_K +
                                            __builtin_amdgcn_perm(zl4[ii], e[ii], 0x0C0C0500u | (uint32_t)jt));
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(A, B[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ahi, B[jt], s[jt]);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Alo, B[jt], s[jt]);
       }
       // V code words, issued after the key words are consumed (their latency
       // is covered by the softmax): k-tile kt, slot ii -> token 16kt+4g+ii,
