@@ -117,6 +117,18 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads):
     return el / reps
 
 
+def copy_calibration(mib, steps):
+    """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
+    calibrates the same counters on the decode kernel."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    ms = time_region(lambda i: dst.copy_(src), steps, stream)
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "ms": round(ms, 5),
+                      "GBps_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,12 +142,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (HBM counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the packed-KV decode path is sharded by batch or kv-head "
               "with no exchange inside the path (see DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration_mb:
+        copy_calibration(args.copy_calibration_mb, args.steps)
+        return
 
     from muzero_amd.kernels.loader import DecodePlan
     dev = torch.device("cuda:0")
