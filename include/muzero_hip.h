@@ -132,8 +132,9 @@ typedef struct mz_decode_args {
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
   /* 4-bit (P, N) fold tables for alpha_key / alpha_value: 16 x 16 pairs of
-   * fp16 (P, N) packed in uint32, see muzero_amd/tables.py ("fold4").  Needed
-   * by the 4-bit fast path; may be null (the generic path is used then). */
+   * fp16 (P, N) packed in uint32 (P in the low half), row = zero level,
+   * column = code; see muzero_amd/tables.py ("fold4").  Needed by the 4-bit
+   * fast path; may be null (the generic path is used then). */
   const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;

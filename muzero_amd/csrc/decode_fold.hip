@@ -10,7 +10,7 @@
 //   q.k = sum_c (Q_c*a_c) + sum_c [(Q_c*bp_c) P + (Q_c*bn_c) N]
 // is an MFMA whose A operand carries the group scalars times the query (for
 // P.V: the softmax weight times the token's scalars) and whose B operand is
-// one table lookup (an fp16 pair) per code, contracting over (channel, side)
+// a table lookup (an fp16 pair) per code, contracting over (channel, side)
 // pairs.  The constant part sum_c Q_c*a_c is one more MFMA against a ones
 // operand.  No element is ever dequantized to memory.  The dequantized
 // values are those of the reference's fused CUDA kernels: full precision
@@ -18,17 +18,20 @@
 //
 // Work of one wave: a 64-token tile = one key group (or 64 residual tokens).
 //   QK: MFMA M rows = query heads of the kv-head (GQA grouping), columns =
-//   token positions 4n+{0,2,1,3} of N-tiles 0..3; lane (n, g) of k-tile kt
-//   holds channels 16kt+4g+{0..3}, and reads for each one 16 bits of the
-//   channel's packed row (4 codes) straight from HBM.
-//   PV: columns = channels 64vg+4n+{0,2,1,3}, k = (token, side); lane (n, g)
-//   reads 16 bits of a token's packed row per value group (4 channels).
-// The 16 lanes of a lane group always look up one zero-level row of the
-// table, and each lane group has its own copy of the table in a disjoint
-// bank range, so the per-code lookups are bank-conflict free.  The softmax of
-// a tile is redistributed through LDS so every lane computes exps.  fp16
-// operands are kept in range by a power-of-two scale per key group and per
-// value tile, folded into the logits and into the online-softmax rescale.
+//   tokens 4n+jt of N-tiles jt = 0..3; lane (n, g) of k-tile kt holds
+//   channels 16kt+4g+{0..3} and needs, for each, 16 bits of the channel's
+//   packed row (tokens 4n..4n+3).
+//   PV: columns = channels 64vg+4n+jt, k = (token, side); lane (n, g) needs
+//   16 bits of a token's packed row per value group (channels 4n..4n+3).
+//   Both are loaded straight from HBM as 32-bit words shared by lane pairs.
+// Each code is one conflict-free ds_read_b32 from a per-lane-group copy of
+// the (P, N) table in LDS, addressed with 1.5 VALU ops per code.  The key-side products q*bp, q*bn are formed once per (head,
+// channel) per tile as fp16 hi + lo pairs (two MFMAs per k-tile keep them at
+// fp32 accuracy).  The next tile's code words and metadata are loaded into
+// registers while the current tile is computed.  The softmax of a tile is
+// redistributed through LDS so every lane computes exps.  fp16 operands are
+// kept in range by a power-of-two scale per key group and per value tile,
+// folded into the logits and into the online-softmax rescale.
 //
 // Launch: one workgroup of 4 waves per (batch, kv-head, split); a split is a
 // run of tiles, waves take every 4th tile; the split's (m, l, acc) goes to the
@@ -44,50 +47,58 @@ constexpr int QB = 32;       // bytes per packed 64-code group (4-bit)
 constexpr int NG = 2;        // value groups per token
 constexpr int TILE = 64;     // tokens per tile
 constexpr int WAVES = 4;
+// (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
+// zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
+// level (one channel / one token-group), and each group owns a disjoint bank
+// range, so the per-code lookups are free of bank conflicts.
+constexpr int TBL = 16 * 4 * 16 * 4;  // 4 KB
 constexpr uint32_t ONES_F16X2 = 0x3C003C00u;
-// N-tile jt of a 16-bit code word holds code PERM_POS[jt] of its 4 codes
-// (byte order produced by expand(): q0, q2, q1, q3).
-__device__ constexpr int PERM_POS[4] = {0, 2, 1, 3};
 
-// Static LDS layout (bytes).  Per workgroup: the two (P, N) tables (16 zero
-// levels x 4 lane-group copies x 16 codes, uint32 each) and the query in three
-// forms; per wave: group scalars, logits, weights, rescale factors.
+// Padded row lengths (in 4-byte words) of the [head][...] arrays so that the
+// rows read together by lanes of different heads start in different banks.
+constexpr int AROW = D + 4;     // uint32 per head row of the key A operand
+constexpr int HROW = D / 2 + 4;  // uint32 per head row of fp16 [D] arrays
+constexpr int LROW = TILE + 4;  // uint32 per head row of per-token arrays
+constexpr int PROW = TILE / 2 + 4;
+
+// Static LDS layout (bytes).  Per workgroup: the byte tables and the query
+// in two forms; per wave: the current tile's operands and softmax state.
 template <int NREP>
 struct Smem {
-  static constexpr int TBL = 16 * 4 * 16 * 4;  // 4 KB per table
   static constexpr int TBL_K = 0;
   static constexpr int TBL_V = TBL;
-  static constexpr int Q16 = 2 * TBL;              // fp16 [NREP][D]
-  static constexpr int Q_IO = Q16 + NREP * D * 2;   // io dtype [NREP][D]
-  static constexpr int WAVE0 = Q_IO + NREP * D * 2;
+  static constexpr int Q16 = 2 * TBL;                 // fp16 [NREP][HROW*2]
+  static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
+  static constexpr int WAVE0 = Q_IO + NREP * HROW * 4;
   // per-wave region
-  static constexpr int KZL = 0;                        // uint32 [D]      zl << 8
-  static constexpr int KBP = KZL + D * 4;              // float2 [D]      (bp, bn), scaled
-  static constexpr int KA = KBP + D * 8;               // fp16 [D]        a, scaled
-  static constexpr int VZL = KA + D * 2;               // uint32 [NG][TILE]
-  static constexpr int VBP = VZL + NG * TILE * 4;      // uint32 [NG][TILE]
-  static constexpr int VA = VBP + NG * TILE * 4;       // fp16 [NG][TILE]
-  static constexpr int LOGIT = VA + NG * TILE * 2;     // f32 [NREP][TILE]
-  static constexpr int P2 = LOGIT + NREP * TILE * 4;   // uint32 [NREP][TILE]  (p, p)
-  static constexpr int P1 = P2 + NREP * TILE * 4;      // fp16 [NREP][TILE]
-  static constexpr int CORR = P1 + NREP * TILE * 2;    // f32 [NREP]
+  static constexpr int KZL = 0;                      // uint32 [D]            zl << 8
+  static constexpr int AHI = KZL + D * 4;            // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
+  static constexpr int ALO = AHI + NREP * AROW * 4;  // uint32 [NREP][AROW]   low part
+  static constexpr int QA = ALO + NREP * AROW * 4;   // fp16 [NREP][HROW*2]   q*a
+  static constexpr int VZL = QA + NREP * HROW * 4;   // uint32 [NG][TILE]     zl << 8
+  static constexpr int VBP = VZL + NG * TILE * 4;    // uint32 [NG][TILE]     (bp, bn) fp16
+  static constexpr int VA = VBP + NG * TILE * 4;     // fp16 [NG][TILE]       a
+  static constexpr int LOGIT = VA + NG * TILE * 2;   // f32 [NREP][LROW]
+  static constexpr int P2 = LOGIT + NREP * LROW * 4;  // uint32 [NREP][LROW]  (p, p)
+  static constexpr int P1 = P2 + NREP * LROW * 4;    // fp16 [NREP][PROW*2]
+  static constexpr int CORR = P1 + NREP * PROW * 4;  // f32 [NREP]
   static constexpr int PER_WAVE = (CORR + NREP * 4 + 15) / 16 * 16;
   static constexpr int MERGE = (2 * NREP + NREP * D) * 4;  // per wave at the end (aliases the wave area)
   static constexpr int WAVE_AREA = WAVES * (PER_WAVE > MERGE ? PER_WAVE : MERGE);
   static constexpr int TOTAL = WAVE0 + WAVE_AREA;
 };
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
 }
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t y) {
   const h2 r = __builtin_bit_cast(h2, x) * __builtin_bit_cast(h2, y);
   return __builtin_bit_cast(uint32_t, r);
 }
-
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 // q*b0 and q*b1 as fp16 pairs hi + lo with hi + lo = q*b to about 2^-22
 // relative: one fp16 rounding of the product would cost 2^-12 per channel,
@@ -112,7 +123,7 @@ __device__ __forceinline__ int range_exp(float mx) {
 
 struct GroupScalars {
   float a, bp, bn;
-  uint32_t zlb;  // zl << 8
+  uint32_t zrow;  // zl << 8: byte offset of the group's zero-level row in the table
 };
 
 // (a, bp, bn, zl) of one stored group (mn, s); the scale is guarded like the
@@ -129,20 +140,105 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   r.a = mn + s * za;
   r.bp = s * pe;
   r.bn = -(s * ne);
-  r.zlb = (uint32_t)(zl == zl ? (int)zl : 0) << 8;
+  r.zrow = (uint32_t)(zl == zl ? (int)zl : 0) << 8;
   return r;
 }
 
-// 16-bit word of 4 codes -> bytes (4*q0, 4*q2, 4*q1, 4*q3) | lane-group copy.
-__device__ __forceinline__ uint32_t expand(uint32_t h, uint32_t grep) {
-  return (((h << 2) | (h << 14)) & 0x3C3C3C3Cu) | grep;
+// Raw bits of the metadata entries i, i+1 (two words for fp32, one for the
+// 16-bit types).  Loaded without converting: a conversion inside a dtype
+// branch would make the compiler wait for every load issued before it.
+__device__ __forceinline__ uint2 meta_raw(const void* p, int64_t i, int dt) {
+  const int es = dt == MZ_F32 ? 4 : 2;
+  const uint8_t* q = (const uint8_t*)p + i * es;
+  return uint2{*(const uint32_t*)q, *(const uint32_t*)(q + (dt == MZ_F32 ? 4 : 0))};
+}
+
+__device__ __forceinline__ float2 meta_cvt(uint2 w, int dt) {
+  if (dt == MZ_F32) return float2{__builtin_bit_cast(float, w.x), __builtin_bit_cast(float, w.y)};
+  if (dt == MZ_F16) return float2{h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16))};
+  return float2{bf2f((uint16_t)w.x), bf2f((uint16_t)(w.x >> 16))};
+}
+
+// Global data of one quantized tile, loaded one tile ahead.  Code words are
+// loaded 32 bits per lane: lanes 2m and 2m+1 of a lane group read the same 4
+// bytes (8 codes) of the two channels (key) / tokens (value) of a pair, and
+// code_pair() later swaps halves between them, so each lane ends with the 16
+// bits of both rows that hold ITS four tokens / channels.
+struct TileData {
+  uint32_t kw[16];  // key rows 16kt+4g+2p+(n&1), bytes 4*(n>>1): [kt][p]
+  uint32_t vw[16];  // value tokens 16kt+4g+2p+(n&1), bytes 32vg+4*(n>>1): [kt][vg][p]
+  uint2 kmn, ksc;   // key groups of channels 2*lane, 2*lane+1 (raw bits)
+  uint2 vmn, vsc;   // value groups 0, 1 of token lane (raw bits)
+};
+
+// Key code words and all metadata of a tile (issued at the start of the
+// previous tile) ...
+__device__ __forceinline__ void load_tile_k(TileData& t, const mz_decode_args& a, const uint8_t* kp_bh,
+                                            int64_t km_bh, int64_t vm_bh, int tile, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  // metadata first: its consumer then need not wait for the code words
+  const int64_t ki = km_bh + (int64_t)tile * D + 2 * lane;
+  t.kmn = meta_raw(a.k_mn, ki, a.meta_dtype);
+  t.ksc = meta_raw(a.k_scale, ki, a.meta_dtype);
+  const int64_t vi = vm_bh + ((int64_t)tile * TILE + lane) * NG;
+  t.vmn = meta_raw(a.v_mn, vi, a.meta_dtype);
+  t.vsc = meta_raw(a.v_scale, vi, a.meta_dtype);
+  const uint32_t* kq = (const uint32_t*)(kp_bh + (int64_t)tile * D * QB + (4 * g + (n & 1)) * QB + 4 * (n >> 1));
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) t.kw[kt * 2 + p] = kq[(16 * kt + 2 * p) * (QB / 4)];
+}
+
+// ... and its value code words (issued once the previous tile's key words
+// are consumed, so the two register sets overlap less).
+__device__ __forceinline__ void load_tile_v(TileData& t, const uint8_t* vp_bh, int tile, int lane) {
+  const int n = lane & 15, g = lane >> 4;
+  const uint32_t* vq =
+      (const uint32_t*)(vp_bh + ((int64_t)tile * TILE + 4 * g + (n & 1)) * (NG * QB) + 4 * (n >> 1));
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int vg = 0; vg < NG; ++vg)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) t.vw[(kt * NG + vg) * 2 + p] = vq[((16 * kt + 2 * p) * (NG * QB) + QB * vg) / 4];
+}
+
+// This lane's two 16-bit code rows of a pair: low half = row 2p, high half =
+// row 2p+1, each holding the codes of tokens / channels 4n..4n+3.  `sel`
+// is the lane's v_perm selector (even lanes keep the low halves of both
+// words, odd lanes the high halves).
+__device__ __forceinline__ uint32_t code_pair(uint32_t own, uint32_t sel) {
+  const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, DPP_QUAD_XOR1, 0xF, 0xF, false);
+  return __builtin_amdgcn_perm(other, own, sel);
+}
+
+// The B operands of one k-tile from two code words w01, w23 (channels or
+// tokens ii = 0, 1 in the low / high half of w01, ii = 2, 3 in w23; each half
+// holds the codes of tokens / channels 4n+0..3 of N-tiles jt = 0..3).  The
+// even and odd nibbles of a word are spread to bytes as table offsets
+// 4*q + 64*group (two ops per 4 codes); one v_perm per code then places the
+// offset under the zero-level row (zr = zl << 8) and one ds_read_b32 fetches
+// the (P, N) pair straight into the operand register.
+template <int TBASE>
+__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, const uint32_t w01, const uint32_t w23,
+                                             const u32x4 zr, const uint32_t grep, u32x4 B[4]) {
+  const uint32_t ev[2] = {((w01 << 2) & 0x3C3C3C3Cu) | grep, ((w23 << 2) & 0x3C3C3C3Cu) | grep};
+  const uint32_t od[2] = {((w01 >> 2) & 0x3C3C3C3Cu) | grep, ((w23 >> 2) & 0x3C3C3C3Cu) | grep};
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const uint32_t e = (jt & 1) ? od[ii >> 1] : ev[ii >> 1];
+      const uint32_t sel = 0x0C0C0500u | (uint32_t)((ii & 1) * 2 + (jt >> 1));
+      B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], e, sel));
+    }
 }
 
 template <int IO, int NREP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
-    const mz_decode_args a, int tiles_per_split, int n_split,
-                                                   const uint32_t* __restrict__ ftab_k,
-                                                   const uint32_t* __restrict__ ftab_v) {
+    const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
+    const uint32_t* __restrict__ ftab_v) {
   using M = Mfma<IO>;
   using S = Smem<NREP>;
   constexpr int LPH = 64 / NREP;   // softmax layout: lanes per head
@@ -150,16 +246,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __align__(16) uint8_t smem[S::TOTAL];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (the compiler cannot see that threadIdx.x >> 6 is): tile
+  // bookkeeping and load bases then live in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
 
+  const int n_tiles_d = (a.n_residual + TILE - 1) / TILE;
+  const int n_tiles = a.n_groups + n_tiles_d;
+  const int t_begin = split * tiles_per_split;
+  const int t_end = min(n_tiles, t_begin + tiles_per_split);
+  const uint8_t* kp_bh = a.k_packed + b * a.kp_sb + kvh * a.kp_sh;
+  const uint8_t* vp_bh = a.v_packed + b * a.vp_sb + kvh * a.vp_sh;
+  const int64_t km_bh = b * a.km_sb + kvh * a.km_sh;
+  const int64_t vm_bh = b * a.vm_sb + kvh * a.vm_sh;
+
+  // Tile loads are issued unconditionally (the compiler's wait counts then
+  // stay exact and a prefetch is never waited for early); a tile index that
+  // is not a quantized tile of this wave is replaced by one this split reads
+  // anyway, so the spare load hits the cache.
+  const int q_last = max(0, min(t_end, a.n_groups) - 1);
+  TileData T0, T1;
+  const int tile0 = t_begin + wave;
+  load_tile_k(T0, a, kp_bh, km_bh, vm_bh, min(tile0, q_last), lane);
+  load_tile_v(T0, vp_bh, min(tile0, q_last), lane);
+
   // ---------------- workgroup setup: tables and query in LDS
-  // entry (zl, q) is replicated for the 4 lane groups at byte zl*256 + 64*group + 4*q
-  for (int i = threadIdx.x; i < 1024; i += 256) {
+  for (int i = threadIdx.x; i < TBL / 4; i += 256) {
     const int zl = i >> 6, q = i & 15;
     ((uint32_t*)(smem + S::TBL_K))[i] = ftab_k[zl * 16 + q];
     ((uint32_t*)(smem + S::TBL_V))[i] = ftab_v[zl * 16 + q];
@@ -169,9 +285,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int h = i / D, c = i - h * D;
     const uint16_t raw = ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c];
     const float qf = M::load(raw);
-    const uint16_t qh = f2h(qf);
-    ((uint16_t*)(smem + S::Q16))[i] = qh;
-    ((uint16_t*)(smem + S::Q_IO))[i] = raw;
+    ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = f2h(qf);
+    ((uint16_t*)(smem + S::Q_IO))[h * HROW * 2 + c] = raw;
     qabs = fmaxf(qabs, fabsf(qf));
   }
   qabs = wave_max(qabs);
@@ -190,7 +305,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // A-operand row of this lane: a query head; rows >= NREP (MFMA padding)
   // repeat head 0 and their outputs are never read
   const int hA = n < NREP ? n : 0;
-  const uint32_t grep = 0x40404040u * (uint32_t)g;
+  const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
+  // even lanes: (own lo, other lo); odd lanes: (other hi, own hi)
+  const uint32_t psel = (n & 1) ? 0x03020706u : 0x05040100u;
   const int sh = lane / LPH;           // softmax layout: head
   const int st0 = (lane % LPH) * TPL;  // and first token
 
@@ -205,16 +322,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int kacc = 0;  // acc holds sum p * x * 2^kacc
   bool kacc_init = false;
 
-  const int n_tiles_d = (a.n_residual + TILE - 1) / TILE;
-  const int n_tiles = a.n_groups + n_tiles_d;
-  const int t_begin = split * tiles_per_split;
-  const int t_end = min(n_tiles, t_begin + tiles_per_split);
-  const uint8_t* kp_bh = a.k_packed + b * a.kp_sb + kvh * a.kp_sh;
-  const uint8_t* vp_bh = a.v_packed + b * a.vp_sb + kvh * a.vp_sh;
-  const int64_t km_bh = b * a.km_sb + kvh * a.km_sh;
-  const int64_t vm_bh = b * a.vm_sb + kvh * a.vm_sh;
-
-  for (int tile = t_begin + wave; tile < t_end; tile += WAVES) {
+  // one tile; the next quantized tile tn of this wave (if any) is loaded into Tn
+  auto process = [&](const int tile, const TileData& T, TileData& Tn, const int tn) {
+    const int tl = min(tn, q_last);
+    load_tile_k(Tn, a, kp_bh, km_bh, vm_bh, tl, lane);
     const bool quant = tile < a.n_groups;
     int n_valid, pos0, r0 = 0;
     if (quant) {
@@ -229,117 +340,66 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     f32x4 s[4];
     int kv_exp = 0;
     float unscale = a.scaling;
-    uint32_t vc[4][4][NG];  // value code words (16 bits each) of a quantized tile
     if (quant) {
-      // ---------- loads: metadata first, then code words
-      float kmn[2], ksc[2], vmn[NG], vsc[NG];
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const int64_t mi = km_bh + (int64_t)tile * D + lane + 64 * cc;
-        kmn[cc] = meta_load(a.k_mn, mi, a.meta_dtype);
-        ksc[cc] = meta_load(a.k_scale, mi, a.meta_dtype);
-      }
-#pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
-        const int64_t mi = vm_bh + (int64_t)(pos0 + lane) * NG + vg;
-        vmn[vg] = meta_load(a.v_mn, mi, a.meta_dtype);
-        vsc[vg] = meta_load(a.v_scale, mi, a.meta_dtype);
-      }
-      // K: k-tile kt, slot ii -> channel 16kt+4g+ii, 16 bits at byte 2n of its row
-      uint32_t kc[8][4];
-      const uint16_t* kgrp = (const uint16_t*)(kp_bh + (int64_t)tile * D * QB + 4 * g * QB + 2 * n);
-#pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) kc[kt][ii] = kgrp[(16 * kt + ii) * (QB / 2)];
-
-      // ---------- key group scalars (lane: channels lane, lane+64)
-      GroupScalars ks[2];
-      float kmx = 0.f;
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        ks[cc] = group_scalars(kmn[cc], ksc[cc]);
-        kmx = fmaxf(kmx, fmaxf(fabsf(ks[cc].a), fmaxf(ks[cc].bp, -ks[cc].bn)));
-      }
-      kmx = wave_max(kmx);
+      // ---------- key group scalars (lane: channels 2*lane, 2*lane+1)
+      const float2 kmn = meta_cvt(T.kmn, a.meta_dtype), ksc = meta_cvt(T.ksc, a.meta_dtype);
+      const GroupScalars k0 = group_scalars(kmn.x, ksc.x);
+      const GroupScalars k1 = group_scalars(kmn.y, ksc.y);
+      float kmx = fmaxf(fmaxf(fabsf(k0.a), fmaxf(k0.bp, -k0.bn)), fmaxf(fabsf(k1.a), fmaxf(k1.bp, -k1.bn)));
+      kmx = wave_max_fast(kmx);
       const int kexp = min(range_exp(kmx * fmaxf(qabs, 1.f)), range_exp(kmx));
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        const int c = lane + 64 * cc;
-        ((uint32_t*)(W + S::KZL))[c] = ks[cc].zlb;
-        ((float2*)(W + S::KBP))[c] = float2{ldexpf(ks[cc].bp, kexp), ldexpf(ks[cc].bn, kexp)};
-        ((uint16_t*)(W + S::KA))[c] = f2h(ldexpf(ks[cc].a, kexp));
-      }
       unscale = ldexpf(a.scaling, -kexp);
+      const float bp0 = ldexpf(k0.bp, kexp), bn0 = ldexpf(k0.bn, kexp);
+      const float bp1 = ldexpf(k1.bp, kexp), bn1 = ldexpf(k1.bn, kexp);
+      const uint32_t ka = pack_h2(ldexpf(k0.a, kexp), ldexpf(k1.a, kexp));
+      *(uint2*)(W + S::KZL + 8 * lane) = uint2{k0.zrow, k1.zrow};
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        const uint32_t q01 = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
+        const h2 qh = __builtin_bit_cast(h2, q01);
+        const uint2 p0 = split_product(qh.x, bp0, bn0);
+        const uint2 p1_ = split_product(qh.y, bp1, bn1);
+        *(uint2*)(W + S::AHI + (h * AROW + 2 * lane) * 4) = uint2{p0.x, p1_.x};
+        *(uint2*)(W + S::ALO + (h * AROW + 2 * lane) * 4) = uint2{p0.y, p1_.y};
+        *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, ka);
+      }
       // ---------- value scalars (lane: token lane, both value groups)
-      GroupScalars vs[NG];
-      float vmx = 0.f;
-#pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
-        vs[vg] = group_scalars(vmn[vg], vsc[vg]);
-        vmx = fmaxf(vmx, fmaxf(fabsf(vs[vg].a), fmaxf(vs[vg].bp, -vs[vg].bn)));
-      }
+      const float2 vmn = meta_cvt(T.vmn, a.meta_dtype), vsc = meta_cvt(T.vsc, a.meta_dtype);
+      const GroupScalars v0 = group_scalars(vmn.x, vsc.x);
+      const GroupScalars v1 = group_scalars(vmn.y, vsc.y);
+      const float vmx = fmaxf(fmaxf(fabsf(v0.a), fmaxf(v0.bp, -v0.bn)), fmaxf(fabsf(v1.a), fmaxf(v1.bp, -v1.bn)));
       // keep the accumulators' exponent unless this tile needs a smaller one
-      kv_exp = min(kacc_init ? kacc : 60, range_exp(wave_max(vmx)));
-#pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
-        ((uint32_t*)(W + S::VZL))[vg * TILE + lane] = vs[vg].zlb;
-        ((uint32_t*)(W + S::VBP))[vg * TILE + lane] = pack_h2(ldexpf(vs[vg].bp, kv_exp), ldexpf(vs[vg].bn, kv_exp));
-        ((uint16_t*)(W + S::VA))[vg * TILE + lane] = f2h(ldexpf(vs[vg].a, kv_exp));
-      }
+      kv_exp = min(kacc_init ? kacc : 60, range_exp(wave_max_fast(vmx)));
+      ((uint32_t*)(W + S::VZL))[lane] = v0.zrow;
+      ((uint32_t*)(W + S::VZL))[TILE + lane] = v1.zrow;
+      ((uint32_t*)(W + S::VBP))[lane] = pack_h2(ldexpf(v0.bp, kv_exp), ldexpf(v0.bn, kv_exp));
+      ((uint32_t*)(W + S::VBP))[TILE + lane] = pack_h2(ldexpf(v1.bp, kv_exp), ldexpf(v1.bn, kv_exp));
+      ((uint16_t*)(W + S::VA))[lane] = f2h(ldexpf(v0.a, kv_exp));
+      ((uint16_t*)(W + S::VA))[TILE + lane] = f2h(ldexpf(v1.a, kv_exp));
       wave_lds_sync();
 
       // ---------- S = Q K^T: constant part (ones operand), then the folded codes
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 qv = *(const u32x4*)(smem + S::Q16 + (hA * D + 32 * kq + 8 * g) * 2);
-        const u32x4 av = *(const u32x4*)(W + S::KA + (32 * kq + 8 * g) * 2);
-        u32x4 A;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) A[p] = pk_mul(qv[p], av[p]);
+        const u32x4 A = *(const u32x4*)(W + S::QA + (hA * HROW * 2 + 32 * kq + 8 * g) * 2);
         s0 = Mfma<MZ_F16>::run(A, u32x4{ONES_F16X2, ONES_F16X2, ONES_F16X2, ONES_F16X2}, s0);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = s0;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
-        const h4 q4 = *(const h4*)(smem + S::Q16 + (hA * D + 16 * kt + 4 * g) * 2);
-        const f32x4 b01 = *(const f32x4*)(W + S::KBP + (16 * kt + 4 * g) * 8);
-        const f32x4 b23 = *(const f32x4*)(W + S::KBP + (16 * kt + 4 * g) * 8 + 16);
-        const u32x4 zl4 = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
-        const uint2 p0 = split_product(q4[0], b01[0], b01[1]);
-        const uint2 p1_ = split_product(q4[1], b01[2], b01[3]);
-        const uint2 p2_ = split_product(q4[2], b23[0], b23[1]);
-        const uint2 p3 = split_product(q4[3], b23[2], b23[3]);
-        const u32x4 Ahi = u32x4{p0.x, p1_.x, p2_.x, p3.x};
-        const u32x4 Alo = u32x4{p0.y, p1_.y, p2_.y, p3.y};
-        uint32_t e[4];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) e[ii] = expand(kc[kt][ii], grep);
+        const u32x4 Ahi = *(const u32x4*)(W + S::AHI + (hA * AROW + 16 * kt + 4 * g) * 4);
+        const u32x4 Alo = *(const u32x4*)(W + S::ALO + (hA * AROW + 16 * kt + 4 * g) * 4);
+        const u32x4 zr = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
         u32x4 B[4];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii)
-            B[jt][ii] = *(const uint32_t*)(smem + S::TBL_K +
-                                           __builtin_amdgcn_perm(zl4[ii], e[ii], 0x0C0C0500u | (uint32_t)jt));
+        lookup_ktile<S::TBL_K>(smem, code_pair(T.kw[2 * kt], psel), code_pair(T.kw[2 * kt + 1], psel), zr, grep,
+                               B);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ahi, B[jt], s[jt]);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Alo, B[jt], s[jt]);
       }
-      // V code words, issued after the key words are consumed (their latency
-      // is covered by the softmax): k-tile kt, slot ii -> token 16kt+4g+ii,
-      // 16 bits at byte 32vg+2n of its row
-      const uint16_t* vtok = (const uint16_t*)(vp_bh + (int64_t)(pos0 + 4 * g) * (NG * QB) + 2 * n);
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii)
-#pragma unroll
-          for (int vg = 0; vg < NG; ++vg)
-            vc[kt][ii][vg] = vtok[((16 * kt + ii) * (NG * QB) + QB * vg) / 2];
     } else {
       // ---------- residual tile: S = Q K^T with dense operands
 #pragma unroll
@@ -347,23 +407,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const uint16_t* kres = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 qv = *(const u32x4*)(smem + S::Q_IO + (hA * D + 32 * kq + 8 * g) * 2);
+        const u32x4 qv = *(const u32x4*)(smem + S::Q_IO + (hA * HROW * 2 + 32 * kq + 8 * g) * 2);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-          const int t = 4 * n + PERM_POS[jt];
+          const int t = 4 * n + jt;
           const u32x4 kb = t < n_valid ? *(const u32x4*)(kres + (int64_t)(r0 + t) * a.kr_st + 32 * kq + 8 * g)
                                        : u32x4{0, 0, 0, 0};
           s[jt] = M::run(qv, kb, s[jt]);
         }
       }
     }
+    load_tile_v(Tn, vp_bh, tl, lane);
 
     // ---------- softmax over the tile (redistributed: lane -> head sh, tokens st0..)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * g + i;
-      if (h < NREP)
-        *(f32x4*)(logit + h * TILE + 4 * n) = f32x4{s[0][i], s[2][i], s[1][i], s[3][i]} * unscale;
+      if (h < NREP) *(f32x4*)(logit + h * LROW + 4 * n) = f32x4{s[0][i], s[1][i], s[2][i], s[3][i]} * unscale;
     }
     wave_lds_sync();
     float x[TPL];
@@ -371,14 +431,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int t = 0; t < TPL; ++t) {
       const int tt = st0 + t;
-      float v = logit[sh * TILE + tt];
+      float v = logit[sh * LROW + tt];
       if (tt >= n_valid) v = -INFINITY;
       else if (a.mask) v += a.mask[b * a.mask_sb + pos0 + tt];
       x[t] = v;
       tmax = fmaxf(tmax, v);
     }
-#pragma unroll
-    for (int o = LPH / 2; o > 0; o >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+    tmax = group_reduce<LPH>(tmax, OpMax());
     const float m_new = fmaxf(m_run, tmax);
     const float corr = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
     m_run = m_new;
@@ -388,11 +447,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float p = (x[t] == -INFINITY) ? 0.f : __expf(x[t] - m_new);
       const uint16_t ph = f2h(p);
       psum += h2f(ph);
-      p2[sh * TILE + st0 + t] = (uint32_t)ph | ((uint32_t)ph << 16);
-      p1[sh * TILE + st0 + t] = ph;
+      p2[sh * LROW + st0 + t] = (uint32_t)ph | ((uint32_t)ph << 16);
+      p1[sh * PROW * 2 + st0 + t] = ph;
     }
-#pragma unroll
-    for (int o = LPH / 2; o > 0; o >>= 1) psum += __shfl_xor(psum, o, 64);
+    psum = group_reduce<LPH>(psum, OpAdd());
     l_run = l_run * corr + psum;
     if ((lane % LPH) == 0) corrs[sh] = corr;
     wave_lds_sync();
@@ -421,24 +479,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (quant) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 pd = *(const u32x4*)(p2 + hA * TILE + 16 * kt + 4 * g);
+        const u32x4 pd = *(const u32x4*)(p2 + hA * LROW + 16 * kt + 4 * g);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
           const u32x4 bq = *(const u32x4*)(W + S::VBP + (vg * TILE + 16 * kt + 4 * g) * 4);
-          const u32x4 zl4 = *(const u32x4*)(W + S::VZL + (vg * TILE + 16 * kt + 4 * g) * 4);
+          const u32x4 zr = *(const u32x4*)(W + S::VZL + (vg * TILE + 16 * kt + 4 * g) * 4);
           u32x4 A;
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) A[ii] = pk_mul(pd[ii], bq[ii]);
-          uint32_t e[4];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) e[ii] = expand(vc[kt][ii][vg], grep);
           u32x4 B[4];
-#pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-              B[jt][ii] = *(const uint32_t*)(smem + S::TBL_V +
-                                             __builtin_amdgcn_perm(zl4[ii], e[ii], 0x0C0C0500u | (uint32_t)jt));
+          lookup_ktile<S::TBL_V>(smem, code_pair(T.vw[(kt * NG + vg) * 2], psel),
+                                 code_pair(T.vw[(kt * NG + vg) * 2 + 1], psel), zr, grep, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(A, B[jt], acc[vg][jt]);
         }
@@ -446,7 +497,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // constant part: sum_t p_t * a_t against a ones operand
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
-        const u32x4 pv = *(const u32x4*)(p1 + hA * TILE + 32 * kq + 8 * g);
+        const u32x4 pv = *(const u32x4*)(p1 + hA * PROW * 2 + 32 * kq + 8 * g);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
           const u32x4 av = *(const u32x4*)(W + S::VA + (vg * TILE + 32 * kq + 8 * g) * 2);
@@ -461,7 +512,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const uint16_t* vres = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 pd = *(const u32x4*)(p2 + hA * TILE + 16 * kt + 4 * g);
+        const u32x4 pd = *(const u32x4*)(p2 + hA * LROW + 16 * kt + 4 * g);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
           uint32_t v4[4][2];
@@ -478,13 +529,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
           }
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt) {
-            const int ch = PERM_POS[jt];  // channel 4n + ch
+          for (int jt = 0; jt < 4; ++jt) {  // channel 64vg + 4n + jt
             u32x4 B;
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-              const uint32_t w = v4[ii][ch >> 1];
-              const uint16_t h = (ch & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFFu);
+              const uint32_t w = v4[ii][jt >> 1];
+              const uint16_t h = (jt & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xFFFFu);
               B[ii] = IO == MZ_F16 ? (uint32_t)h : (uint32_t)f2h(bf2f(h));
             }
             acc[vg][jt] = Mfma<MZ_F16>::run(pd, B, acc[vg][jt]);
@@ -493,6 +543,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
     wave_lds_sync();
+  };
+
+  // tiles of this wave: tile0, tile0 + 4, ...; the next quantized tile's data
+  // is in flight while the current one is computed (two register sets)
+  for (int tile = tile0; tile < t_end; tile += 2 * WAVES) {
+    const int t1 = tile + WAVES;
+    process(tile, T0, T1, t1);
+    if (t1 >= t_end) break;
+    process(t1, T1, T0, t1 + WAVES);
   }
 
   // ---------------- merge the 4 waves and write this split's partial records
@@ -501,7 +560,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D]
   {
     float* w = red + wave * RED;
-    if ((lane % LPH) == 0) { w[sh] = m_run; w[NREP + sh] = l_run; }
+    if ((lane % LPH) == 0) {
+      w[sh] = m_run;
+      w[NREP + sh] = l_run;
+    }
     const float unit = ldexpf(1.f, -kacc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -509,9 +571,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (h < NREP) {
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg)
-#pragma unroll
-          for (int jt = 0; jt < 4; ++jt)
-            w[2 * NREP + h * D + 64 * vg + 4 * n + PERM_POS[jt]] = (acc[vg][jt][i] + acc_a[vg][i]) * unit;
+          *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n) =
+              f32x4{acc[vg][0][i] + acc_a[vg][i], acc[vg][1][i] + acc_a[vg][i], acc[vg][2][i] + acc_a[vg][i],
+                    acc[vg][3][i] + acc_a[vg][i]} * unit;
       }
     }
   }
@@ -540,18 +602,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 // ------------------------------------------------------------------ host side
 
+static bool fold_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
+  const int pair = dt == MZ_F32 ? 8 : 4;  // two adjacent entries are read at once
+  return ((uintptr_t)p % pair) == 0 && sb % 2 == 0 && sh % 2 == 0;
+}
+
 bool fold_supported(const mz_decode_args* a) {
   return a->bits == 4 && a->head_dim == 128 && a->n_groups > 0 &&
-         (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v;
+         (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v &&
+         ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
+         fold_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
+         fold_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
+         fold_meta_aligned(a->v_mn, a->vm_sb, a->vm_sh, a->meta_dtype) &&
+         fold_meta_aligned(a->v_scale, a->vm_sb, a->vm_sh, a->meta_dtype);
+}
+
+static int fold_cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+      n = cus;
+    else
+      n = 256;
+  }
+  return n;
 }
 
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + fold::TILE - 1) / fold::TILE;
   int ns = a->n_split;
   if (ns <= 0) {
+    // fill the resident workgroup slots (two per CU) once: every workgroup
+    // then runs its tiles in one pass with its tables loaded once
     const int64_t units = (int64_t)a->batch * a->kv_heads;
-    const int64_t target = 2048;  // workgroups: several per CU on 256 CUs
-    ns = (int)((target + units - 1) / units);
+    const int64_t slots = 2 * (int64_t)fold_cu_count();
+    ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
   }
   ns = min(ns, n_tiles);
