@@ -1,0 +1,78 @@
+"""The C ABI of libmuzero_hip.so (CPU checks; no kernel is launched).
+
+* every entry point declared in include/muzero_hip.h is exported and has a
+  ctypes signature in muzero_amd/_lib.py;
+* the ctypes mirror of ``mz_decode_args`` has exactly the field offsets and
+  size that a C compiler gives the header's struct;
+* argument validation that happens before any device work (status codes,
+  error strings) behaves as documented.
+"""
+
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from muzero_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "muzero_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(muzero_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for required in ("muzero_quantize_rows", "muzero_quantize_keys", "muzero_quantize_values",
+                     "muzero_dequantize_rows", "muzero_decode_attention", "muzero_decode_workspace_bytes"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version_and_strerror():
+    lib = _lib.load()
+    assert lib.muzero_version().decode().startswith("muzero_hip")
+    for code in (0, -1, -2, -3):
+        assert lib.muzero_strerror(code)
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_decode_args_layout_matches_c(tmp_path):
+    fields = [f for f, _ in _lib.DecodeArgs._fields_]
+    src = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {",
+           '  printf("size %zu\\n", sizeof(mz_decode_args));']
+    src += [f'  printf("{f} %zu\\n", offsetof(mz_decode_args, {f}));' for f in fields]
+    src += ["  return 0;", "}"]
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(c)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict(line.split() for line in out if line)
+    assert int(got["size"]) == ctypes.sizeof(_lib.DecodeArgs)
+    for f in fields:
+        assert int(got[f]) == getattr(_lib.DecodeArgs, f).offset, f
+
+
+def test_decode_workspace_rejects_bad_args_without_a_device():
+    """Host-side validation: unsupported head_dim / n_rep / bits are rejected (-1) before any launch."""
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = 1, 1, 4, 96, 4
+    a.n_groups, a.n_residual = 0, 16
+    assert lib.muzero_decode_workspace_bytes(ctypes.byref(a), None) == -1
+    a.head_dim, a.bits = 128, 9
+    assert lib.muzero_decode_workspace_bytes(ctypes.byref(a), None) == -1

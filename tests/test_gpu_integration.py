@@ -1,0 +1,123 @@
+"""The cache layer, its decode hook and the transformers integration on the GPU.
+
+* A ``MuZeroCacheLayer`` fed a prefill and then one token per decode step
+  holds, after every flush, exactly the packed prefix, metadata and residual
+  that the oracle's cache restatement produces for the same token sequence
+  (bit for bit), and its decode hook matches the oracle's attention.
+* ``model.generate`` with ``cache_implementation="mu_zero_4bit"`` on a small
+  random-weight Qwen3 / Llama runs the fused decode kernel (statistics
+  counters), and its decode-step logits match the same model run with the
+  prefix dequantised and attended by the model's own attention
+  (``MUZERO_DISABLE_FUSED_DECODE=1``).
+"""
+
+import os
+
+import pytest
+import torch
+
+import muzero_amd as mz
+from muzero_amd.cache.layer import MuZeroCacheLayer
+from oracle import reference_torch as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+class _Module:
+    def __init__(self, n_rep):
+        self.num_key_value_groups = n_rep
+        self.training = False
+
+
+def _feed(layer, k, v, prefill):
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    for t in range(prefill, k.shape[2]):
+        layer.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), {"materialize_full_kv": False})
+
+
+@pytest.mark.parametrize("bits,dtype,meta", [(4, torch.bfloat16, "float16"), (2, torch.bfloat16, "float16"),
+                                             (4, torch.float16, "bfloat16"), (3, torch.bfloat16, "float32")])
+def test_cache_layer_matches_oracle_cache(bits, dtype, meta):
+    B, hkv, n_rep, d, prefill, steps = 2, 2, 4, 128, 700, 100
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=11, dtype=dtype)
+    cfg = mz.MuZeroConfig(bits=bits, amax_dtype=meta, alpha_key=2.0, alpha_value=2.0)
+    layer = MuZeroCacheLayer(cfg)
+    _feed(layer, k, v, prefill)
+    fold = bits == 4
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     amax_dtype=getattr(torch, meta),
+                                     dequant_dtype=torch.float32 if fold else None)
+    state = layer.get_attention_state()
+    assert state["key_prefix_length"] == st["lq"] == state["value_prefix_length"]
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    for got, want in ((layer._key_mn, st["k_mn"]), (layer._key_scale, st["k_scale"]),
+                      (layer._value_mn, st["v_mn"]), (layer._value_scale, st["v_scale"])):
+        assert torch.equal(got.cpu().contiguous().view(torch.uint8), want.contiguous().view(torch.uint8))
+    assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+
+    mz.reset_mu_zero_decode_stats()
+    out, w = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    assert w is None and out.shape == (B, 1, hkv * n_rep, d) and out.dtype == dtype
+    assert mz.get_mu_zero_decode_stats()["hip_fused_decode"] == 1
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
+
+
+def test_materialized_kv_matches_dequantized_oracle():
+    """``update(materialize_full_kv=True)`` returns the dequantised prefix + residual, bit-exact
+    to the reference's torch dequantisation in the layer dtype."""
+    k, v, _, _ = ref.synthetic_kv(1, 2, 640, 128, 8, seed=5)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(alpha_key=2.0, alpha_value=2.0))
+    layer.update(k[:, :, :600].to(DEV), v[:, :, :600].to(DEV))
+    fk, fv = layer.update(k[:, :, 600:601].to(DEV), v[:, :, 600:601].to(DEV))
+    _, st = ref.reference_decode(torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16), k[:, :, :601], v[:, :, :601],
+                                 bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    want_k = torch.cat([st["key_prefix"], st["res_k"]], dim=2)
+    want_v = torch.cat([st["value_prefix"], st["res_v"]], dim=2)
+    assert torch.equal(fk.cpu(), want_k) and torch.equal(fv.cpu(), want_v)
+
+
+def _tiny_model(arch):
+    transformers = pytest.importorskip("transformers")
+    torch.manual_seed(0)
+    common = dict(vocab_size=512, hidden_size=512, intermediate_size=1024, num_hidden_layers=2,
+                  num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=4096,
+                  rms_norm_eps=1e-6, attn_implementation="eager")
+    if arch == "qwen3":
+        cfg = transformers.Qwen3Config(**common, rope_theta=1e6)
+        model = transformers.Qwen3ForCausalLM(cfg)
+    else:
+        cfg = transformers.LlamaConfig(**common)
+        model = transformers.LlamaForCausalLM(cfg)
+    for p in model.parameters():
+        torch.nn.init.normal_(p, std=0.02)
+    return model.to(DEV, torch.bfloat16).eval()
+
+
+@pytest.mark.parametrize("arch", ["qwen3", "llama"])
+def test_generate_uses_fused_decode_and_matches_dequant_path(arch, monkeypatch):
+    mz.patch_transformers()
+    model = _tiny_model(arch)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 512, (2, 300), generator=g).to(DEV)
+    kw = dict(max_new_tokens=3, do_sample=False, cache_implementation="mu_zero_4bit",
+              cache_config={"residual_length": 128}, output_scores=True, return_dict_in_generate=True,
+              pad_token_id=0)
+    mz.reset_mu_zero_decode_stats()
+    with torch.no_grad():
+        fused = model.generate(ids, **kw)
+    stats = mz.get_mu_zero_decode_stats()
+    assert stats.get("hip_fused_decode", 0) == 2 * 2  # 2 decode steps x 2 layers
+    monkeypatch.setenv("MUZERO_DISABLE_FUSED_DECODE", "1")
+    with torch.no_grad():
+        dense = model.generate(ids, **kw)
+    # step 0 is the prefill (no cache read); steps 1, 2 read the packed prefix
+    for s in (1, 2):
+        a, b = fused.scores[s].float(), dense.scores[s].float()
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
+    assert torch.equal(fused.sequences[:, :301], dense.sequences[:, :301])

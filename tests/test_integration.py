@@ -1,0 +1,216 @@
+"""Host-side integration layer on the CPU: config validation, the transformers
+registration, and the cache's flush bookkeeping.
+
+The flush tests replace the two HIP quantize entry points with recorders
+that write a fingerprint of each group (its first element) into the output
+views, so the storage layout, growth and slicing are checked without a GPU;
+the kernels themselves are covered by the ``gpu`` tests.
+
+Flush policy under test (reference ``muzero/cache/layer.py:369-396``): after
+an update, ``floor((len - R) / unit) * unit`` residual tokens move to the
+packed prefix, ``unit = G`` at prefill and, with ``decode_flush_by_group``
+(default), at decode; ``unit = 4G`` at decode otherwise.  The value prefix
+stays aligned with the key prefix.
+"""
+
+import pytest
+import torch
+
+import muzero_amd as mz
+from muzero_amd.cache.layer import MuZeroCacheLayer
+from muzero_amd.kernels import loader as L
+
+G = 64
+
+
+# --------------------------------------------------------------------------- config
+
+def test_config_defaults_and_validation():
+    c = mz.MuZeroConfig()
+    assert (c.bits, c.q_group_size, c.residual_length, c.amax_dtype) == (4, 64, 128, "float16")
+    for bad in ({"bits": 5}, {"bits": 6}, {"q_group_size": 0}, {"amax_dtype": "int8"},
+                {"backend": "bogus"}, {"residual_length": 100}):
+        with pytest.raises(ValueError):
+            mz.MuZeroConfig(**bad)
+    # residual need not be a group multiple when flushing in 4-group batches
+    mz.MuZeroConfig(residual_length=100, decode_flush_by_group=False)
+
+
+def test_config_rejects_non_hip_backends():
+    for b in ("triton", "torch"):
+        with pytest.raises(ValueError, match="HIP"):
+            mz.MuZeroConfig(backend=b)
+    for b in ("auto", "hip", "cuda"):
+        assert mz.MuZeroConfig(backend=b).backend == b
+
+
+def test_config_from_dict_ignores_unknown_keys():
+    c = mz.MuZeroConfig.from_dict({"bits": 2, "residual_length": 64, "not_a_field": 1})
+    assert c.bits == 2 and c.residual_length == 64
+
+
+def test_select_alpha_four_bit_is_constant():
+    x = torch.randn(2, 2, 128, 64)
+    assert mz.select_alpha(x, bits=4, q_group_size=64, kind="key") == 2.0
+    assert mz.select_alpha(x, bits=4, q_group_size=64, kind="value") == 2.0
+
+
+def test_select_alpha_values_in_reference_set():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 2, 256, 128, generator=g)
+    x[..., :4] *= 10
+    for bits in (1, 2, 3, 7, 8):
+        for kind in ("key", "value"):
+            a = mz.select_alpha(x, bits=bits, q_group_size=64, kind=kind)
+            assert a in (2.0, 4.0, 16.0)
+    # a heavy tail on 1-bit keys selects a larger alpha (quantizer.py:61-66)
+    y = torch.randn(1, 1, 256, 64, generator=g)
+    y.view(-1)[::97] *= 50
+    assert mz.select_alpha(y, bits=1, q_group_size=64, kind="key") > 2.0
+
+
+# --------------------------------------------------------------------------- transformers registration
+
+def test_patch_transformers_registers_cache_classes():
+    transformers = pytest.importorskip("transformers")
+    mz.patch_transformers()
+    mz.patch_transformers()  # idempotent
+    import transformers.cache_utils as cu
+    import transformers.generation.configuration_utils as gcc
+    for bits in (1, 2, 3, 4, 7, 8):
+        cls = cu.CACHE_CLASS_REGISTRY[f"mu_zero_{bits}bit"]
+        cache = cls(q_group_size=64, residual_length=128, quant_backend="auto")
+        assert isinstance(cache, mz.MuZeroCache) and cache.cfg.bits == bits
+        assert f"mu_zero_{bits}bit" in gcc.ALL_CACHE_IMPLEMENTATIONS
+    transformers.GenerationConfig(cache_implementation="mu_zero_2bit").validate()
+
+
+def test_prepare_cache_builds_mu_zero_cache():
+    transformers = pytest.importorskip("transformers")
+    mz.patch_transformers()
+    from transformers.generation.utils import GenerationMixin
+
+    class _Cfg:
+        is_encoder_decoder = False
+
+    class _Model:
+        config = _Cfg()
+
+    for impl, cfg in (("mu_zero_2bit", {"residual_length": 64}),
+                      ("quantized", {"backend": "logq4_zeroanchor_stat_cuda", "residual_length": 128})):
+        gc = transformers.GenerationConfig(cache_implementation=impl, cache_config=cfg)
+        kw = {}
+        GenerationMixin._prepare_cache_for_generation(_Model(), gc, kw, None, 1, 4096)
+        cache = kw["past_key_values"]
+        assert isinstance(cache, mz.MuZeroCache) and cache.defer_prefill_quantization
+        assert cache.cfg.bits == (2 if impl == "mu_zero_2bit" else 4)
+        assert cache.cfg.residual_length == cfg["residual_length"]
+
+
+# --------------------------------------------------------------------------- flush bookkeeping
+
+@pytest.fixture
+def recorded_quantize(monkeypatch):
+    """Stand-ins for the HIP block quantizers: mn <- the group's first element, packed/scale <- 0."""
+    calls = []
+
+    def keys_into(x, bits, alpha, eps, packed, mn, scale):
+        b, h, t, d = x.shape
+        assert t % G == 0 and packed.shape[2] == t // G
+        mn.copy_(x.reshape(b, h, t // G, G, d)[:, :, :, 0, :].unsqueeze(-1).to(mn.dtype))
+        packed.zero_()
+        scale.zero_()
+        calls.append(("k", t))
+
+    def values_into(x, bits, alpha, eps, packed, mn, scale):
+        b, h, t, d = x.shape
+        assert packed.shape[2] == t
+        mn.copy_(x[..., ::G].unsqueeze(-1).to(mn.dtype))
+        packed.zero_()
+        scale.zero_()
+        calls.append(("v", t))
+
+    monkeypatch.setattr(L, "quantize_key_block_into", keys_into)
+    monkeypatch.setattr(L, "quantize_value_block_into", values_into)
+    return calls
+
+
+def _expected_prefix(total, r, unit):
+    return max(total - r, 0) // unit * unit
+
+
+@pytest.mark.parametrize("by_group", [True, False])
+def test_flush_schedule_and_storage(recorded_quantize, by_group):
+    cfg = mz.MuZeroConfig(residual_length=128, decode_flush_by_group=by_group)
+    layer = MuZeroCacheLayer(cfg)
+    B, H, D = 2, 2, 128
+    g = torch.Generator().manual_seed(3)
+    total_tokens = 700 + 300
+    K = torch.randn(B, H, total_tokens, D, generator=g).to(torch.float16)
+    V = torch.randn(B, H, total_tokens, D, generator=g).to(torch.float16)
+    k0, v0 = layer.update(K[:, :, :700], V[:, :, :700], {"materialize_full_kv": False})
+    assert k0.shape[2] == 700  # the first call returns the raw prefill KV
+    prefix = _expected_prefix(700, 128, G)
+    for step in range(300):
+        t = 700 + step
+        layer.update(K[:, :, t:t + 1], V[:, :, t:t + 1], {"materialize_full_kv": False})
+        total = t + 1
+        st = layer.get_attention_state()
+        new = total - prefix - 128
+        unit = G if by_group else 4 * G
+        if new >= unit:
+            prefix += new // unit * unit
+        assert st["key_prefix_length"] == prefix == st["value_prefix_length"], (step, st)
+        assert layer.keys.shape[2] == total - prefix
+        torch.testing.assert_close(layer.keys, K[:, :, prefix:total], rtol=0, atol=0)
+        torch.testing.assert_close(layer.values, V[:, :, prefix:total], rtol=0, atol=0)
+    assert layer.get_seq_length() == total_tokens
+    # packed storage holds every flushed group in order, across capacity growth
+    ng = prefix // G
+    kmn = layer._key_mn
+    assert kmn.shape == (B, H, ng, D, 1)
+    torch.testing.assert_close(kmn[..., 0], K[:, :, :prefix:G].to(kmn.dtype), rtol=0, atol=0)
+    vmn = layer._value_mn
+    assert vmn.shape == (B, H, prefix, 2, 1)
+    torch.testing.assert_close(vmn[..., 0], V[:, :, :prefix, ::G].to(vmn.dtype), rtol=0, atol=0)
+    assert layer._kstore.capacity >= ng and layer._vstore.capacity >= prefix
+
+
+def test_deferred_prefill_then_finalize(recorded_quantize):
+    cache = mz.MuZeroCache(mz.MuZeroConfig())
+    K = torch.randn(1, 2, 500, 128).to(torch.bfloat16)
+    for layer_idx in range(3):
+        cache.update(K, K, layer_idx, {"materialize_full_kv": True, "defer_quantize": True})
+    assert all(st["key_prefix_length"] == 0 for st in (cache.get_attention_state(i) for i in range(3)))
+    assert recorded_quantize == []
+    cache.finalize_prefill_quantization()
+    for i in range(3):
+        st = cache.get_attention_state(i)
+        assert st["key_prefix_length"] == _expected_prefix(500, 128, G) == st["value_prefix_length"]
+    assert cache.get_seq_length() == 500 and cache.seen_tokens == 500 and len(cache) == 3
+
+
+def test_beam_reorder_applies_to_packed_prefix(recorded_quantize):
+    layer = MuZeroCacheLayer(mz.MuZeroConfig())
+    K = torch.randn(3, 2, 400, 128).to(torch.float16)
+    layer.update(K, K, {"materialize_full_kv": False})
+    layer.update(K[:, :, :1], K[:, :, :1], {"materialize_full_kv": False})
+    before = layer._key_mn.clone()
+    res_before = layer.keys.clone()
+    idx = torch.tensor([2, 0, 0])
+    layer.reorder_cache(idx)
+    torch.testing.assert_close(layer._key_mn, before[idx], rtol=0, atol=0)
+    torch.testing.assert_close(layer.keys, res_before[idx], rtol=0, atol=0)
+    layer.batch_repeat_interleave(2)
+    assert layer._key_mn.shape[0] == 6 and layer.keys.shape[0] == 6
+    # decode continues after the reorder (residual buffer re-created)
+    layer.update(K[:3].repeat_interleave(2, 0)[:, :, :1], K[:3].repeat_interleave(2, 0)[:, :, :1],
+                 {"materialize_full_kv": False})
+    assert layer.get_seq_length() == 402
+
+
+def test_cpu_tensors_are_rejected_by_the_kernels():
+    """No CPU path in the product: the HIP entry points refuse host tensors."""
+    from muzero_amd._lib import MuZeroHipError
+    with pytest.raises(MuZeroHipError):
+        mz.quantize_rows(torch.randn(4, 64), 4, 2.0, 1e-8, torch.float16)
