@@ -131,10 +131,11 @@ typedef struct mz_decode_args {
   const void* v_res; int64_t vr_sb, vr_sh, vr_st;
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
-  /* 4-bit (P, N) fold tables for alpha_key / alpha_value: 16 x 16 pairs of
-   * fp16 (P, N) packed in uint32 (P in the low half), row = zero level,
-   * column = code; see muzero_amd/tables.py ("fold4").  Needed by the 4-bit
-   * fast path; may be null (the generic path is used then). */
+  /* (P, N) fold tables for alpha_key / alpha_value (bits 4 and 2): 16 x 16
+   * pairs of fp16 (P, N) packed in uint32 (P in the low half), row = zero
+   * level, column = code, zero beyond 2^bits - 1; see muzero_amd/tables.py
+   * ("fold4", "fold2").  Needed by the fold fast path; may be null (the
+   * generic path is used then). */
   const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;
@@ -142,8 +143,8 @@ typedef struct mz_decode_args {
   int kernel_path;  /* MZ_PATH_AUTO, or force MZ_PATH_EXACT / MZ_PATH_FOLD */
 } mz_decode_args;
 
-/* kernel paths of muzero_decode_attention: AUTO uses the 4-bit fold kernel
- * when it applies (bits 4, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
+/* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
+ * applies (bits 4 or 2, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
  * and the exact-dequantize kernel otherwise. */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 

@@ -1,11 +1,11 @@
-// Packed-KV decode attention, fast path for 4-bit codes (gfx950, wave64).
+// Packed-KV decode attention, fast path for 4-bit and 2-bit codes (gfx950, wave64).
 //
 // Dequantization folded into the MFMA operands.  For a group with stored
 // (mn, s) the reference dequantizes code q as (muzero/quantizer.py:241-255)
 //   x = mn + s * (za + pe * E[pb][q - zl])   (q >= zl)
 //   x = mn + s * (za - ne * E[nb][zl - q])   (q <  zl)
 // which is x = a + bp * P(zl, q) + bn * N(zl, q) with per-group scalars
-// a = mn + s*za, bp = s*pe, bn = -s*ne and a 16 x 16 table of pairs
+// a = mn + s*za, bp = s*pe, bn = -s*ne and a (qmax+1)^2 table of pairs
 // (P, N) = (E[pb][q-zl], 0) or (0, E[nb][zl-q]).  So
 //   q.k = sum_c (Q_c*a_c) + sum_c [(Q_c*bp_c) P + (Q_c*bn_c) N]
 // is an MFMA whose A operand carries the group scalars times the query (for
@@ -17,21 +17,24 @@
 // (their fp32 codebooks, loader.py:197-263), not rounded to the layer dtype.
 //
 // Work of one wave: a 64-token tile = one key group (or 64 residual tokens).
-//   QK: MFMA M rows = query heads of the kv-head (GQA grouping), columns =
-//   tokens 4n+jt of N-tiles jt = 0..3; lane (n, g) of k-tile kt holds
-//   channels 16kt+4g+{0..3} and needs, for each, 16 bits of the channel's
-//   packed row (tokens 4n..4n+3).
+//   QK: MFMA columns = tokens 4n+jt of N-tiles jt = 0..3; lane (n, g) of
+//   k-tile kt holds channels 16kt+4g+{0..3} and needs, for each, the 4 codes
+//   of its tokens 4n..4n+3 (16 bits of the channel's row at 4 bits, 8 at 2).
 //   PV: columns = channels 64vg+4n+jt, k = (token, side); lane (n, g) needs
-//   16 bits of a token's packed row per value group (channels 4n..4n+3).
-//   Both are loaded straight from HBM as 32-bit words shared by lane pairs.
+//   the codes of channels 4n..4n+3 of tokens 16kt+4g+{0..3}.
+//   Lane pairs load the rows' shared words straight from HBM (buffer loads,
+//   the tile offset in a scalar register) and swap halves with one DPP move.
+//   MFMA rows = query heads of the kv-head, spread to rows h*16/NREP: every
+//   lane group of the MFMA output then holds real logits, so the softmax
+//   runs in registers (row reductions on DPP) with no LDS round trip.
 // Each code is one conflict-free ds_read_b32 from a per-lane-group copy of
-// the (P, N) table in LDS, addressed with 1.5 VALU ops per code.  The key-side products q*bp, q*bn are formed once per (head,
-// channel) per tile as fp16 hi + lo pairs (two MFMAs per k-tile keep them at
-// fp32 accuracy).  The next tile's code words and metadata are loaded into
-// registers while the current tile is computed.  The softmax of a tile is
-// redistributed through LDS so every lane computes exps.  fp16 operands are
-// kept in range by a power-of-two scale per key group and per value tile,
-// folded into the logits and into the online-softmax rescale.
+// the (P, N) table in LDS, addressed with about 1.5 VALU ops per code, read
+// straight into the MFMA B register.  The key-side products q*bp, q*bn are
+// formed once per (head, channel) per tile as fp16 hi + lo pairs (two MFMAs
+// per k-tile keep them at fp32 accuracy).  The next tile's code words and
+// metadata are loaded while the current tile is computed.  fp16 operands
+// are kept in range by a power-of-two scale per key group and per value
+// tile, folded into the logits and into the online-softmax rescale.
 //
 // Launch: one workgroup of 4 waves per (batch, kv-head, split); a split is a
 // run of tiles, waves take every 4th tile; the split's (m, l, acc) goes to the
@@ -43,26 +46,32 @@ namespace mz {
 namespace fold {
 
 constexpr int D = 128;
-constexpr int QB = 32;       // bytes per packed 64-code group (4-bit)
-constexpr int NG = 2;        // value groups per token
-constexpr int TILE = 64;     // tokens per tile
+constexpr int NG = 2;     // value groups per token
+constexpr int TILE = 64;  // tokens per tile
 constexpr int WAVES = 4;
+constexpr uint32_t ONES_F16X2 = 0x3C003C00u;
 // (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
 // zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
 // level (one channel / one token-group), and each group owns a disjoint bank
 // range, so the per-code lookups are free of bank conflicts.
 constexpr int TBL = 16 * 4 * 16 * 4;  // 4 KB
-constexpr uint32_t ONES_F16X2 = 0x3C003C00u;
+
+template <int BITS>
+struct Fmt {
+  static constexpr int QMAX = (1 << BITS) - 1;
+  static constexpr int QB = 8 * BITS;  // bytes per packed 64-code row
+  static constexpr int LB = BITS / 2;  // bytes per lane per row (its 4 codes)
+};
 
 // Padded row lengths (in 4-byte words) of the [head][...] arrays so that the
 // rows read together by lanes of different heads start in different banks.
-constexpr int AROW = D + 4;     // uint32 per head row of the key A operand
-constexpr int HROW = D / 2 + 4;  // uint32 per head row of fp16 [D] arrays
-constexpr int LROW = TILE + 4;  // uint32 per head row of per-token arrays
-constexpr int PROW = TILE / 2 + 4;
+constexpr int AROW = D + 4;         // uint32 per head row of the key A operand
+constexpr int HROW = D / 2 + 4;     // uint32 per head row of fp16 [D] arrays
+constexpr int LROW = TILE + 4;      // uint32 per head row of per-token arrays
+constexpr int PROW = TILE / 2 + 4;  // uint32 per head row of fp16 per-token arrays
 
-// Static LDS layout (bytes).  Per workgroup: the byte tables and the query
-// in two forms; per wave: the current tile's operands and softmax state.
+// Static LDS layout (bytes).  Per workgroup: the two (P, N) tables and the
+// query in two forms; per wave: the current tile's operands and weights.
 template <int NREP>
 struct Smem {
   static constexpr int TBL_K = 0;
@@ -78,18 +87,15 @@ struct Smem {
   static constexpr int VZL = QA + NREP * HROW * 4;   // uint32 [NG][TILE]     zl << 8
   static constexpr int VBP = VZL + NG * TILE * 4;    // uint32 [NG][TILE]     (bp, bn) fp16
   static constexpr int VA = VBP + NG * TILE * 4;     // fp16 [NG][TILE]       a
-  static constexpr int LOGIT = VA + NG * TILE * 2;   // f32 [NREP][LROW]
-  static constexpr int P2 = LOGIT + NREP * LROW * 4;  // uint32 [NREP][LROW]  (p, p)
+  static constexpr int P2 = VA + NG * TILE * 2;      // uint32 [NREP][LROW]   (p, p)
   static constexpr int P1 = P2 + NREP * LROW * 4;    // fp16 [NREP][PROW*2]
-  static constexpr int CORR = P1 + NREP * PROW * 4;  // f32 [NREP]
-  static constexpr int PER_WAVE = (CORR + NREP * 4 + 15) / 16 * 16;
+  static constexpr int PER_WAVE = (P1 + NREP * PROW * 4 + 15) / 16 * 16;
   static constexpr int MERGE = (2 * NREP + NREP * D) * 4;  // per wave at the end (aliases the wave area)
   static constexpr int WAVE_AREA = WAVES * (PER_WAVE > MERGE ? PER_WAVE : MERGE);
   static constexpr int TOTAL = WAVE0 + WAVE_AREA;
 };
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
@@ -128,8 +134,9 @@ struct GroupScalars {
 
 // (a, bp, bn, zl) of one stored group (mn, s); the scale is guarded like the
 // reference CUDA extension (loader.py:201), so an all-zero group gives x = mn.
+template <int QMAX>
 __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
-  constexpr float qmax = 15.f;
+  constexpr float qmax = (float)QMAX;
   const float eps = 1e-8f;
   if (!(s >= eps)) s = eps;
   const float za = clamp01((0.f - mn) / s);  // IEEE division: zl must match the reference
@@ -144,113 +151,150 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   return r;
 }
 
-// Raw bits of the metadata entries i, i+1 (two words for fp32, one for the
-// 16-bit types).  Loaded without converting: a conversion inside a dtype
-// branch would make the compiler wait for every load issued before it.
-__device__ __forceinline__ uint2 meta_raw(const void* p, int64_t i, int dt) {
-  const int es = dt == MZ_F32 ? 4 : 2;
-  const uint8_t* q = (const uint8_t*)p + i * es;
-  return uint2{*(const uint32_t*)q, *(const uint32_t*)(q + (dt == MZ_F32 ? 4 : 0))};
-}
-
 __device__ __forceinline__ float2 meta_cvt(uint2 w, int dt) {
   if (dt == MZ_F32) return float2{__builtin_bit_cast(float, w.x), __builtin_bit_cast(float, w.y)};
   if (dt == MZ_F16) return float2{h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16))};
   return float2{bf2f((uint16_t)w.x), bf2f((uint16_t)(w.x >> 16))};
 }
 
-// Global data of one quantized tile, loaded one tile ahead.  Code words are
-// loaded 32 bits per lane: lanes 2m and 2m+1 of a lane group read the same 4
-// bytes (8 codes) of the two channels (key) / tokens (value) of a pair, and
-// code_pair() later swaps halves between them, so each lane ends with the 16
-// bits of both rows that hold ITS four tokens / channels.
-struct TileData {
-  uint32_t kw[16];  // key rows 16kt+4g+2p+(n&1), bytes 4*(n>>1): [kt][p]
-  uint32_t vw[16];  // value tokens 16kt+4g+2p+(n&1), bytes 32vg+4*(n>>1): [kt][vg][p]
-  uint2 kmn, ksc;   // key groups of channels 2*lane, 2*lane+1 (raw bits)
-  uint2 vmn, vsc;   // value groups 0, 1 of token lane (raw bits)
+// Buffer resources of one (batch, kv-head): the packed prefix and metadata
+// (bounded by their filled length, so a load past it reads 0, never faults).
+struct Bufs {
+  __amdgpu_buffer_rsrc_t kp, vp, kmn, ksc, vmn, vsc;
 };
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
+}
+
+// Global data of one quantized tile, loaded one tile ahead.  Code words:
+// lanes 2m and 2m+1 of a lane group read the same 2*LB bytes of two rows of a
+// pair (key: channels, value: tokens); code_pair() later swaps halves between
+// them so each lane ends with the bytes of both rows that hold ITS codes.
+//   4-bit: kw[kt*2+p] = 32 bits of row 16kt+4g+2p+(n&1)
+//   2-bit: kw[kt*2+h] = 16 bits of row 16kt+4g+2h+(n&1)
+// (values: vw[(kt*NG+vg)*2 + p|h], rows = tokens, bytes of value group vg).
+struct TileData {
+  uint32_t kw[16];
+  uint32_t vw[16];
+  uint2 kmn, ksc;  // key groups of channels 2*lane, 2*lane+1 (raw bits)
+  uint2 vmn, vsc;  // value groups 0, 1 of token lane (raw bits)
+};
+
+template <int BITS>
+__device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int imm) {
+  if constexpr (BITS == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, voff + imm, soff, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff + imm, soff, 0);
+}
+
 // Key code words and all metadata of a tile (issued at the start of the
-// previous tile) ...
-__device__ __forceinline__ void load_tile_k(TileData& t, const mz_decode_args& a, const uint8_t* kp_bh,
-                                            int64_t km_bh, int64_t vm_bh, int tile, int lane) {
+// previous tile; metadata first, so its consumer need not wait for the codes).
+template <int BITS>
+__device__ __forceinline__ void load_tile_k(TileData& t, const Bufs& bf, int tile, int lane, int meta_es,
+                                            int meta_hi) {
+  using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  // metadata first: its consumer then need not wait for the code words
-  const int64_t ki = km_bh + (int64_t)tile * D + 2 * lane;
-  t.kmn = meta_raw(a.k_mn, ki, a.meta_dtype);
-  t.ksc = meta_raw(a.k_scale, ki, a.meta_dtype);
-  const int64_t vi = vm_bh + ((int64_t)tile * TILE + lane) * NG;
-  t.vmn = meta_raw(a.v_mn, vi, a.meta_dtype);
-  t.vsc = meta_raw(a.v_scale, vi, a.meta_dtype);
-  const uint32_t* kq = (const uint32_t*)(kp_bh + (int64_t)tile * D * QB + (4 * g + (n & 1)) * QB + 4 * (n >> 1));
+  const int kmo = 2 * lane * meta_es, kms = tile * D * meta_es;
+  t.kmn = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.kmn, kmo, kms, 0),
+                __builtin_amdgcn_raw_buffer_load_b32(bf.kmn, kmo + meta_hi, kms, 0)};
+  t.ksc = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.ksc, kmo, kms, 0),
+                __builtin_amdgcn_raw_buffer_load_b32(bf.ksc, kmo + meta_hi, kms, 0)};
+  const int vmo = NG * lane * meta_es, vms = tile * TILE * NG * meta_es;
+  t.vmn = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.vmn, vmo, vms, 0),
+                __builtin_amdgcn_raw_buffer_load_b32(bf.vmn, vmo + meta_hi, vms, 0)};
+  t.vsc = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.vsc, vmo, vms, 0),
+                __builtin_amdgcn_raw_buffer_load_b32(bf.vsc, vmo + meta_hi, vms, 0)};
+  const int voff = (4 * g + (n & 1)) * F::QB + 2 * F::LB * (n >> 1);
+  const int soff = tile * D * F::QB;
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) t.kw[kt * 2 + p] = kq[(16 * kt + 2 * p) * (QB / 4)];
+    for (int p = 0; p < 2; ++p) t.kw[kt * 2 + p] = load_code_word<BITS>(bf.kp, voff, soff, (16 * kt + 2 * p) * F::QB);
 }
 
 // ... and its value code words (issued once the previous tile's key words
 // are consumed, so the two register sets overlap less).
-__device__ __forceinline__ void load_tile_v(TileData& t, const uint8_t* vp_bh, int tile, int lane) {
+template <int BITS>
+__device__ __forceinline__ void load_tile_v(TileData& t, const Bufs& bf, int tile, int lane) {
+  using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const uint32_t* vq =
-      (const uint32_t*)(vp_bh + ((int64_t)tile * TILE + 4 * g + (n & 1)) * (NG * QB) + 4 * (n >> 1));
+  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + 2 * F::LB * (n >> 1);
+  const int soff = tile * TILE * NG * F::QB;
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
     for (int vg = 0; vg < NG; ++vg)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) t.vw[(kt * NG + vg) * 2 + p] = vq[((16 * kt + 2 * p) * (NG * QB) + QB * vg) / 4];
+      for (int p = 0; p < 2; ++p)
+        t.vw[(kt * NG + vg) * 2 + p] =
+            load_code_word<BITS>(bf.vp, voff, soff, (16 * kt + 2 * p) * (NG * F::QB) + F::QB * vg);
 }
 
-// This lane's two 16-bit code rows of a pair: low half = row 2p, high half =
-// row 2p+1, each holding the codes of tokens / channels 4n..4n+3.  `sel`
-// is the lane's v_perm selector (even lanes keep the low halves of both
-// words, odd lanes the high halves).
-__device__ __forceinline__ uint32_t code_pair(uint32_t own, uint32_t sel) {
-  const uint32_t other = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)own, DPP_QUAD_XOR1, 0xF, 0xF, false);
-  return __builtin_amdgcn_perm(other, own, sel);
+__device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_XOR1, 0xF, 0xF, false);
 }
 
-// The B operands of one k-tile from two code words w01, w23 (channels or
-// tokens ii = 0, 1 in the low / high half of w01, ii = 2, 3 in w23; each half
-// holds the codes of tokens / channels 4n+0..3 of N-tiles jt = 0..3).  The
-// even and odd nibbles of a word are spread to bytes as table offsets
-// 4*q + 64*group (two ops per 4 codes); one v_perm per code then places the
-// offset under the zero-level row (zr = zl << 8) and one ds_read_b32 fetches
-// the (P, N) pair straight into the operand register.
-template <int TBASE>
-__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, const uint32_t w01, const uint32_t w23,
-                                             const u32x4 zr, const uint32_t grep, u32x4 B[4]) {
-  const uint32_t ev[2] = {((w01 << 2) & 0x3C3C3C3Cu) | grep, ((w23 << 2) & 0x3C3C3C3Cu) | grep};
-  const uint32_t od[2] = {((w01 >> 2) & 0x3C3C3C3Cu) | grep, ((w23 >> 2) & 0x3C3C3C3Cu) | grep};
+// The B operands of one k-tile (4 rows ii of this lane's k-slice x its 4
+// codes, jt = code index) from the two raw words w0, w1 of the k-tile.  The
+// codes are spread to bytes as table offsets 4*q + 64*group (two ops per 4
+// codes); one v_perm per code then places the offset under the zero-level
+// row (zr = zl << 8) and one ds_read_b32 fetches the (P, N) pair straight into
+// the operand register.  `odd` = lane n is odd.
+template <int BITS, int TBASE>
+__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, uint32_t w1, const u32x4 zr,
+                                             uint32_t grep, bool odd, u32x4 B[4]) {
+  if constexpr (BITS == 4) {
+    // w0 / w1: rows (0,1) / (2,3) of the pair, 32 bits = codes of lanes 2m, 2m+1;
+    // this lane keeps 16 bits of each row: low half = row 2p, high half = row 2p+1
+    const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+    const uint32_t r01 = __builtin_amdgcn_perm(dpp_swap_pairs(w0), w0, sel);
+    const uint32_t r23 = __builtin_amdgcn_perm(dpp_swap_pairs(w1), w1, sel);
+    // even / odd nibbles of each half: bytes (4*q0 | 4*q2 | ...) of rows ii
+    const uint32_t ev[2] = {((r01 << 2) & 0x3C3C3C3Cu) | grep, ((r23 << 2) & 0x3C3C3C3Cu) | grep};
+    const uint32_t od[2] = {((r01 >> 2) & 0x3C3C3C3Cu) | grep, ((r23 >> 2) & 0x3C3C3C3Cu) | grep};
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii)
+    for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const uint32_t e = (jt & 1) ? od[ii >> 1] : ev[ii >> 1];
+        const uint32_t s = 0x0C0C0500u | (uint32_t)((ii & 1) * 2 + (jt >> 1));
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], e, s));
+      }
+  } else {
+    // w0 / w1: 16 bits of rows (0 | 1) / (2 | 3) (even / odd lane), one byte per
+    // lane of the pair; gather this lane's byte of rows 0..3 into one word
+    const uint32_t own = w0 | (w1 << 16);
+    const uint32_t sel = odd ? 0x03070105u : 0x06020400u;
+    const uint32_t w = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, sel);  // byte ii = row ii
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
-      const uint32_t e = (jt & 1) ? od[ii >> 1] : ev[ii >> 1];
-      const uint32_t sel = 0x0C0C0500u | (uint32_t)((ii & 1) * 2 + (jt >> 1));
-      B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], e, sel));
+      const uint32_t e = (jt == 0 ? (w << 2) : (w >> (2 * jt - 2))) & 0x0C0C0C0Cu;
+      const uint32_t ej = e | grep;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], ej, 0x0C0C0500u | (uint32_t)ii));
     }
+  }
 }
 
-template <int IO, int NREP>
+template <int IO, int NREP, int BITS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
     const uint32_t* __restrict__ ftab_v) {
   using M = Mfma<IO>;
   using S = Smem<NREP>;
-  constexpr int LPH = 64 / NREP;   // softmax layout: lanes per head
-  constexpr int TPL = TILE / LPH;  // tokens per lane
+  using F = Fmt<BITS>;
+  constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
+  constexpr int HS = NREP > 4 ? NREP / 4 : 1;   // head slots per lane of the MFMA output
   __shared__ __align__(16) uint8_t smem[S::TOTAL];
 
   const int lane = threadIdx.x & 63;
   // wave-uniform (the compiler cannot see that threadIdx.x >> 6 is): tile
-  // bookkeeping and load bases then live in scalar registers
+  // bookkeeping and load offsets then live in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
+  const bool odd = (n & 1) != 0;
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -259,10 +303,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n_tiles = a.n_groups + n_tiles_d;
   const int t_begin = split * tiles_per_split;
   const int t_end = min(n_tiles, t_begin + tiles_per_split);
-  const uint8_t* kp_bh = a.k_packed + b * a.kp_sb + kvh * a.kp_sh;
-  const uint8_t* vp_bh = a.v_packed + b * a.vp_sb + kvh * a.vp_sh;
-  const int64_t km_bh = b * a.km_sb + kvh * a.km_sh;
-  const int64_t vm_bh = b * a.vm_sb + kvh * a.vm_sh;
+  const int meta_es = a.meta_dtype == MZ_F32 ? 4 : 2;
+  const int meta_hi = a.meta_dtype == MZ_F32 ? 4 : 0;  // second word of an fp32 pair
+  Bufs bf;
+  {
+    const int64_t ng = a.n_groups;
+    bf.kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * F::QB);
+    bf.vp = make_buf(a.v_packed + b * a.vp_sb + kvh * a.vp_sh, ng * TILE * NG * F::QB);
+    const int64_t km = b * a.km_sb + kvh * a.km_sh, vm = b * a.vm_sb + kvh * a.vm_sh;
+    bf.kmn = make_buf((const uint8_t*)a.k_mn + km * meta_es, ng * D * meta_es);
+    bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * D * meta_es);
+    bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NG * meta_es);
+    bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NG * meta_es);
+  }
 
   // Tile loads are issued unconditionally (the compiler's wait counts then
   // stay exact and a prefetch is never waited for early); a tile index that
@@ -271,8 +324,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int q_last = max(0, min(t_end, a.n_groups) - 1);
   TileData T0, T1;
   const int tile0 = t_begin + wave;
-  load_tile_k(T0, a, kp_bh, km_bh, vm_bh, min(tile0, q_last), lane);
-  load_tile_v(T0, vp_bh, min(tile0, q_last), lane);
+  load_tile_k<BITS>(T0, bf, min(tile0, q_last), lane, meta_es, meta_hi);
+  load_tile_v<BITS>(T0, bf, min(tile0, q_last), lane);
 
   // ---------------- workgroup setup: tables and query in LDS
   for (int i = threadIdx.x; i < TBL / 4; i += 256) {
@@ -289,7 +342,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     ((uint16_t*)(smem + S::Q_IO))[h * HROW * 2 + c] = raw;
     qabs = fmaxf(qabs, fabsf(qf));
   }
-  qabs = wave_max(qabs);
+  qabs = wave_max_fast(qabs);
   float* wq = (float*)(smem + S::WAVE0);
   if (lane == 0) wq[wave] = qabs;
   __syncthreads();
@@ -297,21 +350,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __syncthreads();
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
-  float* logit = (float*)(W + S::LOGIT);
   uint32_t* p2 = (uint32_t*)(W + S::P2);
   uint16_t* p1 = (uint16_t*)(W + S::P1);
-  float* corrs = (float*)(W + S::CORR);
 
-  // A-operand row of this lane: a query head; rows >= NREP (MFMA padding)
-  // repeat head 0 and their outputs are never read
-  const int hA = n < NREP ? n : 0;
+  // A-operand row n of this lane: query head n / RS when n % RS == 0; the
+  // other rows (MFMA padding) repeat head 0 and their outputs are never read
+  const int hA = (n % RS) == 0 ? n / RS : 0;
   const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
-  // even lanes: (own lo, other lo); odd lanes: (other hi, own hi)
-  const uint32_t psel = (n & 1) ? 0x03020706u : 0x05040100u;
-  const int sh = lane / LPH;           // softmax layout: head
-  const int st0 = (lane % LPH) * TPL;  // and first token
+  // MFMA output element (g, i) = row 4g+i: head slot s is element i = s*RS
+  // when 4g % RS == 0 (the lane group holds query heads), head 4g/RS + s
+  const bool owner = ((4 * g) % RS) == 0;
+  const int h0 = (4 * g) / RS;
 
-  float m_run = -INFINITY, l_run = 0.f;  // head sh
+  float m_run[HS], l_run[HS];
+#pragma unroll
+  for (int s = 0; s < HS; ++s) m_run[s] = -INFINITY, l_run[s] = 0.f;
   f32x4 acc[NG][4], acc_a[NG];
 #pragma unroll
   for (int vg = 0; vg < NG; ++vg) {
@@ -325,7 +378,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // one tile; the next quantized tile tn of this wave (if any) is loaded into Tn
   auto process = [&](const int tile, const TileData& T, TileData& Tn, const int tn) {
     const int tl = min(tn, q_last);
-    load_tile_k(Tn, a, kp_bh, km_bh, vm_bh, tl, lane);
+    load_tile_k<BITS>(Tn, bf, tl, lane, meta_es, meta_hi);
     const bool quant = tile < a.n_groups;
     int n_valid, pos0, r0 = 0;
     if (quant) {
@@ -343,8 +396,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (quant) {
       // ---------- key group scalars (lane: channels 2*lane, 2*lane+1)
       const float2 kmn = meta_cvt(T.kmn, a.meta_dtype), ksc = meta_cvt(T.ksc, a.meta_dtype);
-      const GroupScalars k0 = group_scalars(kmn.x, ksc.x);
-      const GroupScalars k1 = group_scalars(kmn.y, ksc.y);
+      const GroupScalars k0 = group_scalars<F::QMAX>(kmn.x, ksc.x);
+      const GroupScalars k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
       float kmx = fmaxf(fmaxf(fabsf(k0.a), fmaxf(k0.bp, -k0.bn)), fmaxf(fabsf(k1.a), fmaxf(k1.bp, -k1.bn)));
       kmx = wave_max_fast(kmx);
       const int kexp = min(range_exp(kmx * fmaxf(qabs, 1.f)), range_exp(kmx));
@@ -365,8 +418,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       // ---------- value scalars (lane: token lane, both value groups)
       const float2 vmn = meta_cvt(T.vmn, a.meta_dtype), vsc = meta_cvt(T.vsc, a.meta_dtype);
-      const GroupScalars v0 = group_scalars(vmn.x, vsc.x);
-      const GroupScalars v1 = group_scalars(vmn.y, vsc.y);
+      const GroupScalars v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
+      const GroupScalars v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
       const float vmx = fmaxf(fmaxf(fabsf(v0.a), fmaxf(v0.bp, -v0.bn)), fmaxf(fabsf(v1.a), fmaxf(v1.bp, -v1.bn)));
       // keep the accumulators' exponent unless this tile needs a smaller one
       kv_exp = min(kacc_init ? kacc : 60, range_exp(wave_max_fast(vmx)));
@@ -393,8 +446,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const u32x4 Alo = *(const u32x4*)(W + S::ALO + (hA * AROW + 16 * kt + 4 * g) * 4);
         const u32x4 zr = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
         u32x4 B[4];
-        lookup_ktile<S::TBL_K>(smem, code_pair(T.kw[2 * kt], psel), code_pair(T.kw[2 * kt + 1], psel), zr, grep,
-                               B);
+        lookup_ktile<BITS, S::TBL_K>(smem, T.kw[2 * kt], T.kw[2 * kt + 1], zr, grep, odd, B);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ahi, B[jt], s[jt]);
 #pragma unroll
@@ -417,55 +469,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
-    load_tile_v(Tn, vp_bh, tl, lane);
+    load_tile_v<BITS>(Tn, bf, tl, lane);
 
-    // ---------- softmax over the tile (redistributed: lane -> head sh, tokens st0..)
+    // ---------- online softmax in registers: head slot s of this lane group
+    // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
+    float corr[HS];
+    bool moved = false;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g + i;
-      if (h < NREP) *(f32x4*)(logit + h * LROW + 4 * n) = f32x4{s[0][i], s[1][i], s[2][i], s[3][i]} * unscale;
-    }
-    wave_lds_sync();
-    float x[TPL];
-    float tmax = -INFINITY;
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS;  // MFMA output element of this head slot
+      float x[4];
+      float tmax = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < TPL; ++t) {
-      const int tt = st0 + t;
-      float v = logit[sh * LROW + tt];
-      if (tt >= n_valid) v = -INFINITY;
-      else if (a.mask) v += a.mask[b * a.mask_sb + pos0 + tt];
-      x[t] = v;
-      tmax = fmaxf(tmax, v);
-    }
-    tmax = group_reduce<LPH>(tmax, OpMax());
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = (m_new == -INFINITY) ? 1.f : __expf(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
+      for (int jt = 0; jt < 4; ++jt) {
+        const int tt = 4 * n + jt;
+        float v = s[jt][i] * unscale;
+        if (tt >= n_valid) v = -INFINITY;
+        else if (a.mask) v += a.mask[b * a.mask_sb + pos0 + tt];
+        x[jt] = v;
+        tmax = fmaxf(tmax, v);
+      }
+      tmax = group_reduce<16>(tmax, OpMax());
+      const float m_new = fmaxf(m_run[sl], tmax);
+      corr[sl] = (m_new == -INFINITY) ? 1.f : __expf(m_run[sl] - m_new);
+      moved |= corr[sl] != 1.f;
+      m_run[sl] = m_new;
+      float psum = 0.f;
+      uint32_t pp[4];
+      uint16_t ph[4];
 #pragma unroll
-    for (int t = 0; t < TPL; ++t) {
-      const float p = (x[t] == -INFINITY) ? 0.f : __expf(x[t] - m_new);
-      const uint16_t ph = f2h(p);
-      psum += h2f(ph);
-      p2[sh * LROW + st0 + t] = (uint32_t)ph | ((uint32_t)ph << 16);
-      p1[sh * PROW * 2 + st0 + t] = ph;
+      for (int jt = 0; jt < 4; ++jt) {
+        const float p = (x[jt] == -INFINITY) ? 0.f : __expf(x[jt] - m_new);
+        ph[jt] = f2h(p);
+        psum += h2f(ph[jt]);
+        pp[jt] = (uint32_t)ph[jt] | ((uint32_t)ph[jt] << 16);
+      }
+      psum = group_reduce<16>(psum, OpAdd());
+      l_run[sl] = l_run[sl] * corr[sl] + psum;
+      if (owner) {
+        const int h = h0 + sl;
+        *(u32x4*)(p2 + h * LROW + 4 * n) = u32x4{pp[0], pp[1], pp[2], pp[3]};
+        *(uint2*)(p1 + h * PROW * 2 + 4 * n) =
+            uint2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16), (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
+      }
     }
-    psum = group_reduce<LPH>(psum, OpAdd());
-    l_run = l_run * corr + psum;
-    if ((lane % LPH) == 0) corrs[sh] = corr;
     wave_lds_sync();
 
     // ---------- rescale the accumulators (softmax correction and value-tile exponent),
     // skipped when no head's maximum moved and the exponent is unchanged
     // (residual tiles add p*v unscaled, so they need exponent 0)
-    if (__ballot(corr != 1.f) != 0 || kv_exp != kacc || !kacc_init) {
+    if (__ballot(owner && moved) != 0 || kv_exp != kacc || !kacc_init) {
       const float fexp = ldexpf(1.f, kv_exp - kacc);
       kacc = kv_exp;
       kacc_init = true;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = 4 * g + i;
-        const float f = (h < NREP ? corrs[h] : 1.f) * fexp;
+      for (int sl = 0; sl < HS; ++sl) {
+        const int i = sl * RS;
+        const float f = corr[sl] * fexp;
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
 #pragma unroll
@@ -488,8 +548,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) A[ii] = pk_mul(pd[ii], bq[ii]);
           u32x4 B[4];
-          lookup_ktile<S::TBL_V>(smem, code_pair(T.vw[(kt * NG + vg) * 2], psel),
-                                 code_pair(T.vw[(kt * NG + vg) * 2 + 1], psel), zr, grep, B);
+          lookup_ktile<BITS, S::TBL_V>(smem, T.vw[(kt * NG + vg) * 2], T.vw[(kt * NG + vg) * 2 + 1], zr, grep,
+                                       odd, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(A, B[jt], acc[vg][jt]);
         }
@@ -558,23 +618,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __syncthreads();
   float* red = (float*)(smem + S::WAVE0);
   constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D]
-  {
+  if (owner) {
     float* w = red + wave * RED;
-    if ((lane % LPH) == 0) {
-      w[sh] = m_run;
-      w[NREP + sh] = l_run;
-    }
     const float unit = ldexpf(1.f, -kacc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g + i;
-      if (h < NREP) {
-#pragma unroll
-        for (int vg = 0; vg < NG; ++vg)
-          *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n) =
-              f32x4{acc[vg][0][i] + acc_a[vg][i], acc[vg][1][i] + acc_a[vg][i], acc[vg][2][i] + acc_a[vg][i],
-                    acc[vg][3][i] + acc_a[vg][i]} * unit;
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS, h = h0 + sl;
+      if (n == 0) {
+        w[h] = m_run[sl];
+        w[NREP + h] = l_run[sl];
       }
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg)
+        *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n) =
+            f32x4{acc[vg][0][i] + acc_a[vg][i], acc[vg][1][i] + acc_a[vg][i], acc[vg][2][i] + acc_a[vg][i],
+                  acc[vg][3][i] + acc_a[vg][i]} * unit;
     }
   }
   __syncthreads();
@@ -608,9 +666,16 @@ static bool fold_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
 }
 
 bool fold_supported(const mz_decode_args* a) {
-  return a->bits == 4 && a->head_dim == 128 && a->n_groups > 0 &&
+  const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
+  const int64_t qb = 8 * (int64_t)a->bits;
+  // buffer-resource ranges are 32-bit
+  const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
+                    (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
+  return (a->bits == 4 || a->bits == 2) && a->head_dim == 128 && a->n_groups > 0 && fits &&
          (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
+         ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&
+         a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 && a->vp_sh % 4 == 0 &&
          fold_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
          fold_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
          fold_meta_aligned(a->v_mn, a->vm_sb, a->vm_sh, a->meta_dtype) &&
@@ -653,16 +718,22 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s) {
   const dim3 grid(ns, a->kv_heads, a->batch);
   const uint32_t* fk = (const uint32_t*)a->fold_k;
   const uint32_t* fv = (const uint32_t*)a->fold_v;
-#define MZ_FOLD(IOV, NR) hipLaunchKernelGGL((fold::fold_kernel<IOV, NR>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv)
-#define MZ_FOLD_NREP(IOV)             \
-  switch (a->n_rep) {                 \
-    case 1: MZ_FOLD(IOV, 1); break;   \
-    case 2: MZ_FOLD(IOV, 2); break;   \
-    case 4: MZ_FOLD(IOV, 4); break;   \
-    case 8: MZ_FOLD(IOV, 8); break;   \
-    default: return MZ_EUNSUPPORTED;  \
+#define MZ_FOLD(IOV, NR, BB) \
+  hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv)
+#define MZ_FOLD_NREP(IOV, BB)            \
+  switch (a->n_rep) {                    \
+    case 1: MZ_FOLD(IOV, 1, BB); break;  \
+    case 2: MZ_FOLD(IOV, 2, BB); break;  \
+    case 4: MZ_FOLD(IOV, 4, BB); break;  \
+    case 8: MZ_FOLD(IOV, 8, BB); break;  \
+    default: return MZ_EUNSUPPORTED;     \
   }
-  if (a->io_dtype == MZ_BF16) { MZ_FOLD_NREP(MZ_BF16) } else { MZ_FOLD_NREP(MZ_F16) }
+#define MZ_FOLD_BITS(IOV)                              \
+  if (a->bits == 4) { MZ_FOLD_NREP(IOV, 4) }           \
+  else if (a->bits == 2) { MZ_FOLD_NREP(IOV, 2) }      \
+  else return MZ_EUNSUPPORTED;
+  if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
+#undef MZ_FOLD_BITS
 #undef MZ_FOLD_NREP
 #undef MZ_FOLD
   const hipError_t e = hipGetLastError();

@@ -240,9 +240,9 @@ class DecodePlan:
         ev = tables.device_table("expm1", alpha_value, dev)
         a.e_key, a.e_value = ptr(ek), ptr(ev)
         keep += [ek, ev]
-        if int(bits) == 4:
-            fk = tables.device_table("fold4", alpha_key, dev)
-            fv = tables.device_table("fold4", alpha_value, dev)
+        if int(bits) in (2, 4):
+            fk = tables.device_table(f"fold{int(bits)}", alpha_key, dev)
+            fv = tables.device_table(f"fold{int(bits)}", alpha_value, dev)
             a.fold_k, a.fold_v = ptr(fk), ptr(fv)
             keep += [fk, fv]
         paths = {"auto": _lib.MZ_PATH_AUTO, "exact": _lib.MZ_PATH_EXACT, "fold": _lib.MZ_PATH_FOLD}

@@ -29,13 +29,14 @@ the reference:
     1..255, ``d`` in 0..bins (``muzero/quantizer.py:250-253``).
     Layout: ``E[(bins-1)*(bins+2)/2 + d]``.
 
-``fold_table(alpha)`` (4-bit decode attention)
-    For zero level ``zl`` and code ``q`` (16 x 16), the pair
+``fold4`` / ``fold2`` (4-bit / 2-bit decode attention)
+    For zero level ``zl`` and code ``q`` (``qmax = 2^bits - 1``), the pair
     ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
     as two fp16 packed in one uint32 (P in the low half), with
-    ``pb = max(15-zl, 1)``, ``nb = max(zl, 1)``.  The decode kernel rewrites
-    the reference's dequantization as ``a + bp*P + bn*N`` per group and looks
-    these pairs up per code.
+    ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; a 16 x 16 array (row zl,
+    column q, zero beyond qmax).  The decode kernel rewrites the reference's
+    dequantization as ``a + bp*P + bn*N`` per group and looks these pairs up
+    per code.
 
 These are constants of the format, the way the reference's own
 ``MU_ZERO_ALPHA2_COMPAND`` table is (``muzero/kernels/loader.py:133-150``);
@@ -138,14 +139,15 @@ def _expm1_row(bins: int) -> int:
     return (bins - 1) * (bins + 2) // 2
 
 
-def _build_fold4(alpha: float) -> torch.Tensor:
+def _build_fold(alpha: float, bits: int) -> torch.Tensor:
+    """(P, N) pairs of the ``bits``-bit codes, zero-padded to 16 x 16 (row zl, column q)."""
     e = host_table("expm1", alpha)
-    qmax = 15
+    qmax = (1 << bits) - 1
     p = torch.zeros(16, 16, dtype=torch.float32)
     nq = torch.zeros(16, 16, dtype=torch.float32)
-    for zl in range(16):
+    for zl in range(qmax + 1):
         pb, nb = max(qmax - zl, 1), max(zl, 1)
-        for q in range(16):
+        for q in range(qmax + 1):
             if q >= zl:
                 p[zl, q] = e[_expm1_row(pb) + q - zl]
             else:
@@ -171,7 +173,9 @@ def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> tor
             elif kind == "expm1":
                 t = _build_expm1(alpha)
             elif kind == "fold4":
-                t = _build_fold4(alpha)
+                t = _build_fold(alpha, 4)
+            elif kind == "fold2":
+                t = _build_fold(alpha, 2)
             else:
                 raise ValueError(kind)
             _host_cache[key] = t

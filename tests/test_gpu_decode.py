@@ -6,7 +6,7 @@ the C ABI.  The oracle is fp64 softmax attention over the dequantized prefix +
 bf16 residual, in the dequantization precision of the reference path that the
 kernel mirrors: the exact kernel rounds every dequantized value to the layer
 dtype like the reference's dequantize-then-attend fallback
-(attention.py:213-226, layer.py:263); the 4-bit fold kernel keeps dequantized
+(attention.py:213-226, layer.py:263); the 4-/2-bit fold kernel keeps dequantized
 values at full precision like the reference's fused CUDA qk/av kernels
 (fp32 codebooks, loader.py:197-263).  The two oracles differ from each other
 by up to ~1.3e-2 at short contexts, so each kernel is held to its own.  Tolerances: 2e-3 max-abs and
@@ -48,7 +48,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         if B > 1:
             am[1, ..., 5:9] = torch.finfo(dtype).min
     lq0 = ref.split_prefix(length, residual, 64)
-    fold = (kernel_path == "fold" or (kernel_path == "auto" and bits == 4 and d == 128
+    fold = (kernel_path == "fold" or (kernel_path == "auto" and bits in (2, 4) and d == 128
                                       and n_rep in (1, 2, 4, 8) and lq0 > 0))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
@@ -130,18 +130,26 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 4-bit, head_dim 128, n_rep in {1, 2, 4, 8}: the fold kernel (AUTO picks it); the
-# same cases through the exact-dequantize kernel keep that path covered too.
+# 4-bit and 2-bit, head_dim 128, n_rep in {1, 2, 4, 8}: the fold kernel (AUTO
+# picks it); the same cases through the exact-dequantize kernel keep that path
+# covered too.
 FOLD_CASES = [
     # B, hkv, n_rep, d, length, bits, residual
-    (2, 2, 4, 128, 1024, 4, 128),   # 14 groups: 7 two-group tiles + 1 residual tile
-    (2, 2, 4, 128, 1088, 4, 128),   # 15 groups: last tile has one group
+    (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
+    (2, 2, 4, 128, 1088, 4, 128),   # 15 groups: odd tile count per wave
     (1, 2, 1, 128, 700, 4, 128),
     (1, 2, 2, 128, 700, 4, 128),
     (1, 1, 8, 128, 700, 4, 128),
     (1, 2, 4, 128, 4096, 4, 128),   # many tiles per wave
     (2, 1, 4, 128, 300, 4, 0),      # no residual
     (1, 2, 4, 128, 900, 4, 191),    # residual spans two tiles, partial
+    (2, 2, 4, 128, 1024, 2, 128),
+    (1, 2, 1, 128, 700, 2, 128),
+    (1, 2, 2, 128, 700, 2, 128),
+    (1, 1, 8, 128, 700, 2, 128),
+    (1, 2, 4, 128, 4096, 2, 128),
+    (2, 1, 4, 128, 300, 2, 0),
+    (1, 2, 4, 128, 900, 2, 191),
 ]
 
 
@@ -152,19 +160,30 @@ def test_decode_4bit_paths(case, path):
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", [4, 2])
 @pytest.mark.parametrize("n_split", [1, 3, 16])
-def test_fold_split_and_mask(n_split):
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, 4, 128, mask=True, n_split=n_split, kernel_path="fold")
+def test_fold_split_and_mask(n_split, bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-def test_fold_fp16_io_and_meta():
-    for dtype, meta in ((torch.float16, torch.float16), (torch.bfloat16, torch.float32)):
-        mx, mean, _, _ = _run_case(1, 2, 4, 128, 900, 4, 128, dtype=dtype, meta=meta, kernel_path="fold")
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fold_fp16_io_and_meta(bits):
+    for dtype, meta in ((torch.float16, torch.float16), (torch.bfloat16, torch.float32),
+                        (torch.bfloat16, torch.bfloat16)):
+        mx, mean, _, _ = _run_case(1, 2, 4, 128, 900, bits, 128, dtype=dtype, meta=meta, kernel_path="fold")
         assert mx < MAX_ABS and mean < MEAN_ABS, (dtype, meta, mx, mean)
 
 
-def test_fold_large_magnitudes():
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fold_large_magnitudes(bits):
     """Key groups with spans ~1e3 and queries ~30 exercise the per-group fp16 range scaling."""
-    mx, mean, _, exact = _run_case(1, 2, 4, 128, 640, 4, 128, outliers=8, kernel_path="fold")
+    mx, mean, _, exact = _run_case(1, 2, 4, 128, 640, bits, 128, outliers=8, kernel_path="fold")
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fold_alpha_per_kind(bits):
+    """Different key / value alphas select different (P, N) tables."""
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, 800, bits, 128, alpha_k=16.0, alpha_v=4.0, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)

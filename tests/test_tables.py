@@ -70,6 +70,24 @@ def test_expm1_table_alpha2_closed_form():
         assert e[off].item() == 0.0 and e[off + n].item() == 1.0
 
 
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fold_table_entries(bits):
+    qmax = (1 << bits) - 1
+    for alpha in (2.0, 4.0):
+        e = tables.host_table("expm1", alpha)
+        f = tables.host_table(f"fold{bits}", alpha).view(torch.int16).view(torch.float16).reshape(16, 16, 2)
+        off = lambda n: (n - 1) * (n + 2) // 2
+        for zl in range(16):
+            for q in range(16):
+                P, N = f[zl, q, 0].item(), f[zl, q, 1].item()
+                if zl > qmax or q > qmax:
+                    assert P == 0.0 and N == 0.0
+                elif q >= zl:
+                    assert P == float(e[off(max(qmax - zl, 1)) + q - zl].half()) and N == 0.0
+                else:
+                    assert N == float(e[off(max(zl, 1)) + zl - q].half()) and P == 0.0
+
+
 def test_fold_table_pairs():
     alpha = 2.0
     e = tables.host_table("expm1", alpha)
