@@ -30,8 +30,9 @@
 // Each code is one conflict-free ds_read_b32 from a per-lane-group copy of
 // the (P, N) table in LDS, addressed with about 1.5 VALU ops per code, read
 // straight into the MFMA B register.  The key-side products q*bp, q*bn are
-// formed once per (head, channel) per tile as fp16 hi + lo pairs (two MFMAs
-// per k-tile keep them at fp32 accuracy).  The next tile's code words and
+// formed once per (head, channel) per tile as fp16 hi + lo pairs, on two
+// rows of the same MFMA (fp32 accuracy at no extra MFMA); the PV operands
+// p*bp, p*bn, p*a are formed once per (head, token) by the softmax.  The next tile's code words and
 // metadata are loaded while the current tile is computed.  fp16 operands
 // are kept in range by a power-of-two scale per key group and per value
 // tile, folded into the logits and into the online-softmax rescale.
@@ -78,7 +79,8 @@ struct Smem {
   static constexpr int TBL_V = TBL;
   static constexpr int Q16 = 2 * TBL;                 // fp16 [NREP][HROW*2]
   static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
-  static constexpr int WAVE0 = Q_IO + NREP * HROW * 4;
+  static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
+  static constexpr int WAVE0 = ZERO + AROW * 4;
   // per-wave region
   static constexpr int KZL = 0;                      // uint32 [D]            zl << 8
   static constexpr int AHI = KZL + D * 4;            // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
@@ -87,9 +89,9 @@ struct Smem {
   static constexpr int VZL = QA + NREP * HROW * 4;   // uint32 [NG][TILE]     zl << 8
   static constexpr int VBP = VZL + NG * TILE * 4;    // uint32 [NG][TILE]     (bp, bn) fp16
   static constexpr int VA = VBP + NG * TILE * 4;     // fp16 [NG][TILE]       a
-  static constexpr int P2 = VA + NG * TILE * 2;      // uint32 [NREP][LROW]   (p, p)
-  static constexpr int P1 = P2 + NREP * LROW * 4;    // fp16 [NREP][PROW*2]
-  static constexpr int PER_WAVE = (P1 + NREP * PROW * 4 + 15) / 16 * 16;
+  static constexpr int PA = VA + NG * TILE * 2;         // uint32 [NG][NREP][LROW]   (p*bp, p*bn) fp16
+  static constexpr int PA1 = PA + NG * NREP * LROW * 4;  // fp16 [NG][NREP][PROW*2]   p*a
+  static constexpr int PER_WAVE = (PA1 + NG * NREP * PROW * 4 + 15) / 16 * 16;
   static constexpr int MERGE = (2 * NREP + NREP * D) * 4;  // per wave at the end (aliases the wave area)
   static constexpr int WAVE_AREA = WAVES * (PER_WAVE > MERGE ? PER_WAVE : MERGE);
   static constexpr int TOTAL = WAVE0 + WAVE_AREA;
@@ -151,12 +153,6 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   return r;
 }
 
-__device__ __forceinline__ float2 meta_cvt(uint2 w, int dt) {
-  if (dt == MZ_F32) return float2{__builtin_bit_cast(float, w.x), __builtin_bit_cast(float, w.y)};
-  if (dt == MZ_F16) return float2{h2f((uint16_t)w.x), h2f((uint16_t)(w.x >> 16))};
-  return float2{bf2f((uint16_t)w.x), bf2f((uint16_t)(w.x >> 16))};
-}
-
 // Buffer resources of one (batch, kv-head): the packed prefix and metadata
 // (bounded by their filled length, so a load past it reads 0, never faults).
 struct Bufs {
@@ -174,12 +170,30 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_
 //   4-bit: kw[kt*2+p] = 32 bits of row 16kt+4g+2p+(n&1)
 //   2-bit: kw[kt*2+h] = 16 bits of row 16kt+4g+2h+(n&1)
 // (values: vw[(kt*NG+vg)*2 + p|h], rows = tokens, bytes of value group vg).
+// Metadata words: MW = 1 (fp16 / bf16: one word holds both entries) or 2 (fp32).
+template <int MW>
 struct TileData {
   uint32_t kw[16];
   uint32_t vw[16];
-  uint2 kmn, ksc;  // key groups of channels 2*lane, 2*lane+1 (raw bits)
-  uint2 vmn, vsc;  // value groups 0, 1 of token lane (raw bits)
+  uint32_t kmn[MW], ksc[MW];  // key groups of channels 2*lane, 2*lane+1 (raw bits)
+  uint32_t vmn[MW], vsc[MW];  // value groups 0, 1 of token lane (raw bits)
 };
+
+template <int MW>
+__device__ __forceinline__ float2 meta_cvt(const uint32_t (&w)[MW], int dt) {
+  if constexpr (MW == 2) {
+    return float2{__builtin_bit_cast(float, w[0]), __builtin_bit_cast(float, w[1])};
+  } else {
+    if (dt == MZ_F16) return float2{h2f((uint16_t)w[0]), h2f((uint16_t)(w[0] >> 16))};
+    return float2{bf2f((uint16_t)w[0]), bf2f((uint16_t)(w[0] >> 16))};
+  }
+}
+
+template <int MW>
+__device__ __forceinline__ void load_meta(uint32_t (&w)[MW], const __amdgpu_buffer_rsrc_t& r, int voff, int soff) {
+  w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  if constexpr (MW == 2) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4, soff, 0);
+}
 
 template <int BITS>
 __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int imm) {
@@ -189,21 +203,17 @@ __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t&
 
 // Key code words and all metadata of a tile (issued at the start of the
 // previous tile; metadata first, so its consumer need not wait for the codes).
-template <int BITS>
-__device__ __forceinline__ void load_tile_k(TileData& t, const Bufs& bf, int tile, int lane, int meta_es,
-                                            int meta_hi) {
+template <int BITS, int MW>
+__device__ __forceinline__ void load_tile_k(TileData<MW>& t, const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
+  constexpr int ES = 2 * MW;  // bytes per metadata entry
   const int n = lane & 15, g = lane >> 4;
-  const int kmo = 2 * lane * meta_es, kms = tile * D * meta_es;
-  t.kmn = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.kmn, kmo, kms, 0),
-                __builtin_amdgcn_raw_buffer_load_b32(bf.kmn, kmo + meta_hi, kms, 0)};
-  t.ksc = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.ksc, kmo, kms, 0),
-                __builtin_amdgcn_raw_buffer_load_b32(bf.ksc, kmo + meta_hi, kms, 0)};
-  const int vmo = NG * lane * meta_es, vms = tile * TILE * NG * meta_es;
-  t.vmn = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.vmn, vmo, vms, 0),
-                __builtin_amdgcn_raw_buffer_load_b32(bf.vmn, vmo + meta_hi, vms, 0)};
-  t.vsc = uint2{__builtin_amdgcn_raw_buffer_load_b32(bf.vsc, vmo, vms, 0),
-                __builtin_amdgcn_raw_buffer_load_b32(bf.vsc, vmo + meta_hi, vms, 0)};
+  const int kmo = 2 * lane * ES, kms = tile * D * ES;
+  load_meta<MW>(t.kmn, bf.kmn, kmo, kms);
+  load_meta<MW>(t.ksc, bf.ksc, kmo, kms);
+  const int vmo = NG * lane * ES, vms = tile * TILE * NG * ES;
+  load_meta<MW>(t.vmn, bf.vmn, vmo, vms);
+  load_meta<MW>(t.vsc, bf.vsc, vmo, vms);
   const int voff = (4 * g + (n & 1)) * F::QB + 2 * F::LB * (n >> 1);
   const int soff = tile * D * F::QB;
 #pragma unroll
@@ -214,8 +224,8 @@ __device__ __forceinline__ void load_tile_k(TileData& t, const Bufs& bf, int til
 
 // ... and its value code words (issued once the previous tile's key words
 // are consumed, so the two register sets overlap less).
-template <int BITS>
-__device__ __forceinline__ void load_tile_v(TileData& t, const Bufs& bf, int tile, int lane) {
+template <int BITS, int MW>
+__device__ __forceinline__ void load_tile_v(TileData<MW>& t, const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
   const int voff = (4 * g + (n & 1)) * (NG * F::QB) + 2 * F::LB * (n >> 1);
@@ -277,7 +287,7 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
   }
 }
 
-template <int IO, int NREP, int BITS>
+template <int IO, int NREP, int BITS, int MW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
     const uint32_t* __restrict__ ftab_v) {
@@ -285,6 +295,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   using S = Smem<NREP>;
   using F = Fmt<BITS>;
   constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
+  static_assert(RS >= 2, "QK needs a second row per head for the low part of the key product");
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;   // head slots per lane of the MFMA output
   __shared__ __align__(16) uint8_t smem[S::TOTAL];
 
@@ -303,8 +314,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n_tiles = a.n_groups + n_tiles_d;
   const int t_begin = split * tiles_per_split;
   const int t_end = min(n_tiles, t_begin + tiles_per_split);
-  const int meta_es = a.meta_dtype == MZ_F32 ? 4 : 2;
-  const int meta_hi = a.meta_dtype == MZ_F32 ? 4 : 0;  // second word of an fp32 pair
+  constexpr int meta_es = 2 * MW;
   Bufs bf;
   {
     const int64_t ng = a.n_groups;
@@ -322,10 +332,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // is not a quantized tile of this wave is replaced by one this split reads
   // anyway, so the spare load hits the cache.
   const int q_last = max(0, min(t_end, a.n_groups) - 1);
-  TileData T0, T1;
+  TileData<MW> T0, T1;
   const int tile0 = t_begin + wave;
-  load_tile_k<BITS>(T0, bf, min(tile0, q_last), lane, meta_es, meta_hi);
-  load_tile_v<BITS>(T0, bf, min(tile0, q_last), lane);
+  load_tile_k<BITS, MW>(T0, bf, min(tile0, q_last), lane);
+  load_tile_v<BITS, MW>(T0, bf, min(tile0, q_last), lane);
 
   // ---------------- workgroup setup: tables and query in LDS
   for (int i = threadIdx.x; i < TBL / 4; i += 256) {
@@ -333,6 +343,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     ((uint32_t*)(smem + S::TBL_K))[i] = ftab_k[zl * 16 + q];
     ((uint32_t*)(smem + S::TBL_V))[i] = ftab_v[zl * 16 + q];
   }
+  for (int i = threadIdx.x; i < AROW; i += 256) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
   float qabs = 0.f;
   for (int i = threadIdx.x; i < NREP * D; i += 256) {
     const int h = i / D, c = i - h * D;
@@ -350,12 +361,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __syncthreads();
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
-  uint32_t* p2 = (uint32_t*)(W + S::P2);
-  uint16_t* p1 = (uint16_t*)(W + S::P1);
+  uint32_t* pa = (uint32_t*)(W + S::PA);
+  uint16_t* pa1 = (uint16_t*)(W + S::PA1);
 
-  // A-operand row n of this lane: query head n / RS when n % RS == 0; the
-  // other rows (MFMA padding) repeat head 0 and their outputs are never read
-  const int hA = (n % RS) == 0 ? n / RS : 0;
+  // A-operand row n of this lane belongs to query head hA = n / RS.  For
+  // QK, row 0 of a head's rows carries the high fp16 part of the key-side
+  // product and row 1 its low part (both against the same codes, summed per
+  // logit); the head's remaining rows are zero.  For PV only row 0 is used.
+  const int hA = n / RS;
+  const int rA = n % RS;
+  const uint8_t* a_hi_row = rA == 0 ? W + S::AHI + hA * AROW * 4
+                                    : (rA == 1 ? W + S::ALO + hA * AROW * 4 : smem + S::ZERO);
+  const uint8_t* qa_row = rA == 0 ? W + S::QA + hA * HROW * 4 : smem + S::ZERO;
+  const uint8_t* qio_row = rA == 0 ? smem + S::Q_IO + hA * HROW * 4 : smem + S::ZERO;
   const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
   // MFMA output element (g, i) = row 4g+i: head slot s is element i = s*RS
   // when 4g % RS == 0 (the lane group holds query heads), head 4g/RS + s
@@ -376,9 +394,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   bool kacc_init = false;
 
   // one tile; the next quantized tile tn of this wave (if any) is loaded into Tn
-  auto process = [&](const int tile, const TileData& T, TileData& Tn, const int tn) {
+  auto process = [&](const int tile, const TileData<MW>& T, TileData<MW>& Tn, const int tn) {
     const int tl = min(tn, q_last);
-    load_tile_k<BITS>(Tn, bf, tl, lane, meta_es, meta_hi);
+    load_tile_k<BITS, MW>(Tn, bf, tl, lane);
     const bool quant = tile < a.n_groups;
     int n_valid, pos0, r0 = 0;
     if (quant) {
@@ -395,7 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float unscale = a.scaling;
     if (quant) {
       // ---------- key group scalars (lane: channels 2*lane, 2*lane+1)
-      const float2 kmn = meta_cvt(T.kmn, a.meta_dtype), ksc = meta_cvt(T.ksc, a.meta_dtype);
+      const float2 kmn = meta_cvt<MW>(T.kmn, a.meta_dtype), ksc = meta_cvt<MW>(T.ksc, a.meta_dtype);
       const GroupScalars k0 = group_scalars<F::QMAX>(kmn.x, ksc.x);
       const GroupScalars k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
       float kmx = fmaxf(fmaxf(fabsf(k0.a), fmaxf(k0.bp, -k0.bn)), fmaxf(fabsf(k1.a), fmaxf(k1.bp, -k1.bn)));
@@ -417,7 +435,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, ka);
       }
       // ---------- value scalars (lane: token lane, both value groups)
-      const float2 vmn = meta_cvt(T.vmn, a.meta_dtype), vsc = meta_cvt(T.vsc, a.meta_dtype);
+      const float2 vmn = meta_cvt<MW>(T.vmn, a.meta_dtype), vsc = meta_cvt<MW>(T.vsc, a.meta_dtype);
       const GroupScalars v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
       const GroupScalars v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
       const float vmx = fmaxf(fmaxf(fabsf(v0.a), fmaxf(v0.bp, -v0.bn)), fmaxf(fabsf(v1.a), fmaxf(v1.bp, -v1.bn)));
@@ -435,31 +453,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 A = *(const u32x4*)(W + S::QA + (hA * HROW * 2 + 32 * kq + 8 * g) * 2);
+        const u32x4 A = *(const u32x4*)(qa_row + (32 * kq + 8 * g) * 2);
         s0 = Mfma<MZ_F16>::run(A, u32x4{ONES_F16X2, ONES_F16X2, ONES_F16X2, ONES_F16X2}, s0);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = s0;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
-        const u32x4 Ahi = *(const u32x4*)(W + S::AHI + (hA * AROW + 16 * kt + 4 * g) * 4);
-        const u32x4 Alo = *(const u32x4*)(W + S::ALO + (hA * AROW + 16 * kt + 4 * g) * 4);
+        const u32x4 A = *(const u32x4*)(a_hi_row + (16 * kt + 4 * g) * 4);
         const u32x4 zr = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
         u32x4 B[4];
         lookup_ktile<BITS, S::TBL_K>(smem, T.kw[2 * kt], T.kw[2 * kt + 1], zr, grep, odd, B);
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ahi, B[jt], s[jt]);
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Alo, B[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(A, B[jt], s[jt]);
+        // keep each k-tile's lookups next to its MFMAs: hoisting later k-tiles'
+        // lookups gains no latency hiding here (two waves per SIMD) and costs
+        // the registers that would otherwise spill
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
-      // ---------- residual tile: S = Q K^T with dense operands
+      // ---------- residual tile: S = Q K^T with dense operands; the weight
+      // products below then use (bp, bn) = (1, 0) and a = 0: A = (p, 0)
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg) {
+        ((uint32_t*)(W + S::VBP))[vg * TILE + lane] = (uint32_t)ONES_F16X2 & 0xFFFFu;
+        ((uint16_t*)(W + S::VA))[vg * TILE + lane] = 0;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
       const uint16_t* kres = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 qv = *(const u32x4*)(smem + S::Q_IO + (hA * HROW * 2 + 32 * kq + 8 * g) * 2);
+        const u32x4 qv = *(const u32x4*)(qio_row + (32 * kq + 8 * g) * 2);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
           const int t = 4 * n + jt;
@@ -468,8 +493,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           s[jt] = M::run(qv, kb, s[jt]);
         }
       }
+      wave_lds_sync();  // the (1, 0) / 0 scalars above are read by other lanes below
     }
-    load_tile_v<BITS>(Tn, bf, tl, lane);
+    load_tile_v<BITS, MW>(Tn, bf, tl, lane);
 
     // ---------- online softmax in registers: head slot s of this lane group
     // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
@@ -483,7 +509,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         const int tt = 4 * n + jt;
-        float v = s[jt][i] * unscale;
+        float v = (s[jt][i] + s[jt][i + 1]) * unscale;
         if (tt >= n_valid) v = -INFINITY;
         else if (a.mask) v += a.mask[b * a.mask_sb + pos0 + tt];
         x[jt] = v;
@@ -507,10 +533,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       psum = group_reduce<16>(psum, OpAdd());
       l_run[sl] = l_run[sl] * corr[sl] + psum;
       if (owner) {
+        // PV A operands of this head's 4 tokens: p times the token's (bp, bn) and a
         const int h = h0 + sl;
-        *(u32x4*)(p2 + h * LROW + 4 * n) = u32x4{pp[0], pp[1], pp[2], pp[3]};
-        *(uint2*)(p1 + h * PROW * 2 + 4 * n) =
-            uint2{(uint32_t)ph[0] | ((uint32_t)ph[1] << 16), (uint32_t)ph[2] | ((uint32_t)ph[3] << 16)};
+        const uint32_t ph01 = (uint32_t)ph[0] | ((uint32_t)ph[1] << 16);
+        const uint32_t ph23 = (uint32_t)ph[2] | ((uint32_t)ph[3] << 16);
+#pragma unroll
+        for (int vg = 0; vg < NG; ++vg) {
+          const u32x4 bq = *(const u32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 4);
+          const uint2 av = *(const uint2*)(W + S::VA + (vg * TILE + 4 * n) * 2);
+          *(u32x4*)(pa + (vg * NREP + h) * LROW + 4 * n) =
+              u32x4{pk_mul(pp[0], bq[0]), pk_mul(pp[1], bq[1]), pk_mul(pp[2], bq[2]), pk_mul(pp[3], bq[3])};
+          *(uint2*)(pa1 + (vg * NREP + h) * PROW * 2 + 4 * n) = uint2{pk_mul(ph01, av.x), pk_mul(ph23, av.y)};
+        }
       }
     }
     wave_lds_sync();
@@ -539,40 +573,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (quant) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 pd = *(const u32x4*)(p2 + hA * LROW + 16 * kt + 4 * g);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
-          const u32x4 bq = *(const u32x4*)(W + S::VBP + (vg * TILE + 16 * kt + 4 * g) * 4);
+          const u32x4 A = *(const u32x4*)(pa + (vg * NREP + hA) * LROW + 16 * kt + 4 * g);
           const u32x4 zr = *(const u32x4*)(W + S::VZL + (vg * TILE + 16 * kt + 4 * g) * 4);
-          u32x4 A;
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) A[ii] = pk_mul(pd[ii], bq[ii]);
           u32x4 B[4];
           lookup_ktile<BITS, S::TBL_V>(smem, T.vw[(kt * NG + vg) * 2], T.vw[(kt * NG + vg) * 2 + 1], zr, grep,
                                        odd, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(A, B[jt], acc[vg][jt]);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
       // constant part: sum_t p_t * a_t against a ones operand
 #pragma unroll
       for (int kq = 0; kq < 2; ++kq) {
-        const u32x4 pv = *(const u32x4*)(p1 + hA * PROW * 2 + 32 * kq + 8 * g);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
-          const u32x4 av = *(const u32x4*)(W + S::VA + (vg * TILE + 32 * kq + 8 * g) * 2);
-          u32x4 A;
-#pragma unroll
-          for (int p = 0; p < 4; ++p) A[p] = pk_mul(pv[p], av[p]);
+          const u32x4 A = *(const u32x4*)(pa1 + (vg * NREP + hA) * PROW * 2 + 32 * kq + 8 * g);
           acc_a[vg] = Mfma<MZ_F16>::run(A, u32x4{ONES_F16X2, ONES_F16X2, ONES_F16X2, ONES_F16X2}, acc_a[vg]);
         }
       }
     } else {
-      // residual values: B pairs (v, 0) against A pairs (p, p)
+      // residual values: B pairs (v, 0) against A pairs (p, 0)
       const uint16_t* vres = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 pd = *(const u32x4*)(p2 + hA * LROW + 16 * kt + 4 * g);
+        const u32x4 pd = *(const u32x4*)(pa + hA * LROW + 16 * kt + 4 * g);  // (p, 0) pairs
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
           uint32_t v4[4][2];
@@ -718,8 +745,11 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s) {
   const dim3 grid(ns, a->kv_heads, a->batch);
   const uint32_t* fk = (const uint32_t*)a->fold_k;
   const uint32_t* fv = (const uint32_t*)a->fold_v;
-#define MZ_FOLD(IOV, NR, BB) \
-  hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv)
+#define MZ_FOLD(IOV, NR, BB)                                                                            \
+  if (a->meta_dtype == MZ_F32)                                                                          \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv); \
+  else                                                                                                  \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv)
 #define MZ_FOLD_NREP(IOV, BB)            \
   switch (a->n_rep) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
