@@ -151,10 +151,19 @@ enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 /* Bytes of workspace muzero_decode_attention needs for these arguments
  * (and the split count it will use, written to *n_split_out if non-null). */
 int64_t muzero_decode_workspace_bytes(const mz_decode_args* args, int* n_split_out);
+
+/* 1 if muzero_decode_attention runs the fold kernel for these arguments, 0 if
+ * the exact-dequantize kernel, -1 if the arguments are rejected.  An
+ * introspection helper with no counterpart in the reference (its dispatcher,
+ * loader.py:1360-1687, picks kernels internally); used by tests and the
+ * benchmark to report which kernel they measured. */
+int muzero_decode_uses_fold(const mz_decode_args* args);
 int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
 
 /* The two launches of muzero_decode_attention, for callers that time or merge
- * them separately.  muzero_decode_partials writes one (acc[D], m, l) fp32
+ * them separately.  (When the fold kernel runs with a single split,
+ * muzero_decode_attention launches only that kernel, which then writes `out`
+ * itself; these two entry points always go through the workspace.)  muzero_decode_partials writes one (acc[D], m, l) fp32
  * record per (batch, q-head, split) into the workspace, laid out
  * [B][Hq][n_split][D + 2]; muzero_decode_combine merges the splits of each
  * (batch, q-head) with a log-sum-exp reduction and writes `out`.

@@ -72,6 +72,7 @@ SIGNATURES = {
                                        c_int, c_vp, c_vp]),
     "muzero_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(c_int)]),
     "muzero_decode_attention": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_uses_fold": (c_int, [ctypes.POINTER(DecodeArgs)]),
     "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
 }

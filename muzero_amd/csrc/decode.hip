@@ -323,7 +323,7 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(const float* __restri
 
 bool fold_supported(const mz_decode_args* a);
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
-int fold_launch_partials(const mz_decode_args* a, hipStream_t s);
+int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + kTile - 1) / kTile;
@@ -393,6 +393,11 @@ extern "C" int64_t muzero_decode_workspace_bytes(const mz_decode_args* a, int* n
   return (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
 }
 
+extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
+  if (check_args(a) != MZ_OK) return -1;
+  return use_fold(a) ? 1 : 0;
+}
+
 template <int D, int IO>
 static int launch_partials(const mz_decode_args* a, hipStream_t s) {
   int tps;
@@ -449,7 +454,7 @@ extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t strea
     const int ns = fold_choose_split(a, &tps);
     const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
     if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
-    return fold_launch_partials(a, s);
+    return fold_launch_partials(a, s, false);
   }
   if (a->head_dim == 128)
     return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s) : launch_partials<128, MZ_F16>(a, s);
@@ -467,6 +472,11 @@ extern "C" int muzero_decode_combine(const mz_decode_args* a, mz_stream_t stream
 }
 
 extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stream) {
+  // fold path with one split: the split kernel writes the output (no workspace, no combine)
+  if (decode_check_launchable(a) == MZ_OK && a->out && use_fold(a)) {
+    int tps;
+    if (fold_choose_split(a, &tps) == 1) return fold_launch_partials(a, (hipStream_t)stream, true);
+  }
   const int st = muzero_decode_partials(a, stream);
   if (st != MZ_OK) return st;
   return muzero_decode_combine(a, stream);

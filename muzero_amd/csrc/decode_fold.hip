@@ -39,7 +39,8 @@
 //
 // Launch: one workgroup of 4 waves per (batch, kv-head, split); a split is a
 // run of tiles, waves take every 4th tile; the split's (m, l, acc) goes to the
-// workspace and the shared combine kernel merges splits.
+// workspace and the shared combine kernel merges splits.  With a single split
+// (the grid already fills the GPU) the kernel writes the output itself.
 #include "decode_common.hpp"
 
 namespace mz {
@@ -290,7 +291,7 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
 template <int IO, int NREP, int BITS, int MW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
-    const uint32_t* __restrict__ ftab_v) {
+    const uint32_t* __restrict__ ftab_v, int direct) {
   using M = Mfma<IO>;
   using S = Smem<NREP>;
   using F = Fmt<BITS>;
@@ -663,6 +664,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
   __syncthreads();
+  if (direct) {
+    // one split: the final output, exactly as the combine kernel would form it
+    for (int e = threadIdx.x; e < NREP * D; e += 256) {
+      const int h = e / D;
+      const int c = e - h * D;
+      float M_ = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
+      float num = 0.f, den = 0.f;
+      if (M_ != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+          const float f = __expf(red[w * RED + h] - M_);
+          num += f * red[w * RED + 2 * NREP + h * D + c];
+          den += f * red[w * RED + NREP + h];
+        }
+      }
+      store_val(a.out, b * a.out_sb + (int64_t)(kvh * NREP + h) * a.out_sh + c, den > 0.f ? num / den : 0.f,
+                a.out_dtype);
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < NREP * (D + 2); e += 256) {
     const int h = e / (D + 2);
     const int c = e - h * (D + 2);
@@ -739,17 +762,18 @@ int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
   return (n_tiles + tps - 1) / tps;
 }
 
-int fold_launch_partials(const mz_decode_args* a, hipStream_t s) {
+int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   int tps;
   const int ns = fold_choose_split(a, &tps);
   const dim3 grid(ns, a->kv_heads, a->batch);
   const uint32_t* fk = (const uint32_t*)a->fold_k;
   const uint32_t* fv = (const uint32_t*)a->fold_v;
+  const int dir = direct ? 1 : 0;
 #define MZ_FOLD(IOV, NR, BB)                                                                            \
   if (a->meta_dtype == MZ_F32)                                                                          \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv); \
-  else                                                                                                  \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv)
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv, dir); \
+  else                                                                                                       \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv, dir)
 #define MZ_FOLD_NREP(IOV, BB)            \
   switch (a->n_rep) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \

@@ -285,6 +285,8 @@ class DecodePlan:
         a.workspace, a.workspace_bytes = ptr(ws), int(need)
         self.args = a
         self.n_split = ns.value
+        # whether the library runs the fold kernel for these arguments (bits 4/2, hd 128, ...)
+        self.uses_fold = bool(lib.muzero_decode_uses_fold(ctypes.byref(a)))
         self.out = out
         self.workspace = ws
         self._keep = keep

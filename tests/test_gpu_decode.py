@@ -187,3 +187,24 @@ def test_fold_alpha_per_kind(bits):
     """Different key / value alphas select different (P, N) tables."""
     mx, mean, _, _ = _run_case(1, 2, 4, 128, 800, bits, 128, alpha_k=16.0, alpha_v=4.0, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_single_split_direct_output_matches_two_kernel_path(bits):
+    """With one split the fold kernel writes the output itself; the result is bit-identical to
+    the workspace + combine path (same operations in the same order)."""
+    from muzero_amd.kernels import loader as L
+    k, v, q, _ = ref.synthetic_kv(2, 2, 900, 128, 8, seed=3)
+    _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=2.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1)
+    plan = L.DecodePlan(q.to(DEV), **kw)
+    assert plan.n_split == 1 and plan.uses_fold
+    direct = plan.run().clone()
+    plan.out.zero_()
+    plan.partials()
+    two = plan.combine().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
