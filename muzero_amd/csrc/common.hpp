@@ -34,7 +34,10 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 // Value of an op result after ATen stores it in the input dtype DT.
 template <int DT> __device__ __forceinline__ float rnd(float x);
 template <> __device__ __forceinline__ float rnd<MZ_F32>(float x) { return x; }
-template <> __device__ __forceinline__ float rnd<MZ_BF16>(float x) { return bf2f(f2bf(x)); }
+// gfx950 converts to bf16 in hardware (v_cvt_pk_bf16_f32, round to nearest
+// even, the same as f2bf for every non-NaN input; a NaN stays a NaN but its
+// payload is not canonicalised, so stores go through f2bf).
+template <> __device__ __forceinline__ float rnd<MZ_BF16>(float x) { return (float)(__bf16)x; }
 template <> __device__ __forceinline__ float rnd<MZ_F16>(float x) { return h2f(f2h(x)); }
 
 template <int DT> __device__ __forceinline__ float load_val(const void* p, int64_t i);
@@ -77,6 +80,31 @@ __device__ __forceinline__ float wave_min(float v) {
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = nmax(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Cross-lane reductions on DPP (no LDS round trips).  dpp_sel<CTRL>(v) reads v
+// from the lane that the gfx9 DPP control CTRL names.
+template <int CTRL>
+__device__ __forceinline__ float dpp_sel(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8
+constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i within 16
+
+// Reduction over aligned groups of N lanes (N a power of two <= 64); every
+// lane of a group gets the same result (each step combines the lane's value
+// with a partner holding the other half, in a fixed order).
+template <int N, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  if constexpr (N >= 2) v = op(v, dpp_sel<DPP_QUAD_XOR1>(v));
+  if constexpr (N >= 4) v = op(v, dpp_sel<DPP_QUAD_XOR2>(v));
+  if constexpr (N >= 8) v = op(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+  if constexpr (N >= 16) v = op(v, dpp_sel<DPP_ROW_MIRROR>(v));
+  if constexpr (N >= 32) v = op(v, __shfl_xor(v, 16, 64));
+  if constexpr (N >= 64) v = op(v, __shfl_xor(v, 32, 64));
   return v;
 }
 

@@ -37,31 +37,6 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ float meta_load(const void* p, int64_t i, int dt) { return load_any(p, i, dt); }
 
-// Cross-lane reductions on DPP (no LDS round trips).  dpp_sel<CTRL>(v) reads v
-// from the lane that the gfx9 DPP control CTRL names.
-template <int CTRL>
-__device__ __forceinline__ float dpp_sel(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
-constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
-constexpr int DPP_ROW_HALF_MIRROR = 0x141;  // lane i <- 7 - i within 8
-constexpr int DPP_ROW_MIRROR = 0x140;       // lane i <- 15 - i within 16
-
-// Reduction over aligned groups of N lanes (N a power of two <= 64); every
-// lane of a group gets the same result (each step combines the lane's value
-// with a partner holding the other half, in a fixed order).
-template <int N, typename Op>
-__device__ __forceinline__ float group_reduce(float v, Op op) {
-  if constexpr (N >= 2) v = op(v, dpp_sel<DPP_QUAD_XOR1>(v));
-  if constexpr (N >= 4) v = op(v, dpp_sel<DPP_QUAD_XOR2>(v));
-  if constexpr (N >= 8) v = op(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
-  if constexpr (N >= 16) v = op(v, dpp_sel<DPP_ROW_MIRROR>(v));
-  if constexpr (N >= 32) v = op(v, __shfl_xor(v, 16, 64));
-  if constexpr (N >= 64) v = op(v, __shfl_xor(v, 32, 64));
-  return v;
-}
-
 struct OpMax {
   __device__ __forceinline__ float operator()(float x, float y) const { return fmaxf(x, y); }
 };

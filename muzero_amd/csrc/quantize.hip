@@ -1,36 +1,119 @@
 // Quantize + bit-pack and dequantize kernels (gfx950, wave64).
 //
-// One wavefront per 64-value group: lane i holds value i.  The group min/max
-// is a wave reduction, every per-element op of the reference quantizer
-// (muzero/quantizer.py:161-186) is evaluated in its own dtype with IEEE
-// rounding and no contraction, and the one transcendental step
-// (round(log1p(alpha*p)/lb*bins)) comes from a host-built constant table, so
-// codes and metadata are bit-identical to the reference torch path.
+// Quantize: 8 lanes per 64-value group, 8 consecutive values per lane, so a
+// wave quantizes 8 groups.  The group min/max is an in-lane reduction plus 3
+// DPP steps; the group's compander parameters are computed once per lane; every
+// per-element op of the reference quantizer (muzero/quantizer.py:161-186) is
+// evaluated in its own dtype with IEEE rounding and no contraction, and the
+// one transcendental step (round(log1p(alpha*p)/lb*bins)) comes from a
+// host-built constant table staged in LDS, so codes and metadata are
+// bit-identical to the reference torch path.  8 codes of BITS bits are exactly
+// BITS bytes of the LSB-first bitstream (quantizer.py:189-202), so each lane
+// packs and stores its own bytes and a wave's stores are contiguous.  The grid
+// is persistent (a few workgroups per CU loop over the groups), so each
+// workgroup stages the table once.
 #include "common.hpp"
+
+#include <algorithm>
 
 namespace mz {
 
-// Code of one lane's value given the group's min and scale.  DT is the dtype
-// every reference op rounds to.  `table` is the fp32 threshold table (DT ==
-// F32) or the 16-bit ratio table indexed by the pattern of p (DT == BF16/F16).
+constexpr int QWG = 256;           // threads per quantize workgroup
+constexpr int QGROUPS_PER_WAVE = 8;
+
+// Compander parameters of one group (quantizer.py:169-181), every op rounded
+// to the input dtype DT.
+struct QParams {
+  float mn, sc, za, zl, pb, nb, pe, ne, eps;
+  float rsc, rpe, rne;  // v_rcp_f32 of sc, pe, ne (16-bit inputs only)
+};
+
+// rnd<DT>(a / b) for a, b values of the 16-bit input dtype, given r = rcp(b).
+// bf16: a and b have 8-bit significands, so a / b is never a bf16 rounding
+// midpoint and lies at least 2^7 fp32 ulps from one (a = b * odd 9-bit
+// significand is impossible; the distance is >= 1/B bf16 half-ulps with the
+// odd part B < 2^8); a * rcp(b) is within 3 ulps, so rounding it to bf16 gives
+// the reference's round(fp32 division).  fp16 (11-bit significands, distance
+// >= 2 ulps) takes one residual correction (< 1 ulp) except where b is 0 or
+// inf, where a * rcp(b) is already the IEEE quotient (inf, NaN or 0).  rcp of
+// a b above 2^126 would be denormal: such groups use the IEEE division.
+template <int DT, bool FAST>
+__device__ __forceinline__ float qdiv(float a, float b, float r) {
+  if constexpr (DT == MZ_F32 || !FAST) {
+    return rnd<DT>(a / b);
+  } else if constexpr (DT == MZ_BF16) {
+    return rnd<DT>(a * r);
+  } else {
+    const float q0 = a * r;
+    const float q1 = fmaf(fmaf(-b, q0, a), r, q0);
+    return rnd<DT>((b != 0.f && b != __builtin_inff()) ? q1 : q0);
+  }
+}
+
+// Whether the reciprocal form applies to every division of the group.
+template <int DT>
+__device__ __forceinline__ bool qfast(const struct QParams& g) {
+  if constexpr (DT == MZ_F16) return true;  // an fp16 scale is <= 65504 or inf
+  return DT != MZ_F32 && !(g.sc > 0x1p126f && g.sc < __builtin_inff());
+}
+
 template <int DT, int BITS>
-__device__ __forceinline__ uint32_t lane_code(float v, float mn, float sc, float eps, const void* table) {
+__device__ __forceinline__ QParams qparams(float mn, float mx, float eps_in) {
   constexpr float qmax = (float)((1 << BITS) - 1);
-  const float norm = clamp01(rnd<DT>(rnd<DT>(v - mn) / sc));
-  const float za = clamp01(rnd<DT>(rnd<DT>(0.f - mn) / sc));
-  const float zl = rintf(rnd<DT>(za * qmax));
-  const float pb = clamp_min(rnd<DT>(qmax - zl), 1.f);
-  const float nb = clamp_min(zl, 1.f);
-  const float pe = clamp_min(rnd<DT>(1.f - za), eps);
-  const float ne = clamp_min(za, eps);
-  const bool up = norm >= za;  // torch.where(norm >= za, q_pos, q_neg); false on NaN
-  const float p = up ? clamp01(rnd<DT>(rnd<DT>(norm - za) / pe))
-                     : clamp01(rnd<DT>(rnd<DT>(za - norm) / ne));
-  const float bins = up ? pb : nb;
+  QParams g;
+  g.eps = rnd<DT>(eps_in);
+  g.mn = mn;
+  g.sc = clamp_min(rnd<DT>(mx - mn), g.eps);
+  g.za = clamp01(rnd<DT>(rnd<DT>(0.f - mn) / g.sc));
+  g.zl = rintf(rnd<DT>(g.za * qmax));
+  g.pb = clamp_min(rnd<DT>(qmax - g.zl), 1.f);
+  g.nb = clamp_min(g.zl, 1.f);
+  g.pe = clamp_min(rnd<DT>(1.f - g.za), g.eps);
+  g.ne = clamp_min(g.za, g.eps);
+  if constexpr (DT != MZ_F32) {
+    g.rsc = __builtin_amdgcn_rcpf(g.sc);
+    g.rpe = __builtin_amdgcn_rcpf(g.pe);
+    g.rne = __builtin_amdgcn_rcpf(g.ne);
+  }
+  return g;
+}
+
+// Compander table in LDS: fp32 inputs use the threshold rows of bins 1..qmax
+// (#{k : p >= T[bins][k]}, binary search); bf16/fp16 inputs the 16-bit ratio
+// table indexed by the pattern of p.  Table bytes staged per workgroup:
+template <int DT, int BITS>
+struct QTable {
+  static constexpr int QMAX = (1 << BITS) - 1;
+  static constexpr int BYTES = DT == MZ_F32 ? QMAX * (QMAX + 1) / 2 * 4
+                                            : ((DT == MZ_BF16 ? 0x3F80 : 0x3C00) + 1) * 2;
+  static constexpr bool IN_LDS = BYTES <= 40 * 1024;  // 8-bit fp32 thresholds (128 KB) stay in global memory
+  static constexpr int LDS_BYTES = IN_LDS ? (BYTES + 15) / 16 * 16 : 16;
+};
+
+template <int DT, int BITS>
+__device__ __forceinline__ void stage_table(uint8_t* lds, const void* table) {
+  using TB = QTable<DT, BITS>;
+  if constexpr (TB::IN_LDS) {
+    const uint16_t* src = (const uint16_t*)table;
+    for (int i = threadIdx.x; i < TB::BYTES / 2; i += QWG) ((uint16_t*)lds)[i] = src[i];
+    __syncthreads();
+  }
+}
+
+// Code of one value given its group's parameters (quantizer.py:172-184).
+template <int DT, int BITS, bool FAST>
+__device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const uint8_t* lds, const void* table) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const float norm = clamp01(qdiv<DT, FAST>(rnd<DT>(v - g.mn), g.sc, g.rsc));
+  const bool up = norm >= g.za;  // torch.where(norm >= za, q_pos, q_neg); false on NaN
+  // Only the selected side is evaluated: operands are chosen before the one
+  // division, which computes exactly what the unselected-branch form would.
+  const float p = clamp01(qdiv<DT, FAST>(rnd<DT>(up ? norm - g.za : g.za - norm), up ? g.pe : g.ne,
+                                         up ? g.rpe : g.rne));
+  const float bins = up ? g.pb : g.nb;
   float off;
   if constexpr (DT == MZ_F32) {
-    // #{k : p >= T[bins][k]} by binary search over the bins thresholds.
-    const float* T = (const float*)table;
+    const float* T = QTable<DT, BITS>::IN_LDS ? (const float*)lds : (const float*)table;
     const int ib = (bins == bins) ? (int)bins : 1;
     const float* row = T + ib * (ib - 1) / 2;
     int lo = 0, hi = ib;
@@ -40,109 +123,273 @@ __device__ __forceinline__ uint32_t lane_code(float v, float mn, float sc, float
     }
     off = (p == p) ? (float)lo : __builtin_nanf("");
   } else {
-    const uint16_t* Y = (const uint16_t*)table;
+    const uint16_t* Y = (const uint16_t*)lds;
     float y;
     if (p == p) {
-      const uint32_t pat = (DT == MZ_BF16 ? (uint32_t)f2bf(p) : (uint32_t)f2h(p)) & 0x7FFFu;  // -0 -> 0
+      const uint32_t pat = (DT == MZ_BF16 ? (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p)  // p is not NaN
+                                          : (uint32_t)f2h(p)) & 0x7FFFu;                          // -0 -> 0
       y = DT == MZ_BF16 ? bf2f(Y[pat]) : h2f(Y[pat]);
     } else {
       y = p;
     }
     off = rintf(rnd<DT>(y * bins));
   }
-  const float q = up ? rnd<DT>(zl + off) : rnd<DT>(zl - off);
+  const float q = rnd<DT>(up ? g.zl + off : g.zl - off);
   // clamp(0, qmax).to(uint8); a NaN code converts to 0 (as on the reference CPU)
   if (!(q == q)) return 0u;
   return (uint32_t)fminf(fmaxf(q, 0.f), qmax);
 }
 
-// Quantize the wave's group (lane value v) and store packed bytes and metadata.
+// Min / max over the 8 lanes of a group (lanes 8k..8k+7), NaN-propagating.
+__device__ __forceinline__ float group8_min(float v) {
+  v = nmin(v, dpp_sel<DPP_QUAD_XOR1>(v));
+  v = nmin(v, dpp_sel<DPP_QUAD_XOR2>(v));
+  return nmin(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+}
+__device__ __forceinline__ float group8_max(float v) {
+  v = nmax(v, dpp_sel<DPP_QUAD_XOR1>(v));
+  v = nmax(v, dpp_sel<DPP_QUAD_XOR2>(v));
+  return nmax(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+}
+
+// Quantize this lane's 8 values x[0..7] (positions 8*part .. 8*part+7 of its
+// group) and store its BITS packed bytes at prow + part*BITS; lane part 0
+// stores the group's metadata at index midx.
 template <int DT, int BITS>
-__device__ __forceinline__ void quantize_group(float v, int lane, uint8_t* prow, void* mn_out, void* sc_out,
-                                               int64_t midx, int meta_dtype, float eps_in, const void* table) {
-  const float mn = wave_min(v);
-  const float mx = wave_max(v);
-  const float eps = rnd<DT>(eps_in);
-  const float sc = clamp_min(rnd<DT>(mx - mn), eps);
-  const uint32_t code = lane_code<DT, BITS>(v, mn, sc, eps, table);
-  const uint32_t byte = pack_byte<BITS>(code, lane);
-  if (lane < 8 * BITS) prow[lane] = (uint8_t)byte;
-  if (lane == 0) {
+__device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, uint8_t* prow, void* mn_out,
+                                               void* sc_out, int64_t midx, int meta_dtype, float eps,
+                                               const uint8_t* lds, const void* table) {
+  float mn = x[0], mx = x[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mn = nmin(mn, x[i]), mx = nmax(mx, x[i]);
+  mn = group8_min(mn);
+  mx = group8_max(mx);
+  const QParams g = qparams<DT, BITS>(mn, mx, eps);
+  uint64_t w = 0;
+  if (qfast<DT>(g)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true>(x[i], g, lds, table) << (i * BITS);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false>(x[i], g, lds, table) << (i * BITS);
+  }
+  uint8_t* dst = prow + part * BITS;
+  if constexpr (BITS == 8) *(uint64_t*)dst = w;
+  else if constexpr (BITS == 4) *(uint32_t*)dst = (uint32_t)w;
+  else if constexpr (BITS == 2) *(uint16_t*)dst = (uint16_t)w;
+  else if constexpr (BITS == 1) *dst = (uint8_t)w;
+  else {
+#pragma unroll
+    for (int k = 0; k < BITS; ++k) dst[k] = (uint8_t)(w >> (8 * k));
+  }
+  if (part == 0) {
     store_val(mn_out, midx, mn, meta_dtype);
-    store_val(sc_out, midx, sc, meta_dtype);
+    store_val(sc_out, midx, g.sc, meta_dtype);
+  }
+}
+
+// 8 consecutive values at p[i..i+7] (VEC: one or two 16-byte loads).
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(float (&x)[8], const void* p, int64_t i) {
+  if constexpr (VEC && DT == MZ_F32) {
+    const float4 a = *(const float4*)((const float*)p + i);
+    const float4 b = *(const float4*)((const float*)p + i + 4);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  } else if constexpr (VEC) {
+    const uint4 a = *(const uint4*)((const uint16_t*)p + i);
+    const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = DT == MZ_BF16 ? bf2f((uint16_t)u[k]) : h2f((uint16_t)u[k]);
+      x[2 * k + 1] = DT == MZ_BF16 ? bf2f((uint16_t)(u[k] >> 16)) : h2f((uint16_t)(u[k] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = load_val<DT>(p, i + k);
   }
 }
 
 // ------------------------------------------------------------- rows
-template <int DT, int BITS>
-__global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int64_t nrows,
+template <int DT, int BITS, bool VEC>
+__global__ __launch_bounds__(QWG) void quantize_rows_kernel(const void* __restrict__ x, int64_t nrows,
                                                             int64_t xs, uint8_t* __restrict__ packed, int64_t ps,
                                                             void* mn, void* sc, int meta_dtype, int64_t ms,
                                                             float eps, const void* __restrict__ table) {
+  __shared__ __align__(16) uint8_t lds[QTable<DT, BITS>::LDS_BYTES];
+  stage_table<DT, BITS>(lds, table);
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= nrows) return;
-  const float v = load_val<DT>(x, row * xs + lane);
-  quantize_group<DT, BITS>(v, lane, packed + row * ps, mn, sc, row * ms, meta_dtype, eps, table);
+  const int part = lane & 7;
+  const int64_t stride = (int64_t)gridDim.x * (QWG / 64) * QGROUPS_PER_WAVE;
+  for (int64_t row = ((int64_t)blockIdx.x * (QWG / 64) + (threadIdx.x >> 6)) * QGROUPS_PER_WAVE + (lane >> 3);
+       row - (lane >> 3) < nrows; row += stride) {
+    if (row < nrows) {  // lanes of a group share `row`: the whole group takes this branch
+      float v[8];
+      load8<DT, VEC>(v, x, row * xs + 8 * part);
+      quantize_lane8<DT, BITS>(v, part, packed + row * ps, mn, sc, row * ms, meta_dtype, eps, lds, table);
+    }
+  }
+}
+
+// ------------------------------------------------------------- index math
+// n / d for 0 <= n < 2^31 by multiply-high (Granlund-Montgomery): l =
+// ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, m) + n) >> l.
+struct FastDiv {
+  uint32_t d, m, l;
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return (__umulhi(n, m) + n) >> l; }
+};
+
+static FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  const uint64_t m = (((1ull << 32) * ((1ull << l) - d)) / d) + 1;
+  return FastDiv{d, (uint32_t)m, l};
 }
 
 // ------------------------------------------------------------- values
-// Row (b, h, t, j): channels 64j..64j+63 of token t, zero beyond D.
-template <int DT, int BITS>
-__global__ __launch_bounds__(256) void quantize_values_kernel(const void* __restrict__ x, int B, int H, int T, int D,
-                                                              int64_t sb, int64_t sh, int64_t st,
-                                                              uint8_t* __restrict__ packed, int64_t psb, int64_t psh,
-                                                              void* mn, void* sc, int meta_dtype, int64_t msb,
-                                                              int64_t msh, float eps, const void* __restrict__ table) {
-  const int ng = (D + 63) / 64;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nrows = (int64_t)B * H * T * ng;
-  if (row >= nrows) return;
-  const int j = (int)(row % ng);
-  const int64_t r1 = row / ng;
-  const int t = (int)(r1 % T);
-  const int64_t r2 = r1 / T;
-  const int h = (int)(r2 % H);
-  const int b = (int)(r2 / H);
-  const int c = 64 * j + lane;
-  const float v = c < D ? load_val<DT>(x, b * sb + h * sh + t * st + c) : 0.f;
+// Row (b, h, t, j): channels 64j..64j+63 of token t, zero beyond D.  Rows
+// are numbered b-major with j fastest; nrows < 2^31 per launch (the host
+// splits the batch).
+template <int DT, int BITS, bool VEC>
+__global__ __launch_bounds__(QWG) void quantize_values_kernel(const void* __restrict__ x, int nrows, FastDiv fng,
+                                                              FastDiv fT, FastDiv fH, int D, int64_t sb, int64_t sh,
+                                                              int64_t st, uint8_t* __restrict__ packed, int64_t psb,
+                                                              int64_t psh, void* mn, void* sc, int meta_dtype,
+                                                              int64_t msb, int64_t msh, float eps,
+                                                              const void* __restrict__ table) {
+  __shared__ __align__(16) uint8_t lds[QTable<DT, BITS>::LDS_BYTES];
+  stage_table<DT, BITS>(lds, table);
   constexpr int QB = 8 * BITS;
-  uint8_t* prow = packed + b * psb + h * psh + ((int64_t)t * ng + j) * QB;
-  const int64_t midx = b * msb + h * msh + (int64_t)t * ng + j;
-  quantize_group<DT, BITS>(v, lane, prow, mn, sc, midx, meta_dtype, eps, table);
+  const int ng = (int)fng.d, T = (int)fT.d, H = (int)fH.d;
+  const int lane = threadIdx.x & 63;
+  const int part = lane & 7;
+  const int stride = gridDim.x * (QWG / 64) * QGROUPS_PER_WAVE;
+  for (int row = (blockIdx.x * (QWG / 64) + (threadIdx.x >> 6)) * QGROUPS_PER_WAVE + (lane >> 3);
+       row - (lane >> 3) < nrows; row += stride) {
+    if (row < nrows) {  // lanes of a group share `row`: the whole group takes this branch
+      const int r1 = (int)fng.div((uint32_t)row);
+      const int j = row - r1 * ng;
+      const int r2 = (int)fT.div((uint32_t)r1);
+      const int t = r1 - r2 * T;
+      const int b = (int)fH.div((uint32_t)r2);
+      const int h = r2 - b * H;
+      const int c = 64 * j + 8 * part;
+      const int64_t src = b * sb + h * sh + t * st + c;
+      float v[8];
+      if (c + 8 <= D) {  // VEC only picks the load width; lanes past D (D % 64 != 0) read nothing
+        load8<DT, VEC>(v, x, src);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = c + k < D ? load_val<DT>(x, src + k) : 0.f;
+      }
+      uint8_t* prow = packed + b * psb + h * psh + ((int64_t)t * ng + j) * QB;
+      const int64_t midx = b * msb + h * msh + (int64_t)t * ng + j;
+      quantize_lane8<DT, BITS>(v, part, prow, mn, sc, midx, meta_dtype, eps, lds, table);
+    }
+  }
 }
 
 // ------------------------------------------------------------- keys
-// One workgroup per (b, h, token group): the [64 x D] tile is staged in LDS
-// (coalesced along D), and each wave quantizes channels reading the tile's
-// columns, so the reference's permute+contiguous copy never touches HBM.
-template <int DT, int BITS>
-__global__ __launch_bounds__(256) void quantize_keys_kernel(const void* __restrict__ x, int B, int H, int T, int D,
+// A workgroup loops over (b, h, token group) tiles: the [64 x D] tile is
+// staged in LDS as fp32 [64][D + 1] (row pitch D + 1 keeps the column reads
+// conflict-free) and each wave quantizes 8 channels at a time reading the
+// tile's columns, so the reference's permute + contiguous copy
+// (layer.py:276-278) never touches HBM.  VEC: the tile arrives as 16-byte
+// vectors (D % 8 == 0, D <= 256, aligned rows), and the next tile's vectors
+// are loaded into registers before the current tile is quantized.
+constexpr int KEY_MAX_VEC = 8;  // 16-byte vectors per thread per tile: 64 * 256 / 8 / QWG
+
+template <int DT>
+struct Vec16 {
+  static constexpr int N = DT == MZ_F32 ? 4 : 8;  // elements per 16 bytes
+};
+
+template <int DT>
+__device__ __forceinline__ void vec16_store_lds(float* dst, const uint4 u) {
+  if constexpr (DT == MZ_F32) {
+    dst[0] = __uint_as_float(u.x), dst[1] = __uint_as_float(u.y), dst[2] = __uint_as_float(u.z),
+    dst[3] = __uint_as_float(u.w);
+  } else {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      dst[2 * k] = DT == MZ_BF16 ? bf2f((uint16_t)w[k]) : h2f((uint16_t)w[k]);
+      dst[2 * k + 1] = DT == MZ_BF16 ? bf2f((uint16_t)(w[k] >> 16)) : h2f((uint16_t)(w[k] >> 16));
+    }
+  }
+}
+
+template <int DT, int BITS, bool VEC>
+__global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restrict__ x, int B, int H, int T, int D,
                                                             int64_t sb, int64_t sh, int64_t st,
                                                             uint8_t* __restrict__ packed, int64_t psb, int64_t psh,
                                                             void* mn, void* sc, int meta_dtype, int64_t msb,
                                                             int64_t msh, float eps, const void* __restrict__ table) {
-  extern __shared__ float tile[];  // [64][D + 1]
+  extern __shared__ __align__(16) uint8_t dyn[];
+  uint8_t* lds = dyn;                                                 // compander table
+  float* tile = (float*)(dyn + QTable<DT, BITS>::LDS_BYTES);          // [64][D + 1]
+  stage_table<DT, BITS>(lds, table);
   const int nsg = T / 64;
-  const int s = blockIdx.x % nsg;
-  const int h = (blockIdx.x / nsg) % H;
-  const int b = blockIdx.x / (nsg * H);
+  const int ntiles = B * H * nsg;  // < 2^31 (host check)
   const int ld = D + 1;
-  const int64_t base = b * sb + h * sh + (int64_t)(64 * s) * st;
-  for (int e = threadIdx.x; e < 64 * D; e += 256) {
-    const int t = e / D, c = e - t * D;
-    tile[t * ld + c] = load_val<DT>(x, base + t * st + c);
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int part = lane & 7;
   constexpr int QB = 8 * BITS;
-  uint8_t* gbase = packed + b * psb + h * psh + (int64_t)s * D * QB;
-  const int64_t mbase = b * msb + h * msh + (int64_t)s * D;
-  for (int c = wave; c < D; c += 4) {
-    const float v = tile[lane * ld + c];
-    quantize_group<DT, BITS>(v, lane, gbase + (int64_t)c * QB, mn, sc, mbase + c, meta_dtype, eps, table);
+  constexpr int NE = Vec16<DT>::N;
+  const int vpr = D / NE;             // vectors per token row (VEC)
+  const int nvec = 64 * vpr;          // vectors per tile (VEC)
+  auto tile_base = [&](int ti) -> int64_t {
+    const int s = ti % nsg, h = (ti / nsg) % H, b = ti / (nsg * H);
+    return b * sb + h * sh + (int64_t)(64 * s) * st;
+  };
+  uint4 nxt[KEY_MAX_VEC];
+  auto fetch = [&](int ti) {
+    if constexpr (VEC) {
+      const int64_t base = tile_base(ti);
+      const char* xb = (const char*)x;
+#pragma unroll
+      for (int k = 0; k < KEY_MAX_VEC; ++k) {
+        const int e = threadIdx.x + k * QWG;
+        if (e < nvec) {
+          const int t = e / vpr, c = (e - t * vpr) * NE;
+          nxt[k] = *(const uint4*)(xb + (base + (int64_t)t * st + c) * (DT == MZ_F32 ? 4 : 2));
+        }
+      }
+    }
+  };
+  if (blockIdx.x < ntiles) fetch(blockIdx.x);
+  for (int ti = blockIdx.x; ti < ntiles; ti += gridDim.x) {
+    const int s = ti % nsg, h = (ti / nsg) % H, b = ti / (nsg * H);
+    __syncthreads();  // the previous tile's columns are consumed
+    if constexpr (VEC) {
+#pragma unroll
+      for (int k = 0; k < KEY_MAX_VEC; ++k) {
+        const int e = threadIdx.x + k * QWG;
+        if (e < nvec) {
+          const int t = e / vpr, c = (e - t * vpr) * NE;
+          vec16_store_lds<DT>(tile + t * ld + c, nxt[k]);
+        }
+      }
+      if (ti + (int)gridDim.x < ntiles) fetch(ti + gridDim.x);  // lands while this tile is quantized
+    } else {
+      const int64_t base = tile_base(ti);
+      for (int e = threadIdx.x; e < 64 * D; e += QWG) {
+        const int t = e / D, c = e - t * D;
+        tile[t * ld + c] = load_val<DT>(x, base + t * st + c);
+      }
+    }
+    __syncthreads();
+    uint8_t* gbase = packed + b * psb + h * psh + (int64_t)s * D * QB;
+    const int64_t mbase = b * msb + h * msh + (int64_t)s * D;
+    for (int c0 = 8 * wave; c0 < D; c0 += 8 * (QWG / 64)) {
+      const int c = c0 + (lane >> 3);
+      if (c < D) {  // a group's 8 lanes share c
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = tile[(8 * part + k) * ld + c];
+        quantize_lane8<DT, BITS>(v, part, gbase + (int64_t)c * QB, mn, sc, mbase + c, meta_dtype, eps, lds, table);
+      }
+    }
   }
 }
 
@@ -194,6 +441,32 @@ static inline int launch_status() {
 
 using namespace mz;
 
+static int cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return cus;
+}
+
+// Persistent grid: enough workgroups to fill the GPU a few times over, each
+// looping over its share of the 64-value groups (table staged once).
+static int quantize_grid(int64_t work_groups) {
+  const int64_t per_wg = (int64_t)(QWG / 64) * QGROUPS_PER_WAVE;
+  const int64_t need = (work_groups + per_wg - 1) / per_wg;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)cu_count() * 8));
+}
+
+// Alignment the packed rows need: a lane stores its `bits` bytes as one
+// 2/4/8-byte word when bits is 2/4/8, byte by byte otherwise.
+static int packed_align(int bits) { return (bits == 2 || bits == 4 || bits == 8) ? bits : 1; }
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static int64_t dtype_size(int dt) { return dt == MZ_F32 ? 4 : 2; }
+
 extern "C" int muzero_quantize_rows(const void* x, int x_dtype, int64_t nrows, int64_t x_row_stride,
                                     uint8_t* packed, int64_t packed_row_stride, void* mn, void* scale,
                                     int meta_dtype, int64_t meta_stride, int bits, float eps, const void* table,
@@ -202,11 +475,18 @@ extern "C" int muzero_quantize_rows(const void* x, int x_dtype, int64_t nrows, i
   if (nrows == 0) return MZ_OK;
   if (!x || !packed || !mn || !scale || !table) return MZ_EINVAL;
   if (x_row_stride < 64 || packed_row_stride < 8 * bits || meta_stride < 1) return MZ_EINVAL;
-  const dim3 grid((unsigned)((nrows + 3) / 4));
+  // packed bytes are stored 1/2/4/8 at a time at offsets part*bits: rows must keep that alignment
+  if (((uintptr_t)packed | (uintptr_t)packed_row_stride) % packed_align(bits) != 0) return MZ_EINVAL;
+  const bool vec = aligned16(x) && x_row_stride % 8 == 0;
+  const dim3 grid((unsigned)quantize_grid(nrows));
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
-      hipLaunchKernelGGL((quantize_rows_kernel<D_, B_>), grid, dim3(256), 0, s, x, nrows, x_row_stride, packed,
-                         packed_row_stride, mn, scale, meta_dtype, meta_stride, eps, table)));
+      if (vec) hipLaunchKernelGGL((quantize_rows_kernel<D_, B_, true>), grid, dim3(QWG), 0, s, x, nrows,
+                                  x_row_stride, packed, packed_row_stride, mn, scale, meta_dtype, meta_stride, eps,
+                                  table);
+      else hipLaunchKernelGGL((quantize_rows_kernel<D_, B_, false>), grid, dim3(QWG), 0, s, x, nrows,
+                              x_row_stride, packed, packed_row_stride, mn, scale, meta_dtype, meta_stride, eps,
+                              table)));
   return launch_status();
 }
 
@@ -227,18 +507,26 @@ extern "C" int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H,
   if (st == 1) return MZ_OK;
   if (st) return st;
   if (T % 64) return MZ_EINVAL;
-  const size_t lds = (size_t)64 * (D + 1) * sizeof(float);
-  if (lds > 160 * 1024) return MZ_EUNSUPPORTED;
-  const dim3 grid((unsigned)((int64_t)B * H * (T / 64)));
+  if (((uintptr_t)packed | (uintptr_t)p_sb | (uintptr_t)p_sh) % packed_align(bits) != 0) return MZ_EINVAL;
+  const int64_t ntiles = (int64_t)B * H * (T / 64);
+  if (ntiles >= (int64_t)1 << 31) return MZ_EINVAL;
+  const size_t es = x_dtype == MZ_F32 ? 4 : 2;
+  const bool vec = aligned16(keys) && D % 8 == 0 && D <= 256 && (x_sb * es) % 16 == 0 && (x_sh * es) % 16 == 0 &&
+                   (x_st * es) % 16 == 0;
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
+      const size_t lds = (size_t)QTable<D_, B_>::LDS_BYTES + (size_t)64 * (D + 1) * sizeof(float);
+      if (lds > 160 * 1024) return MZ_EUNSUPPORTED;
+      const void* fn = vec ? (const void*)quantize_keys_kernel<D_, B_, true> : (const void*)quantize_keys_kernel<D_, B_, false>;
       if (lds > 64 * 1024) {
-        const hipError_t e = hipFuncSetAttribute((const void*)quantize_keys_kernel<D_, B_>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return (int)e;
       }
-      hipLaunchKernelGGL((quantize_keys_kernel<D_, B_>), grid, dim3(256), lds, s, keys, B, H, T, D, x_sb, x_sh, x_st,
-                         packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table)));
+      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ntiles, 2 * (int64_t)cu_count())));
+      if (vec) hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, true>), grid, dim3(QWG), lds, s, keys, B, H, T, D,
+                                  x_sb, x_sh, x_st, packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table);
+      else hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, false>), grid, dim3(QWG), lds, s, keys, B, H, T, D,
+                              x_sb, x_sh, x_st, packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table)));
   return launch_status();
 }
 
@@ -249,13 +537,36 @@ extern "C" int muzero_quantize_values(const void* values, int x_dtype, int B, in
   int st = check_block(values, x_dtype, B, H, T, D, packed, mn, scale, meta_dtype, bits, table);
   if (st == 1) return MZ_OK;
   if (st) return st;
-  const int64_t nrows = (int64_t)B * H * T * ((D + 63) / 64);
-  const dim3 grid((unsigned)((nrows + 3) / 4));
+  if (((uintptr_t)packed | (uintptr_t)p_sb | (uintptr_t)p_sh) % packed_align(bits) != 0) return MZ_EINVAL;
+  const int ng = (D + 63) / 64;
+  const int64_t rows_per_b = (int64_t)H * T * ng;
+  if (rows_per_b >= (int64_t)1 << 31) return MZ_EINVAL;
+  const size_t es = x_dtype == MZ_F32 ? 4 : 2;
+  const bool vec = aligned16(values) && D % 8 == 0 && (x_sb * es) % 16 == 0 && (x_sh * es) % 16 == 0 &&
+                   (x_st * es) % 16 == 0;
+  const FastDiv fng = make_fastdiv((uint32_t)ng), fT = make_fastdiv((uint32_t)T), fH = make_fastdiv((uint32_t)H);
   hipStream_t s = (hipStream_t)stream;
-  MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
-      hipLaunchKernelGGL((quantize_values_kernel<D_, B_>), grid, dim3(256), 0, s, values, B, H, T, D, x_sb, x_sh,
-                         x_st, packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table)));
-  return launch_status();
+  // row numbers stay below 2^31 per launch: batches go in slices of bstep
+  const int bstep = (int)std::min<int64_t>(B, (((int64_t)1 << 31) - 1) / rows_per_b);
+  for (int b0 = 0; b0 < B; b0 += bstep) {
+    const int nb = std::min(bstep, B - b0);
+    const int nrows = (int)(nb * rows_per_b);
+    const void* xs = (const char*)values + b0 * x_sb * (int64_t)es;
+    uint8_t* ps = packed + b0 * p_sb;
+    void* mns = (char*)mn + b0 * m_sb * (int64_t)dtype_size(meta_dtype);
+    void* scs = (char*)scale + b0 * m_sb * (int64_t)dtype_size(meta_dtype);
+    const dim3 grid((unsigned)quantize_grid(nrows));
+    MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
+        if (vec) hipLaunchKernelGGL((quantize_values_kernel<D_, B_, true>), grid, dim3(QWG), 0, s, xs, nrows, fng, fT,
+                                    fH, D, x_sb, x_sh, x_st, ps, p_sb, p_sh, mns, scs, meta_dtype, m_sb, m_sh, eps,
+                                    table);
+        else hipLaunchKernelGGL((quantize_values_kernel<D_, B_, false>), grid, dim3(QWG), 0, s, xs, nrows, fng, fT,
+                                fH, D, x_sb, x_sh, x_st, ps, p_sb, p_sh, mns, scs, meta_dtype, m_sb, m_sh, eps,
+                                table)));
+    const int st2 = launch_status();
+    if (st2 != MZ_OK) return st2;
+  }
+  return MZ_OK;
 }
 
 extern "C" int muzero_dequantize_rows(const uint8_t* packed, int64_t nrows, int64_t packed_row_stride,

@@ -159,3 +159,84 @@ def test_dequantize_rows_golden(qgold, dname, bits, alpha, oname):
         rec = out.cpu().float()[torch.from_numpy(bad)]
         assert torch.isfinite(rec).all()
         assert torch.equal(rec, mn.cpu().float()[torch.from_numpy(bad)].expand_as(rec))
+
+
+def _meta_equal(a, b):
+    """Equal metadata, NaN == NaN whatever the payload, +0 == -0.
+
+    The sign of a zero min / max is not part of the contract: torch's CPU
+    reduction returns the sign of one fixed element of a row of signed zeros
+    (element 48 of 64 for 16-bit dtypes on an AVX2 host), an artifact of its
+    vector width.  Codes do not depend on it (0 - (+-0) = +0)."""
+    a, b = a.float().reshape(-1), b.float().reshape(-1)
+    both_nan = torch.isnan(a) & torch.isnan(b)
+    return bool(((a == b) | both_nan).all())
+
+
+@pytest.mark.parametrize("dname", list(DT))
+@pytest.mark.parametrize("bits", [1, 2, 4, 8])
+def test_quantize_rows_nonfinite_and_degenerate(dname, bits):
+    """NaN / +-inf inputs, constant and all-zero rows, denormal and near-overflow rows give the
+    reference's codes and metadata."""
+    g = torch.Generator().manual_seed(7 * bits)
+    x = torch.randn(64, 64, generator=g)
+    x[1, 5] = float("nan")
+    x[2, 0] = float("inf")
+    x[3, 63] = float("-inf")
+    x[4, :] = float("inf")
+    x[5, 10] = float("inf")
+    x[5, 11] = float("-inf")
+    x[6, :] = 0.0
+    x[7, :] = 3.25
+    x[8, :] = float("nan")
+    x[9, :] *= 1e-38   # bf16 / fp32 denormals and tiny normals
+    x[10, :] *= 1e-40
+    x[11, :] *= 1e38   # scale above 2^126 (bf16 / fp32), inf in fp16
+    x[12, :] = torch.rand(64, generator=g) * 3e38
+    x = x.to(DT[dname])
+    pq, mn, sc = _quantize_gpu(x, bits, 2.0)
+    epq, emn, esc = ref.quantize_rows(x, bits, 2.0, 1e-8, torch.float16)
+    np.testing.assert_array_equal(pq.numpy(), epq.numpy())
+    assert _meta_equal(mn, emn) and _meta_equal(sc, esc)
+
+
+@pytest.mark.parametrize("dname", list(DT))
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_rows_many_rows(dname, bits):
+    """More rows than one pass of the persistent grid covers (each workgroup loops)."""
+    g = torch.Generator().manual_seed(bits)
+    x = (torch.randn(300_000, 64, generator=g) * 3).to(DT[dname])
+    pq, mn, sc = _quantize_gpu(x, bits, 2.0)
+    epq, emn, esc = ref.quantize_rows(x, bits, 2.0, 1e-8, torch.float16)
+    np.testing.assert_array_equal(pq.numpy(), epq.numpy())
+    np.testing.assert_array_equal(bits_of(mn), bits_of(emn))
+    np.testing.assert_array_equal(bits_of(sc), bits_of(esc))
+
+
+@pytest.mark.parametrize("dname", ["bfloat16", "float32"])
+@pytest.mark.parametrize("bits", [2, 4])
+def test_quantize_blocks_aligned_vector_path(dname, bits):
+    """Contiguous, 16-byte aligned blocks take the vector-load path of the value kernel."""
+    from muzero_amd.kernels import loader as L
+    g = torch.Generator().manual_seed(50 + bits)
+    B, H, T, d = 3, 2, 640, 128
+    x = (torch.randn(B, H, T, d, generator=g) * 2).to(DT[dname])
+    dx = x.to(DEV)
+    qb, ng = 8 * bits, 2
+    pv = torch.empty((B, H, T, ng, qb), dtype=torch.uint8, device=DEV)
+    vmn = torch.empty((B, H, T, ng, 1), dtype=torch.float16, device=DEV)
+    vsc = torch.empty_like(vmn)
+    L.quantize_value_block_into(dx, bits, 2.0, 1e-8, pv, vmn, vsc)
+    pk = torch.empty((B, H, T // 64, d, qb), dtype=torch.uint8, device=DEV)
+    kmn = torch.empty((B, H, T // 64, d, 1), dtype=torch.float16, device=DEV)
+    ksc = torch.empty_like(kmn)
+    L.quantize_key_block_into(dx, bits, 2.0, 1e-8, pk, kmn, ksc)
+    torch.cuda.synchronize()
+    epv, evmn, evsc = ref.quantize_value_block(x, bits, 2.0, 64)
+    epk, ekmn, eksc = ref.quantize_key_block(x, bits, 2.0, 64)
+    np.testing.assert_array_equal(pv.cpu().numpy(), epv.numpy())
+    np.testing.assert_array_equal(bits_of(vmn), bits_of(evmn))
+    np.testing.assert_array_equal(bits_of(vsc), bits_of(evsc))
+    np.testing.assert_array_equal(pk.cpu().numpy(), epk.numpy())
+    np.testing.assert_array_equal(bits_of(kmn), bits_of(ekmn))
+    np.testing.assert_array_equal(bits_of(ksc), bits_of(eksc))
