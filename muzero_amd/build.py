@@ -11,6 +11,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -23,7 +24,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # the reference evaluates every elementwise op separately: no FMA contraction
     "-ffp-contract=off",
     # no packed-FP32 instructions (v_pk_*_f32) anywhere in this library
@@ -40,13 +40,27 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = True) -> str:
-    """Compile every HIP source into one shared library (always rebuilds)."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"),
-           *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    subprocess.run(cmd, check=True)
+    """Compile every HIP source into one shared library (always rebuilds).
+
+    Each source compiles to an object in its own hipcc process (in parallel),
+    then one link step writes the library."""
+    inc = ["-I", os.path.join(ROOT, "include")]
+    with tempfile.TemporaryDirectory(prefix="muzero_build_") as tmpdir:
+        procs = []
+        for src in SOURCES:
+            obj = os.path.join(tmpdir, os.path.splitext(src)[0] + ".o")
+            cmd = [hipcc(), *HIPCC_FLAGS, *inc, "-c", os.path.join(CSRC, src), "-o", obj]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((cmd, obj, subprocess.Popen(cmd)))
+        failed = [cmd for cmd, _, p in procs if p.wait() != 0]
+        if failed:
+            raise subprocess.CalledProcessError(1, failed[0])
+        tmp = LIB + ".tmp"
+        link = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *[o for _, o, _ in procs], "-o", tmp]
+        if verbose:
+            print(" ".join(link), flush=True)
+        subprocess.run(link, check=True)
     os.replace(tmp, LIB)
     return LIB
 

@@ -83,12 +83,12 @@ struct Smem {
   static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
   static constexpr int WAVE0 = ZERO + AROW * 4;
   // per-wave region
-  static constexpr int KZL = 0;                      // uint32 [D]            zl << 8
-  static constexpr int AHI = KZL + D * 4;            // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
+  static constexpr int KZP = 0;                      // uint32 [4 g][8 kt]    zl of channels 16kt+4g+{0..3}
+  static constexpr int AHI = KZP + 4 * 8 * 4;        // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
   static constexpr int ALO = AHI + NREP * AROW * 4;  // uint32 [NREP][AROW]   low part
   static constexpr int QA = ALO + NREP * AROW * 4;   // fp16 [NREP][HROW*2]   q*a
-  static constexpr int VZL = QA + NREP * HROW * 4;   // uint32 [NG][TILE]     zl << 8
-  static constexpr int VBP = VZL + NG * TILE * 4;    // uint32 [NG][TILE]     (bp, bn) fp16
+  static constexpr int VZP = QA + NREP * HROW * 4;   // uint32 [NG][4 g][4 kt] zl of tokens 16kt+4g+{0..3}
+  static constexpr int VBP = VZP + NG * 4 * 4 * 4;   // uint32 [NG][TILE]     (bp, bn) fp16
   static constexpr int VA = VBP + NG * TILE * 4;     // fp16 [NG][TILE]       a
   static constexpr int PA = VA + NG * TILE * 2;         // uint32 [NG][NREP][LROW]   (p*bp, p*bn) fp16
   static constexpr int PA1 = PA + NG * NREP * LROW * 4;  // fp16 [NG][NREP][PROW*2]   p*a
@@ -132,7 +132,7 @@ __device__ __forceinline__ int range_exp(float mx) {
 
 struct GroupScalars {
   float a, bp, bn;
-  uint32_t zrow;  // zl << 8: byte offset of the group's zero-level row in the table
+  uint32_t zl;    // zero level: the group's row of the (P, N) table
 };
 
 // (a, bp, bn, zl) of one stored group (mn, s); the scale is guarded like the
@@ -150,7 +150,7 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   r.a = mn + s * za;
   r.bp = s * pe;
   r.bn = -(s * ne);
-  r.zrow = (uint32_t)(zl == zl ? (int)zl : 0) << 8;
+  r.zl = (uint32_t)(zl == zl ? (int)zl : 0);
   return r;
 }
 
@@ -164,18 +164,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
 }
 
-// Global data of one quantized tile, loaded one tile ahead.  Code words:
-// lanes 2m and 2m+1 of a lane group read the same 2*LB bytes of two rows of a
-// pair (key: channels, value: tokens); code_pair() later swaps halves between
-// them so each lane ends with the bytes of both rows that hold ITS codes.
+// Global data of one quantized tile.  Code words: lanes 2m and 2m+1 of a
+// lane group read the same 2*LB bytes of two rows of a pair (key: channels,
+// value: tokens); lookup_ktile() later swaps halves between them so each lane
+// ends with the bytes of both rows that hold ITS codes.
 //   4-bit: kw[kt*2+p] = 32 bits of row 16kt+4g+2p+(n&1)
 //   2-bit: kw[kt*2+h] = 16 bits of row 16kt+4g+2h+(n&1)
 // (values: vw[(kt*NG+vg)*2 + p|h], rows = tokens, bytes of value group vg).
 // Metadata words: MW = 1 (fp16 / bf16: one word holds both entries) or 2 (fp32).
 template <int MW>
-struct TileData {
-  uint32_t kw[16];
-  uint32_t vw[16];
+struct MetaWords {
   uint32_t kmn[MW], ksc[MW];  // key groups of channels 2*lane, 2*lane+1 (raw bits)
   uint32_t vmn[MW], vsc[MW];  // value groups 0, 1 of token lane (raw bits)
 };
@@ -202,31 +200,36 @@ __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t&
   else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff + imm, soff, 0);
 }
 
-// Key code words and all metadata of a tile (issued at the start of the
-// previous tile; metadata first, so its consumer need not wait for the codes).
-template <int BITS, int MW>
-__device__ __forceinline__ void load_tile_k(TileData<MW>& t, const Bufs& bf, int tile, int lane) {
-  using F = Fmt<BITS>;
+// All metadata of a tile (loaded one tile ahead of its use).
+template <int MW>
+__device__ __forceinline__ void load_meta_tile(MetaWords<MW>& t, const Bufs& bf, int tile, int lane) {
   constexpr int ES = 2 * MW;  // bytes per metadata entry
-  const int n = lane & 15, g = lane >> 4;
   const int kmo = 2 * lane * ES, kms = tile * D * ES;
   load_meta<MW>(t.kmn, bf.kmn, kmo, kms);
   load_meta<MW>(t.ksc, bf.ksc, kmo, kms);
   const int vmo = NG * lane * ES, vms = tile * TILE * NG * ES;
   load_meta<MW>(t.vmn, bf.vmn, vmo, vms);
   load_meta<MW>(t.vsc, bf.vsc, vmo, vms);
+}
+
+// Key code words of a tile (issued once the previous tile's key words are
+// consumed: they land while the previous tile's P.V runs).
+template <int BITS>
+__device__ __forceinline__ void load_kw(uint32_t (&kw)[16], const Bufs& bf, int tile, int lane) {
+  using F = Fmt<BITS>;
+  const int n = lane & 15, g = lane >> 4;
   const int voff = (4 * g + (n & 1)) * F::QB + 2 * F::LB * (n >> 1);
   const int soff = tile * D * F::QB;
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) t.kw[kt * 2 + p] = load_code_word<BITS>(bf.kp, voff, soff, (16 * kt + 2 * p) * F::QB);
+    for (int p = 0; p < 2; ++p) kw[kt * 2 + p] = load_code_word<BITS>(bf.kp, voff, soff, (16 * kt + 2 * p) * F::QB);
 }
 
-// ... and its value code words (issued once the previous tile's key words
-// are consumed, so the two register sets overlap less).
-template <int BITS, int MW>
-__device__ __forceinline__ void load_tile_v(TileData<MW>& t, const Bufs& bf, int tile, int lane) {
+// Value code words of a tile (issued at the start of the tile: they land
+// while its Q.K runs).
+template <int BITS>
+__device__ __forceinline__ void load_vw(uint32_t (&vw)[16], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
   const int voff = (4 * g + (n & 1)) * (NG * F::QB) + 2 * F::LB * (n >> 1);
@@ -237,22 +240,23 @@ __device__ __forceinline__ void load_tile_v(TileData<MW>& t, const Bufs& bf, int
     for (int vg = 0; vg < NG; ++vg)
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        t.vw[(kt * NG + vg) * 2 + p] =
+        vw[(kt * NG + vg) * 2 + p] =
             load_code_word<BITS>(bf.vp, voff, soff, (16 * kt + 2 * p) * (NG * F::QB) + F::QB * vg);
 }
 
 __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_XOR1, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_XOR1, 0xF, 0xF, true);
 }
 
 // The B operands of one k-tile (4 rows ii of this lane's k-slice x its 4
 // codes, jt = code index) from the two raw words w0, w1 of the k-tile.  The
 // codes are spread to bytes as table offsets 4*q + 64*group (two ops per 4
-// codes); one v_perm per code then places the offset under the zero-level
-// row (zr = zl << 8) and one ds_read_b32 fetches the (P, N) pair straight into
-// the operand register.  `odd` = lane n is odd.
+// codes); one v_perm per code then joins the offset (low byte) with row ii's
+// zero level (byte ii of zp, as the high byte: the table row zl*256) and one
+// ds_read_b32 fetches the (P, N) pair straight into the operand register.
+// `odd` = lane n is odd.
 template <int BITS, int TBASE>
-__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, uint32_t w1, const u32x4 zr,
+__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, uint32_t w1, uint32_t zp,
                                              uint32_t grep, bool odd, u32x4 B[4]) {
   if constexpr (BITS == 4) {
     // w0 / w1: rows (0,1) / (2,3) of the pair, 32 bits = codes of lanes 2m, 2m+1;
@@ -268,8 +272,8 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         const uint32_t e = (jt & 1) ? od[ii >> 1] : ev[ii >> 1];
-        const uint32_t s = 0x0C0C0500u | (uint32_t)((ii & 1) * 2 + (jt >> 1));
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], e, s));
+        const uint32_t s = 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | (uint32_t)((ii & 1) * 2 + (jt >> 1));
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zp, e, s));
       }
   } else {
     // w0 / w1: 16 bits of rows (0 | 1) / (2 | 3) (even / odd lane), one byte per
@@ -283,7 +287,8 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
       const uint32_t ej = e | grep;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zr[ii], ej, 0x0C0C0500u | (uint32_t)ii));
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
+                                       __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii));
     }
   }
 }
@@ -333,10 +338,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // is not a quantized tile of this wave is replaced by one this split reads
   // anyway, so the spare load hits the cache.
   const int q_last = max(0, min(t_end, a.n_groups) - 1);
-  TileData<MW> T0, T1;
   const int tile0 = t_begin + wave;
-  load_tile_k<BITS, MW>(T0, bf, min(tile0, q_last), lane);
-  load_tile_v<BITS, MW>(T0, bf, min(tile0, q_last), lane);
+  MetaWords<MW> MT;              // metadata of the current tile
+  uint32_t KW[16], VW[16];       // key / value code words of the current tile
+  load_meta_tile<MW>(MT, bf, min(tile0, q_last), lane);
+  load_kw<BITS>(KW, bf, min(tile0, q_last), lane);
 
   // ---------------- workgroup setup: tables and query in LDS
   for (int i = threadIdx.x; i < TBL / 4; i += 256) {
@@ -394,10 +400,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int kacc = 0;  // acc holds sum p * x * 2^kacc
   bool kacc_init = false;
 
-  // one tile; the next quantized tile tn of this wave (if any) is loaded into Tn
-  auto process = [&](const int tile, const TileData<MW>& T, TileData<MW>& Tn, const int tn) {
+  // one tile.  Loads in flight: this tile's value words (issued here, used by
+  // its P.V), the next tile tn's metadata (issued here, used by its scalars)
+  // and the next tile's key words (issued after this tile's Q.K).
+  auto process = [&](const int tile, const int tn) {
     const int tl = min(tn, q_last);
-    load_tile_k<BITS, MW>(Tn, bf, tl, lane);
+    load_vw<BITS>(VW, bf, min(tile, q_last), lane);
+    MetaWords<MW> MN;
+    load_meta_tile<MW>(MN, bf, tl, lane);
     const bool quant = tile < a.n_groups;
     int n_valid, pos0, r0 = 0;
     if (quant) {
@@ -414,7 +424,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float unscale = a.scaling;
     if (quant) {
       // ---------- key group scalars (lane: channels 2*lane, 2*lane+1)
-      const float2 kmn = meta_cvt<MW>(T.kmn, a.meta_dtype), ksc = meta_cvt<MW>(T.ksc, a.meta_dtype);
+      const float2 kmn = meta_cvt<MW>(MT.kmn, a.meta_dtype), ksc = meta_cvt<MW>(MT.ksc, a.meta_dtype);
       const GroupScalars k0 = group_scalars<F::QMAX>(kmn.x, ksc.x);
       const GroupScalars k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
       float kmx = fmaxf(fmaxf(fabsf(k0.a), fmaxf(k0.bp, -k0.bn)), fmaxf(fabsf(k1.a), fmaxf(k1.bp, -k1.bn)));
@@ -424,7 +434,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float bp0 = ldexpf(k0.bp, kexp), bn0 = ldexpf(k0.bn, kexp);
       const float bp1 = ldexpf(k1.bp, kexp), bn1 = ldexpf(k1.bn, kexp);
       const uint32_t ka = pack_h2(ldexpf(k0.a, kexp), ldexpf(k1.a, kexp));
-      *(uint2*)(W + S::KZL + 8 * lane) = uint2{k0.zrow, k1.zrow};
+      // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
+      *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
+          (uint16_t)(k0.zl | (k1.zl << 8));
 #pragma unroll
       for (int h = 0; h < NREP; ++h) {
         const uint32_t q01 = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
@@ -436,14 +448,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, ka);
       }
       // ---------- value scalars (lane: token lane, both value groups)
-      const float2 vmn = meta_cvt<MW>(T.vmn, a.meta_dtype), vsc = meta_cvt<MW>(T.vsc, a.meta_dtype);
+      const float2 vmn = meta_cvt<MW>(MT.vmn, a.meta_dtype), vsc = meta_cvt<MW>(MT.vsc, a.meta_dtype);
       const GroupScalars v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
       const GroupScalars v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
       const float vmx = fmaxf(fmaxf(fabsf(v0.a), fmaxf(v0.bp, -v0.bn)), fmaxf(fabsf(v1.a), fmaxf(v1.bp, -v1.bn)));
       // keep the accumulators' exponent unless this tile needs a smaller one
       kv_exp = min(kacc_init ? kacc : 60, range_exp(wave_max_fast(vmx)));
-      ((uint32_t*)(W + S::VZL))[lane] = v0.zrow;
-      ((uint32_t*)(W + S::VZL))[TILE + lane] = v1.zrow;
+      // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
+      const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
+      W[S::VZP + vzo] = (uint8_t)v0.zl;
+      W[S::VZP + 64 + vzo] = (uint8_t)v1.zl;
       ((uint32_t*)(W + S::VBP))[lane] = pack_h2(ldexpf(v0.bp, kv_exp), ldexpf(v0.bn, kv_exp));
       ((uint32_t*)(W + S::VBP))[TILE + lane] = pack_h2(ldexpf(v1.bp, kv_exp), ldexpf(v1.bn, kv_exp));
       ((uint16_t*)(W + S::VA))[lane] = f2h(ldexpf(v0.a, kv_exp));
@@ -459,18 +473,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = s0;
+      // k-tiles software-pipelined: the lookups of k-tile kt+1 are issued
+      // before the MFMAs of k-tile kt, so the LDS latency overlaps the MFMAs
+      const u32x4 kz0 = *(const u32x4*)(W + S::KZP + g * 32);
+      const u32x4 kz1 = *(const u32x4*)(W + S::KZP + g * 32 + 16);
+      u32x4 Ac = *(const u32x4*)(a_hi_row + (4 * g) * 4);
+      u32x4 Bc[4], Bn[4];
+      lookup_ktile<BITS, S::TBL_K>(smem, KW[0], KW[1], kz0[0], grep, odd, Bc);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
-        const u32x4 A = *(const u32x4*)(a_hi_row + (16 * kt + 4 * g) * 4);
-        const u32x4 zr = *(const u32x4*)(W + S::KZL + (16 * kt + 4 * g) * 4);
-        u32x4 B[4];
-        lookup_ktile<BITS, S::TBL_K>(smem, T.kw[2 * kt], T.kw[2 * kt + 1], zr, grep, odd, B);
+        u32x4 An;
+        if (kt < 7) {
+          An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
+          lookup_ktile<BITS, S::TBL_K>(smem, KW[2 * kt + 2], KW[2 * kt + 3], kt + 1 < 4 ? kz0[kt + 1] : kz1[kt - 3],
+                                       grep, odd, Bn);
+        }
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(A, B[jt], s[jt]);
-        // keep each k-tile's lookups next to its MFMAs: hoisting later k-tiles'
-        // lookups gains no latency hiding here (two waves per SIMD) and costs
-        // the registers that would otherwise spill
+        for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], s[jt]);
         __builtin_amdgcn_sched_barrier(0);
+        if (kt < 7) {
+          Ac = An;
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
+        }
       }
     } else {
       // ---------- residual tile: S = Q K^T with dense operands; the weight
@@ -496,7 +521,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       wave_lds_sync();  // the (1, 0) / 0 scalars above are read by other lanes below
     }
-    load_tile_v<BITS, MW>(Tn, bf, tl, lane);
+    load_kw<BITS>(KW, bf, tl, lane);
 
     // ---------- online softmax in registers: head slot s of this lane group
     // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
@@ -572,18 +597,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // ---------- acc += P V
     if (quant) {
+      // steps st = (kt, vg), software-pipelined like Q.K
+      u32x4 vz[NG];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int vg = 0; vg < NG; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
+      u32x4 Ac = *(const u32x4*)(pa + hA * LROW + 4 * g);
+      u32x4 Bc[4], Bn[4];
+      lookup_ktile<BITS, S::TBL_V>(smem, VW[0], VW[1], vz[0][0], grep, odd, Bc);
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
-          const u32x4 A = *(const u32x4*)(pa + (vg * NREP + hA) * LROW + 16 * kt + 4 * g);
-          const u32x4 zr = *(const u32x4*)(W + S::VZL + (vg * TILE + 16 * kt + 4 * g) * 4);
-          u32x4 B[4];
-          lookup_ktile<BITS, S::TBL_V>(smem, T.vw[(kt * NG + vg) * 2], T.vw[(kt * NG + vg) * 2 + 1], zr, grep,
-                                       odd, B);
+      for (int st = 0; st < 4 * NG; ++st) {
+        const int kt = st / NG, vg = st % NG;
+        u32x4 An;
+        if (st + 1 < 4 * NG) {
+          const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
+          An = *(const u32x4*)(pa + (vg1 * NREP + hA) * LROW + 16 * kt1 + 4 * g);
+          lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, Bn);
+        }
 #pragma unroll
-          for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(A, B[jt], acc[vg][jt]);
-          __builtin_amdgcn_sched_barrier(0);
+        for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], acc[vg][jt]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 1 < 4 * NG) {
+          Ac = An;
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
         }
       }
       // constant part: sum_t p_t * a_t against a ones operand
@@ -631,16 +667,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
     wave_lds_sync();
+    MT = MN;
   };
 
-  // tiles of this wave: tile0, tile0 + 4, ...; the next quantized tile's data
-  // is in flight while the current one is computed (two register sets)
-  for (int tile = tile0; tile < t_end; tile += 2 * WAVES) {
-    const int t1 = tile + WAVES;
-    process(tile, T0, T1, t1);
-    if (t1 >= t_end) break;
-    process(t1, T1, T0, t1 + WAVES);
-  }
+  // tiles of this wave: tile0, tile0 + 4, ...
+  for (int tile = tile0; tile < t_end; tile += WAVES) process(tile, tile + WAVES);
 
   // ---------------- merge the 4 waves and write this split's partial records
   __syncthreads();
