@@ -141,6 +141,7 @@ def main():
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--residual", type=int, default=128)
     ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))
@@ -168,7 +169,7 @@ def main():
         caches.append({k_: t.clone() for k_, t in caches[0].items()})
     del k, v
     plans = [DecodePlan(q, bits=bits, n_groups=lq // 64, alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5,
-                        **c) for c in caches]
+                        n_split=args.n_split, **c) for c in caches]
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
         plans[i % len(plans)].run()

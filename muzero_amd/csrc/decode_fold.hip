@@ -50,7 +50,9 @@ namespace fold {
 constexpr int D = 128;
 constexpr int NG = 2;     // value groups per token
 constexpr int TILE = 64;  // tokens per tile
-constexpr int WAVES = 4;
+// Waves per workgroup (one per SIMD; two workgroups share a CU).
+template <int NREP>
+constexpr int waves_for() { return 4; }
 constexpr uint32_t ONES_F16X2 = 0x3C003C00u;
 // (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
 // zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
@@ -74,7 +76,7 @@ constexpr int PROW = TILE / 2 + 4;  // uint32 per head row of fp16 per-token arr
 
 // Static LDS layout (bytes).  Per workgroup: the two (P, N) tables and the
 // query in two forms; per wave: the current tile's operands and weights.
-template <int NREP>
+template <int NREP, int WAVES>
 struct Smem {
   static constexpr int TBL_K = 0;
   static constexpr int TBL_V = TBL;
@@ -158,6 +160,7 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
 // (bounded by their filled length, so a load past it reads 0, never faults).
 struct Bufs {
   __amdgpu_buffer_rsrc_t kp, vp, kmn, ksc, vmn, vsc;
+  __amdgpu_buffer_rsrc_t kr, vr;  // residual rows (bounded by the filled rows: padding tokens read 0)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_t bytes) {
@@ -294,11 +297,13 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
 }
 
 template <int IO, int NREP, int BITS, int MW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
+__global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
-    const uint32_t* __restrict__ ftab_v, int direct) {
+    const uint32_t* __restrict__ ftab_v, int direct, int cus) {
+  constexpr int WAVES = waves_for<NREP>();
+  constexpr int NT = 64 * WAVES;  // threads per workgroup
   using M = Mfma<IO>;
-  using S = Smem<NREP>;
+  using S = Smem<NREP, WAVES>;
   using F = Fmt<BITS>;
   constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
   static_assert(RS >= 2, "QK needs a second row per head for the low part of the key product");
@@ -331,30 +336,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * D * meta_es);
     bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NG * meta_es);
     bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NG * meta_es);
+    const int64_t nr = a.n_residual;
+    bf.kr = make_buf((const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh, nr ? ((nr - 1) * a.kr_st + D) * 2 : 0);
+    bf.vr = make_buf((const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh, nr ? ((nr - 1) * a.vr_st + D) * 2 : 0);
   }
 
+  // The split's tiles in virtual order: residual tiles first (their loads
+  // then overlap the setup), quantized tiles after; wave w takes virtual
+  // tiles w, w + WAVES, ...
+  const int n_quant = max(0, min(t_end, a.n_groups) - t_begin);  // quantized tiles of the split
+  const int n_res = (t_end - t_begin) - n_quant;                  // residual tiles of the split
+  const int n_virt = t_end - t_begin;
+  auto tile_of = [&](int v) { return v < n_res ? max(t_begin, a.n_groups) + v : t_begin + (v - n_res); };
   // Tile loads are issued unconditionally (the compiler's wait counts then
   // stay exact and a prefetch is never waited for early); a tile index that
-  // is not a quantized tile of this wave is replaced by one this split reads
-  // anyway, so the spare load hits the cache.
+  // is not a quantized tile is replaced by one this split reads anyway, so
+  // the spare load hits the cache.
   const int q_last = max(0, min(t_end, a.n_groups) - 1);
-  const int tile0 = t_begin + wave;
+  const int v0 = wave;  // first virtual tile of this wave
+
+  // ---------------- workgroup setup: tables and query in LDS.  Their loads
+  // are issued before the first tile's, so the setup waits for them only.
+  constexpr int TW = TBL / 4 / NT;                // table words per thread (each table)
+  constexpr int QW = (NREP * D + NT - 1) / NT;    // query elements per thread
+  uint32_t tk[TW], tv[TW];
+  uint16_t qraw[QW];
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    const int i = threadIdx.x + j * NT, zl = i >> 6, q = i & 15;
+    tk[j] = ftab_k[zl * 16 + q];
+    tv[j] = ftab_v[zl * 16 + q];
+  }
+#pragma unroll
+  for (int j = 0; j < QW; ++j) {
+    const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
+    qraw[j] = i < NREP * D ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c] : 0;
+  }
   MetaWords<MW> MT;              // metadata of the current tile
   uint32_t KW[16], VW[16];       // key / value code words of the current tile
-  load_meta_tile<MW>(MT, bf, min(tile0, q_last), lane);
-  load_kw<BITS>(KW, bf, min(tile0, q_last), lane);
-
-  // ---------------- workgroup setup: tables and query in LDS
-  for (int i = threadIdx.x; i < TBL / 4; i += 256) {
-    const int zl = i >> 6, q = i & 15;
-    ((uint32_t*)(smem + S::TBL_K))[i] = ftab_k[zl * 16 + q];
-    ((uint32_t*)(smem + S::TBL_V))[i] = ftab_v[zl * 16 + q];
+  load_meta_tile<MW>(MT, bf, min(tile_of(v0), q_last), lane);
+  load_kw<BITS>(KW, bf, min(tile_of(v0), q_last), lane);
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    ((uint32_t*)(smem + S::TBL_K))[threadIdx.x + j * NT] = tk[j];
+    ((uint32_t*)(smem + S::TBL_V))[threadIdx.x + j * NT] = tv[j];
   }
-  for (int i = threadIdx.x; i < AROW; i += 256) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
+  for (int i = threadIdx.x; i < AROW; i += NT) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
   float qabs = 0.f;
-  for (int i = threadIdx.x; i < NREP * D; i += 256) {
-    const int h = i / D, c = i - h * D;
-    const uint16_t raw = ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c];
+#pragma unroll
+  for (int j = 0; j < QW; ++j) {
+    const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
+    if (i >= NREP * D) break;
+    const uint16_t raw = qraw[j];
     const float qf = M::load(raw);
     ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = f2h(qf);
     ((uint16_t*)(smem + S::Q_IO))[h * HROW * 2 + c] = raw;
@@ -364,7 +397,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* wq = (float*)(smem + S::WAVE0);
   if (lane == 0) wq[wave] = qabs;
   __syncthreads();
-  qabs = fmaxf(fmaxf(wq[0], wq[1]), fmaxf(wq[2], wq[3]));
+  {
+    float m4 = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) m4 = fmaxf(m4, wq[w]);
+    qabs = m4;
+  }
   __syncthreads();
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
@@ -499,24 +537,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     } else {
       // ---------- residual tile: S = Q K^T with dense operands; the weight
-      // products below then use (bp, bn) = (1, 0) and a = 0: A = (p, 0)
+      // products below then use (bp, bn) = (2^kv_exp, 0) and a = 0: A =
+      // (p * 2^kv_exp, 0), so the accumulators keep their exponent (at most
+      // 15: p * 2^15 stays finite in fp16) whatever the tile order
+      kv_exp = min(kacc_init ? kacc : 15, 15);
+      const uint32_t unit_h = (uint32_t)f2h(ldexpf(1.f, kv_exp));
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) {
-        ((uint32_t*)(W + S::VBP))[vg * TILE + lane] = (uint32_t)ONES_F16X2 & 0xFFFFu;
+        ((uint32_t*)(W + S::VBP))[vg * TILE + lane] = unit_h;
         ((uint16_t*)(W + S::VA))[vg * TILE + lane] = 0;
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* kres = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
+      // key vectors in two batches of 8 per lane, each batch in flight at once
+      // (rows past the residual read 0 through the bounded buffer; their
+      // logits are masked)
+      const int kst = a.kr_st * 2;
 #pragma unroll
-      for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 qv = *(const u32x4*)(qio_row + (32 * kq + 8 * g) * 2);
+      for (int kh = 0; kh < 2; ++kh) {
+        u32x4 kb[2][4];
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          const int t = 4 * n + jt;
-          const u32x4 kb = t < n_valid ? *(const u32x4*)(kres + (int64_t)(r0 + t) * a.kr_st + 32 * kq + 8 * g)
-                                       : u32x4{0, 0, 0, 0};
-          s[jt] = M::run(qv, kb, s[jt]);
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            kb[k2][jt] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           bf.kr, (4 * n + jt) * kst + (32 * (2 * kh + k2) + 8 * g) * 2, r0 * kst, 0));
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const u32x4 qv = *(const u32x4*)(qio_row + (32 * (2 * kh + k2) + 8 * g) * 2);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qv, kb[k2][jt], s[jt]);
         }
       }
       wave_lds_sync();  // the (1, 0) / 0 scalars above are read by other lanes below
@@ -577,7 +628,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // ---------- rescale the accumulators (softmax correction and value-tile exponent),
     // skipped when no head's maximum moved and the exponent is unchanged
-    // (residual tiles add p*v unscaled, so they need exponent 0)
     if (__ballot(owner && moved) != 0 || kv_exp != kacc || !kacc_init) {
       const float fexp = ldexpf(1.f, kv_exp - kacc);
       kacc = kv_exp;
@@ -632,26 +682,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     } else {
-      // residual values: B pairs (v, 0) against A pairs (p, 0)
-      const uint16_t* vres = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
+      // residual values: B pairs (v, 0) against A pairs (p, 0); each k-tile's
+      // 8 value vectors are loaded together (padding rows read 0, p = 0 there)
+      const int vst = a.vr_st * 2;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const u32x4 pd = *(const u32x4*)(pa + hA * LROW + 16 * kt + 4 * g);  // (p, 0) pairs
+        uint32_t vv[NG][4][2];
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
-          uint32_t v4[4][2];
+        for (int vg = 0; vg < NG; ++vg)
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
-            const int t = 16 * kt + 4 * g + ii;
-            if (t < n_valid) {
-              const uint2 raw = *(const uint2*)(vres + (int64_t)(r0 + t) * a.vr_st + 64 * vg + 4 * n);
-              v4[ii][0] = raw.x;
-              v4[ii][1] = raw.y;
-            } else {
-              v4[ii][0] = 0u;
-              v4[ii][1] = 0u;
-            }
+            const auto raw = __builtin_amdgcn_raw_buffer_load_b64(
+                bf.vr, (16 * kt + 4 * g + ii) * vst + (64 * vg + 4 * n) * 2, r0 * vst, 0);
+            vv[vg][ii][0] = raw[0];
+            vv[vg][ii][1] = raw[1];
           }
+#pragma unroll
+        for (int vg = 0; vg < NG; ++vg) {
+          uint32_t (&v4)[4][2] = vv[vg];
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) {  // channel 64vg + 4n + jt
             u32x4 B;
@@ -671,13 +720,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
 
   // tiles of this wave: tile0, tile0 + 4, ...
-  for (int tile = tile0; tile < t_end; tile += WAVES) process(tile, tile + WAVES);
+  // Two waves (of two workgroups) share a SIMD and its issue slots go to the
+  // older one first: with equal shares one wave would finish early and leave
+  // the other to run alone.  Every wave has the same number of tiles, so a
+  // wave's priority falls with its progress (4 levels) and the SIMD favours
+  // the wave that is behind.  Workgroups are placed in launch order, one per
+  // CU and then a second one, so the younger workgroup of a CU (linear index
+  // >= `cus`) starts one level higher.  The tile assignment itself is fixed:
+  // results do not depend on timing.
+  const int n_mine = (n_virt - v0 + WAVES - 1) / WAVES;
+  const int wg_lin = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const int older = wg_lin < cus ? 1 : 0;  // the first workgroup of its CU: one level lower
+  int done = 0;
+  if (older) __builtin_amdgcn_s_setprio(2);
+  else __builtin_amdgcn_s_setprio(3);
+  for (int v = v0; v < n_virt; v += WAVES) {
+    process(tile_of(v), v + WAVES < n_virt ? tile_of(v + WAVES) : q_last);
+    ++done;
+    switch ((4 * done) / max(n_mine, 1) + older) {  // wave-uniform
+      case 0: break;
+      case 1: __builtin_amdgcn_s_setprio(2); break;
+      case 2: __builtin_amdgcn_s_setprio(1); break;
+      default: __builtin_amdgcn_s_setprio(0); break;
+    }
+  }
+  __builtin_amdgcn_s_setprio(0);
 
-  // ---------------- merge the 4 waves and write this split's partial records
+  // ---------------- merge the waves and write this split's partial records
   __syncthreads();
   float* red = (float*)(smem + S::WAVE0);
   constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D]
-  if (owner) {
+  // lane-derived indices recomputed from the lane id (mbcnt) instead of kept
+  // live across the tile loop, where every register is taken
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int n_e = lane_e & 15, g_e = lane_e >> 4;
+  if (((4 * g_e) % RS) == 0) {
+    const int h0 = (4 * g_e) / RS, n = n_e;
     float* w = red + wave * RED;
     const float unit = ldexpf(1.f, -kacc);
 #pragma unroll
@@ -697,7 +775,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __syncthreads();
   if (direct) {
     // one split: the final output, exactly as the combine kernel would form it
-    for (int e = threadIdx.x; e < NREP * D; e += 256) {
+    for (int e = threadIdx.x; e < NREP * D; e += NT) {
       const int h = e / D;
       const int c = e - h * D;
       float M_ = -INFINITY;
@@ -717,7 +795,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     return;
   }
-  for (int e = threadIdx.x; e < NREP * (D + 2); e += 256) {
+  for (int e = threadIdx.x; e < NREP * (D + 2); e += NT) {
     const int h = e / (D + 2);
     const int c = e - h * (D + 2);
     float M_ = -INFINITY;
@@ -800,11 +878,12 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const uint32_t* fk = (const uint32_t*)a->fold_k;
   const uint32_t* fv = (const uint32_t*)a->fold_v;
   const int dir = direct ? 1 : 0;
+  const int cus = fold_cu_count();
 #define MZ_FOLD(IOV, NR, BB)                                                                            \
   if (a->meta_dtype == MZ_F32)                                                                          \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv, dir); \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
   else                                                                                                       \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(256), 0, s, *a, tps, ns, fk, fv, dir)
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(64 * fold::waves_for<NR>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
 #define MZ_FOLD_NREP(IOV, BB)            \
   switch (a->n_rep) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
