@@ -87,7 +87,13 @@ __device__ __forceinline__ float wave_max(float v) {
 // from the lane that the gfx9 DPP control CTRL names.
 template <int CTRL>
 __device__ __forceinline__ float dpp_sel(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  // every control used here reads a lane of the same row, so no lane takes the
+  // bound value (bound_ctrl set: no register to preload)
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_sel_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
 constexpr int DPP_QUAD_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;       // quad_perm [2,3,0,1]

@@ -55,6 +55,29 @@ __device__ __forceinline__ float wave_max_fast(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Upper bounds of the wave-wide maxima of two non-negative floats, reduced
+// together: each is cut to its top 16 bits rounded up (at most 2^-8 above the
+// value, same or next binade), so both ride one DPP chain as u16 pairs.  NaN
+// and overflowing inputs come back as the largest finite bound.
+__device__ __forceinline__ void wave_max2_bound(float& x, float& y) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t hx = min(__float_as_uint(x) >> 16, 0x7F7Eu) + 1u;
+  const uint32_t hy = min(__float_as_uint(y) >> 16, 0x7F7Eu) + 1u;
+  u16x2 p = __builtin_bit_cast(u16x2, hx | (hy << 16));
+  p = __builtin_elementwise_max(p, __builtin_bit_cast(u16x2, dpp_sel_u<DPP_QUAD_XOR1>(__builtin_bit_cast(uint32_t, p))));
+  p = __builtin_elementwise_max(p, __builtin_bit_cast(u16x2, dpp_sel_u<DPP_QUAD_XOR2>(__builtin_bit_cast(uint32_t, p))));
+  p = __builtin_elementwise_max(p, __builtin_bit_cast(u16x2, dpp_sel_u<DPP_ROW_HALF_MIRROR>(__builtin_bit_cast(uint32_t, p))));
+  p = __builtin_elementwise_max(p, __builtin_bit_cast(u16x2, dpp_sel_u<DPP_ROW_MIRROR>(__builtin_bit_cast(uint32_t, p))));
+  const uint32_t b = __builtin_bit_cast(uint32_t, p);
+  u16x2 r = __builtin_bit_cast(u16x2, (uint32_t)__builtin_amdgcn_readlane((int)b, 0));
+  r = __builtin_elementwise_max(r, __builtin_bit_cast(u16x2, (uint32_t)__builtin_amdgcn_readlane((int)b, 16)));
+  r = __builtin_elementwise_max(r, __builtin_bit_cast(u16x2, (uint32_t)__builtin_amdgcn_readlane((int)b, 32)));
+  r = __builtin_elementwise_max(r, __builtin_bit_cast(u16x2, (uint32_t)__builtin_amdgcn_readlane((int)b, 48)));
+  const uint32_t rb = __builtin_bit_cast(uint32_t, r);
+  x = __uint_as_float(rb << 16);
+  y = __uint_as_float(rb & 0xFFFF0000u);
+}
+
 // Workspace record of one (batch, q-head, split): acc[D], m, l (fp32).
 template <int D>
 __device__ __forceinline__ float* ws_record(const mz_decode_args& a, int b, int qh, int split, int n_split) {

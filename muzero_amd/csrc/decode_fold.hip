@@ -438,9 +438,79 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   int kacc = 0;  // acc holds sum p * x * 2^kacc
   bool kacc_init = false;
 
+  // ---------------- per-tile scalars, computed for the NEXT tile in 8 chunks
+  // that ride along the current tile's 8 P.V steps (their division, DPP and
+  // LDS latencies then hide behind the lookups and MFMAs).  They write the
+  // next tile's Q.K operands (AHI, ALO, QA), zero levels (KZP, VZP) and value
+  // scalars (VBP, VA): the current tile read its own before its P.V began.
+  struct ScalState {
+    GroupScalars k0, k1, v0, v1;
+    float kmx, vmx;
+    uint32_t ka;
+  } sc;
+  float unscale_n = a.scaling;  // next tile's logit factor: scaling * 2^-kexp
+  int kvexp_n = 0;              // next tile's value exponent
+  auto scal_chunk = [&](const MetaWords<MW>& Mw, const int chunk) __attribute__((always_inline)) {
+    constexpr int HPC = (NREP + 3) / 4;  // heads per chunk 4..7
+    if (chunk == 0) {
+      // key group scalars (lane: channels 2*lane, 2*lane+1)
+      const float2 kmn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), ksc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
+      sc.k0 = group_scalars<F::QMAX>(kmn.x, ksc.x);
+      sc.k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
+      sc.kmx = fmaxf(fmaxf(fabsf(sc.k0.a), fmaxf(sc.k0.bp, -sc.k0.bn)),
+                     fmaxf(fabsf(sc.k1.a), fmaxf(sc.k1.bp, -sc.k1.bn)));
+      // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
+      *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
+          (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
+    } else if (chunk == 1) {
+      // value group scalars (lane: token lane, both value groups)
+      const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
+      sc.v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
+      sc.v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
+      sc.vmx = fmaxf(fmaxf(fabsf(sc.v0.a), fmaxf(sc.v0.bp, -sc.v0.bn)),
+                     fmaxf(fabsf(sc.v1.a), fmaxf(sc.v1.bp, -sc.v1.bn)));
+      // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
+      const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
+      W[S::VZP + vzo] = (uint8_t)sc.v0.zl;
+      W[S::VZP + 64 + vzo] = (uint8_t)sc.v1.zl;
+    } else if (chunk == 2) {
+      // power-of-two scales keeping the fp16 operands in range (one reduction for both)
+      wave_max2_bound(sc.kmx, sc.vmx);
+      const int kexp = min(range_exp(sc.kmx * fmaxf(qabs, 1.f)), range_exp(sc.kmx));
+      unscale_n = ldexpf(a.scaling, -kexp);
+      sc.k0.bp = ldexpf(sc.k0.bp, kexp), sc.k0.bn = ldexpf(sc.k0.bn, kexp);
+      sc.k1.bp = ldexpf(sc.k1.bp, kexp), sc.k1.bn = ldexpf(sc.k1.bn, kexp);
+      sc.ka = pack_h2(ldexpf(sc.k0.a, kexp), ldexpf(sc.k1.a, kexp));
+      kvexp_n = range_exp(sc.vmx);
+    } else if (chunk == 3) {
+      // keep the accumulators' exponent unless the tile needs a smaller one
+      kvexp_n = min(kacc_init ? kacc : 60, kvexp_n);
+      ((uint32_t*)(W + S::VBP))[lane] = pack_h2(ldexpf(sc.v0.bp, kvexp_n), ldexpf(sc.v0.bn, kvexp_n));
+      ((uint32_t*)(W + S::VBP))[TILE + lane] = pack_h2(ldexpf(sc.v1.bp, kvexp_n), ldexpf(sc.v1.bn, kvexp_n));
+      ((uint16_t*)(W + S::VA))[lane] = f2h(ldexpf(sc.v0.a, kvexp_n));
+      ((uint16_t*)(W + S::VA))[TILE + lane] = f2h(ldexpf(sc.v1.a, kvexp_n));
+    } else {
+      // key-side products of heads HPC*(chunk-4) ...: q*bp, q*bn as fp16 hi + lo, and q*a
+#pragma unroll
+      for (int hh = 0; hh < HPC; ++hh) {
+        const int h = HPC * (chunk - 4) + hh;
+        if (h < NREP) {
+          const uint32_t q01 = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
+          const h2 qh = __builtin_bit_cast(h2, q01);
+          const uint2 p0 = split_product(qh.x, sc.k0.bp, sc.k0.bn);
+          const uint2 p1_ = split_product(qh.y, sc.k1.bp, sc.k1.bn);
+          *(uint2*)(W + S::AHI + (h * AROW + 2 * lane) * 4) = uint2{p0.x, p1_.x};
+          *(uint2*)(W + S::ALO + (h * AROW + 2 * lane) * 4) = uint2{p0.y, p1_.y};
+          *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, sc.ka);
+        }
+      }
+    }
+  };
+
   // one tile.  Loads in flight: this tile's value words (issued here, used by
-  // its P.V), the next tile tn's metadata (issued here, used by its scalars)
-  // and the next tile's key words (issued after this tile's Q.K).
+  // its P.V), the next tile tn's metadata (issued here, used by the scalars
+  // computed during this tile's P.V) and the next tile's key words (issued
+  // after this tile's Q.K).
   auto process = [&](const int tile, const int tn) {
     const int tl = min(tn, q_last);
     load_vw<BITS>(VW, bf, min(tile, q_last), lane);
@@ -458,50 +528,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     }
 
     f32x4 s[4];
-    int kv_exp = 0;
-    float unscale = a.scaling;
+    int kv_exp = kvexp_n;
+    float unscale = unscale_n;
     if (quant) {
-      // ---------- key group scalars (lane: channels 2*lane, 2*lane+1)
-      const float2 kmn = meta_cvt<MW>(MT.kmn, a.meta_dtype), ksc = meta_cvt<MW>(MT.ksc, a.meta_dtype);
-      const GroupScalars k0 = group_scalars<F::QMAX>(kmn.x, ksc.x);
-      const GroupScalars k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
-      float kmx = fmaxf(fmaxf(fabsf(k0.a), fmaxf(k0.bp, -k0.bn)), fmaxf(fabsf(k1.a), fmaxf(k1.bp, -k1.bn)));
-      kmx = wave_max_fast(kmx);
-      const int kexp = min(range_exp(kmx * fmaxf(qabs, 1.f)), range_exp(kmx));
-      unscale = ldexpf(a.scaling, -kexp);
-      const float bp0 = ldexpf(k0.bp, kexp), bn0 = ldexpf(k0.bn, kexp);
-      const float bp1 = ldexpf(k1.bp, kexp), bn1 = ldexpf(k1.bn, kexp);
-      const uint32_t ka = pack_h2(ldexpf(k0.a, kexp), ldexpf(k1.a, kexp));
-      // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
-      *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
-          (uint16_t)(k0.zl | (k1.zl << 8));
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const uint32_t q01 = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
-        const h2 qh = __builtin_bit_cast(h2, q01);
-        const uint2 p0 = split_product(qh.x, bp0, bn0);
-        const uint2 p1_ = split_product(qh.y, bp1, bn1);
-        *(uint2*)(W + S::AHI + (h * AROW + 2 * lane) * 4) = uint2{p0.x, p1_.x};
-        *(uint2*)(W + S::ALO + (h * AROW + 2 * lane) * 4) = uint2{p0.y, p1_.y};
-        *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, ka);
-      }
-      // ---------- value scalars (lane: token lane, both value groups)
-      const float2 vmn = meta_cvt<MW>(MT.vmn, a.meta_dtype), vsc = meta_cvt<MW>(MT.vsc, a.meta_dtype);
-      const GroupScalars v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
-      const GroupScalars v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
-      const float vmx = fmaxf(fmaxf(fabsf(v0.a), fmaxf(v0.bp, -v0.bn)), fmaxf(fabsf(v1.a), fmaxf(v1.bp, -v1.bn)));
-      // keep the accumulators' exponent unless this tile needs a smaller one
-      kv_exp = min(kacc_init ? kacc : 60, range_exp(wave_max_fast(vmx)));
-      // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
-      const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
-      W[S::VZP + vzo] = (uint8_t)v0.zl;
-      W[S::VZP + 64 + vzo] = (uint8_t)v1.zl;
-      ((uint32_t*)(W + S::VBP))[lane] = pack_h2(ldexpf(v0.bp, kv_exp), ldexpf(v0.bn, kv_exp));
-      ((uint32_t*)(W + S::VBP))[TILE + lane] = pack_h2(ldexpf(v1.bp, kv_exp), ldexpf(v1.bn, kv_exp));
-      ((uint16_t*)(W + S::VA))[lane] = f2h(ldexpf(v0.a, kv_exp));
-      ((uint16_t*)(W + S::VA))[TILE + lane] = f2h(ldexpf(v1.a, kv_exp));
-      wave_lds_sync();
-
+      wave_lds_sync();  // this tile's scalars were written by other lanes
       // ---------- S = Q K^T: constant part (ones operand), then the folded codes
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -541,6 +571,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       // (p * 2^kv_exp, 0), so the accumulators keep their exponent (at most
       // 15: p * 2^15 stays finite in fp16) whatever the tile order
       kv_exp = min(kacc_init ? kacc : 15, 15);
+      unscale = a.scaling;
       const uint32_t unit_h = (uint32_t)f2h(ldexpf(1.f, kv_exp));
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) {
@@ -663,6 +694,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
           An = *(const u32x4*)(pa + (vg1 * NREP + hA) * LROW + 16 * kt1 + 4 * g);
           lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, Bn);
         }
+        scal_chunk(MN, st);  // the next tile's scalars, chunk st
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], acc[vg][jt]);
         __builtin_amdgcn_sched_barrier(0);
@@ -714,9 +746,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
           }
         }
       }
+    #pragma unroll
+      for (int c = 0; c < 8; ++c) scal_chunk(MN, c);  // the next tile's scalars
     }
     wave_lds_sync();
-    MT = MN;
   };
 
   // tiles of this wave: tile0, tile0 + 4, ...
@@ -728,6 +761,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   // CU and then a second one, so the younger workgroup of a CU (linear index
   // >= `cus`) starts one level higher.  The tile assignment itself is fixed:
   // results do not depend on timing.
+#pragma unroll
+  for (int c = 0; c < 8; ++c) scal_chunk(MT, c);  // the first tile's scalars
   const int n_mine = (n_virt - v0 + WAVES - 1) / WAVES;
   const int wg_lin = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
   const int older = wg_lin < cus ? 1 : 0;  // the first workgroup of its CU: one level lower
