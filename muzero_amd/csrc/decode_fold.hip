@@ -64,8 +64,22 @@ template <int BITS>
 struct Fmt {
   static constexpr int QMAX = (1 << BITS) - 1;
   static constexpr int QB = 8 * BITS;  // bytes per packed 64-code row
-  static constexpr int LB = BITS / 2;  // bytes per lane per row (its 4 codes)
 };
+
+// Lanes 2m and 2m+1 of a lane group need the codes of tokens 8m..8m+7 of a
+// row: 8*BITS bits starting at byte BITS*m.  The pair's word (1-bit: a byte,
+// 2-bit: 16 bits, 4-bit: 32 bits, 3-bit: a dword read unaligned, the last
+// pair's moved back inside the row) starts at pair_byte(m); pair_shift(n) is
+// the bit offset of lane n's own 4 codes in it.
+template <int BITS>
+__device__ __forceinline__ int pair_byte(int m) {
+  return BITS == 3 ? min(3 * m, 3 * 8 - 4) : BITS * m;
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t pair_shift(int n) {
+  const int m = n >> 1;
+  return (uint32_t)(8 * (BITS * m - pair_byte<BITS>(m)) + 4 * BITS * (n & 1));
+}
 
 // Padded row lengths (in 4-byte words) of the [head][...] arrays so that the
 // rows read together by lanes of different heads start in different banks.
@@ -199,8 +213,9 @@ __device__ __forceinline__ void load_meta(uint32_t (&w)[MW], const __amdgpu_buff
 
 template <int BITS>
 __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int imm) {
-  if constexpr (BITS == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, voff + imm, soff, 0);
-  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff + imm, soff, 0);
+  if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff + imm, soff, 0);
+  else if constexpr (BITS == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff + imm, soff, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff + imm, soff, 0);
 }
 
 // All metadata of a tile (loaded one tile ahead of its use).
@@ -221,7 +236,7 @@ template <int BITS>
 __device__ __forceinline__ void load_kw(uint32_t (&kw)[16], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const int voff = (4 * g + (n & 1)) * F::QB + 2 * F::LB * (n >> 1);
+  const int voff = (4 * g + (n & 1)) * F::QB + pair_byte<BITS>(n >> 1);
   const int soff = tile * D * F::QB;
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
@@ -235,7 +250,7 @@ template <int BITS>
 __device__ __forceinline__ void load_vw(uint32_t (&vw)[16], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + 2 * F::LB * (n >> 1);
+  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + pair_byte<BITS>(n >> 1);
   const int soff = tile * TILE * NG * F::QB;
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
@@ -260,8 +275,39 @@ __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
 // `odd` = lane n is odd.
 template <int BITS, int TBASE>
 __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, uint32_t w1, uint32_t zp,
-                                             uint32_t grep, bool odd, u32x4 B[4]) {
-  if constexpr (BITS == 4) {
+                                             uint32_t grep, bool odd, uint32_t sh, u32x4 B[4]) {
+  if constexpr (BITS == 3) {
+    // w0 / w1: the pair's dword of rows (0 | 1) / (2 | 3); after the swap the
+    // lane holds all four rows and takes its 12 bits (4 codes) from each at
+    // bit sh, spread to bytes as table offsets 4*q + 64*group
+    const uint32_t s0 = dpp_swap_pairs(w0), s1 = dpp_swap_pairs(w1);
+    const uint32_t r[4] = {odd ? s0 : w0, odd ? w0 : s0, odd ? s1 : w1, odd ? w1 : s1};
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      uint32_t e = grep;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) e |= __builtin_amdgcn_ubfe(r[ii], sh + 3 * jt, 3) << (8 * jt + 2);
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
+                                       __builtin_amdgcn_perm(zp, e, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | jt));
+    }
+  } else if constexpr (BITS == 1) {
+    // w0 / w1: byte m of rows (0 | 1) / (2 | 3) (even / odd lane); gather the
+    // byte of rows 0..3 into one word, then this lane's nibble (bit jt = code
+    // jt) of each byte
+    const uint32_t own = w0 | (w1 << 16);
+    const uint32_t w = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, odd ? 0x02060004u : 0x06020400u);
+    const uint32_t w4 = sh ? (w >> (sh - 2)) : (w << 2);  // byte ii: the nibble's code jt at bit 2 + jt
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const uint32_t ej = ((w4 >> jt) & 0x04040404u) | grep;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
+                                       __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii));
+    }
+  } else if constexpr (BITS == 4) {
     // w0 / w1: rows (0,1) / (2,3) of the pair, 32 bits = codes of lanes 2m, 2m+1;
     // this lane keeps 16 bits of each row: low half = row 2p, high half = row 2p+1
     const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
@@ -317,6 +363,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   const int n = lane & 15;
   const int g = lane >> 4;
   const bool odd = (n & 1) != 0;
+  const uint32_t lsh = pair_shift<BITS>(n);  // bit offset of this lane's codes in its pair's word
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
@@ -547,14 +594,14 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       const u32x4 kz1 = *(const u32x4*)(W + S::KZP + g * 32 + 16);
       u32x4 Ac = *(const u32x4*)(a_hi_row + (4 * g) * 4);
       u32x4 Bc[4], Bn[4];
-      lookup_ktile<BITS, S::TBL_K>(smem, KW[0], KW[1], kz0[0], grep, odd, Bc);
+      lookup_ktile<BITS, S::TBL_K>(smem, KW[0], KW[1], kz0[0], grep, odd, lsh, Bc);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         u32x4 An;
         if (kt < 7) {
           An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
           lookup_ktile<BITS, S::TBL_K>(smem, KW[2 * kt + 2], KW[2 * kt + 3], kt + 1 < 4 ? kz0[kt + 1] : kz1[kt - 3],
-                                       grep, odd, Bn);
+                                       grep, odd, lsh, Bn);
         }
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], s[jt]);
@@ -684,7 +731,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       for (int vg = 0; vg < NG; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
       u32x4 Ac = *(const u32x4*)(pa + hA * LROW + 4 * g);
       u32x4 Bc[4], Bn[4];
-      lookup_ktile<BITS, S::TBL_V>(smem, VW[0], VW[1], vz[0][0], grep, odd, Bc);
+      lookup_ktile<BITS, S::TBL_V>(smem, VW[0], VW[1], vz[0][0], grep, odd, lsh, Bc);
 #pragma unroll
       for (int st = 0; st < 4 * NG; ++st) {
         const int kt = st / NG, vg = st % NG;
@@ -692,7 +739,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
         if (st + 1 < 4 * NG) {
           const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
           An = *(const u32x4*)(pa + (vg1 * NREP + hA) * LROW + 16 * kt1 + 4 * g);
-          lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, Bn);
+          lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, lsh, Bn);
         }
         scal_chunk(MN, st);  // the next tile's scalars, chunk st
 #pragma unroll
@@ -865,7 +912,7 @@ bool fold_supported(const mz_decode_args* a) {
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
-  return (a->bits == 4 || a->bits == 2) && a->head_dim == 128 && a->n_groups > 0 && fits &&
+  return a->bits >= 1 && a->bits <= 4 && a->head_dim == 128 && a->n_groups > 0 && fits &&
          (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
          ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&
@@ -929,7 +976,9 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   }
 #define MZ_FOLD_BITS(IOV)                              \
   if (a->bits == 4) { MZ_FOLD_NREP(IOV, 4) }           \
+  else if (a->bits == 3) { MZ_FOLD_NREP(IOV, 3) }      \
   else if (a->bits == 2) { MZ_FOLD_NREP(IOV, 2) }      \
+  else if (a->bits == 1) { MZ_FOLD_NREP(IOV, 1) }      \
   else return MZ_EUNSUPPORTED;
   if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
 #undef MZ_FOLD_BITS

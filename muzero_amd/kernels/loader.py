@@ -240,7 +240,7 @@ class DecodePlan:
         ev = tables.device_table("expm1", alpha_value, dev)
         a.e_key, a.e_value = ptr(ek), ptr(ev)
         keep += [ek, ev]
-        if int(bits) in (2, 4):
+        if 1 <= int(bits) <= 4:
             fk = tables.device_table(f"fold{int(bits)}", alpha_key, dev)
             fv = tables.device_table(f"fold{int(bits)}", alpha_value, dev)
             a.fold_k, a.fold_v = ptr(fk), ptr(fv)

@@ -174,8 +174,8 @@ def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> tor
                 t = _build_expm1(alpha)
             elif kind == "fold4":
                 t = _build_fold(alpha, 4)
-            elif kind == "fold2":
-                t = _build_fold(alpha, 2)
+            elif kind in ("fold1", "fold2", "fold3"):
+                t = _build_fold(alpha, int(kind[-1]))
             else:
                 raise ValueError(kind)
             _host_cache[key] = t

@@ -48,7 +48,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         if B > 1:
             am[1, ..., 5:9] = torch.finfo(dtype).min
     lq0 = ref.split_prefix(length, residual, 64)
-    fold = (kernel_path == "fold" or (kernel_path == "auto" and bits in (2, 4) and d == 128
+    fold = (kernel_path == "fold" or (kernel_path == "auto" and 1 <= bits <= 4 and d == 128
                                       and n_rep in (1, 2, 4, 8) and lq0 > 0))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
@@ -150,24 +150,34 @@ FOLD_CASES = [
     (1, 2, 4, 128, 4096, 2, 128),
     (2, 1, 4, 128, 300, 2, 0),
     (1, 2, 4, 128, 900, 2, 191),
+    (2, 2, 4, 128, 1024, 3, 128),
+    (1, 2, 1, 128, 700, 3, 128),
+    (1, 1, 8, 128, 700, 3, 128),
+    (1, 2, 4, 128, 4096, 3, 128),
+    (1, 2, 4, 128, 900, 3, 191),
+    (2, 2, 4, 128, 1024, 1, 128),
+    (1, 2, 2, 128, 700, 1, 128),
+    (1, 1, 8, 128, 700, 1, 128),
+    (1, 2, 4, 128, 4096, 1, 128),
+    (2, 1, 4, 128, 300, 1, 0),
 ]
 
 
 @pytest.mark.parametrize("path", ["fold", "exact"])
 @pytest.mark.parametrize("case", FOLD_CASES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_b{}_R{}".format(*c))
-def test_decode_4bit_paths(case, path):
+def test_decode_fold_and_exact_paths(case, path):
     mx, mean, _, _ = _run_case(*case, kernel_path=path)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 @pytest.mark.parametrize("n_split", [1, 3, 16])
 def test_fold_split_and_mask(n_split, bits):
     mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 def test_fold_fp16_io_and_meta(bits):
     for dtype, meta in ((torch.float16, torch.float16), (torch.bfloat16, torch.float32),
                         (torch.bfloat16, torch.bfloat16)):
@@ -175,21 +185,21 @@ def test_fold_fp16_io_and_meta(bits):
         assert mx < MAX_ABS and mean < MEAN_ABS, (dtype, meta, mx, mean)
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 def test_fold_large_magnitudes(bits):
     """Key groups with spans ~1e3 and queries ~30 exercise the per-group fp16 range scaling."""
     mx, mean, _, exact = _run_case(1, 2, 4, 128, 640, bits, 128, outliers=8, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 def test_fold_alpha_per_kind(bits):
     """Different key / value alphas select different (P, N) tables."""
     mx, mean, _, _ = _run_case(1, 2, 4, 128, 800, bits, 128, alpha_k=16.0, alpha_v=4.0, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 def test_single_split_direct_output_matches_two_kernel_path(bits):
     """With one split the fold kernel writes the output itself; the result is bit-identical to
     the workspace + combine path (same operations in the same order)."""

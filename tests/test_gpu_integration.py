@@ -44,7 +44,7 @@ def test_cache_layer_matches_oracle_cache(bits, dtype, meta):
     cfg = mz.MuZeroConfig(bits=bits, amax_dtype=meta, alpha_key=2.0, alpha_value=2.0)
     layer = MuZeroCacheLayer(cfg)
     _feed(layer, k, v, prefill)
-    fold = bits in (2, 4)  # the fold kernel (fp32 dequantized values) serves 4- and 2-bit
+    fold = 1 <= bits <= 4  # the fold kernel (fp32 dequantized values) serves 1- to 4-bit
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
                                      amax_dtype=getattr(torch, meta),
                                      dequant_dtype=torch.float32 if fold else None)

@@ -70,7 +70,7 @@ def test_expm1_table_alpha2_closed_form():
         assert e[off].item() == 0.0 and e[off + n].item() == 1.0
 
 
-@pytest.mark.parametrize("bits", [4, 2])
+@pytest.mark.parametrize("bits", [4, 3, 2, 1])
 def test_fold_table_entries(bits):
     qmax = (1 << bits) - 1
     for alpha in (2.0, 4.0):
