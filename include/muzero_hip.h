@@ -131,10 +131,10 @@ typedef struct mz_decode_args {
   const void* v_res; int64_t vr_sb, vr_sh, vr_st;
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
-  /* (P, N) fold tables for alpha_key / alpha_value (bits 4 and 2): 16 x 16
+  /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 4): 16 x 16
    * pairs of fp16 (P, N) packed in uint32 (P in the low half), row = zero
    * level, column = code, zero beyond 2^bits - 1; see muzero_amd/tables.py
-   * ("fold4", "fold2").  Needed by the fold fast path; may be null (the
+   * ("fold1" .. "fold4").  Needed by the fold fast path; may be null (the
    * generic path is used then). */
   const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
@@ -144,7 +144,7 @@ typedef struct mz_decode_args {
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 4 or 2, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
+ * applies (bits 1 to 4, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
  * and the exact-dequantize kernel otherwise. */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 
