@@ -1,4 +1,4 @@
-// Packed-KV decode attention, fast path for 4-bit and 2-bit codes (gfx950, wave64).
+// Packed-KV decode attention, fast path for 1- to 4-bit codes (gfx950, wave64).
 //
 // Dequantization folded into the MFMA operands.  For a group with stored
 // (mn, s) the reference dequantizes code q as (muzero/quantizer.py:241-255)
@@ -19,28 +19,31 @@
 // Work of one wave: a 64-token tile = one key group (or 64 residual tokens).
 //   QK: MFMA columns = tokens 4n+jt of N-tiles jt = 0..3; lane (n, g) of
 //   k-tile kt holds channels 16kt+4g+{0..3} and needs, for each, the 4 codes
-//   of its tokens 4n..4n+3 (16 bits of the channel's row at 4 bits, 8 at 2).
+//   of its tokens 4n..4n+3 (4*BITS bits of the channel's row).
 //   PV: columns = channels 64vg+4n+jt, k = (token, side); lane (n, g) needs
 //   the codes of channels 4n..4n+3 of tokens 16kt+4g+{0..3}.
 //   Lane pairs load the rows' shared words straight from HBM (buffer loads,
-//   the tile offset in a scalar register) and swap halves with one DPP move.
+//   the tile offset in a scalar register) and swap them with one DPP move.
 //   MFMA rows = query heads of the kv-head, spread to rows h*16/NREP: every
 //   lane group of the MFMA output then holds real logits, so the softmax
 //   runs in registers (row reductions on DPP) with no LDS round trip.
 // Each code is one conflict-free ds_read_b32 from a per-lane-group copy of
-// the (P, N) table in LDS, addressed with about 1.5 VALU ops per code, read
-// straight into the MFMA B register.  The key-side products q*bp, q*bn are
-// formed once per (head, channel) per tile as fp16 hi + lo pairs, on two
-// rows of the same MFMA (fp32 accuracy at no extra MFMA); the PV operands
-// p*bp, p*bn, p*a are formed once per (head, token) by the softmax.  The next tile's code words and
-// metadata are loaded while the current tile is computed.  fp16 operands
-// are kept in range by a power-of-two scale per key group and per value
-// tile, folded into the logits and into the online-softmax rescale.
+// the (P, N) table in LDS, addressed by one v_perm (plus about 0.75 VALU ops
+// of code extraction), read straight into the MFMA B register; the lookups of
+// the next k-tile are issued before the MFMAs of the current one.  The
+// key-side products q*bp, q*bn are formed per (head, channel) per tile as
+// fp16 hi + lo pairs, on two rows of the same MFMA (fp32 accuracy at no extra
+// MFMA); the PV operands p*bp, p*bn, p*a are formed per (head, token) by the
+// softmax.  A tile's group scalars are computed during the previous tile's
+// P.V, in chunks between its MFMA steps.  fp16 operands are kept in range by
+// a power-of-two scale per key group and an accumulator exponent for the
+// values, folded into the logits and into the online-softmax rescale.
 //
 // Launch: one workgroup of 4 waves per (batch, kv-head, split); a split is a
-// run of tiles, waves take every 4th tile; the split's (m, l, acc) goes to the
-// workspace and the shared combine kernel merges splits.  With a single split
-// (the grid already fills the GPU) the kernel writes the output itself.
+// run of tiles (residual tiles first), waves take every 4th; the split's
+// (m, l, acc) goes to the workspace and the shared combine kernel merges
+// splits.  With a single split (the grid already fills the GPU) the kernel
+// writes the output itself.
 #include "decode_common.hpp"
 
 namespace mz {
