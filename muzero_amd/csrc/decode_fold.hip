@@ -838,6 +838,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   // lane-derived indices recomputed from the lane id (mbcnt) instead of kept
   // live across the tile loop, where every register is taken
   const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int tid_e = wave * 64 + lane_e;  // threadIdx.x, recomputed for the same reason
   const int n_e = lane_e & 15, g_e = lane_e >> 4;
   if (((4 * g_e) % RS) == 0) {
     const int h0 = (4 * g_e) / RS, n = n_e;
@@ -860,7 +861,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   __syncthreads();
   if (direct) {
     // one split: the final output, exactly as the combine kernel would form it
-    for (int e = threadIdx.x; e < NREP * D; e += NT) {
+    for (int e = tid_e; e < NREP * D; e += NT) {
       const int h = e / D;
       const int c = e - h * D;
       float M_ = -INFINITY;
@@ -880,7 +881,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     }
     return;
   }
-  for (int e = threadIdx.x; e < NREP * (D + 2); e += NT) {
+  for (int e = tid_e; e < NREP * (D + 2); e += NT) {
     const int h = e / (D + 2);
     const int c = e - h * (D + 2);
     float M_ = -INFINITY;
