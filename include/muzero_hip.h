@@ -141,6 +141,11 @@ typedef struct mz_decode_args {
   void* workspace; int64_t workspace_bytes;
   int n_split;      /* 0 = let the library choose */
   int kernel_path;  /* MZ_PATH_AUTO, or force MZ_PATH_EXACT / MZ_PATH_FOLD */
+  /* The compander alphas the expm1 tables were built for.  The general
+   * kernel evaluates the 7- and 8-bit expm1 rows from them (those rows do not
+   * fit in LDS); they must be > 0 when bits >= 7 and there is a quantized
+   * prefix, and are not read otherwise. */
+  float alpha_key, alpha_value;
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it

@@ -51,6 +51,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_vp), ("workspace_bytes", c_i64),
         ("n_split", c_int),
         ("kernel_path", c_int),
+        ("alpha_key", c_float), ("alpha_value", c_float),
     ]
 
 MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2

@@ -1,4 +1,5 @@
-// Packed-KV decode attention (gfx950, wave64, MFMA 16x16x32).
+// Packed-KV decode attention, general path (gfx950, wave64, MFMA 16x16x32):
+// every bit width 1-8, head_dim 64 or 128, up to 16 query heads per kv-head.
 //
 // Work decomposition: one workgroup (4 waves) per (batch, kv-head, token
 // split).  A split is a run of 64-token tiles: first the quantized prefix
@@ -10,13 +11,26 @@
 // the splits with a log-sum-exp merge.  No float atomics: results are
 // deterministic.
 //
-// Per tile:
-//   K tile -> LDS [64 tokens][D] in the io dtype (dequantized exactly as the
-//   reference's _dequantize_rows_torch and rounded to the layer dtype, or
-//   copied from the residual), QK^T with MFMA (A = Q rows, B = K tile),
-//   online softmax on the MFMA accumulator layout, P -> LDS in fp16,
-//   V tile -> LDS [D][64] in fp16 (transposed so an MFMA B operand is 8
-//   consecutive tokens of one channel), acc += P V with an fp16 MFMA.
+// Per tile, through one per-wave LDS staging buffer:
+//   K in chunks of 32 tokens (head_dim 64: one chunk of 64) -> [token][D] in
+//   the io dtype, dequantized like the reference's _dequantize_rows_torch and
+//   rounded to the layer dtype; QK^T with MFMA (A = Q rows, B = the chunk);
+//   online softmax on the MFMA accumulator layout, P -> LDS in fp16;
+//   V in chunks of 64 channels (one value group) -> [channel][64 tokens] in
+//   fp16 (an MFMA B operand is 8 consecutive tokens of one channel), then
+//   acc += P V.
+// Dequantization runs in registers, two codes per lane per LDS store: a lane
+// owns two adjacent channels of a K chunk (two key groups) or two adjacent
+// tokens of a V chunk (two value groups), so a group's parameters are formed
+// once per tile and each code costs one table read and a few branch-free ops.
+// Codes of up to 6 bits read the reference's fp32 expm1 rows from LDS and
+// reproduce its dequantized value bit for bit before the rounding; the 7- and
+// 8-bit rows (32 KB and 128 KB per alpha) do not fit next to the staging
+// buffers, so those widths evaluate expm1 with the hardware exp2 (a few fp32
+// ulp from the reference's value before the same rounding to the layer dtype).
+// A tile's packed words are loaded one tile ahead: the next tile's key words
+// are issued as soon as this tile's keys are staged, its value words as soon
+// as this tile's values are.
 // P V runs in fp16 whatever the io dtype: weights keep 11 mantissa bits (bf16
 // weights cost up to 2^-9 relative each, too coarse for peaked softmax rows),
 // and every bf16 value in fp16's normal range converts to fp16 exactly.  The
@@ -31,28 +45,130 @@ constexpr int kPad = 8;  // halfwords of padding per LDS row
 
 template <int D>
 struct Lds {
-  static constexpr int K_LD = D + kPad;       // K tile row: one token
-  static constexpr int V_LD = kTile + kPad;   // V tile row: one channel
-  static constexpr int KV_HALVES = (kTile * K_LD > D * V_LD) ? kTile * K_LD : D * V_LD;
+  static constexpr int KT = D == 128 ? 32 : 64;  // tokens per K chunk
+  static constexpr int KCH = kTile / KT;         // K chunks per tile
+  static constexpr int NG = D / 64;              // V chunks (value groups) per tile
+  static constexpr int K_LD = D + kPad;          // K chunk row: one token
+  static constexpr int V_LD = kTile + kPad;      // V chunk row: one channel
+  static constexpr int STAGE = (KT * K_LD > 64 * V_LD) ? KT * K_LD : 64 * V_LD;
   static constexpr int P_LD = kTile + kPad;
   static constexpr int P_HALVES = 16 * P_LD;
-  static constexpr int WAVE_HALVES = KV_HALVES + P_HALVES;
-  static constexpr int E_FLOATS = 528;  // expm1 table rows for bins <= 31 (bits <= 5)
-  static constexpr size_t BYTES = (size_t)kWaves * WAVE_HALVES * 2 + 2 * E_FLOATS * 4;
+  static constexpr int WAVE_HALVES = STAGE + P_HALVES;
+  static constexpr int RED_FLOATS = 32 + 16 * D;  // per wave at the end (aliases the wave areas)
+  static constexpr int WAVES_BYTES =
+      kWaves * WAVE_HALVES * 2 > kWaves * RED_FLOATS * 4 ? kWaves * WAVE_HALVES * 2 : kWaves * RED_FLOATS * 4;
+  // expm1 rows for bins 1..qmax (codes of up to 6 bits), one table per alpha
+  static constexpr int e_floats(int bits) { return bits <= 6 ? ((1 << bits) - 1) * ((1 << bits) + 2) / 2 : 0; }
+  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 2 * (size_t)e_floats(bits) * 4; }
 };
 
+// One group's dequantization parameters (muzero/quantizer.py:241-255, from the
+// stored metadata, scale guarded as in loader.py:201).
+struct DeqG {
+  float za, s, mn, pe, mne;  // mne = -ne
+  float cp, cn;              // 7/8 bits: log2(1 + alpha) / pb, / nb
+  int zl;                    // zero level, an integer in 0..qmax
+  int bp, bn;                // <= 6 bits: byte offset of code q's expm1 entry: q >= zl ? bp + 4q : bn - 4q
+};
+
+template <int BITS>
+__device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const DeqRow r = deq_row(mn, s, qmax, true);
+  DeqG g;
+  g.za = r.za;
+  g.s = r.s;
+  g.mn = r.mn;
+  g.pe = r.pe;
+  g.mne = -r.ne;
+  g.zl = r.zl == r.zl ? (int)r.zl : 0;  // a NaN zero level reads row 1 (pb = nb = 1), never past the table
+  g.bp = 4 * (r.offp - g.zl);
+  g.bn = 4 * (r.offn + g.zl);
+  if constexpr (BITS > 6) {
+    g.cp = lb2 / r.pb;
+    g.cn = lb2 / r.nb;
+  }
+  return g;
+}
+
+// Dequantized fp32 value of code q.  Up to 6 bits this is the reference's
+// value exactly: norm = za + pe*E[pb][q-zl] or za - ne*E[nb][zl-q] (the sign
+// folded into mne is exact), clamped, times s, plus mn, with no contraction.
+template <int BITS>
+__device__ __forceinline__ float deq_code(const DeqG& g, int q, const uint8_t* E, float inv_alpha) {
+  const bool pos = q >= g.zl;
+  float e;
+  if constexpr (BITS <= 6) {
+    e = *(const float*)(E + (pos ? g.bp + 4 * q : g.bn - 4 * q));
+  } else {
+    const int d = pos ? q - g.zl : g.zl - q;
+    e = (__builtin_amdgcn_exp2f((float)d * (pos ? g.cp : g.cn)) - 1.f) * inv_alpha;
+  }
+  const float t = (pos ? g.pe : g.mne) * e;
+  const float norm = __builtin_amdgcn_fmed3f(g.za + t, 0.f, 1.f);
+  return norm * g.s + g.mn;
+}
+
+// Code `idx` of an LSB-first bitstream held in registers (idx is a constant
+// after unrolling, so this is one bit-field extract, or two ops when the code
+// straddles two words).
+template <int BITS>
+__device__ __forceinline__ int code_at(const uint32_t* w, const int idx) {
+  const int bit = idx * BITS, i = bit >> 5, o = bit & 31;
+  constexpr uint32_t mask = (1u << BITS) - 1u;
+  if (o + BITS <= 32) return (int)((w[i] >> o) & mask);
+  return (int)(__builtin_amdgcn_alignbit(w[i + 1], w[i], o) & mask);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two values rounded to the io dtype, packed (first value in the low half).
+template <int IO>
+__device__ __forceinline__ uint32_t pack_io(float x0, float x1) {
+  if constexpr (IO == MZ_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x0, x1}), bf16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{x0, x1}), f16x2_t));
+}
+// Two values rounded to the io dtype, then converted to fp16 (exact for
+// normal-range bf16 values), packed.
+template <int IO>
+__device__ __forceinline__ uint32_t pack_io_f16(float x0, float x1) {
+  if constexpr (IO == MZ_BF16) {
+    const uint32_t b = pack_io<MZ_BF16>(x0, x1);
+    const f32x2_t f{__uint_as_float(b << 16), __uint_as_float(b & 0xFFFF0000u)};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
+  } else {
+    return pack_io<MZ_F16>(x0, x1);
+  }
+}
+// A pair of io-dtype halves converted to fp16.
+template <int IO>
+__device__ __forceinline__ uint32_t io_pair_to_f16(uint16_t h0, uint16_t h1) {
+  if constexpr (IO == MZ_F16) return (uint32_t)h0 | ((uint32_t)h1 << 16);
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{bf2f(h0), bf2f(h1)}), f16x2_t));
+}
+
 template <int D, int BITS, int IO>
-__global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args a, int tiles_per_split, int n_split) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split_kernel(
+    const mz_decode_args a, int tiles_per_split, int n_split) {
   using L = Lds<D>;
   using M = Mfma<IO>;
-  constexpr int QB = 8 * BITS;
-  constexpr int NG = (D + 63) / 64;
-  constexpr float qmax = (float)((1 << BITS) - 1);
-  constexpr bool kLdsE = BITS <= 5;
+  constexpr int QB = 8 * BITS;      // bytes per packed 64-code row
+  constexpr int NG = L::NG;
+  constexpr int KT = L::KT;
+  constexpr int KCH = L::KCH;
+  constexpr int CPW = D / 2;        // K: channel pairs (one per lane, D = 64: two token halves)
+  constexpr int KTPL = D == 128 ? 64 : 32;  // K tokens per lane and tile
+  constexpr int KWR = KTPL * BITS / 32;  // K words per row and lane
+  constexpr int EF = L::e_floats(BITS);
+  constexpr bool kTab = BITS <= 6;
 
   extern __shared__ __align__(16) uint16_t lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
   const int split = blockIdx.x;
@@ -61,23 +177,26 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
   const int n_rep = a.n_rep;
 
   uint16_t* kv = lds + wave * L::WAVE_HALVES;
-  uint16_t* pb = kv + L::KV_HALVES;
-  float* eK = (float*)(lds + kWaves * L::WAVE_HALVES);
-  float* eV = eK + L::E_FLOATS;
-  const float* EK = a.e_key;
-  const float* EV = a.e_value;
-  if constexpr (kLdsE) {
+  uint16_t* pb = kv + L::STAGE;
+  float* eK = (float*)((uint8_t*)lds + L::WAVES_BYTES);
+  float* eV = eK + EF;
+  if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
     if (a.n_groups > 0) {
-      for (int i = threadIdx.x; i < L::E_FLOATS; i += 256) {
+      for (int i = threadIdx.x; i < EF; i += 256) {
         eK[i] = a.e_key[i];
         eV[i] = a.e_value[i];
       }
     }
     __syncthreads();
-    EK = eK;
-    EV = eV;
   }
+  const uint8_t* EKb = (const uint8_t*)eK;
+  const uint8_t* EVb = (const uint8_t*)eV;
+  // 7/8 bits: expm1(d/bins * log1p(alpha)) / alpha = (2^(d * log2(1+alpha)/bins) - 1) / alpha
+  const float lb2k = kTab ? 0.f : __log2f(1.f + a.alpha_key);
+  const float lb2v = kTab ? 0.f : __log2f(1.f + a.alpha_value);
+  const float iak = kTab ? 0.f : 1.f / a.alpha_key;
+  const float iav = kTab ? 0.f : 1.f / a.alpha_value;
 
   // Q rows as the MFMA A operand: lane (m=n, g) holds Q[m][32*ks + 8g .. +7].
   u32x4 qa[D / 32];
@@ -104,57 +223,111 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
   const int t_end = min(n_tiles, t_begin + tiles_per_split);
   const float scale = a.scaling;
 
+  // Lane roles.  K: channels 2cp, 2cp+1, token range ts (D = 64: two halves).
+  // V: tokens 2tp, 2tp+1 of the tile, channels 32cs..32cs+31 of each value group.
+  const int cp = lane % CPW;
+  const int ts = lane / CPW;
+  const int tp = lane & 31;
+  const int cs = lane >> 5;
+  const uint8_t* kbase = a.k_packed + b * a.kp_sb + kvh * a.kp_sh;
+  const uint8_t* vbase = a.v_packed + b * a.vp_sb + kvh * a.vp_sh;
+  const int64_t kmb = b * a.km_sb + kvh * a.km_sh;
+  const int64_t vmb = b * a.vm_sb + kvh * a.vm_sh;
+
+  // packed words and metadata of the tile being staged next (loaded one tile ahead)
+  uint32_t kw[2][KWR];
+  uint32_t vw[NG][2][BITS];
+  float kmeta[2][2], vmeta[NG][2][2];
+  auto load_k = [&](int tile) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t* row = (const uint32_t*)(kbase + ((int64_t)tile * D + 2 * cp + r) * QB) + ts * KWR;
+#pragma unroll
+      for (int i = 0; i < KWR; ++i) kw[r][i] = row[i];
+      const int64_t mi = kmb + (int64_t)tile * D + 2 * cp + r;
+      kmeta[r][0] = meta_load(a.k_mn, mi, a.meta_dtype);
+      kmeta[r][1] = meta_load(a.k_scale, mi, a.meta_dtype);
+    }
+  };
+  auto load_v = [&](int tile) __attribute__((always_inline)) {
+#pragma unroll
+    for (int vg = 0; vg < NG; ++vg)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int64_t tok = (int64_t)tile * kTile + 2 * tp + r;
+        const uint32_t* row = (const uint32_t*)(vbase + (tok * NG + vg) * QB) + cs * BITS;
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) vw[vg][r][i] = row[i];
+        const int64_t mi = vmb + tok * NG + vg;
+        vmeta[vg][r][0] = meta_load(a.v_mn, mi, a.meta_dtype);
+        vmeta[vg][r][1] = meta_load(a.v_scale, mi, a.meta_dtype);
+      }
+  };
+  {
+    const int t0 = t_begin + wave;
+    if (t0 < t_end && t0 < a.n_groups) {
+      load_k(t0);
+      load_v(t0);
+    }
+  }
+
   for (int tile = t_begin + wave; tile < t_end; tile += kWaves) {
     const bool quant = tile < a.n_groups;
     const int r0 = quant ? 0 : (tile - a.n_groups) * kTile;
     const int n_valid = quant ? kTile : min(kTile, a.n_residual - r0);
     const int pos0 = quant ? tile * kTile : a.n_groups * kTile + r0;
+    const int next = tile + kWaves;
+    const bool next_quant = next < t_end && next < a.n_groups;
 
-    // ---------------- K tile -> kv[t * K_LD + c]
-    if (quant) {
-      // lane = channel: the channel's packed row holds its 64 tokens' codes
-#pragma unroll
-      for (int cc = 0; cc < D / 64; ++cc) {
-        const int c = lane + 64 * cc;
-        const int64_t midx = b * a.km_sb + kvh * a.km_sh + (int64_t)tile * D + c;
-        const DeqRow r = deq_row(meta_load(a.k_mn, midx, a.meta_dtype), meta_load(a.k_scale, midx, a.meta_dtype),
-                                 qmax, true);
-        const uint8_t* prow = a.k_packed + b * a.kp_sb + kvh * a.kp_sh + ((int64_t)tile * D + c) * QB;
-        uint32_t w[QB / 4];
-#pragma unroll
-        for (int i = 0; i < QB / 4; ++i) w[i] = ((const uint32_t*)prow)[i];
-        const uint8_t* bytes = (const uint8_t*)w;
-#pragma unroll
-        for (int t = 0; t < kTile; ++t) {
-          const uint32_t q = unpack_code<BITS>(bytes, t);
-          kv[t * L::K_LD + c] = M::cvt(deq_value(r, q, EK));
-        }
-      }
-    } else {
-      // lane = token: copy the residual row
-      const int t = lane;
-      if (t < n_valid) {
-        const uint16_t* src = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh + (int64_t)(r0 + t) * a.kr_st;
-#pragma unroll
-        for (int c = 0; c < D; c += 8) *(u32x4*)(kv + t * L::K_LD + c) = *(const u32x4*)(src + c);
-      } else {
-#pragma unroll
-        for (int c = 0; c < D; c += 8) *(u32x4*)(kv + t * L::K_LD + c) = u32x4{0, 0, 0, 0};
-      }
-    }
-    wave_lds_sync();
-
-    // ---------------- S = Q K^T : lane (n, g) gets heads 4g+i of token 16j+n
+    // ---------------- S = Q K^T, one K chunk at a time: lane (n, g) gets heads 4g+i of token 16j+n
     f32x4 s[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    DeqG gk[2];
+    if (quant) {
 #pragma unroll
-      for (int ks = 0; ks < D / 32; ++ks) {
-        const u32x4 kb = *(const u32x4*)(kv + (16 * j + n) * L::K_LD + 32 * ks + 8 * g);
-        s[j] = M::run(qa[ks], kb, s[j]);
-      }
+      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], lb2k);
     }
+#pragma unroll
+    for (int kc = 0; kc < KCH; ++kc) {
+      if (quant) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int wi = KCH == 2 ? 32 * kc + i : i;  // code index in the lane's words
+          const int row = KCH == 2 ? i : 32 * ts + i;  // token row of the chunk
+          const float x0 = deq_code<BITS>(gk[0], code_at<BITS>(kw[0], wi), EKb, iak);
+          const float x1 = deq_code<BITS>(gk[1], code_at<BITS>(kw[1], wi), EKb, iak);
+          *(uint32_t*)(kv + row * L::K_LD + 2 * cp) = pack_io<IO>(x0, x1);
+        }
+      } else {
+        // residual rows: LPT lanes per token, each copying D / LPT halves (rows past the window are 0)
+        constexpr int LPT = 64 / KT;
+        const int t = lane / LPT, part = lane % LPT;
+        const int tok = KT * kc + t;
+        u32x4* dst = (u32x4*)(kv + t * L::K_LD + part * (D / LPT));
+        if (tok < n_valid) {
+          const uint16_t* src = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh + (int64_t)(r0 + tok) * a.kr_st +
+                                part * (D / LPT);
+#pragma unroll
+          for (int c = 0; c < D / LPT / 8; ++c) dst[c] = ((const u32x4*)src)[c];
+        } else {
+#pragma unroll
+          for (int c = 0; c < D / LPT / 8; ++c) dst[c] = u32x4{0, 0, 0, 0};
+        }
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int jj = 0; jj < KT / 16; ++jj) {
+        const int j = kc * (KT / 16) + jj;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+          const u32x4 kb = *(const u32x4*)(kv + (16 * jj + n) * L::K_LD + 32 * ks + 8 * g);
+          s[j] = M::run(qa[ks], kb, s[j]);
+        }
+      }
+      wave_lds_sync();
+    }
+    if (next_quant) load_k(next);
 
     // ---------------- online softmax over this tile
     float tmax[4];
@@ -173,10 +346,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) tmax[i] = fmaxf(tmax[i], __shfl_xor(tmax[i], o, 16));
-    }
+    for (int i = 0; i < 4; ++i) tmax[i] = group_reduce<16>(tmax[i], OpMax());
     float corr[4], psum[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -197,8 +367,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) psum[i] += __shfl_xor(psum[i], o, 16);
+      psum[i] = group_reduce<16>(psum[i], OpAdd());
       l_run[i] = l_run[i] * corr[i] + psum[i];
     }
 #pragma unroll
@@ -207,62 +376,63 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const mz_decode_args 
       for (int i = 0; i < 4; ++i) acc[jn][i] *= corr[i];
     }
 
-    // ---------------- V tile -> kv[c * V_LD + t]  (lane = token)
-    {
-      const int t = lane;
+    // ---------------- acc += P V, one value group (64 channels) at a time
+#pragma unroll
+    for (int vc = 0; vc < NG; ++vc) {
+      // V^T chunk -> kv[c * V_LD + t]: lane = tokens 2tp, 2tp+1, channels 32cs..32cs+31
       if (quant) {
-        const int tok = tile * kTile + t;
+        DeqG gv[2];
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
-          const int64_t midx = b * a.vm_sb + kvh * a.vm_sh + (int64_t)tok * NG + vg;
-          const DeqRow r = deq_row(meta_load(a.v_mn, midx, a.meta_dtype), meta_load(a.v_scale, midx, a.meta_dtype),
-                                   qmax, true);
-          const uint8_t* prow = a.v_packed + b * a.vp_sb + kvh * a.vp_sh + ((int64_t)tok * NG + vg) * QB;
-          uint32_t w[QB / 4];
+        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v);
 #pragma unroll
-          for (int i = 0; i < QB / 4; ++i) w[i] = ((const uint32_t*)prow)[i];
-          const uint8_t* bytes = (const uint8_t*)w;
-#pragma unroll
-          for (int c = 0; c < 64; ++c) {
-            if (64 * vg + c < D) {
-              const uint32_t q = unpack_code<BITS>(bytes, c);
-              kv[(64 * vg + c) * L::V_LD + t] = f2h(M::load(M::cvt(deq_value(r, q, EV))));
-            }
-          }
-        }
-      } else if (t < n_valid) {
-        const uint16_t* src = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh + (int64_t)(r0 + t) * a.vr_st;
-#pragma unroll
-        for (int c = 0; c < D; c += 8) {
-          const u32x4 v = *(const u32x4*)(src + c);
-          const uint16_t* hv = (const uint16_t*)&v;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kv[(c + e) * L::V_LD + t] = IO == MZ_F16 ? hv[e] : f2h(bf2f(hv[e]));
+        for (int i = 0; i < 32; ++i) {
+          const float x0 = deq_code<BITS>(gv[0], code_at<BITS>(vw[vc][0], i), EVb, iav);
+          const float x1 = deq_code<BITS>(gv[1], code_at<BITS>(vw[vc][1], i), EVb, iav);
+          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = pack_io_f16<IO>(x0, x1);
         }
       } else {
+        u32x4 rv[2][4];
 #pragma unroll
-        for (int c = 0; c < D; ++c) kv[c * L::V_LD + t] = 0;
+        for (int r = 0; r < 2; ++r) {
+          const int tok = 2 * tp + r;
+          if (tok < n_valid) {
+            const uint16_t* src = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh +
+                                  (int64_t)(r0 + tok) * a.vr_st + 64 * vc + 32 * cs;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rv[r][c] = ((const u32x4*)src)[c];
+          } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) rv[r][c] = u32x4{0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const uint32_t w0 = rv[0][i >> 3][(i >> 1) & 3], w1 = rv[1][i >> 3][(i >> 1) & 3];
+          const uint16_t h0 = (i & 1) ? (uint16_t)(w0 >> 16) : (uint16_t)w0;
+          const uint16_t h1 = (i & 1) ? (uint16_t)(w1 >> 16) : (uint16_t)w1;
+          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = io_pair_to_f16<IO>(h0, h1);
+        }
       }
-    }
-    wave_lds_sync();
-
-    // ---------------- acc += P V : A = P[m=n][32ks+8g..], B = V[32ks+8g..][16jn+n]
+      wave_lds_sync();
+      // A = P[m=n][32ks+8g..], B = V[32ks+8g..][16jn+n]
 #pragma unroll
-    for (int ks = 0; ks < kTile / 32; ++ks) {
-      const u32x4 pa = *(const u32x4*)(pb + n * L::P_LD + 32 * ks + 8 * g);
+      for (int ks = 0; ks < kTile / 32; ++ks) {
+        const u32x4 pa = *(const u32x4*)(pb + n * L::P_LD + 32 * ks + 8 * g);
 #pragma unroll
-      for (int jn = 0; jn < D / 16; ++jn) {
-        const u32x4 vb = *(const u32x4*)(kv + (16 * jn + n) * L::V_LD + 32 * ks + 8 * g);
-        acc[jn] = Mfma<MZ_F16>::run(pa, vb, acc[jn]);
+        for (int jj = 0; jj < 4; ++jj) {
+          const u32x4 vb = *(const u32x4*)(kv + (16 * jj + n) * L::V_LD + 32 * ks + 8 * g);
+          acc[4 * vc + jj] = Mfma<MZ_F16>::run(pa, vb, acc[4 * vc + jj]);
+        }
       }
+      wave_lds_sync();
     }
-    wave_lds_sync();
+    if (next_quant) load_v(next);
   }
 
   // ---------------- merge the 4 waves' states, write the split partial
   __syncthreads();
   float* red = (float*)lds;  // per wave: m[16], l[16], acc[16][D]
-  constexpr int RED = 32 + 16 * D;
+  constexpr int RED = L::RED_FLOATS;
   {
     float* w = red + wave * RED;
     if (n == 0) {
@@ -358,6 +528,7 @@ static int check_args(const mz_decode_args* a) {
                           !a->e_key || !a->e_value))
     return MZ_EINVAL;
   if (a->n_residual > 0 && (!a->k_res || !a->v_res)) return MZ_EINVAL;
+  if (a->n_groups > 0 && a->bits >= 7 && !(a->alpha_key > 0.f && a->alpha_value > 0.f)) return MZ_EINVAL;
   // 16-byte vector loads of query rows and residual rows
   if (((uintptr_t)a->query & 15) || (a->q_sh & 7) || (a->q_sb & 7)) return MZ_EINVAL;
   if (a->n_residual > 0 && (((uintptr_t)a->k_res & 15) || ((uintptr_t)a->v_res & 15) || (a->kr_st & 7) ||
@@ -406,10 +577,10 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s) {
   const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (D + 2) * (int64_t)sizeof(float);
   if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
   const dim3 grid(ns, a->kv_heads, a->batch);
-  const size_t lds = Lds<D>::BYTES;
   switch (a->bits) {
 #define MZ_CASE(BB)                                                                                      \
   case BB: {                                                                                             \
+    const size_t lds = Lds<D>::bytes(BB);                                                                \
     static const hipError_t attr = hipFuncSetAttribute(                                                  \
         (const void*)decode_split_kernel<D, BB, IO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
     if (attr != hipSuccess) return (int)attr;                                                            \

@@ -239,6 +239,7 @@ class DecodePlan:
         ek = tables.device_table("expm1", alpha_key, dev)
         ev = tables.device_table("expm1", alpha_value, dev)
         a.e_key, a.e_value = ptr(ek), ptr(ev)
+        a.alpha_key, a.alpha_value = float(alpha_key), float(alpha_value)
         keep += [ek, ev]
         if 1 <= int(bits) <= 4:
             fk = tables.device_table(f"fold{int(bits)}", alpha_key, dev)
