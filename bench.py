@@ -4,7 +4,7 @@ Default workload = BASELINE config 1: Qwen3-8B layer shape, query [64, 32, 1,
 128] bf16, KV cache [64, 8, 4096, 128] of which the oldest 3968 tokens are
 mu_zero 4-bit packed (group 64, fp16 min/scale) and the last 128 are the bf16
 residual window.  One step = one decode-attention call of one layer as the
-library runs it (one fold kernel when a single split fills the GPU, else split
+library runs it (one kernel when a single split fills the GPU, else split
 kernel + cross-split combine) with inputs already resident in HBM.
 
 Inputs: K, V, Q ~ N(0,1) from a seeded generator (seed 1234, drawn K, V, Q),
@@ -16,7 +16,7 @@ the working set.
 Prints ONE JSON line.  `value` = algorithmic bytes per call / ms_per_step
 (whole call, GB/s); `roofline` uses the dominant kernel's own average
 duration (HIP events around back-to-back launches on the launch stream): the
-single fold kernel when one split covers the GPU, else the split kernel alone;
+single kernel when one split covers the GPU, else the split kernel alone;
 `cpu_baseline` times the reference's CPU path (dequantize then attend, the
 oracle restatement of muzero/cache/attention.py:179-295) on a bounded batch
 sample and scales it to the full batch.
@@ -178,9 +178,9 @@ def main():
     # one step = one decode-attention call as the library runs it: a single
     # kernel when one split fills the GPU, else split kernel + combine
     ms_step = time_region(lambda i: plans[i % len(plans)].run(), args.steps, stream)
-    single = plans[0].n_split == 1 and plans[0].uses_fold
+    single = plans[0].n_split == 1
     if single:
-        kernels_ms = {"decode_fold_direct": round(ms_step, 5)}
+        kernels_ms = {("decode_fold_direct" if plans[0].uses_fold else "decode_general_direct"): round(ms_step, 5)}
         ms_kernel = ms_step
     else:
         ms_split = time_region(lambda i: plans[i % len(plans)].partials(), args.steps, stream)

@@ -57,23 +57,29 @@ struct Lds {
   static constexpr int RED_FLOATS = 32 + 16 * D;  // per wave at the end (aliases the wave areas)
   static constexpr int WAVES_BYTES =
       kWaves * WAVE_HALVES * 2 > kWaves * RED_FLOATS * 4 ? kWaves * WAVE_HALVES * 2 : kWaves * RED_FLOATS * 4;
-  // expm1 rows for bins 1..qmax (codes of up to 6 bits), one table per alpha
+  // expm1 rows for bins 1..qmax (codes of up to 6 bits), forward and
+  // reversed, one pair of tables per alpha
   static constexpr int e_floats(int bits) { return bits <= 6 ? ((1 << bits) - 1) * ((1 << bits) + 2) / 2 : 0; }
-  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 2 * (size_t)e_floats(bits) * 4; }
+  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 4 * (size_t)e_floats(bits) * 4; }
 };
 
 // One group's dequantization parameters (muzero/quantizer.py:241-255, from the
 // stored metadata, scale guarded as in loader.py:201).
 struct DeqG {
-  float za, s, mn, pe, mne;  // mne = -ne
+  float za, s, mn, pe, mne;  // mne = -ne (7/8 bits: pe / alpha and -ne / alpha)
   float cp, cn;              // 7/8 bits: log2(1 + alpha) / pb, / nb
   int zl;                    // zero level, an integer in 0..qmax
-  int bp, bn;                // <= 6 bits: byte offset of code q's expm1 entry: q >= zl ? bp + 4q : bn - 4q
+  int bp, bn;                // <= 6 bits: LDS byte address of code q's expm1 entry is (q >= zl ? bp : bn) + 4q
 };
 
+// `ebase`: LDS byte address of the forward expm1 rows E[bins][d]; the reversed
+// rows R[bins][k] = E[bins][bins - k] follow them (same row offsets), so a
+// code below the zero level reads R[nb][q] = E[nb][zl - q] (nb = zl then)
+// and both sides index with +q.
 template <int BITS>
-__device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2) {
+__device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float inv_alpha, int ebase) {
   constexpr float qmax = (float)((1 << BITS) - 1);
+  constexpr int EF = ((1 << BITS) - 1) * ((1 << BITS) + 2) / 2;
   const DeqRow r = deq_row(mn, s, qmax, true);
   DeqG g;
   g.za = r.za;
@@ -82,29 +88,39 @@ __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2) {
   g.pe = r.pe;
   g.mne = -r.ne;
   g.zl = r.zl == r.zl ? (int)r.zl : 0;  // a NaN zero level reads row 1 (pb = nb = 1), never past the table
-  g.bp = 4 * (r.offp - g.zl);
-  g.bn = 4 * (r.offn + g.zl);
+  g.bp = ebase + 4 * (r.offp - g.zl);
+  g.bn = ebase + 4 * (EF + r.offn);
   if constexpr (BITS > 6) {
     g.cp = lb2 / r.pb;
     g.cn = lb2 / r.nb;
+    g.pe *= inv_alpha;
+    g.mne *= inv_alpha;
   }
   return g;
+}
+
+// An LDS load from a byte address (the dynamic LDS array starts at address 0:
+// these kernels have no static LDS).
+__device__ __forceinline__ float lds_load_f32(int addr) {
+  return *(const __attribute__((address_space(3))) float*)(size_t)(uint32_t)addr;
 }
 
 // Dequantized fp32 value of code q.  Up to 6 bits this is the reference's
 // value exactly: norm = za + pe*E[pb][q-zl] or za - ne*E[nb][zl-q] (the sign
 // folded into mne is exact), clamped, times s, plus mn, with no contraction.
 template <int BITS>
-__device__ __forceinline__ float deq_code(const DeqG& g, int q, const uint8_t* E, float inv_alpha) {
+__device__ __forceinline__ float deq_code(const DeqG& g, int q) {
   const bool pos = q >= g.zl;
-  float e;
+  float t;
   if constexpr (BITS <= 6) {
-    e = *(const float*)(E + (pos ? g.bp + 4 * q : g.bn - 4 * q));
+    const float e = lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
+    t = (pos ? g.pe : g.mne) * e;
   } else {
-    const int d = pos ? q - g.zl : g.zl - q;
-    e = (__builtin_amdgcn_exp2f((float)d * (pos ? g.cp : g.cn)) - 1.f) * inv_alpha;
+    // pe * expm1(|q - zl| / bins * log1p(alpha)) / alpha, the 1/alpha folded into pe (ne)
+    const float c = pos ? g.pe : g.mne;
+    const float e = __builtin_amdgcn_exp2f(fabsf((float)(q - g.zl)) * (pos ? g.cp : g.cn));
+    t = __builtin_fmaf(c, e, -c);
   }
-  const float t = (pos ? g.pe : g.mne) * e;
   const float norm = __builtin_amdgcn_fmed3f(g.za + t, 0.f, 1.f);
   return norm * g.s + g.mn;
 }
@@ -153,7 +169,7 @@ __device__ __forceinline__ uint32_t io_pair_to_f16(uint16_t h0, uint16_t h1) {
 
 template <int D, int BITS, int IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split_kernel(
-    const mz_decode_args a, int tiles_per_split, int n_split) {
+    const mz_decode_args a, int tiles_per_split, int n_split, int direct) {
   using L = Lds<D>;
   using M = Mfma<IO>;
   constexpr int QB = 8 * BITS;      // bytes per packed 64-code row
@@ -178,20 +194,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   uint16_t* kv = lds + wave * L::WAVE_HALVES;
   uint16_t* pb = kv + L::STAGE;
-  float* eK = (float*)((uint8_t*)lds + L::WAVES_BYTES);
-  float* eV = eK + EF;
+  constexpr int EK_BASE = L::WAVES_BYTES;       // key rows: forward, then reversed
+  constexpr int EV_BASE = L::WAVES_BYTES + 8 * EF;  // value rows: forward, then reversed
   if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
     if (a.n_groups > 0) {
+      float* eK = (float*)((uint8_t*)lds + EK_BASE);
+      float* eV = (float*)((uint8_t*)lds + EV_BASE);
       for (int i = threadIdx.x; i < EF; i += 256) {
+        // row of entry i: the largest bins with (bins - 1)(bins + 2)/2 <= i
+        int bins = (int)((__builtin_sqrtf((float)(8 * i + 9)) - 1.f) * 0.5f);
+        if ((bins - 1) * (bins + 2) / 2 > i) --bins;
+        if (bins * (bins + 3) / 2 <= i) ++bins;
+        const int off = (bins - 1) * (bins + 2) / 2, k = i - off;
         eK[i] = a.e_key[i];
         eV[i] = a.e_value[i];
+        eK[EF + i] = a.e_key[off + bins - k];
+        eV[EF + i] = a.e_value[off + bins - k];
       }
     }
     __syncthreads();
   }
-  const uint8_t* EKb = (const uint8_t*)eK;
-  const uint8_t* EVb = (const uint8_t*)eV;
   // 7/8 bits: expm1(d/bins * log1p(alpha)) / alpha = (2^(d * log2(1+alpha)/bins) - 1) / alpha
   const float lb2k = kTab ? 0.f : __log2f(1.f + a.alpha_key);
   const float lb2v = kTab ? 0.f : __log2f(1.f + a.alpha_value);
@@ -286,7 +309,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     DeqG gk[2];
     if (quant) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], lb2k);
+      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], lb2k, iak, EK_BASE);
     }
 #pragma unroll
     for (int kc = 0; kc < KCH; ++kc) {
@@ -295,8 +318,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int i = 0; i < 32; ++i) {
           const int wi = KCH == 2 ? 32 * kc + i : i;  // code index in the lane's words
           const int row = KCH == 2 ? i : 32 * ts + i;  // token row of the chunk
-          const float x0 = deq_code<BITS>(gk[0], code_at<BITS>(kw[0], wi), EKb, iak);
-          const float x1 = deq_code<BITS>(gk[1], code_at<BITS>(kw[1], wi), EKb, iak);
+          const float x0 = deq_code<BITS>(gk[0], code_at<BITS>(kw[0], wi));
+          const float x1 = deq_code<BITS>(gk[1], code_at<BITS>(kw[1], wi));
           *(uint32_t*)(kv + row * L::K_LD + 2 * cp) = pack_io<IO>(x0, x1);
         }
       } else {
@@ -383,11 +406,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (quant) {
         DeqG gv[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v);
+        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v, iav, EV_BASE);
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-          const float x0 = deq_code<BITS>(gv[0], code_at<BITS>(vw[vc][0], i), EVb, iav);
-          const float x1 = deq_code<BITS>(gv[1], code_at<BITS>(vw[vc][1], i), EVb, iav);
+          const float x0 = deq_code<BITS>(gv[0], code_at<BITS>(vw[vc][0], i));
+          const float x1 = deq_code<BITS>(gv[1], code_at<BITS>(vw[vc][1], i));
           *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = pack_io_f16<IO>(x0, x1);
         }
       } else {
@@ -446,6 +469,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
   __syncthreads();
+  if (direct) {
+    // one split: the final output, exactly as the combine kernel would form it
+    for (int e = threadIdx.x; e < n_rep * D; e += 256) {
+      const int h = e / D;
+      const int c = e - h * D;
+      float M_ = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M_ = fmaxf(M_, red[w * RED + h]);
+      float num = 0.f, den = 0.f;
+      if (M_ != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float f = __expf(red[w * RED + h] - M_);
+          num += f * red[w * RED + 32 + h * D + c];
+          den += f * red[w * RED + 16 + h];
+        }
+      }
+      store_val(a.out, b * a.out_sb + (int64_t)(kvh * n_rep + h) * a.out_sh + c, den > 0.f ? num / den : 0.f,
+                a.out_dtype);
+    }
+    return;
+  }
   float* ws = (float*)a.workspace;
   const int Hq = a.kv_heads * n_rep;
   for (int e = threadIdx.x; e < n_rep * (D + 2); e += 256) {
@@ -495,16 +540,30 @@ bool fold_supported(const mz_decode_args* a);
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 
+static int decode_cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+      n = cus;
+    else
+      n = 256;
+  }
+  return n;
+}
+
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + kTile - 1) / kTile;
   if (n_tiles <= 0) { *tiles_per_split = 1; return 1; }
   int ns = a->n_split;
   if (ns <= 0) {
+    // fill the resident workgroup slots (two per CU) once: each workgroup then
+    // loads its tables and query once and runs all its tiles in one pass
     const int64_t units = (int64_t)a->batch * a->kv_heads;
-    const int64_t target = 2048;  // workgroups: several per CU on 256 CUs
-    ns = (int)((target + units - 1) / units);
-    // at least 4 tiles per split so each wave has work
-    ns = max(1, min(ns, (n_tiles + 3) / 4));
+    const int64_t slots = 2 * (int64_t)decode_cu_count();
+    ns = (int)((slots + units - 1) / units);
+    ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
   }
   ns = min(ns, n_tiles);
   const int tps = (n_tiles + ns - 1) / ns;
@@ -570,12 +629,13 @@ extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
 }
 
 template <int D, int IO>
-static int launch_partials(const mz_decode_args* a, hipStream_t s) {
+static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   int tps;
   const int ns = choose_split(a, &tps);
   static_assert(D == 64 || D == 128, "head_dim");
   const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (D + 2) * (int64_t)sizeof(float);
-  if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
+  if (!direct && (!a->workspace || a->workspace_bytes < need)) return MZ_EWORKSPACE;
+  const int dir = direct ? 1 : 0;
   const dim3 grid(ns, a->kv_heads, a->batch);
   switch (a->bits) {
 #define MZ_CASE(BB)                                                                                      \
@@ -584,7 +644,7 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s) {
     static const hipError_t attr = hipFuncSetAttribute(                                                  \
         (const void*)decode_split_kernel<D, BB, IO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
     if (attr != hipSuccess) return (int)attr;                                                            \
-    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO>), grid, dim3(256), lds, s, *a, tps, ns);          \
+    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO>), grid, dim3(256), lds, s, *a, tps, ns, dir);          \
   } break;
     MZ_CASE(1) MZ_CASE(2) MZ_CASE(3) MZ_CASE(4) MZ_CASE(5) MZ_CASE(6) MZ_CASE(7) MZ_CASE(8)
 #undef MZ_CASE
@@ -615,6 +675,14 @@ static int decode_check_launchable(const mz_decode_args* a) {
   return MZ_OK;
 }
 
+static int launch_general(const mz_decode_args* a, hipStream_t s, bool direct) {
+  if (a->head_dim == 128)
+    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s, direct)
+                                  : launch_partials<128, MZ_F16>(a, s, direct);
+  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16>(a, s, direct)
+                                : launch_partials<64, MZ_F16>(a, s, direct);
+}
+
 extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t stream) {
   const int st = decode_check_launchable(a);
   if (st) return st == 1 ? MZ_OK : st;
@@ -627,9 +695,7 @@ extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t strea
     if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
     return fold_launch_partials(a, s, false);
   }
-  if (a->head_dim == 128)
-    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s) : launch_partials<128, MZ_F16>(a, s);
-  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16>(a, s) : launch_partials<64, MZ_F16>(a, s);
+  return launch_general(a, s, false);
 }
 
 extern "C" int muzero_decode_combine(const mz_decode_args* a, mz_stream_t stream) {
@@ -643,10 +709,12 @@ extern "C" int muzero_decode_combine(const mz_decode_args* a, mz_stream_t stream
 }
 
 extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stream) {
-  // fold path with one split: the split kernel writes the output (no workspace, no combine)
-  if (decode_check_launchable(a) == MZ_OK && a->out && use_fold(a)) {
+  // one split: the split kernel writes the output (no workspace, no combine)
+  if (decode_check_launchable(a) == MZ_OK && a->out && !(a->kernel_path == MZ_PATH_FOLD && !fold_supported(a))) {
     int tps;
-    if (fold_choose_split(a, &tps) == 1) return fold_launch_partials(a, (hipStream_t)stream, true);
+    if (plan_split(a, &tps) == 1)
+      return use_fold(a) ? fold_launch_partials(a, (hipStream_t)stream, true)
+                         : launch_general(a, (hipStream_t)stream, true);
   }
   const int st = muzero_decode_partials(a, stream);
   if (st != MZ_OK) return st;

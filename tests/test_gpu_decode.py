@@ -218,3 +218,24 @@ def test_single_split_direct_output_matches_two_kernel_path(bits):
     two = plan.combine().clone()
     torch.cuda.synchronize()
     assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
+
+
+@pytest.mark.parametrize("bits,d", [(5, 128), (8, 128), (4, 64), (7, 64)])
+def test_general_single_split_direct_output_matches_two_kernel_path(bits, d):
+    """The general kernel with one split writes the output itself, bit-identical to its workspace +
+    combine path; 5-8 bits and head_dim 64 always take this kernel."""
+    from muzero_amd.kernels import loader as L
+    k, v, q, _ = ref.synthetic_kv(2, 2, 900, d, 8, seed=5)
+    _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=3.0, group_size=64, residual=128)
+    kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=2.0, alpha_value=3.0, scaling=d ** -0.5, n_split=1)
+    plan = L.DecodePlan(q.to(DEV), **kw)
+    assert plan.n_split == 1 and not plan.uses_fold
+    direct = plan.run().clone()
+    plan.out.zero_()
+    plan.partials()
+    two = plan.combine().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
