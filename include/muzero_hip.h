@@ -146,6 +146,14 @@ typedef struct mz_decode_args {
    * fit in LDS); they must be > 0 when bits >= 7 and there is a quantized
    * prefix, and are not read otherwise. */
   float alpha_key, alpha_value;
+  /* Quantized value tokens when they differ from the 64*n_groups quantized
+   * key tokens (logq_compatible_layout flushes values per token,
+   * muzero/cache/layer.py:389-396): 64*n_groups <= v_prefix <= 64*n_groups
+   * + n_residual; v_packed / v_mn / v_scale then hold v_prefix tokens and
+   * v_res holds the 64*n_groups + n_residual - v_prefix tokens after them.
+   * 0 = aligned prefixes (v_prefix = 64*n_groups).  The fold kernel needs
+   * aligned prefixes; a misaligned call runs the general kernel. */
+  int v_prefix;
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it

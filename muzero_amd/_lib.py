@@ -52,6 +52,7 @@ class DecodeArgs(ctypes.Structure):
         ("n_split", c_int),
         ("kernel_path", c_int),
         ("alpha_key", c_float), ("alpha_value", c_float),
+        ("v_prefix", c_int),
     ]
 
 MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2

@@ -64,11 +64,11 @@ def mu_zero_decode_attention_forward(
     _MU_ZERO_DECODE_STATS["calls"] += 1
 
     key_prefix_length = int(kv_cache_state.get("key_prefix_length", 0))
-    value_prefix_length = int(kv_cache_state.get("value_prefix_length", 0))
-    if key_prefix_length != value_prefix_length:
-        raise NotImplementedError(
-            "the fused HIP decode needs aligned key/value prefixes (the default layout); "
-            "logq_compatible_layout with an unaligned value prefix is not supported")
+    # logq_compatible_layout flushes values per token, so the quantized value
+    # prefix can run past the key prefix (layer.py:389-396); the kernel then
+    # takes those tokens' values from the packed store and their keys from the
+    # residual window
+    value_prefix_length = int(kv_cache_state.get("value_prefix_length", key_prefix_length))
     n_groups = key_prefix_length // layer.q_group_size
     keys, values = layer.keys, layer.values
     has_res = keys is not None and keys.dim() == 4 and keys.shape[2] > 0
@@ -86,6 +86,7 @@ def mu_zero_decode_attention_forward(
         alpha_value=float(layer._selected_alpha_value if layer._selected_alpha_value is not None else 2.0),
         scaling=float(scaling),
         attention_mask=attention_mask,
+        value_prefix=value_prefix_length,
     )
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int EV_BASE = L::WAVES_BYTES + 8 * EF;  // value rows: forward, then reversed
   if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
-    if (a.n_groups > 0) {
+    if (a.n_groups > 0 || a.v_prefix > 0) {
       float* eK = (float*)((uint8_t*)lds + EK_BASE);
       float* eV = (float*)((uint8_t*)lds + EV_BASE);
       for (int i = threadIdx.x; i < EF; i += 256) {
@@ -256,6 +256,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint8_t* vbase = a.v_packed + b * a.vp_sb + kvh * a.vp_sh;
   const int64_t kmb = b * a.km_sb + kvh * a.km_sh;
   const int64_t vmb = b * a.vm_sb + kvh * a.vm_sh;
+  // quantized value tokens past the key prefix (logq_compatible_layout), 0 when aligned
+  const int dv = a.v_prefix > 0 ? a.v_prefix - a.n_groups * kTile : 0;
 
   // packed words and metadata of the tile being staged next (loaded one tile ahead)
   uint32_t kw[2][KWR];
@@ -412,6 +414,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const float x0 = deq_code<BITS>(gv[0], code_at<BITS>(vw[vc][0], i));
           const float x1 = deq_code<BITS>(gv[1], code_at<BITS>(vw[vc][1], i));
           *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = pack_io_f16<IO>(x0, x1);
+        }
+      } else if (dv > 0) {
+        // misaligned value prefix (logq_compatible_layout): the first dv
+        // tokens past the key prefix have quantized values, the rest dense
+        // ones starting at v_res row 0; one token at a time
+#pragma unroll 1
+        for (int r = 0; r < 2; ++r) {
+          const int tok = 2 * tp + r;
+          const int vt = r0 + tok;  // token index past the key prefix
+          uint16_t* col = kv + (32 * cs) * L::V_LD + tok;
+          if (tok < n_valid && vt < dv) {
+            const int64_t at = (int64_t)a.n_groups * kTile + vt;
+            const uint32_t* row = (const uint32_t*)(vbase + (at * NG + vc) * QB) + cs * BITS;
+            uint32_t w[BITS];
+#pragma unroll
+            for (int i = 0; i < BITS; ++i) w[i] = row[i];
+            const int64_t mi = vmb + at * NG + vc;
+            const DeqG gq = deq_group<BITS>(meta_load(a.v_mn, mi, a.meta_dtype), meta_load(a.v_scale, mi, a.meta_dtype),
+                                            lb2v, iav, EV_BASE);
+#pragma unroll
+            for (int i = 0; i < 32; i += 2) {
+              const uint32_t h = pack_io_f16<IO>(deq_code<BITS>(gq, code_at<BITS>(w, i)),
+                                                 deq_code<BITS>(gq, code_at<BITS>(w, i + 1)));
+              col[i * L::V_LD] = (uint16_t)h;
+              col[(i + 1) * L::V_LD] = (uint16_t)(h >> 16);
+            }
+          } else if (tok < n_valid) {
+            const uint16_t* src = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh +
+                                  (int64_t)(vt - dv) * a.vr_st + 64 * vc + 32 * cs;
+#pragma unroll
+            for (int i = 0; i < 32; i += 2)
+              {
+                const uint32_t h = io_pair_to_f16<IO>(src[i], src[i + 1]);
+                col[i * L::V_LD] = (uint16_t)h;
+                col[(i + 1) * L::V_LD] = (uint16_t)(h >> 16);
+              }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) col[i * L::V_LD] = 0;
+          }
         }
       } else {
         u32x4 rv[2][4];
@@ -586,15 +628,25 @@ static int check_args(const mz_decode_args* a) {
   if (a->n_groups > 0 && (!a->k_packed || !a->k_mn || !a->k_scale || !a->v_packed || !a->v_mn || !a->v_scale ||
                           !a->e_key || !a->e_value))
     return MZ_EINVAL;
-  if (a->n_residual > 0 && (!a->k_res || !a->v_res)) return MZ_EINVAL;
+  // dense value rows: the residual window minus the quantized value tokens past the key prefix
+  const int64_t v_dense = (int64_t)a->n_residual - (a->v_prefix ? a->v_prefix - (int64_t)a->n_groups * 64 : 0);
+  if (a->n_residual > 0 && !a->k_res) return MZ_EINVAL;
+  if (v_dense > 0 && !a->v_res) return MZ_EINVAL;
   if (a->n_groups > 0 && a->bits >= 7 && !(a->alpha_key > 0.f && a->alpha_value > 0.f)) return MZ_EINVAL;
+  if (a->v_prefix != 0) {
+    const int64_t lk = (int64_t)a->n_groups * 64;
+    if (a->v_prefix < lk || a->v_prefix > lk + a->n_residual) return MZ_EINVAL;
+    if (a->v_prefix > lk && (!a->v_packed || !a->v_mn || !a->v_scale || !a->e_value)) return MZ_EINVAL;
+    if (a->v_prefix > lk && a->bits >= 7 && !(a->alpha_value > 0.f)) return MZ_EINVAL;
+  }
   // 16-byte vector loads of query rows and residual rows
   if (((uintptr_t)a->query & 15) || (a->q_sh & 7) || (a->q_sb & 7)) return MZ_EINVAL;
   if (a->n_residual > 0 && (((uintptr_t)a->k_res & 15) || ((uintptr_t)a->v_res & 15) || (a->kr_st & 7) ||
                             (a->kr_sh & 7) || (a->kr_sb & 7) || (a->vr_st & 7) || (a->vr_sh & 7) || (a->vr_sb & 7)))
     return MZ_EINVAL;
-  if (a->n_groups > 0 && (((uintptr_t)a->k_packed & 3) || ((uintptr_t)a->v_packed & 3) || (a->kp_sb & 3) ||
-                          (a->kp_sh & 3) || (a->vp_sb & 3) || (a->vp_sh & 3)))
+  if ((a->n_groups > 0 || a->v_prefix > 0) &&
+      (((uintptr_t)a->k_packed & 3) || ((uintptr_t)a->v_packed & 3) || (a->kp_sb & 3) || (a->kp_sh & 3) ||
+       (a->vp_sb & 3) || (a->vp_sh & 3)))
     return MZ_EINVAL;
   return MZ_OK;
 }

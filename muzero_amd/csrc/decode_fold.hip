@@ -916,7 +916,8 @@ bool fold_supported(const mz_decode_args* a) {
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
-  return a->bits >= 1 && a->bits <= 4 && a->head_dim == 128 && a->n_groups > 0 && fits &&
+  const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
+  return a->bits >= 1 && a->bits <= 4 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned &&
          (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
          ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&

@@ -190,7 +190,7 @@ class DecodePlan:
                  alpha_key: float, alpha_value: float, scaling: float,
                  attention_mask: torch.Tensor | None = None,
                  out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None, n_split: int = 0,
-                 kernel_path: str = "auto"):
+                 kernel_path: str = "auto", value_prefix: int | None = None):
         dev = _on_gpu(query, k_packed, k_mn, k_scale, v_packed, v_mn, v_scale, k_res, v_res, attention_mask)
         self.device = dev
         _require(query.dim() == 4 and query.shape[2] == 1, "query must be [B, Hq, 1, D]")
@@ -199,8 +199,13 @@ class DecodePlan:
         q = query if (query.stride(3) == 1 and query.stride(1) % 8 == 0 and query.stride(0) % 8 == 0
                       and query.data_ptr() % 16 == 0) else query.contiguous()
         r = 0 if k_res is None else k_res.shape[2]
+        lk = GROUP * int(n_groups)
+        # quantized value tokens: 64 * n_groups unless the layout flushes values per token
+        # (logq_compatible_layout, muzero/cache/layer.py:389-396)
+        vp = lk if value_prefix is None else int(value_prefix)
+        _require(lk <= vp <= lk + r, "value_prefix must lie between the key prefix and the end of the cache")
         if k_res is not None:
-            _require(v_res is not None and v_res.shape[2] == r, "residual K/V lengths differ")
+            _require(v_res is not None and v_res.shape[2] == r - (vp - lk), "residual K/V lengths differ")
             hkv = k_res.shape[1]
         else:
             _require(k_packed is not None, "no prefix and no residual")
@@ -210,31 +215,36 @@ class DecodePlan:
         meta_dtype = 0
         keep = [q]
         a = _lib.DecodeArgs()
+        qb = _qbytes(bits)
+        ng = (d + GROUP - 1) // GROUP
         if n_groups > 0:
-            qb = _qbytes(bits)
-            ng = (d + GROUP - 1) // GROUP
-            _require(k_packed.shape[:2] == (b, hkv) and v_packed.shape[:2] == (b, hkv), "packed batch/head dims")
+            _require(k_packed.shape[:2] == (b, hkv), "packed batch/head dims")
             _require(k_packed.shape[2] >= n_groups and tuple(k_packed.shape[3:]) == (d, qb), "packed K layout")
             _require(k_packed.stride(4) == 1 and k_packed.stride(3) == qb and k_packed.stride(2) == d * qb,
                      "packed K strides")
             _require(k_mn.shape[:3] == k_packed.shape[:3] and k_mn.shape[3] == d, "K meta shape")
             _require(k_mn.stride(3) == 1 and k_mn.stride(2) == d and k_mn.stride() == k_scale.stride(),
                      "K meta strides")
-            _require(v_packed.shape[2] >= GROUP * n_groups and tuple(v_packed.shape[3:]) == (ng, qb),
-                     "packed V layout")
+            _require(k_mn.dtype == k_scale.dtype and k_mn.dtype in DTYPE_ENUM, "meta dtypes")
+            meta_dtype = DTYPE_ENUM[k_mn.dtype]
+            a.k_packed, a.kp_sb, a.kp_sh = ptr(k_packed), k_packed.stride(0), k_packed.stride(1)
+            a.k_mn, a.k_scale, a.km_sb, a.km_sh = ptr(k_mn), ptr(k_scale), k_mn.stride(0), k_mn.stride(1)
+            keep += [k_packed, k_mn, k_scale]
+        if vp > 0:
+            _require(v_packed.shape[:2] == (b, hkv), "packed batch/head dims")
+            _require(v_packed.shape[2] >= vp and tuple(v_packed.shape[3:]) == (ng, qb), "packed V layout")
             _require(v_packed.stride(4) == 1 and v_packed.stride(3) == qb and v_packed.stride(2) == ng * qb,
                      "packed V strides")
             _require(v_mn.shape[:3] == v_packed.shape[:3] and v_mn.shape[3] == ng, "V meta shape")
             _require(v_mn.stride(3) == 1 and v_mn.stride(2) == ng and v_mn.stride() == v_scale.stride(),
                      "V meta strides")
-            _require(k_mn.dtype == k_scale.dtype == v_mn.dtype == v_scale.dtype and k_mn.dtype in DTYPE_ENUM,
-                     "meta dtypes")
-            meta_dtype = DTYPE_ENUM[k_mn.dtype]
-            a.k_packed, a.kp_sb, a.kp_sh = ptr(k_packed), k_packed.stride(0), k_packed.stride(1)
-            a.k_mn, a.k_scale, a.km_sb, a.km_sh = ptr(k_mn), ptr(k_scale), k_mn.stride(0), k_mn.stride(1)
+            _require(v_mn.dtype == v_scale.dtype and v_mn.dtype in DTYPE_ENUM
+                     and (n_groups == 0 or v_mn.dtype == k_mn.dtype), "meta dtypes")
+            meta_dtype = DTYPE_ENUM[v_mn.dtype]
             a.v_packed, a.vp_sb, a.vp_sh = ptr(v_packed), v_packed.stride(0), v_packed.stride(1)
             a.v_mn, a.v_scale, a.vm_sb, a.vm_sh = ptr(v_mn), ptr(v_scale), v_mn.stride(0), v_mn.stride(1)
-            keep += [k_packed, k_mn, k_scale, v_packed, v_mn, v_scale]
+            keep += [v_packed, v_mn, v_scale]
+        a.v_prefix = vp if vp != lk else 0
         # expm1 tables are always passed (the kernel reads them only for a quantized prefix)
         ek = tables.device_table("expm1", alpha_key, dev)
         ev = tables.device_table("expm1", alpha_value, dev)
@@ -258,7 +268,8 @@ class DecodePlan:
             return t
 
         if r > 0:
-            k_res, v_res = _res(k_res), _res(v_res)
+            k_res = _res(k_res)
+            v_res = _res(v_res) if v_res.shape[2] > 0 else v_res
             a.k_res, a.kr_sb, a.kr_sh, a.kr_st = ptr(k_res), k_res.stride(0), k_res.stride(1), k_res.stride(2)
             a.v_res, a.vr_sb, a.vr_sh, a.vr_st = ptr(v_res), v_res.stride(0), v_res.stride(1), v_res.stride(2)
             keep += [k_res, v_res]

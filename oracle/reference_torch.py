@@ -332,7 +332,8 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
                      amax_dtype: torch.dtype = torch.float16,
                      attention_mask: Optional[torch.Tensor] = None,
                      scaling: Optional[float] = None,
-                     dequant_dtype: Optional[torch.dtype] = None):
+                     dequant_dtype: Optional[torch.dtype] = None,
+                     value_prefix: Optional[int] = None):
     """Quantize a prefill KV the way the cache does, then attend the decode query.
 
     Returns ``(out_exact_fp64 [B,1,Hq,hd], state)`` where ``state`` holds the
@@ -345,26 +346,35 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
     while its fused CUDA kernels keep the dequantized values in fp32 registers
     (``dequantize_mu_zero_q``/``fill_mu_zero_codebook``, ``loader.py:197-263``).
     Default: the layer dtype (``keys.dtype``).
+
+    ``value_prefix``: quantized value tokens when the layout flushes values per
+    token (``logq_compatible_layout``, ``layer.py:389-396``): ``lq <= value_prefix
+    <= length``; default ``lq`` (the aligned default layout).
     """
     b, hkv, length, d = keys.shape
     lq = split_prefix(length, residual, group_size)
+    lv = lq if value_prefix is None else int(value_prefix)
+    assert lq <= lv <= length
     if scaling is None:
         scaling = d ** -0.5
-    state = {"lq": lq, "scaling": scaling}
+    state = {"lq": lq, "lv": lv, "scaling": scaling}
+    ddt = keys.dtype if dequant_dtype is None else dequant_dtype
     if lq > 0:
         pk, kmn, ksc = quantize_key_block(keys[:, :, :lq].contiguous(), bits, alpha_k, group_size, amax_dtype)
-        pv, vmn, vsc = quantize_value_block(values[:, :, :lq].contiguous(), bits, alpha_v, group_size, amax_dtype)
-        ddt = keys.dtype if dequant_dtype is None else dequant_dtype
         kq = dequantize_key_block(pk, kmn, ksc, bits, alpha_k, group_size, ddt)
-        vq = dequantize_value_block(pv, vmn, vsc, bits, alpha_v, group_size, d, ddt)
-        state.update(packed_k=pk, k_mn=kmn, k_scale=ksc, packed_v=pv, v_mn=vmn, v_scale=vsc,
-                     key_prefix=kq, value_prefix=vq)
+        state.update(packed_k=pk, k_mn=kmn, k_scale=ksc, key_prefix=kq)
     else:
         kq = keys[:, :, :0]
+        state.update(key_prefix=kq)
+    if lv > 0:
+        pv, vmn, vsc = quantize_value_block(values[:, :, :lv].contiguous(), bits, alpha_v, group_size, amax_dtype)
+        vq = dequantize_value_block(pv, vmn, vsc, bits, alpha_v, group_size, d, ddt)
+        state.update(packed_v=pv, v_mn=vmn, v_scale=vsc, value_prefix=vq)
+    else:
         vq = values[:, :, :0]
-        state.update(key_prefix=kq, value_prefix=vq)
+        state.update(value_prefix=vq)
     rk = keys[:, :, lq:]
-    rv = values[:, :, lq:]
+    rv = values[:, :, lv:]
     state.update(res_k=rk, res_v=rv)
     full_k = torch.cat([kq.double(), rk.double()], dim=2)
     full_v = torch.cat([vq.double(), rv.double()], dim=2)

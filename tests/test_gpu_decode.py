@@ -239,3 +239,31 @@ def test_general_single_split_direct_output_matches_two_kernel_path(bits, d):
     two = plan.combine().clone()
     torch.cuda.synchronize()
     assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
+
+
+@pytest.mark.parametrize("bits,d,length,extra", [(4, 128, 900, 37), (2, 128, 700, 63), (5, 128, 800, 1),
+                                                 (8, 128, 800, 20), (3, 64, 640, 50), (4, 128, 150, 22),
+                                                 (4, 128, 840, None)])
+def test_misaligned_value_prefix(bits, d, length, extra):
+    """logq_compatible_layout: the quantized value prefix runs `extra` tokens past the key prefix
+    (layer.py:389-396); those tokens' values come from the packed store, their keys from the residual
+    window (extra=None: every value past the key prefix is quantized, no dense value rows).  Held to
+    the exact (layer-dtype) dequantize-then-attend oracle: misaligned calls run the general kernel."""
+    from muzero_amd.kernels import loader as L
+    B, hkv, n_rep, residual = 2, 2, 4, 128
+    k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=9)
+    lq = ref.split_prefix(length, residual, 64)
+    lv = length if extra is None else lq + extra
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64,
+                                     residual=residual, value_prefix=lv)
+    dev = lambda t: None if t is None else t.to(DEV)
+    plan = L.DecodePlan(dev(q), bits=bits, n_groups=lq // 64, k_packed=dev(st.get("packed_k")),
+                        k_mn=dev(st.get("k_mn")), k_scale=dev(st.get("k_scale")), v_packed=dev(st["packed_v"]),
+                        v_mn=dev(st["v_mn"]), v_scale=dev(st["v_scale"]), k_res=dev(st["res_k"]),
+                        v_res=dev(st["res_v"]), alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5,
+                        out_dtype=torch.float32, value_prefix=lv)
+    assert not plan.uses_fold
+    out = plan.run()
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - exact).abs()
+    assert err.max().item() < MAX_ABS and err.mean().item() < MEAN_ABS, (err.max().item(), err.mean().item())

@@ -67,6 +67,31 @@ def test_cache_layer_matches_oracle_cache(bits, dtype, meta):
     assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
 
 
+@pytest.mark.parametrize("bits", [4, 2])
+def test_logq_compatible_layout_decode(bits):
+    """logq_compatible_layout flushes values per token (layer.py:389-396): the value prefix runs past
+    the key prefix; the stored bytes match the oracle and the fused decode matches the exact oracle."""
+    B, hkv, n_rep, d, prefill, steps = 2, 2, 4, 128, 700, 100
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=13)
+    cfg = mz.MuZeroConfig(bits=bits, alpha_key=2.0, alpha_value=2.0, logq_compatible_layout=True)
+    layer = MuZeroCacheLayer(cfg)
+    _feed(layer, k, v, prefill)
+    state = layer.get_attention_state()
+    length = prefill + steps
+    lq, lv = ref.split_prefix(length, 128, 64), length - 128
+    assert (state["key_prefix_length"], state["value_prefix_length"]) == (lq, lv) and lv > lq
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     value_prefix=lv)
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
+
+
 def test_materialized_kv_matches_dequantized_oracle():
     """``update(materialize_full_kv=True)`` returns the dequantised prefix + residual, bit-exact
     to the reference's torch dequantisation in the layer dtype."""
