@@ -50,7 +50,10 @@ struct Lds {
   static constexpr int NG = D / 64;              // V chunks (value groups) per tile
   static constexpr int K_LD = D + kPad;          // K chunk row: one token
   static constexpr int V_LD = kTile + kPad;      // V chunk row: one channel
-  static constexpr int STAGE = (KT * K_LD > 64 * V_LD) ? KT * K_LD : 64 * V_LD;
+  // V chunk rows 32..63 start 64 halves (32 banks) further on: the two lane
+  // halves of a staging store (rows i and 32 + i) then use disjoint banks
+  static constexpr int V_HI = 64;
+  static constexpr int STAGE = (KT * K_LD > 64 * V_LD + V_HI) ? KT * K_LD : 64 * V_LD + V_HI;
   static constexpr int P_LD = kTile + kPad;
   static constexpr int P_HALVES = 16 * P_LD;
   static constexpr int WAVE_HALVES = STAGE + P_HALVES;
@@ -60,7 +63,11 @@ struct Lds {
   // expm1 rows for bins 1..qmax (codes of up to 6 bits), forward and
   // reversed, one pair of tables per alpha
   static constexpr int e_floats(int bits) { return bits <= 6 ? ((1 << bits) - 1) * ((1 << bits) + 2) / 2 : 0; }
-  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 4 * (size_t)e_floats(bits) * 4; }
+  // fast form: one signed expm1 value per (zero level, code), (2^bits)^2 floats per alpha
+  static constexpr int z_floats(int bits) { return bits <= 6 ? (1 << bits) * (1 << bits) : 0; }
+  static constexpr size_t bytes(int bits, bool fast) {
+    return (size_t)WAVES_BYTES + (fast ? 2 * (size_t)z_floats(bits) : 4 * (size_t)e_floats(bits)) * 4;
+  }
 };
 
 // One group's dequantization parameters (muzero/quantizer.py:241-255, from the
@@ -70,13 +77,19 @@ struct DeqG {
   float cp, cn;              // 7/8 bits: log2(1 + alpha) / pb, / nb
   int zl;                    // zero level, an integer in 0..qmax
   int bp, bn;                // <= 6 bits: LDS byte address of code q's expm1 entry is (q >= zl ? bp : bn) + 4q
+  float fa, fp, fn;          // fast form: x = fa + (q >= zl ? fp : fn) * Z[zl][q]
 };
 
 // `ebase`: LDS byte address of the forward expm1 rows E[bins][d]; the reversed
 // rows R[bins][k] = E[bins][bins - k] follow them (same row offsets), so a
 // code below the zero level reads R[nb][q] = E[nb][zl - q] (nb = zl then)
 // and both sides index with +q.
-template <int BITS>
+// `fast` (codes of up to 6 bits): the table at `ebase` is Z[zl][q] =
+// +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] (q < zl), and the value is
+// a + (s*pe or s*ne) * Z with a = mn + s*za: the reference's value to a few
+// fp32 ulp (its fused CUDA kernels' fp32 codebook form), one table read and
+// about five ops per code.
+template <int BITS, bool FAST>
 __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float inv_alpha, int ebase) {
   constexpr float qmax = (float)((1 << BITS) - 1);
   constexpr int EF = ((1 << BITS) - 1) * ((1 << BITS) + 2) / 2;
@@ -88,6 +101,13 @@ __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float in
   g.pe = r.pe;
   g.mne = -r.ne;
   g.zl = r.zl == r.zl ? (int)r.zl : 0;  // a NaN zero level reads row 1 (pb = nb = 1), never past the table
+  if constexpr (FAST) {
+    g.bp = ebase + 4 * (g.zl << BITS);
+    g.fa = r.mn + r.s * r.za;
+    g.fp = r.s * r.pe;
+    g.fn = r.s * r.ne;
+    return g;
+  }
   g.bp = ebase + 4 * (r.offp - g.zl);
   g.bn = ebase + 4 * (EF + r.offn);
   if constexpr (BITS > 6) {
@@ -108,21 +128,34 @@ __device__ __forceinline__ float lds_load_f32(int addr) {
 // Dequantized fp32 value of code q.  Up to 6 bits this is the reference's
 // value exactly: norm = za + pe*E[pb][q-zl] or za - ne*E[nb][zl-q] (the sign
 // folded into mne is exact), clamped, times s, plus mn, with no contraction.
-template <int BITS>
-__device__ __forceinline__ float deq_code(const DeqG& g, int q) {
+// Split in two so a block of codes can issue all its table reads before
+// using any: deq_fetch returns the table entry (or, for 7/8 bits, evaluates
+// the expm1 term), deq_apply finishes the value.
+template <int BITS, bool FAST>
+__device__ __forceinline__ float deq_fetch(const DeqG& g, int q) {
   const bool pos = q >= g.zl;
-  float t;
-  if constexpr (BITS <= 6) {
-    const float e = lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
-    t = (pos ? g.pe : g.mne) * e;
+  if constexpr (FAST) {
+    return lds_load_f32(g.bp + 4 * q);
+  } else if constexpr (BITS <= 6) {
+    return lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
   } else {
     // pe * expm1(|q - zl| / bins * log1p(alpha)) / alpha, the 1/alpha folded into pe (ne)
     const float c = pos ? g.pe : g.mne;
     const float e = __builtin_amdgcn_exp2f(fabsf((float)(q - g.zl)) * (pos ? g.cp : g.cn));
-    t = __builtin_fmaf(c, e, -c);
+    return __builtin_fmaf(c, e, -c);
   }
+}
+template <int BITS, bool FAST>
+__device__ __forceinline__ float deq_apply(const DeqG& g, int q, float z) {
+  const bool pos = q >= g.zl;
+  if constexpr (FAST) return __builtin_fmaf(pos ? g.fp : g.fn, z, g.fa);
+  const float t = BITS <= 6 ? (pos ? g.pe : g.mne) * z : z;
   const float norm = __builtin_amdgcn_fmed3f(g.za + t, 0.f, 1.f);
   return norm * g.s + g.mn;
+}
+template <int BITS, bool FAST>
+__device__ __forceinline__ float deq_code(const DeqG& g, int q) {
+  return deq_apply<BITS, FAST>(g, q, deq_fetch<BITS, FAST>(g, q));
 }
 
 // Code `idx` of an LSB-first bitstream held in registers (idx is a constant
@@ -167,7 +200,7 @@ __device__ __forceinline__ uint32_t io_pair_to_f16(uint16_t h0, uint16_t h1) {
   else return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{bf2f(h0), bf2f(h1)}), f16x2_t));
 }
 
-template <int D, int BITS, int IO>
+template <int D, int BITS, int IO, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, int direct) {
   using L = Lds<D>;
@@ -180,7 +213,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int KTPL = D == 128 ? 64 : 32;  // K tokens per lane and tile
   constexpr int KWR = KTPL * BITS / 32;  // K words per row and lane
   constexpr int EF = L::e_floats(BITS);
+  constexpr int ZF = L::z_floats(BITS);
   constexpr bool kTab = BITS <= 6;
+  static_assert(!FAST || kTab, "the fast form needs the per-zero-level table (codes of up to 6 bits)");
 
   extern __shared__ __align__(16) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -194,9 +229,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   uint16_t* kv = lds + wave * L::WAVE_HALVES;
   uint16_t* pb = kv + L::STAGE;
-  constexpr int EK_BASE = L::WAVES_BYTES;       // key rows: forward, then reversed
-  constexpr int EV_BASE = L::WAVES_BYTES + 8 * EF;  // value rows: forward, then reversed
-  if constexpr (kTab) {
+  constexpr int EK_BASE = L::WAVES_BYTES;                              // key table
+  constexpr int EV_BASE = L::WAVES_BYTES + (FAST ? 4 * ZF : 8 * EF);  // value table
+  if constexpr (FAST) {
+    // Z[zl][q] = +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] from the expm1 rows
+    if (a.n_groups > 0 || a.v_prefix > 0) {
+      float* zK = (float*)((uint8_t*)lds + EK_BASE);
+      float* zV = (float*)((uint8_t*)lds + EV_BASE);
+      constexpr int QM = (1 << BITS) - 1;
+      for (int i = threadIdx.x; i < ZF; i += 256) {
+        const int zl = i >> BITS, q = i & QM;
+        const int bins = q >= zl ? max(QM - zl, 1) : max(zl, 1);
+        const int idx = (bins - 1) * (bins + 2) / 2 + (q >= zl ? q - zl : zl - q);
+        zK[i] = q >= zl ? a.e_key[idx] : -a.e_key[idx];
+        zV[i] = q >= zl ? a.e_value[idx] : -a.e_value[idx];
+      }
+    }
+    __syncthreads();
+  } else if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
     if (a.n_groups > 0 || a.v_prefix > 0) {
       float* eK = (float*)((uint8_t*)lds + EK_BASE);
@@ -311,18 +361,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     DeqG gk[2];
     if (quant) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], lb2k, iak, EK_BASE);
+      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS, FAST>(kmeta[r][0], kmeta[r][1], lb2k, iak, EK_BASE);
     }
 #pragma unroll
     for (int kc = 0; kc < KCH; ++kc) {
       if (quant) {
+        // blocks of 8 tokens: all 16 table reads issued, then used
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int wi = KCH == 2 ? 32 * kc + i : i;  // code index in the lane's words
-          const int row = KCH == 2 ? i : 32 * ts + i;  // token row of the chunk
-          const float x0 = deq_code<BITS>(gk[0], code_at<BITS>(kw[0], wi));
-          const float x1 = deq_code<BITS>(gk[1], code_at<BITS>(kw[1], wi));
-          *(uint32_t*)(kv + row * L::K_LD + 2 * cp) = pack_io<IO>(x0, x1);
+        for (int i0 = 0; i0 < 32; i0 += 8) {
+          int q0[8], q1[8];
+          float z0[8], z1[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int wi = (KCH == 2 ? 32 * kc : 0) + i0 + u;  // code index in the lane's words
+            q0[u] = code_at<BITS>(kw[0], wi);
+            q1[u] = code_at<BITS>(kw[1], wi);
+            z0[u] = deq_fetch<BITS, FAST>(gk[0], q0[u]);
+            z1[u] = deq_fetch<BITS, FAST>(gk[1], q1[u]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int row = (KCH == 2 ? 0 : 32 * ts) + i0 + u;  // token row of the chunk
+            *(uint32_t*)(kv + row * L::K_LD + 2 * cp) =
+                pack_io<IO>(deq_apply<BITS, FAST>(gk[0], q0[u], z0[u]), deq_apply<BITS, FAST>(gk[1], q1[u], z1[u]));
+          }
         }
       } else {
         // residual rows: LPT lanes per token, each copying D / LPT halves (rows past the window are 0)
@@ -408,12 +471,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (quant) {
         DeqG gv[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v, iav, EV_BASE);
+        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS, FAST>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v, iav, EV_BASE);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const float x0 = deq_code<BITS>(gv[0], code_at<BITS>(vw[vc][0], i));
-          const float x1 = deq_code<BITS>(gv[1], code_at<BITS>(vw[vc][1], i));
-          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = pack_io_f16<IO>(x0, x1);
+        for (int i0 = 0; i0 < 32; i0 += 8) {
+          int q0[8], q1[8];
+          float z0[8], z1[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            q0[u] = code_at<BITS>(vw[vc][0], i0 + u);
+            q1[u] = code_at<BITS>(vw[vc][1], i0 + u);
+            z0[u] = deq_fetch<BITS, FAST>(gv[0], q0[u]);
+            z1[u] = deq_fetch<BITS, FAST>(gv[1], q1[u]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            *(uint32_t*)(kv + (32 * cs + i0 + u) * L::V_LD + cs * L::V_HI + 2 * tp) =
+                pack_io_f16<IO>(deq_apply<BITS, FAST>(gv[0], q0[u], z0[u]), deq_apply<BITS, FAST>(gv[1], q1[u], z1[u]));
         }
       } else if (dv > 0) {
         // misaligned value prefix (logq_compatible_layout): the first dv
@@ -423,7 +497,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int r = 0; r < 2; ++r) {
           const int tok = 2 * tp + r;
           const int vt = r0 + tok;  // token index past the key prefix
-          uint16_t* col = kv + (32 * cs) * L::V_LD + tok;
+          uint16_t* col = kv + (32 * cs) * L::V_LD + cs * L::V_HI + tok;
           if (tok < n_valid && vt < dv) {
             const int64_t at = (int64_t)a.n_groups * kTile + vt;
             const uint32_t* row = (const uint32_t*)(vbase + (at * NG + vc) * QB) + cs * BITS;
@@ -431,12 +505,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int i = 0; i < BITS; ++i) w[i] = row[i];
             const int64_t mi = vmb + at * NG + vc;
-            const DeqG gq = deq_group<BITS>(meta_load(a.v_mn, mi, a.meta_dtype), meta_load(a.v_scale, mi, a.meta_dtype),
+            const DeqG gq = deq_group<BITS, FAST>(meta_load(a.v_mn, mi, a.meta_dtype), meta_load(a.v_scale, mi, a.meta_dtype),
                                             lb2v, iav, EV_BASE);
 #pragma unroll
             for (int i = 0; i < 32; i += 2) {
-              const uint32_t h = pack_io_f16<IO>(deq_code<BITS>(gq, code_at<BITS>(w, i)),
-                                                 deq_code<BITS>(gq, code_at<BITS>(w, i + 1)));
+              const uint32_t h = pack_io_f16<IO>(deq_code<BITS, FAST>(gq, code_at<BITS>(w, i)),
+                                                 deq_code<BITS, FAST>(gq, code_at<BITS>(w, i + 1)));
               col[i * L::V_LD] = (uint16_t)h;
               col[(i + 1) * L::V_LD] = (uint16_t)(h >> 16);
             }
@@ -475,7 +549,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const uint32_t w0 = rv[0][i >> 3][(i >> 1) & 3], w1 = rv[1][i >> 3][(i >> 1) & 3];
           const uint16_t h0 = (i & 1) ? (uint16_t)(w0 >> 16) : (uint16_t)w0;
           const uint16_t h1 = (i & 1) ? (uint16_t)(w1 >> 16) : (uint16_t)w1;
-          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + 2 * tp) = io_pair_to_f16<IO>(h0, h1);
+          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + cs * L::V_HI + 2 * tp) = io_pair_to_f16<IO>(h0, h1);
         }
       }
       wave_lds_sync();
@@ -485,7 +559,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const u32x4 pa = *(const u32x4*)(pb + n * L::P_LD + 32 * ks + 8 * g);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const u32x4 vb = *(const u32x4*)(kv + (16 * jj + n) * L::V_LD + 32 * ks + 8 * g);
+          const u32x4 vb = *(const u32x4*)(kv + (16 * jj + n) * L::V_LD + (jj >= 2 ? L::V_HI : 0) + 32 * ks + 8 * g);
           acc[4 * vc + jj] = Mfma<MZ_F16>::run(pa, vb, acc[4 * vc + jj]);
         }
       }
@@ -680,7 +754,7 @@ extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
   return use_fold(a) ? 1 : 0;
 }
 
-template <int D, int IO>
+template <int D, int IO, bool FAST>
 static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   int tps;
   const int ns = choose_split(a, &tps);
@@ -690,13 +764,14 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) 
   const int dir = direct ? 1 : 0;
   const dim3 grid(ns, a->kv_heads, a->batch);
   switch (a->bits) {
-#define MZ_CASE(BB)                                                                                      \
-  case BB: {                                                                                             \
-    const size_t lds = Lds<D>::bytes(BB);                                                                \
-    static const hipError_t attr = hipFuncSetAttribute(                                                  \
-        (const void*)decode_split_kernel<D, BB, IO>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
-    if (attr != hipSuccess) return (int)attr;                                                            \
-    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO>), grid, dim3(256), lds, s, *a, tps, ns, dir);          \
+#define MZ_CASE(BB)                                                                                           \
+  case BB: {                                                                                                  \
+    constexpr bool F = FAST && BB <= 6;                                                                       \
+    const size_t lds = Lds<D>::bytes(BB, F);                                                                  \
+    static const hipError_t attr = hipFuncSetAttribute(                                                       \
+        (const void*)decode_split_kernel<D, BB, IO, F>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+    if (attr != hipSuccess) return (int)attr;                                                                 \
+    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO, F>), grid, dim3(256), lds, s, *a, tps, ns, dir);       \
   } break;
     MZ_CASE(1) MZ_CASE(2) MZ_CASE(3) MZ_CASE(4) MZ_CASE(5) MZ_CASE(6) MZ_CASE(7) MZ_CASE(8)
 #undef MZ_CASE
@@ -727,12 +802,20 @@ static int decode_check_launchable(const mz_decode_args* a) {
   return MZ_OK;
 }
 
-static int launch_general(const mz_decode_args* a, hipStream_t s, bool direct) {
+template <bool FAST>
+static int launch_general_t(const mz_decode_args* a, hipStream_t s, bool direct) {
   if (a->head_dim == 128)
-    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s, direct)
-                                  : launch_partials<128, MZ_F16>(a, s, direct);
-  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16>(a, s, direct)
-                                : launch_partials<64, MZ_F16>(a, s, direct);
+    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16, FAST>(a, s, direct)
+                                  : launch_partials<128, MZ_F16, FAST>(a, s, direct);
+  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16, FAST>(a, s, direct)
+                                : launch_partials<64, MZ_F16, FAST>(a, s, direct);
+}
+
+// kernel_path "exact" keeps the bit-exact dequantization; otherwise codes of
+// up to 6 bits take the fast (fp32 codebook) form
+static int launch_general(const mz_decode_args* a, hipStream_t s, bool direct) {
+  return a->kernel_path == MZ_PATH_EXACT ? launch_general_t<false>(a, s, direct)
+                                         : launch_general_t<true>(a, s, direct);
 }
 
 extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t stream) {
