@@ -186,6 +186,36 @@ int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
 int muzero_decode_partials(const mz_decode_args* args, mz_stream_t stream);
 int muzero_decode_combine(const mz_decode_args* args, mz_stream_t stream);
 
+/*
+ * Decode-step prologue of one attention layer for a single new token: per
+ * head RMSNorm of q and k (Qwen3's q_norm / k_norm; omitted when both weights
+ * are null), rotary embedding q*cos + rotate_half(q)*sin (transformers'
+ * apply_rotary_pos_emb), the new key and value rows written into the cache
+ * layer's residual window, and the query written as the decode-attention
+ * query.  Replaces the per-op torch work of the patched attention forward
+ * (muzero/integrations/transformers_patch.py:402-431 keeps the model's own
+ * norm, rope and cache.update there) with one launch.  q [B, Hq, D], k / v
+ * [B, Hkv, D] (the projections with the token dimension dropped), cos / sin
+ * [B, D] (cs_sb = 0 broadcasts one row), norm weights [D]; outputs q_out
+ * [B, Hq, D] and the residual rows k_dst / v_dst [B, Hkv, D].  Strides in
+ * elements, last dimension contiguous; head_dim 64 or 128; bf16 or fp16.
+ * The norm's mean of squares is an fp32 wave reduction: normalized values can
+ * differ from torch's in the last bit of the io dtype.  No counterpart in the
+ * reference's extension: the reference leaves these ops to the model.
+ */
+typedef struct mz_prologue_args {
+  int batch, q_heads, kv_heads, head_dim, io_dtype;
+  const void* q; int64_t q_sb, q_sh;
+  const void* k; int64_t k_sb, k_sh;
+  const void* v; int64_t v_sb, v_sh;
+  const void* cos; const void* sin; int64_t cs_sb;
+  const void* q_norm_w; const void* k_norm_w; float eps;
+  void* q_out; int64_t qo_sb, qo_sh;
+  void* k_dst; int64_t kd_sb, kd_sh;
+  void* v_dst; int64_t vd_sb, vd_sh;
+} mz_prologue_args;
+int muzero_decode_prologue(const mz_prologue_args* args, mz_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,22 @@ class DecodeArgs(ctypes.Structure):
         ("v_prefix", c_int),
     ]
 
+class PrologueArgs(ctypes.Structure):
+    """Mirror of ``mz_prologue_args`` (include/muzero_hip.h)."""
+
+    _fields_ = [
+        ("batch", c_int), ("q_heads", c_int), ("kv_heads", c_int), ("head_dim", c_int), ("io_dtype", c_int),
+        ("q", c_vp), ("q_sb", c_i64), ("q_sh", c_i64),
+        ("k", c_vp), ("k_sb", c_i64), ("k_sh", c_i64),
+        ("v", c_vp), ("v_sb", c_i64), ("v_sh", c_i64),
+        ("cos", c_vp), ("sin", c_vp), ("cs_sb", c_i64),
+        ("q_norm_w", c_vp), ("k_norm_w", c_vp), ("eps", c_float),
+        ("q_out", c_vp), ("qo_sb", c_i64), ("qo_sh", c_i64),
+        ("k_dst", c_vp), ("kd_sb", c_i64), ("kd_sh", c_i64),
+        ("v_dst", c_vp), ("vd_sb", c_i64), ("vd_sh", c_i64),
+    ]
+
+
 MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2
 
 
@@ -77,6 +93,7 @@ SIGNATURES = {
     "muzero_decode_uses_fold": (c_int, [ctypes.POINTER(DecodeArgs)]),
     "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_prologue": (c_int, [ctypes.POINTER(PrologueArgs), c_vp]),
 }
 
 _lib = None

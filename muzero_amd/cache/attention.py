@@ -75,19 +75,38 @@ def mu_zero_decode_attention_forward(
     if n_groups == 0 and not has_res:
         raise RuntimeError("MuZero attention produced no output; both quantized prefix and dense residual are empty")
 
-    out = _k.mu_zero_decode_attention_hip(
-        query,
-        bits=layer.nbits,
-        n_groups=n_groups,
-        k_packed=layer._packed_key_q, k_mn=layer._key_mn, k_scale=layer._key_scale,
-        v_packed=layer._packed_value_q, v_mn=layer._value_mn, v_scale=layer._value_scale,
-        k_res=keys if has_res else None, v_res=values if has_res else None,
-        alpha_key=float(layer._selected_alpha_key if layer._selected_alpha_key is not None else 2.0),
-        alpha_value=float(layer._selected_alpha_value if layer._selected_alpha_value is not None else 2.0),
-        scaling=float(scaling),
-        attention_mask=attention_mask,
-        value_prefix=value_prefix_length,
-    )
+    alpha_key = float(layer._selected_alpha_key if layer._selected_alpha_key is not None else 2.0)
+    alpha_value = float(layer._selected_alpha_value if layer._selected_alpha_value is not None else 2.0)
+    r = int(keys.shape[2]) if has_res else 0
+    # Decode steps of one layer differ only in the query, the prefix and
+    # residual lengths and the output: once the arguments have been built and
+    # validated for a layer's storage, later steps only patch those fields.
+    fast = getattr(layer, "_hip_decode", None)
+    key = None
+    if attention_mask is None and has_res and value_prefix_length == key_prefix_length:
+        key = (id(layer._kstore.packed), id(layer._vstore.packed), layer._kstore.count > 0,
+               id(layer._key_buffer), id(layer._value_buffer), layer._key_buffer is not None,
+               query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key, alpha_value,
+               float(scaling))
+    if fast is not None and key is not None and fast.key == key:
+        out = fast.launch(query, n_groups, r)
+    else:
+        plan = _k.DecodePlan(
+            query,
+            bits=layer.nbits,
+            n_groups=n_groups,
+            k_packed=layer._packed_key_q, k_mn=layer._key_mn, k_scale=layer._key_scale,
+            v_packed=layer._packed_value_q, v_mn=layer._value_mn, v_scale=layer._value_scale,
+            k_res=keys if has_res else None, v_res=values if has_res else None,
+            alpha_key=alpha_key, alpha_value=alpha_value,
+            scaling=float(scaling),
+            attention_mask=attention_mask,
+            value_prefix=value_prefix_length,
+        )
+        out = plan.run()
+        # cache the validated arguments only when every pointer they hold is
+        # stable across steps (residual in its capacity buffer, no mask)
+        layer._hip_decode = _k.StepDecode(plan, key) if key is not None and key[5] else None
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1
     return out, None

@@ -245,6 +245,23 @@ class MuZeroCacheLayer:
         self._value_buffer = None
         self._buffer_capacity = 0
 
+    def decode_append_slot(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """Reserve the residual rows of one decode token and return them (key and value views
+        ``[B, H, 1, D]``) for the caller to write; :meth:`decode_append_commit` then appends the
+        token as :meth:`update` would (the fused decode prologue writes the rows in place)."""
+        old_k, old_v = int(self.keys.shape[2]), int(self.values.shape[2])
+        self._reserve_residual_buffer(max(old_k + 1, old_v + 1))
+        self._pending_append = (old_k, old_v)
+        return (self._key_buffer[:, :, old_k:old_k + 1, :], self._value_buffer[:, :, old_v:old_v + 1, :])
+
+    def decode_append_commit(self) -> None:
+        old_k, old_v = self._pending_append
+        self._pending_append = None
+        self.keys = self._key_buffer[:, :, :old_k + 1, :]
+        self.values = self._value_buffer[:, :, :old_v + 1, :]
+        self.cumulative_length += 1
+        self.compress_residual_prefix(decode_flush=True)
+
     def _drop_residual_prefix(self, key_len: int, value_len: int) -> None:
         if key_len > 0:
             remaining = int(self.keys.shape[2]) - key_len

@@ -33,6 +33,7 @@ import torch
 from ..cache.attention import mu_zero_decode_attention_forward
 from ..cache.layer import MuZeroCacheLayer
 from ..config import MuZeroConfig
+from ..kernels import loader as _kernels
 
 try:
     from transformers.cache_utils import Cache as _HFCache
@@ -333,10 +334,56 @@ def _patch_attention_forward(module, cls_name: str) -> None:
     original = cls.forward
     qk_norm = cls_name == "Qwen3Attention"
 
+    def _fused_step(self, hidden_states, position_embeddings, attention_mask, past_key_values, kwargs):
+        """A decode step with the prologue (q/k norm, rope, residual append) in one HIP launch;
+        None when the step does not qualify (then the per-op path runs)."""
+        if os.environ.get("MUZERO_DISABLE_FUSED_DECODE", "0") == "1" or \
+                os.environ.get("MUZERO_DISABLE_FUSED_PROLOGUE", "0") == "1":
+            return None
+        if self.training or hidden_states.dim() != 3 or hidden_states.shape[1] != 1 or \
+                past_key_values.defer_prefill_quantization or self.layer_idx >= len(past_key_values.layers):
+            return None
+        layer = past_key_values.layers[self.layer_idx]
+        if not layer.is_initialized or layer.keys is None or layer.keys.dim() != 4 or layer.keys.shape[2] == 0:
+            return None
+        cos, sin = position_embeddings
+        b = hidden_states.shape[0]
+        d = self.head_dim
+        if d not in (64, 128) or hidden_states.dtype not in (torch.bfloat16, torch.float16) or \
+                cos.dim() != 3 or cos.shape[1] != 1 or cos.shape[0] not in (1, b) or cos.dtype != hidden_states.dtype:
+            return None
+        if qk_norm:
+            qn, kn = self.q_norm, self.k_norm
+            qw, kw, eps = qn.weight, kn.weight, float(qn.variance_epsilon)
+            if float(kn.variance_epsilon) != eps:
+                return None
+        else:
+            qw = kw = None
+            eps = 0.0
+        q = self.q_proj(hidden_states).view(b, -1, d)
+        k = self.k_proj(hidden_states).view(b, -1, d)
+        v = self.v_proj(hidden_states).view(b, -1, d)
+        if self.layer_idx == 0:
+            past_key_values._seen_tokens += 1
+        k_row, v_row = layer.decode_append_slot()
+        query_states = _kernels.decode_prologue(q, k, v, cos[:, 0], sin[:, 0], qw, kw, eps,
+                                                k_row[:, :, 0], v_row[:, :, 0])
+        layer.decode_append_commit()
+        kwargs["kv_cache_state"] = layer.get_attention_state()
+        extra = {"sliding_window": getattr(self, "sliding_window", None)} if qk_norm else {}
+        attn_output, attn_weights = module.eager_attention_forward(
+            self, query_states, layer.keys, layer.values, attention_mask, dropout=0.0,
+            scaling=self.scaling, **extra, **kwargs)
+        attn_output = attn_output.reshape(b, 1, -1).contiguous()
+        return self.o_proj(attn_output), attn_weights
+
     def _muzero_forward(self, hidden_states, position_embeddings=None, attention_mask=None,
                         past_key_values=None, **kwargs):
         if not _is_mu_zero_cache(past_key_values) or position_embeddings is None:
             return original(self, hidden_states, position_embeddings, attention_mask, past_key_values, **kwargs)
+        fused_step = _fused_step(self, hidden_states, position_embeddings, attention_mask, past_key_values, kwargs)
+        if fused_step is not None:
+            return fused_step
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
         q = self.q_proj(hidden_states).view(hidden_shape)

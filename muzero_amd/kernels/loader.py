@@ -317,6 +317,83 @@ class DecodePlan:
         return self.out
 
 
+class StepDecode:
+    """A validated :class:`DecodePlan` re-launched for later decode steps of the same
+    cache layer: the caller guarantees (through ``key``) that every tensor the plan
+    points into is the same storage with the same strides, so only the query, the
+    prefix/residual lengths, the output and the workspace size change."""
+
+    __slots__ = ("key", "args", "argp", "lib", "device", "q_dtype", "out_shape", "workspace", "_keep",
+                 "_keep_query")
+
+    def __init__(self, plan: DecodePlan, key):
+        self.key = key
+        self.args = plan.args
+        self.argp = ctypes.byref(plan.args)
+        self.lib = plan._lib
+        self.device = plan.device
+        self.q_dtype = plan.out.dtype
+        self.out_shape = tuple(plan.out.shape)
+        self.workspace = plan.workspace
+        self._keep = plan._keep  # tables, packed/residual views: kept alive with the arguments
+
+    def launch(self, query: torch.Tensor, n_groups: int, n_residual: int) -> torch.Tensor:
+        a = self.args
+        q = query
+        if q.data_ptr() % 16 or q.stride(0) != a.q_sb or q.stride(1) != a.q_sh or q.stride(3) != 1:
+            q = query.contiguous()  # as the plan did (the key pins the query's layout)
+            _require(q.stride(0) == a.q_sb and q.stride(1) == a.q_sh, "query layout changed")
+        a.query = q.data_ptr()
+        a.n_groups, a.n_residual = int(n_groups), int(n_residual)
+        out = torch.empty(self.out_shape, dtype=self.q_dtype, device=self.device)
+        a.out = out.data_ptr()
+        need = self.lib.muzero_decode_workspace_bytes(self.argp, None)
+        _require(need >= 0, "decode arguments rejected")
+        if need > a.workspace_bytes:
+            self.workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=self.device)
+            a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = max(int(need), int(a.workspace_bytes))
+        check(self.lib.muzero_decode_attention(self.argp, stream_ptr(self.device)), "muzero_decode_attention")
+        self._keep_query = q  # alive until the next launch (the kernel reads it asynchronously)
+        return out
+
+
+def decode_prologue(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                    q_norm_w: torch.Tensor | None, k_norm_w: torch.Tensor | None, eps: float,
+                    k_dst: torch.Tensor, v_dst: torch.Tensor) -> torch.Tensor:
+    """One new token's attention prologue in one launch (``muzero_decode_prologue``).
+
+    ``q [B, Hq, D]``, ``k``/``v`` ``[B, Hkv, D]`` (projections, token dim dropped; last dim
+    contiguous), ``cos``/``sin`` ``[B or 1, D]``, Qwen3 ``q_norm``/``k_norm`` weights ``[D]`` or
+    None (no per-head norm, as Llama), ``k_dst``/``v_dst`` ``[B, Hkv, D]`` views of the cache's
+    residual rows for the token (written).  Returns the decode query ``[B, Hq, 1, D]``.
+    """
+    b, hq, d = q.shape
+    hkv = k.shape[1]
+    _require(q.dtype in (torch.bfloat16, torch.float16) and k.dtype == v.dtype == q.dtype
+             and cos.dtype == sin.dtype == q.dtype, "prologue dtypes")
+    _require(q.stride(2) == k.stride(2) == v.stride(2) == k_dst.stride(2) == v_dst.stride(2) == 1
+             and cos.stride(-1) == sin.stride(-1) == 1 and cos.stride() == sin.stride(), "prologue layouts")
+    _require((q_norm_w is None) == (k_norm_w is None), "q_norm and k_norm go together")
+    out = torch.empty((b, hq, 1, d), dtype=q.dtype, device=q.device)
+    a = _lib.PrologueArgs()
+    a.batch, a.q_heads, a.kv_heads, a.head_dim, a.io_dtype = b, hq, hkv, d, DTYPE_ENUM[q.dtype]
+    a.q, a.q_sb, a.q_sh = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_sb, a.k_sh = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_sb, a.v_sh = v.data_ptr(), v.stride(0), v.stride(1)
+    a.cos, a.sin, a.cs_sb = cos.data_ptr(), sin.data_ptr(), (cos.stride(0) if cos.shape[0] > 1 else 0)
+    if q_norm_w is not None:
+        _require(q_norm_w.dtype == k_norm_w.dtype == q.dtype and q_norm_w.is_contiguous()
+                 and k_norm_w.is_contiguous(), "norm weights")
+        a.q_norm_w, a.k_norm_w = q_norm_w.data_ptr(), k_norm_w.data_ptr()
+    a.eps = float(eps)
+    a.q_out, a.qo_sb, a.qo_sh = out.data_ptr(), out.stride(0), out.stride(1)
+    a.k_dst, a.kd_sb, a.kd_sh = k_dst.data_ptr(), k_dst.stride(0), k_dst.stride(1)
+    a.v_dst, a.vd_sb, a.vd_sh = v_dst.data_ptr(), v_dst.stride(0), v_dst.stride(1)
+    check(load().muzero_decode_prologue(ctypes.byref(a), stream_ptr(q.device)), "muzero_decode_prologue")
+    return out
+
+
 def mu_zero_decode_attention_hip(query: torch.Tensor, **kwargs) -> torch.Tensor:
     """Fused decode attention; returns ``[B, 1, Hq, D]`` in the query dtype.
 

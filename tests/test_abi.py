@@ -50,11 +50,12 @@ def test_version_and_strerror():
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-def test_decode_args_layout_matches_c(tmp_path):
-    fields = [f for f, _ in _lib.DecodeArgs._fields_]
+@pytest.mark.parametrize("cls,cname", [(_lib.DecodeArgs, "mz_decode_args"), (_lib.PrologueArgs, "mz_prologue_args")])
+def test_args_layout_matches_c(tmp_path, cls, cname):
+    fields = [f for f, _ in cls._fields_]
     src = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {",
-           '  printf("size %zu\\n", sizeof(mz_decode_args));']
-    src += [f'  printf("{f} %zu\\n", offsetof(mz_decode_args, {f}));' for f in fields]
+           f'  printf("size %zu\\n", sizeof({cname}));']
+    src += [f'  printf("{f} %zu\\n", offsetof({cname}, {f}));' for f in fields]
     src += ["  return 0;", "}"]
     c = tmp_path / "layout.c"
     c.write_text("\n".join(src))
@@ -62,9 +63,9 @@ def test_decode_args_layout_matches_c(tmp_path):
     subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(c)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     got = dict(line.split() for line in out if line)
-    assert int(got["size"]) == ctypes.sizeof(_lib.DecodeArgs)
+    assert int(got["size"]) == ctypes.sizeof(cls)
     for f in fields:
-        assert int(got[f]) == getattr(_lib.DecodeArgs, f).offset, f
+        assert int(got[f]) == getattr(cls, f).offset, f
 
 
 def test_decode_workspace_rejects_bad_args_without_a_device():

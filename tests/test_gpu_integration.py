@@ -92,6 +92,31 @@ def test_logq_compatible_layout_decode(bits):
     assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
 
 
+def test_step_decode_reuse_matches_fresh_plan():
+    """After its first decode call a layer re-launches cached arguments (only the query, lengths and
+    output change); across 140 steps, two flushes included, every output equals a freshly built plan's."""
+    from muzero_amd.kernels import loader as L
+    B, hkv, n_rep, d, prefill, steps = 2, 2, 4, 128, 600, 140
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=17)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0))
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    qd = q.to(DEV)
+    reused = 0
+    for t in range(prefill, prefill + steps):
+        layer.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), {"materialize_full_kv": False})
+        state = layer.get_attention_state()
+        had = getattr(layer, "_hip_decode", None)
+        out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), qd, None, d ** -0.5, state)
+        reused += had is not None and layer._hip_decode is had
+        fresh = L.DecodePlan(qd, bits=4, n_groups=state["key_prefix_length"] // 64, k_packed=layer._packed_key_q,
+                             k_mn=layer._key_mn, k_scale=layer._key_scale, v_packed=layer._packed_value_q,
+                             v_mn=layer._value_mn, v_scale=layer._value_scale, k_res=layer.keys,
+                             v_res=layer.values, alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5).run()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), fresh.view(torch.int16)), t
+    assert reused >= steps - 4  # cached arguments served all but the steps after a storage change
+
+
 def test_materialized_kv_matches_dequantized_oracle():
     """``update(materialize_full_kv=True)`` returns the dequantised prefix + residual, bit-exact
     to the reference's torch dequantisation in the layer dtype."""
