@@ -91,7 +91,7 @@ def time_region(fn, steps, stream):
     return start.elapsed_time(end) / steps
 
 
-def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads):
+def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alpha_v=2.0):
     """The reference's CPU decode path (oracle restatement) on `sample_batch` batch rows."""
     from oracle import reference_torch as ref
     torch.set_num_threads(threads)
@@ -101,8 +101,9 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads):
 
     def run():
         if lq:
-            kq = ref.dequantize_key_block(c["k_packed"], c["k_mn"], c["k_scale"], bits, 2.0, 64, torch.bfloat16)
-            vq = ref.dequantize_value_block(c["v_packed"], c["v_mn"], c["v_scale"], bits, 2.0, 64, d, torch.bfloat16)
+            kq = ref.dequantize_key_block(c["k_packed"], c["k_mn"], c["k_scale"], bits, alpha_k, 64, torch.bfloat16)
+            vq = ref.dequantize_value_block(c["v_packed"], c["v_mn"], c["v_scale"], bits, alpha_v, 64, d,
+                                            torch.bfloat16)
         else:
             kq = c["k_res"][:, :, :0]
             vq = c["v_res"][:, :, :0]
@@ -117,6 +118,143 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads):
         if el > 8.0 or reps >= 3:
             break
     return el / reps
+
+
+def quantize_bytes(B, hkv, d, tokens, bits, in_bytes=2):
+    """One flush of `tokens` tokens: bf16 K and V read, packed codes + metadata written."""
+    qb, ng = 8 * bits, (d + 63) // 64
+    groups = B * hkv * (tokens // 64) * d + B * hkv * tokens * ng
+    return 2 * B * hkv * tokens * d * in_bytes + groups * (qb + 4)
+
+
+class _Module:
+    """What the decode hook reads from the attention module."""
+
+    def __init__(self, n_rep):
+        self.num_key_value_groups = n_rep
+        self.training = False
+
+
+def run_stream(args):
+    """Config 2: one quantize pass, then `--stream` decode steps through the cache layer.
+
+    Each step appends one token to every (batch, kv-head) (`MuZeroCacheLayer.update`,
+    flushing a 64-token group into the packed store whenever the residual window
+    reaches 192 tokens, decode_flush_by_group=True) and runs the decode attention
+    hook over the packed prefix and the residual.  The timed region is the whole
+    stream (HIP events on the launch stream); per-step events split it into flush
+    steps and plain steps.  Bytes: each step's decode bytes at its own (Lq, R) plus
+    each flush's quantize bytes.
+    """
+    import muzero_amd as mz
+    from muzero_amd.cache.layer import MuZeroCacheLayer
+    dev = torch.device("cuda:0")
+    B, hkv, hq, d = args.batch, 8, 32, 128
+    L, R, bits, steps = args.context, args.residual, args.bits, args.stream
+    k, v, q = make_inputs(B, hkv, hq, L + steps, d, 1234, dev)
+    qs = [torch.randn(q.shape, generator=torch.Generator(device=dev).manual_seed(i), device=dev).to(q.dtype)
+          for i in range(8)]
+    cfg = mz.MuZeroConfig(bits=bits if bits in (1, 2, 3, 4, 7, 8) else 4, residual_length=R,
+                          decode_flush_by_group=True)
+    # 5- and 6-bit are rejected by MuZeroConfig (as by the reference's config,
+    # muzero/config.py:37-39); the kernels serve them, so the stream sets the
+    # width after validation to time config 2's 5-bit case
+    cfg.bits = bits
+    module, scaling = _Module(hq // hkv), d ** -0.5
+    stream = torch.cuda.current_stream(dev)
+
+    def one_pass(timed):
+        layer = MuZeroCacheLayer(cfg)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 2)]
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        layer.update(k[:, :, :L], v[:, :, :L], {"materialize_full_kv": False})
+        ev[1].record(stream)
+        shapes = []
+        for t in range(steps):
+            before = layer._kstore.count
+            layer.update(k[:, :, L + t:L + t + 1], v[:, :, L + t:L + t + 1], {"materialize_full_kv": False})
+            st = layer.get_attention_state()
+            out = mz.mu_zero_decode_attention_forward(module, qs[t % len(qs)], None, scaling, st)
+            if out is None:
+                raise RuntimeError("decode hook declined the step")
+            shapes.append((st["key_prefix_length"], layer.keys.shape[2], layer._kstore.count > before))
+            ev[t + 2].record(stream)
+        torch.cuda.synchronize()
+        if not timed:
+            return None
+        times = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps + 1)]
+        return layer, times, shapes
+
+    one_pass(False)  # warm: library load, alpha selection code paths, allocator
+    mz.reset_mu_zero_decode_stats()
+    layer, times, shapes = one_pass(True)
+    stats = mz.get_mu_zero_decode_stats()
+    lq0 = max(L - R, 0) // 64 * 64
+    quant_ms, step_ms = times[0], times[1:]
+    decode_bytes = sum(algorithmic_bytes(B, hkv, hq, d, lq, r, bits) for lq, r, _ in shapes)
+    flush_bytes = sum(quantize_bytes(B, hkv, d, 64, bits) for _, _, f in shapes if f)
+    stream_ms = sum(step_ms)
+    plain = [t for t, s in zip(step_ms, shapes) if not s[2]]
+    flush = [t for t, s in zip(step_ms, shapes) if s[2]]
+    pass_bytes = quantize_bytes(B, hkv, d, lq0, bits)
+    gbs = (decode_bytes + flush_bytes) / (stream_ms * 1e-3) / 1e9
+    plain_bytes = [algorithmic_bytes(B, hkv, hq, d, lq, r, bits) for lq, r, f in shapes if not f]
+    plain_gbs = sum(plain_bytes) / (sum(plain) * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(os.cpu_count() or 1, 16)
+        lq_last, r_last, _ = shapes[-1]
+        c = dict(k_packed=layer._packed_key_q, k_mn=layer._key_mn, k_scale=layer._key_scale,
+                 v_packed=layer._packed_value_q, v_mn=layer._value_mn, v_scale=layer._value_scale,
+                 k_res=layer.keys, v_res=layer.values)
+        sec = cpu_baseline(c, qs[0], bits, lq_last, d, args.cpu_sample_batch, threads,
+                           alpha_k=layer._selected_alpha_key, alpha_v=layer._selected_alpha_value)
+        sec_stream = sec * B / args.cpu_sample_batch * steps
+        cpu = {"value": round(decode_bytes / sec_stream / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port", "seconds_per_stream_full_batch": round(sec_stream, 1),
+               "cpu": platform.processor() or platform.machine(),
+               "sample": f"the last step's decode (Lq={lq_last}, R={r_last}) on batch rows "
+                         f"0..{args.cpu_sample_batch - 1} of {B} (dequantize prefix + attend, oracle restatement "
+                         f"of attention.py:179-295), time x {B // args.cpu_sample_batch} x {steps} steps "
+                         "(extrapolated; flushes not included)"}
+
+    line = {
+        "metric": "packed-KV decode attn HBM GB/s (% of peak); decode tokens/sec at B=64 ctx 4096",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 1,
+        "ms_per_step": round(stream_ms / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"cfg2 stream: Qwen3-8B layer B={B} Hq=32 Hkv=8 hd=128, prefill {L} tokens "
+                               f"(one quantize pass), then {steps} decode steps through MuZeroCacheLayer + "
+                               f"the decode hook, mu_zero {bits}-bit G64 R={R} fp16 meta, "
+                               "decode_flush_by_group=True",
+                   "batch": B, "context": L, "bits": bits, "residual": R, "decode_steps": steps},
+        "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "quantize_pass_ms": round(quant_ms, 4),
+        "quantize_pass_GBps": round(pass_bytes / (quant_ms * 1e-3) / 1e9, 1),
+        "stream_ms": round(stream_ms, 3),
+        "plain_steps": len(plain), "plain_step_ms_mean": round(sum(plain) / max(len(plain), 1), 5),
+        "flush_steps": len(flush), "flush_step_ms_mean": round(sum(flush) / max(len(flush), 1), 5),
+        "prefix_tokens_first_last": [shapes[0][0], shapes[-1][0]],
+        "decode_bytes": decode_bytes, "flush_bytes": flush_bytes,
+        "one_layer_tokens_per_s": round(B * steps / (stream_ms * 1e-3), 1),
+        "fused_decode_calls": stats.get("hip_fused_decode", 0),
+        "alphas": [layer._selected_alpha_key, layer._selected_alpha_value],
+        "roofline": {"bound": "hbm", "achieved": round(plain_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(plain_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "basis": "plain (non-flush) steps: decode bytes / step time (append + decode kernel)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
 
 
 def copy_calibration(mib, steps):
@@ -147,6 +285,9 @@ def main():
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (HBM counter calibration)")
+    ap.add_argument("--stream", type=int, default=0,
+                    help="config 2: a quantize pass, then this many decode steps through the cache layer "
+                         "with per-group flushes (use with --batch 128 --bits 1|2|3|5)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -155,6 +296,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb, args.steps)
+        return
+    if args.stream:
+        run_stream(args)
         return
 
     from muzero_amd.kernels.loader import DecodePlan

@@ -29,7 +29,7 @@ import torch.nn.functional as F
 
 from ..config import MuZeroConfig
 from ..kernels import loader as _k
-from ..quantizer import dequantize_rows, quantize_rows, select_alpha
+from ..quantizer import dequantize_rows, quantize_rows, select_alpha, select_alpha_block
 
 _STORE_ATTRS = ("packed", "mn", "scale")
 
@@ -299,11 +299,14 @@ class MuZeroCacheLayer:
         if getattr(self, attr) is not None or self.nbits == 4:
             return self._ensure_alpha(block, kind)  # preset, or 4-bit: no statistics
         bs, nh, sl, hd = block.shape
-        if kind == "key":
-            nsg = sl // self.q_group_size
-            flat = block.reshape(bs, nh, nsg, self.q_group_size, hd).permute(0, 1, 2, 4, 3).contiguous()
-        else:
-            flat = F.pad(block, (0, self.v_head_dim_padded - hd)) if self.v_head_dim_padded != hd else block
+        if kind == "key" or self.v_head_dim_padded == hd:
+            # the same statistics gathered from the block itself (no grouped copy)
+            alpha = select_alpha_block(block, bits=self.nbits, q_group_size=self.q_group_size, kind=kind,
+                                       max_points=self.cfg.stats_max_points)
+            setattr(self, attr, alpha)
+            return alpha
+        # values whose head_dim is padded to whole groups: the padded copy, as the reference makes it
+        flat = F.pad(block, (0, self.v_head_dim_padded - hd))
         return self._ensure_alpha(flat.reshape(-1, self.q_group_size), kind)
 
     # ------------------------------------------------------------------

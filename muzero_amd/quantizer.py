@@ -48,28 +48,107 @@ def select_alpha(
     For ``bits == 4`` this is always 2.0 and no statistics are computed
     (``quantizer.py:42-43``).  Otherwise the decision follows the reference's
     percentile and zero-anchor statistics rules (``quantizer.py:46-83``),
-    evaluated with the same torch operations on the tensor's device.
+    evaluated on the tensor's device with the same values: the subsample and
+    the group min / max are taken in the tensor's own dtype and converted to
+    fp32 afterwards (exact), so no fp32 copy of the whole tensor is made.
     """
     if bits == 4:
         return 2.0
+    sample = _subsample(tensor, max_points)
+    mn, mx = torch.aminmax(_prepare_groups(tensor, q_group_size=q_group_size, kind=kind), dim=-1)
+    return _decide_alpha(*_alpha_statistics(sample, mn, mx), bits=bits, kind=kind)
 
-    sample = _subsample(tensor.float(), max_points)
-    abs_sample = sample.abs()
+
+def select_alpha_block(
+    block: torch.Tensor,
+    *,
+    bits: int,
+    q_group_size: int,
+    kind: str,
+    max_points: int = 65536,
+) -> float:
+    """``select_alpha`` of the rows the cache quantizes from ``block [B, H, T, D]``.
+
+    The reference's cache flattens a key block to ``[B, H, T/G, D, G]`` rows
+    (one row per channel and 64-token group, ``layer.py:276-278``) and a value
+    block to ``[B, H, T, D/G, G]`` rows, then calls ``select_alpha`` on them
+    (``layer.py:223-234``).  This computes the same statistics without
+    materializing that copy: the subsample is gathered at the positions the
+    flattened layout would give, and the group min / max are reductions of a
+    view over the token (key) or channel (value) axis, in the flattened
+    layout's group order.
+    Requires ``T`` (keys) or ``D`` (values) to be a
+    multiple of the group size.
+    """
+    if bits == 4:
+        return 2.0
+    return _decide_alpha(*_block_statistics(block, q_group_size, kind, max_points), bits=bits, kind=kind)
+
+
+def _block_statistics(block: torch.Tensor, q_group_size: int, kind: str, max_points: int) -> list[float]:
+    """``_alpha_statistics`` of the rows the cache flattens ``block`` into (see ``select_alpha_block``)."""
+    B, H, T, D = (int(x) for x in block.shape)
+    G = q_group_size
+    dev = block.device
+    if kind == "key":
+        if T % G:
+            raise ValueError(f"key block length {T} is not a multiple of the group size {G}")
+        nsg = T // G
+        pos = _subsample_positions(B * H * nsg * D * G, max_points, dev)  # flat order (b, h, g, c, t)
+        t, r = pos % G, pos // G
+        c, r = r % D, r // D
+        g, bh = r % nsg, r // nsg
+        sample = block[bh // H, bh % H, g * G + t, c]
+        # groups in order (b, h, g, c): a reduction over the strided token axis
+        mn, mx = torch.aminmax(block.reshape(B, H, nsg, G, D), dim=3)
+    else:
+        if D % G:
+            raise ValueError(f"value head_dim {D} is not a multiple of the group size {G}")
+        pos = _subsample_positions(B * H * T * D, max_points, dev)  # flat order (b, h, t, c)
+        c, r = pos % D, pos // D
+        t, bh = r % T, r // T
+        sample = block[bh // H, bh % H, t, c]
+        mn, mx = _halving_minmax(block.reshape(B, H, T, D // G, G))  # groups in order (b, h, t, g)
+    # the reference reduces the group statistics of its [N, G] rows as [1, 1, 1, N]
+    return _alpha_statistics(sample, mn.reshape(1, 1, 1, -1), mx.reshape(1, 1, 1, -1))
+
+
+def _halving_minmax(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """min / max over the last axis (a power of two) by pairwise halving: torch's
+    reduction over a short innermost axis runs far below bandwidth, elementwise
+    minimum / maximum of the two halves do not.  Same values as amin / amax
+    (NaN propagates through both)."""
+    h = x.shape[-1] // 2
+    mn, mx = torch.minimum(x[..., :h], x[..., h:]), torch.maximum(x[..., :h], x[..., h:])
+    while h > 1:
+        h //= 2
+        mn, mx = torch.minimum(mn[..., :h], mn[..., h:]), torch.maximum(mx[..., :h], mx[..., h:])
+    return mn[..., 0], mx[..., 0]
+
+
+def _alpha_statistics(sample: torch.Tensor, mn: torch.Tensor, mx: torch.Tensor) -> list[float]:
+    """(p50, p95, p99 of |sample|, mean zero-anchor offset) with one device sync.
+
+    ``kthvalue(x, k)`` is the k-th smallest element, i.e. ``sort(x)[k - 1]``:
+    one sort serves the three percentiles.
+    """
     eps = 1e-8
-    n = abs_sample.numel()
-    flat = abs_sample.reshape(-1)
-    p50_abs = float(torch.kthvalue(flat, max(1, int(0.50 * n))).values.item())
-    p95_abs = float(torch.kthvalue(flat, max(1, int(0.95 * n))).values.item())
-    p99_abs = float(torch.kthvalue(flat, max(1, int(0.99 * n))).values.item())
+    flat = sample.float().abs().reshape(-1)
+    n = flat.numel()
+    srt = torch.sort(flat).values
+    ks = [max(1, int(f * n)) - 1 for f in (0.50, 0.95, 0.99)]
+    mnf, mxf = mn.float(), mx.float()
+    zero_anchor = ((0.0 - mnf) / (mxf - mnf).clamp_min(eps)).clamp(0.0, 1.0)
+    anchor_offset = (zero_anchor - 0.5).abs().mean()
+    return torch.stack([srt[ks[0]], srt[ks[1]], srt[ks[2]], anchor_offset]).tolist()
 
+
+def _decide_alpha(p50_abs: float, p95_abs: float, p99_abs: float, anchor_offset: float, *,
+                  bits: int, kind: str) -> float:
+    """The reference's alpha rules on the statistics (``quantizer.py:57-83``)."""
+    eps = 1e-8
     tail_ratio = p99_abs / max(p95_abs, eps)
     concentration_ratio = p95_abs / max(p50_abs, eps)
-
-    grouped = _prepare_groups(tensor, q_group_size=q_group_size, kind=kind)
-    mn = grouped.amin(dim=-1)
-    mx = grouped.amax(dim=-1)
-    zero_anchor = ((0.0 - mn) / (mx - mn).clamp_min(eps)).clamp(0.0, 1.0)
-    anchor_offset = float((zero_anchor - 0.5).abs().mean().item())
 
     if kind == "key":
         if bits == 1:
@@ -91,6 +170,14 @@ def select_alpha(
     return 2.0
 
 
+def _subsample_positions(numel: int, max_points: int, device) -> torch.Tensor:
+    """Flat positions ``_subsample`` keeps: every ``numel // max_points``-th, at most ``max_points``."""
+    if numel <= max_points:
+        return torch.arange(numel, device=device)
+    step = max(1, numel // max_points)
+    return torch.arange(min(max_points, -(-numel // step)), device=device) * step
+
+
 def _subsample(tensor: torch.Tensor, max_points: int) -> torch.Tensor:
     """Every ``numel // max_points``-th element, at most ``max_points`` (``quantizer.py:86-91``)."""
     flat = tensor.reshape(-1)
@@ -102,8 +189,9 @@ def _subsample(tensor: torch.Tensor, max_points: int) -> torch.Tensor:
 
 def _prepare_groups(tensor: torch.Tensor, *, q_group_size: int, kind: str) -> torch.Tensor:
     """Groups of ``q_group_size`` values as the cache forms them (``quantizer.py:94-112``):
-    keys per channel over consecutive tokens, values per token over channels."""
-    work = tensor.float()
+    keys per channel over consecutive tokens, values per token over channels.  Kept in
+    the tensor's dtype (the reference converts to fp32 first; min / max are the same values)."""
+    work = tensor
     if work.dim() == 2:
         n, gs = work.shape
         if gs != q_group_size:

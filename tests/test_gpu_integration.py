@@ -117,6 +117,36 @@ def test_step_decode_reuse_matches_fresh_plan():
     assert reused >= steps - 4  # cached arguments served all but the steps after a storage change
 
 
+@pytest.mark.parametrize("kind", ["key", "value"])
+def test_block_alpha_statistics_on_device(kind):
+    """On the GPU the cache's alpha statistics (gathered from the strided block, min / max in
+    bf16, one sort) equal those computed the reference's way on the same device from the
+    materialized fp32 [N, 64] rows (quantizer.py:46-55), bit for bit; so do the alphas."""
+    from muzero_amd import quantizer as Q
+    g = torch.Generator().manual_seed(5)
+    cap = torch.randn(16, 8, 1600, 128, generator=g)
+    cap[..., torch.randperm(128, generator=g)[:4]] *= 10
+    cap[3, 1, :, 7] += 2.5
+    cap = cap.to(torch.bfloat16).to(DEV)
+    block = cap[:, :, 128:1472]
+    B, H, T, D = block.shape
+    if kind == "key":
+        rows = block.reshape(B, H, T // 64, 64, D).permute(0, 1, 2, 4, 3).reshape(-1, 64)
+    else:
+        rows = block.reshape(-1, 64)
+    sample = ref._strided_sample(rows.float(), 65536).abs().reshape(-1)
+    n = sample.numel()
+    want = [float(torch.kthvalue(sample, max(1, int(f * n))).values.item()) for f in (0.50, 0.95, 0.99)]
+    grp = ref._groups_for_stats(rows, 64, "key")
+    lo, hi = grp.amin(dim=-1), grp.amax(dim=-1)
+    za = ((0.0 - lo) / (hi - lo).clamp_min(1e-8)).clamp(0.0, 1.0)
+    want.append(float((za - 0.5).abs().mean().item()))
+    assert Q._block_statistics(block, 64, kind, 65536) == want
+    for bits in (1, 2, 3, 7, 8):
+        assert (Q.select_alpha_block(block, bits=bits, q_group_size=64, kind=kind)
+                == ref.select_alpha(rows, bits=bits, q_group_size=64, kind=kind))
+
+
 def test_materialized_kv_matches_dequantized_oracle():
     """``update(materialize_full_kv=True)`` returns the dequantised prefix + residual, bit-exact
     to the reference's torch dequantisation in the layer dtype."""

@@ -19,6 +19,7 @@ import torch
 import muzero_amd as mz
 from muzero_amd.cache.layer import MuZeroCacheLayer
 from muzero_amd.kernels import loader as L
+from oracle import reference_torch as ref
 
 G = 64
 
@@ -67,6 +68,75 @@ def test_select_alpha_values_in_reference_set():
     y = torch.randn(1, 1, 256, 64, generator=g)
     y.view(-1)[::97] *= 50
     assert mz.select_alpha(y, bits=1, q_group_size=64, kind="key") > 2.0
+
+
+def test_select_alpha_matches_reference_fixture():
+    """The package's select_alpha (statistics in the tensor's dtype, one sort for the three
+    percentiles) returns the alphas the reference computed for the committed tensors."""
+    from conftest import load_golden
+    gold = load_golden("alpha_golden.npz")
+    for name in ("normal", "heavy", "shifted", "outlier"):
+        t = torch.from_numpy(gold[f"t_{name}"])
+        for dt in (torch.float32, torch.bfloat16):
+            x = t if dt == torch.float32 else t.to(dt)
+            for bits in (1, 2, 3, 4, 7, 8):
+                for kind in ("key", "value"):
+                    want = ref.select_alpha(x, bits=bits, q_group_size=32, kind=kind)
+                    if dt == torch.float32:
+                        assert want == float(gold[f"alpha_{name}_b{bits}_{kind}"])
+                    assert mz.select_alpha(x, bits=bits, q_group_size=32, kind=kind) == want, (name, bits, kind)
+                    want = ref.select_alpha(x, bits=bits, q_group_size=64, kind=kind, max_points=4096)
+                    got = mz.select_alpha(x, bits=bits, q_group_size=64, kind=kind, max_points=4096)
+                    assert got == want, (name, bits, kind)
+
+
+def test_halving_minmax_equals_amin_amax():
+    from muzero_amd import quantizer as Q
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(5, 3, 2, 64, generator=g).to(torch.bfloat16)
+    x[0, 0, 0, 17] = float("nan")
+    x[1, 2, 1, 63] = float("inf")
+    x[2, 1, 0, 0] = -float("inf")
+    mn, mx = Q._halving_minmax(x)
+    assert torch.allclose(mn.float(), x.amin(-1).float(), rtol=0, atol=0, equal_nan=True)
+    assert torch.allclose(mx.float(), x.amax(-1).float(), rtol=0, atol=0, equal_nan=True)
+
+
+def _reference_statistics(rows, max_points):
+    """(p50, p95, p99, anchor offset) as the reference computes them for [N, G] rows
+    (quantizer.py:46-55), through the oracle's sampling and grouping."""
+    sample = ref._strided_sample(rows.float(), max_points).abs().reshape(-1)
+    n = sample.numel()
+    ps = [float(torch.kthvalue(sample, max(1, int(f * n))).values.item()) for f in (0.50, 0.95, 0.99)]
+    g = ref._groups_for_stats(rows, rows.shape[-1], "key")
+    lo, hi = g.amin(dim=-1), g.amax(dim=-1)
+    za = ((0.0 - lo) / (hi - lo).clamp_min(1e-8)).clamp(0.0, 1.0)
+    return ps + [float((za - 0.5).abs().mean().item())]
+
+
+@pytest.mark.parametrize("kind", ["key", "value"])
+@pytest.mark.parametrize("max_points", [65536, 1000])
+def test_block_alpha_statistics_match_flattened_rows(kind, max_points):
+    """select_alpha_block gathers the statistics from a strided [B, H, T, D] block; they equal,
+    bit for bit, those of the [N, 64] rows the reference's cache flattens the block into
+    (keys: per channel over 64 tokens, layer.py:276-278; values: per token over 64 channels)."""
+    from muzero_amd import quantizer as Q
+    g = torch.Generator().manual_seed(3)
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        cap = torch.randn(3, 2, 448, 128, generator=g).to(dt)
+        cap[..., torch.randperm(128, generator=g)[:4]] *= 10
+        cap[1, 0, :, 5] += 3.0  # a shifted channel: the zero anchor moves off 0.5
+        block = cap[:, :, 64:384]  # a view into a capacity buffer, as the cache passes it
+        B, H, T, D = block.shape
+        if kind == "key":
+            rows = block.reshape(B, H, T // 64, 64, D).permute(0, 1, 2, 4, 3).reshape(-1, 64)
+        else:
+            rows = block.reshape(-1, 64)
+        got = Q._block_statistics(block, 64, kind, max_points)
+        assert got == _reference_statistics(rows, max_points), (dt, kind)
+        for bits in (1, 2, 3, 7, 8):
+            assert (Q.select_alpha_block(block, bits=bits, q_group_size=64, kind=kind, max_points=max_points)
+                    == ref.select_alpha(rows, bits=bits, q_group_size=64, kind=kind, max_points=max_points))
 
 
 # --------------------------------------------------------------------------- transformers registration
