@@ -257,6 +257,110 @@ def run_stream(args):
     print(json.dumps(line), flush=True)
 
 
+def run_codec(args):
+    """Config 0: the quantize + pack + dequantize round trip of one K and one V tensor.
+
+    K, V [1, 8, 1024, 128] bf16 (seeded CPU generator 1234, drawn K, V, Q; 4 key
+    channels x10); the cache's prefill flush quantizes 896 tokens: 14,336 key rows
+    (per channel over 64 tokens) and 14,336 value rows (per token over 64
+    channels), 4-bit, fp16 metadata; then both are dequantized back to bf16.  One
+    step = the four launches (quantize keys, quantize values, dequantize both row
+    sets) on the GPU; the CPU baseline runs the oracle's restatement of the
+    reference torch path on the host cores.
+    """
+    from muzero_amd.kernels import loader as L
+    dev = torch.device("cuda:0")
+    bits, alpha, T = 4, 2.0, 896
+    g = torch.Generator().manual_seed(1234)
+    k = torch.randn(1, 8, 1024, 128, generator=g)
+    v = torch.randn(1, 8, 1024, 128, generator=g)
+    torch.randn(1, 32, 1, 128, generator=g)
+    k[..., torch.randperm(128, generator=g)[:4]] *= 10.0
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kd, vd = k.to(dev)[:, :, :T], v.to(dev)[:, :, :T]
+    qb = 8 * bits
+    pk = torch.empty((1, 8, T // 64, 128, qb), dtype=torch.uint8, device=dev)
+    kmn = torch.empty((1, 8, T // 64, 128, 1), dtype=torch.float16, device=dev)
+    ksc = torch.empty_like(kmn)
+    pv = torch.empty((1, 8, T, 2, qb), dtype=torch.uint8, device=dev)
+    vmn = torch.empty((1, 8, T, 2, 1), dtype=torch.float16, device=dev)
+    vsc = torch.empty_like(vmn)
+    rows = pk.numel() // qb
+    kout = torch.empty((rows, 64), dtype=torch.bfloat16, device=dev)
+    vout = torch.empty((rows, 64), dtype=torch.bfloat16, device=dev)
+
+    def step(_):
+        L.quantize_key_block_into(kd, bits, alpha, 1e-8, pk, kmn, ksc)
+        L.quantize_value_block_into(vd, bits, alpha, 1e-8, pv, vmn, vsc)
+        L.mu_zero_dequantize_cuda(pk.view(-1, qb), kmn.view(-1, 1), ksc.view(-1, 1), kout, bits, alpha)
+        L.mu_zero_dequantize_cuda(pv.view(-1, qb), vmn.view(-1, 1), vsc.view(-1, 1), vout, bits, alpha)
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        step(i)
+    ms = time_region(step, args.steps, stream)
+    ms_q = time_region(lambda i: (L.quantize_key_block_into(kd, bits, alpha, 1e-8, pk, kmn, ksc),
+                                  L.quantize_value_block_into(vd, bits, alpha, 1e-8, pv, vmn, vsc)),
+                       args.steps, stream)
+    q_in, q_out = 2 * rows * 64 * 2, 2 * rows * (qb + 4)
+    nbytes = 2 * (q_in + q_out)  # quantize (read bf16, write codes + metadata) + dequantize (the reverse)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import reference_torch as ref
+        threads = min(os.cpu_count() or 1, 16)
+        torch.set_num_threads(threads)
+        kc, vc = k[:, :, :T], v[:, :, :T]
+
+        def cpu_step():
+            a = ref.quantize_key_block(kc, bits, alpha)
+            b = ref.quantize_value_block(vc, bits, alpha)
+            ref.dequantize_key_block(*a, bits, alpha, 64, torch.bfloat16)
+            ref.dequantize_value_block(*b, bits, alpha, 64, 128, torch.bfloat16)
+
+        cpu_step()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            cpu_step()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > 10.0 or reps >= 20:
+                break
+        sec = el / reps
+        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+               "seconds_per_round_trip": round(sec, 5), "speedup_gpu_over_cpu": round(sec / (ms * 1e-3), 1),
+               "cpu": platform.processor() or platform.machine(),
+               "sample": f"the whole config-0 round trip ({reps} repetitions), oracle restatement of "
+                         "quantizer.py:161-255 and layer.py:271-345"}
+
+    line = {
+        "metric": "packed-KV decode attn HBM GB/s (% of peak); decode tokens/sec at B=64 ctx 4096",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg0 codec round trip: K, V [1,8,1024,128] bf16, flush 896 tokens = 14,336 key "
+                               "rows + 14,336 value rows, mu_zero 4-bit G64 fp16 meta, quantize + dequantize",
+                   "rows_per_kind": rows, "bits": bits},
+        "quantize_ms": round(ms_q, 5),
+        "bytes_per_round_trip": nbytes,
+        "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "basis": "four launches of a few microseconds each: launch-latency bound at this size"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration(mib, steps):
     """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
     calibrates the same counters on the decode kernel."""
@@ -288,6 +392,8 @@ def main():
     ap.add_argument("--stream", type=int, default=0,
                     help="config 2: a quantize pass, then this many decode steps through the cache layer "
                          "with per-group flushes (use with --batch 128 --bits 1|2|3|5)")
+    ap.add_argument("--codec", action="store_true",
+                    help="config 0: the quantize + dequantize round trip of one [1, 8, 1024, 128] K and V")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -299,6 +405,9 @@ def main():
         return
     if args.stream:
         run_stream(args)
+        return
+    if args.codec:
+        run_codec(args)
         return
 
     from muzero_amd.kernels.loader import DecodePlan

@@ -240,3 +240,43 @@ def test_quantize_blocks_aligned_vector_path(dname, bits):
     np.testing.assert_array_equal(pk.cpu().numpy(), epk.numpy())
     np.testing.assert_array_equal(bits_of(kmn), bits_of(ekmn))
     np.testing.assert_array_equal(bits_of(ksc), bits_of(eksc))
+
+
+def _config0_inputs():
+    """K, V [1, 8, 1024, 128] ~ N(0, 1) from a CPU generator seeded 1234
+    (drawn K, V, Q), 4 of 128 key channels scaled x10."""
+    g = torch.Generator().manual_seed(1234)
+    k = torch.randn(1, 8, 1024, 128, generator=g)
+    v = torch.randn(1, 8, 1024, 128, generator=g)
+    torch.randn(1, 32, 1, 128, generator=g)  # the query, drawn to keep the order
+    k[..., torch.randperm(128, generator=g)[:4]] *= 10.0
+    return k, v
+
+
+@pytest.mark.parametrize("dname", ["float32", "bfloat16"])
+def test_config0_round_trip(dname):
+    """Config 0 through the cache layer: a 1024-token prefill flushes 896 tokens (14,336 key
+    rows + 14,336 value rows, 4-bit, fp16 metadata); codes, metadata and the dequantized
+    prefix equal the oracle's bit for bit, and the reconstruction error is within the
+    reference's 4-bit round-trip bound (tests/test_quantizer.py:16-31: MSE < 0.015 on N(0, 1))."""
+    import muzero_amd as mz
+    from muzero_amd.cache.layer import MuZeroCacheLayer
+    dt = DT[dname]
+    k, v = (t.to(dt) for t in _config0_inputs())
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4))
+    layer.update(k.to(DEV), v.to(DEV), {"materialize_full_kv": False})
+    assert layer._packed_key_q.shape == (1, 8, 14, 128, 32) and layer._packed_value_q.shape == (1, 8, 896, 2, 32)
+    pk, kmn, ksc = ref.quantize_key_block(k[:, :, :896], 4, 2.0)
+    pv, vmn, vsc = ref.quantize_value_block(v[:, :, :896], 4, 2.0)
+    assert torch.equal(layer._packed_key_q.cpu(), pk) and torch.equal(layer._packed_value_q.cpu(), pv)
+    for got, want in ((layer._key_mn, kmn), (layer._key_scale, ksc), (layer._value_mn, vmn),
+                      (layer._value_scale, vsc)):
+        assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
+    dk = layer._dequantize_key_prefix().cpu()
+    dv = layer._dequantize_value_prefix().cpu()
+    assert torch.equal(dk, ref.dequantize_key_block(pk, kmn, ksc, 4, 2.0, 64, dt))
+    assert torch.equal(dv, ref.dequantize_value_block(pv, vmn, vsc, 4, 2.0, 64, 128, dt))
+    assert torch.equal(layer.keys.cpu(), k[:, :, 896:]) and torch.equal(layer.values.cpu(), v[:, :, 896:])
+    kx, vx = k[:, :, :896].float(), v[:, :, :896].float()
+    key_mse = ((kx - dk.float()) ** 2).mean(dim=2) / (kx ** 2).mean(dim=2)  # per channel: outliers are x10
+    assert key_mse.mean().item() < 0.015 and ((vx - dv.float()) ** 2).mean().item() < 0.015
