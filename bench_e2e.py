@@ -14,7 +14,9 @@ ids.  Methods: `bf16` (transformers DynamicCache) and `mu_zero_{b}bit`
 (this package's MuZeroCache through `patch_transformers()`).
 
 Prints one JSON line per method and a last line comparing each mu_zero method
-with bf16.
+with bf16.  `--mode generate` instead times one `model.generate()` call per
+method, prefill included (the reference's generate mode,
+bench_throughput.py:425-436).
 """
 
 from __future__ import annotations
@@ -107,6 +109,37 @@ def decode_only(model, ids: torch.Tensor, method: str, residual: int, chunk: int
     return res
 
 
+@torch.no_grad()
+def generate_mode(model, ids: torch.Tensor, method: str, residual: int, new_tokens: int) -> dict:
+    """The reference's generate mode (bench_throughput.py:425-436): one timed ``model.generate``
+    call, prefill included; tokens/s = generated tokens / wall time."""
+    import muzero_amd as mz
+    kw = dict(max_new_tokens=new_tokens, min_new_tokens=new_tokens, do_sample=False, temperature=None,
+              top_p=None, pad_token_id=0)
+    if method != "bf16":
+        kw.update(cache_implementation=method, cache_config={"q_group_size": 64, "residual_length": residual})
+    torch.cuda.synchronize()
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    mz.reset_mu_zero_decode_stats()
+    t0 = time.perf_counter()
+    out = model.generate(input_ids=ids, attention_mask=torch.ones_like(ids), **kw)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    new = (out.shape[1] - ids.shape[1]) * ids.shape[0]
+    stats = mz.get_mu_zero_decode_stats()
+    res = {"method": method, "mode": "generate", "batch": ids.shape[0], "prompt": ids.shape[1],
+           "new_tokens": out.shape[1] - ids.shape[1], "generate_s": round(elapsed, 3),
+           "tokens_per_s": round(new / elapsed, 1),
+           "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 2),
+           "fused_decode_calls": int(stats.get("hip_fused_decode", 0))}
+    del out
+    gc.collect()
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--batch", type=int, default=64)
@@ -117,6 +150,8 @@ def main():
     ap.add_argument("--residual", type=int, default=128)
     ap.add_argument("--prefill-chunk", type=int, default=1024)
     ap.add_argument("--methods", default="bf16,mu_zero_4bit,mu_zero_2bit")
+    ap.add_argument("--mode", choices=("decode", "generate"), default="decode",
+                    help="decode: prefill excluded from the timing; generate: one timed model.generate() call")
     args = ap.parse_args()
 
     import muzero_amd as mz
@@ -129,13 +164,20 @@ def main():
     g = torch.Generator(device=dev).manual_seed(1234)
     ids = torch.randint(0, model.config.vocab_size, (args.batch, args.context), generator=g, device=dev)
     results = {}
+    if args.mode == "generate":  # untimed warm-up: library load, kernels, allocator
+        for method in args.methods.split(","):
+            generate_mode(model, ids[:, :256], method, args.residual, 2)
     for method in args.methods.split(","):
-        r = decode_only(model, ids, method, args.residual, args.prefill_chunk, args.new_tokens, args.warmup)
+        if args.mode == "generate":
+            r = generate_mode(model, ids, method, args.residual, args.new_tokens)
+        else:
+            r = decode_only(model, ids, method, args.residual, args.prefill_chunk, args.new_tokens, args.warmup)
         results[method] = r
         print(json.dumps(r), flush=True)
     if "bf16" in results:
         base = results["bf16"]["tokens_per_s"]
-        print(json.dumps({"metric": "decode tokens/s vs bf16 cache", "batch": args.batch, "context": args.context,
+        print(json.dumps({"metric": f"{args.mode} tokens/s vs bf16 cache", "batch": args.batch,
+                          "context": args.context,
                           **{m: round(r["tokens_per_s"] / base, 3) for m, r in results.items() if m != "bf16"}}),
               flush=True)
 
