@@ -15,6 +15,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mz {
 
@@ -290,12 +291,14 @@ __global__ __launch_bounds__(QWG) void quantize_values_kernel(const void* __rest
 
 // ------------------------------------------------------------- keys
 // A workgroup loops over (b, h, token group) tiles: the [64 x D] tile is
-// staged in LDS as fp32 [64][D + 1] (row pitch D + 1 keeps the column reads
-// conflict-free) and each wave quantizes 8 channels at a time reading the
-// tile's columns, so the reference's permute + contiguous copy
-// (layer.py:276-278) never touches HBM.  VEC: the tile arrives as 16-byte
-// vectors (D % 8 == 0, D <= 256, aligned rows), and the next tile's vectors
-// are loaded into registers before the current tile is quantized.
+// staged in LDS in the input dtype (16-bit inputs as they arrive, fp32 as
+// fp32) and each wave quantizes 8 channels at a time reading the tile's
+// columns, so the reference's permute + contiguous copy (layer.py:276-278)
+// never touches HBM.  VEC: the tile arrives as 16-byte vectors (D % 8 == 0,
+// D <= 256, aligned rows), and the next tile's vectors are loaded into
+// registers before the current tile is quantized.  The grid holds as many
+// workgroups per CU as the table and the tile leave room for in LDS (at most
+// 4).
 constexpr int KEY_MAX_VEC = 8;  // 16-byte vectors per thread per tile: 64 * 256 / 8 / QWG
 
 template <int DT>
@@ -318,19 +321,36 @@ __device__ __forceinline__ void vec16_store_lds(float* dst, const uint4 u) {
   }
 }
 
+// Staging element of the key tile: 16-bit inputs stay 16-bit in LDS (row
+// pitch D + 2 halves), fp32 inputs stay fp32 (pitch D + 1).  Either pitch is
+// an odd number of dwords, so a column read of a wave's 8 lane groups meets
+// at most two distinct dwords per bank.
+template <int DT>
+struct KeyStage {
+  using T = typename std::conditional<DT == MZ_F32, float, uint16_t>::type;
+  static constexpr int PAD = DT == MZ_F32 ? 1 : 2;
+  static __device__ __forceinline__ float load(const T* p) {
+    if constexpr (DT == MZ_F32) return *p;
+    else if constexpr (DT == MZ_BF16) return bf2f(*p);
+    else return h2f(*p);
+  }
+};
+
 template <int DT, int BITS, bool VEC>
 __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restrict__ x, int B, int H, int T, int D,
                                                             int64_t sb, int64_t sh, int64_t st,
                                                             uint8_t* __restrict__ packed, int64_t psb, int64_t psh,
                                                             void* mn, void* sc, int meta_dtype, int64_t msb,
                                                             int64_t msh, float eps, const void* __restrict__ table) {
+  using KS = KeyStage<DT>;
+  using ET = typename KS::T;
   extern __shared__ __align__(16) uint8_t dyn[];
   uint8_t* lds = dyn;                                                 // compander table
-  float* tile = (float*)(dyn + QTable<DT, BITS>::LDS_BYTES);          // [64][D + 1]
+  ET* tile = (ET*)(dyn + QTable<DT, BITS>::LDS_BYTES);                // [64][D + PAD]
   stage_table<DT, BITS>(lds, table);
   const int nsg = T / 64;
   const int ntiles = B * H * nsg;  // < 2^31 (host check)
-  const int ld = D + 1;
+  const int ld = D + KS::PAD;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int part = lane & 7;
@@ -367,7 +387,12 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
         const int e = threadIdx.x + k * QWG;
         if (e < nvec) {
           const int t = e / vpr, c = (e - t * vpr) * NE;
-          vec16_store_lds<DT>(tile + t * ld + c, nxt[k]);
+          if constexpr (DT == MZ_F32) {
+            vec16_store_lds<DT>(tile + t * ld + c, nxt[k]);
+          } else {
+            uint32_t* d32 = (uint32_t*)(tile + t * ld + c);  // 4-byte aligned: ld and c are even
+            d32[0] = nxt[k].x, d32[1] = nxt[k].y, d32[2] = nxt[k].z, d32[3] = nxt[k].w;
+          }
         }
       }
       if (ti + (int)gridDim.x < ntiles) fetch(ti + gridDim.x);  // lands while this tile is quantized
@@ -375,7 +400,8 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
       const int64_t base = tile_base(ti);
       for (int e = threadIdx.x; e < 64 * D; e += QWG) {
         const int t = e / D, c = e - t * D;
-        tile[t * ld + c] = load_val<DT>(x, base + t * st + c);
+        if constexpr (DT == MZ_F32) tile[t * ld + c] = load_val<DT>(x, base + t * st + c);
+        else tile[t * ld + c] = ((const uint16_t*)x)[base + t * st + c];
       }
     }
     __syncthreads();
@@ -386,7 +412,7 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
       if (c < D) {  // a group's 8 lanes share c
         float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = tile[(8 * part + k) * ld + c];
+        for (int k = 0; k < 8; ++k) v[k] = KS::load(tile + (8 * part + k) * ld + c);
         quantize_lane8<DT, BITS>(v, part, gbase + (int64_t)c * QB, mn, sc, mbase + c, meta_dtype, eps, lds, table);
       }
     }
@@ -515,14 +541,16 @@ extern "C" int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H,
                    (x_st * es) % 16 == 0;
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
-      const size_t lds = (size_t)QTable<D_, B_>::LDS_BYTES + (size_t)64 * (D + 1) * sizeof(float);
+      const size_t lds = (size_t)QTable<D_, B_>::LDS_BYTES +
+                         (size_t)64 * (D + KeyStage<D_>::PAD) * sizeof(typename KeyStage<D_>::T);
       if (lds > 160 * 1024) return MZ_EUNSUPPORTED;
       const void* fn = vec ? (const void*)quantize_keys_kernel<D_, B_, true> : (const void*)quantize_keys_kernel<D_, B_, false>;
       if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return (int)e;
       }
-      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ntiles, 2 * (int64_t)cu_count())));
+      const int per_cu = std::max<int>(1, std::min<int>(4, (int)((160 * 1024) / lds)));
+      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ntiles, per_cu * (int64_t)cu_count())));
       if (vec) hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, true>), grid, dim3(QWG), lds, s, keys, B, H, T, D,
                                   x_sb, x_sh, x_st, packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table);
       else hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, false>), grid, dim3(QWG), lds, s, keys, B, H, T, D,
