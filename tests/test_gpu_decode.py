@@ -16,7 +16,6 @@ to the max bound: rounding the exact fp64 answer itself to bf16 already moves
 outputs near 1.0 by up to 3.9e-3, so no bf16 result can meet 2e-3 there.
 """
 
-import math
 
 import pytest
 import torch

@@ -11,8 +11,6 @@
   (``MUZERO_DISABLE_FUSED_DECODE=1``).
 """
 
-import os
-
 import pytest
 import torch
 
