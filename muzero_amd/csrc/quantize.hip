@@ -102,31 +102,36 @@ __device__ __forceinline__ void stage_table(uint8_t* lds, const void* table) {
 }
 
 // Code of one value given its group's parameters (quantizer.py:172-184).
-template <int DT, int BITS, bool FAST>
+// FINITE: the group's mn and scale are finite and every divisor (scale, pe,
+// ne) is positive, so no intermediate is NaN or infinite and every clamped
+// quantity is >= 0 (v >= mn; the side's offset from za is >= 0): the NaN
+// cases and the lower clamps drop out and give the same results.
+template <int DT, int BITS, bool FAST, bool FINITE>
 __device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const uint8_t* lds, const void* table) {
   constexpr float qmax = (float)((1 << BITS) - 1);
-  const float norm = clamp01(qdiv<DT, FAST>(rnd<DT>(v - g.mn), g.sc, g.rsc));
+  const float n0 = qdiv<DT, FAST>(rnd<DT>(v - g.mn), g.sc, g.rsc);
+  const float norm = FINITE ? fminf(n0, 1.f) : clamp01(n0);
   const bool up = norm >= g.za;  // torch.where(norm >= za, q_pos, q_neg); false on NaN
   // Only the selected side is evaluated: operands are chosen before the one
   // division, which computes exactly what the unselected-branch form would.
-  const float p = clamp01(qdiv<DT, FAST>(rnd<DT>(up ? norm - g.za : g.za - norm), up ? g.pe : g.ne,
-                                         up ? g.rpe : g.rne));
+  const float p0 = qdiv<DT, FAST>(rnd<DT>(up ? norm - g.za : g.za - norm), up ? g.pe : g.ne, up ? g.rpe : g.rne);
+  const float p = FINITE ? fminf(p0, 1.f) : clamp01(p0);
   const float bins = up ? g.pb : g.nb;
   float off;
   if constexpr (DT == MZ_F32) {
     const float* T = QTable<DT, BITS>::IN_LDS ? (const float*)lds : (const float*)table;
-    const int ib = (bins == bins) ? (int)bins : 1;
+    const int ib = (FINITE || bins == bins) ? (int)bins : 1;
     const float* row = T + ib * (ib - 1) / 2;
     int lo = 0, hi = ib;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (row[mid] <= p) lo = mid + 1; else hi = mid;
     }
-    off = (p == p) ? (float)lo : __builtin_nanf("");
+    off = (FINITE || p == p) ? (float)lo : __builtin_nanf("");
   } else {
     const uint16_t* Y = (const uint16_t*)lds;
     float y;
-    if (p == p) {
+    if (FINITE || p == p) {
       const uint32_t pat = (DT == MZ_BF16 ? (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p)  // p is not NaN
                                           : (uint32_t)f2h(p)) & 0x7FFFu;                          // -0 -> 0
       y = DT == MZ_BF16 ? bf2f(Y[pat]) : h2f(Y[pat]);
@@ -137,7 +142,7 @@ __device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const 
   }
   const float q = rnd<DT>(up ? g.zl + off : g.zl - off);
   // clamp(0, qmax).to(uint8); a NaN code converts to 0 (as on the reference CPU)
-  if (!(q == q)) return 0u;
+  if (!FINITE && !(q == q)) return 0u;
   return (uint32_t)fminf(fmaxf(q, 0.f), qmax);
 }
 
@@ -167,12 +172,23 @@ __device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, ui
   mx = group8_max(mx);
   const QParams g = qparams<DT, BITS>(mn, mx, eps);
   uint64_t w = 0;
-  if (qfast<DT>(g)) {
+  // (fp16 rounds eps to 0: a constant group, or za at 0 or 1, then divides by 0).
+  // The fp32 8-bit thresholds stay in global memory, where the plain form's
+  // binary search measured faster.
+  const bool finite = QTable<DT, BITS>::IN_LDS && __builtin_isfinite(g.mn) && __builtin_isfinite(g.sc) &&
+                      g.sc > 0.f && g.pe > 0.f && g.ne > 0.f;
+  if (qfast<DT>(g) && finite) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true>(x[i], g, lds, table) << (i * BITS);
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true, true>(x[i], g, lds, table) << (i * BITS);
+  } else if (finite) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false, true>(x[i], g, lds, table) << (i * BITS);
+  } else if (qfast<DT>(g)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true, false>(x[i], g, lds, table) << (i * BITS);
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false>(x[i], g, lds, table) << (i * BITS);
+    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false, false>(x[i], g, lds, table) << (i * BITS);
   }
   uint8_t* dst = prow + part * BITS;
   if constexpr (BITS == 8) *(uint64_t*)dst = w;
