@@ -146,6 +146,44 @@ __device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const 
   return (uint32_t)fminf(fmaxf(q, 0.f), qmax);
 }
 
+// value_code<MZ_BF16, BITS, true, true> of two values at once: each of the
+// chain's roundings to bf16 converts the pair with one v_cvt_pk_bf16_f32.
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void rnd_bf16_pair(float& a, float& b) {
+  const bf16x2v r = __builtin_convertvector(f32x2v{a, b}, bf16x2v);
+  a = (float)r.x;
+  b = (float)r.y;
+}
+
+template <int BITS>
+__device__ __forceinline__ void value_code_bf16_pair(float v0, float v1, const QParams& g, const uint8_t* lds,
+                                                     uint32_t& c0, uint32_t& c1) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  float a0 = v0 - g.mn, a1 = v1 - g.mn;
+  rnd_bf16_pair(a0, a1);
+  float n0 = a0 * g.rsc, n1 = a1 * g.rsc;
+  rnd_bf16_pair(n0, n1);
+  n0 = fminf(n0, 1.f), n1 = fminf(n1, 1.f);
+  const bool up0 = n0 >= g.za, up1 = n1 >= g.za;
+  float d0 = up0 ? n0 - g.za : g.za - n0, d1 = up1 ? n1 - g.za : g.za - n1;
+  rnd_bf16_pair(d0, d1);
+  float p0 = d0 * (up0 ? g.rpe : g.rne), p1 = d1 * (up1 ? g.rpe : g.rne);
+  rnd_bf16_pair(p0, p1);
+  p0 = fminf(p0, 1.f), p1 = fminf(p1, 1.f);
+  // p0, p1 are bf16 values >= 0: their pattern is the high half of the fp32 bits
+  const uint16_t* Y = (const uint16_t*)lds;
+  const float y0 = bf2f(Y[(__float_as_uint(p0) >> 16) & 0x7FFFu]);
+  const float y1 = bf2f(Y[(__float_as_uint(p1) >> 16) & 0x7FFFu]);
+  float o0 = y0 * (up0 ? g.pb : g.nb), o1 = y1 * (up1 ? g.pb : g.nb);
+  rnd_bf16_pair(o0, o1);
+  o0 = rintf(o0), o1 = rintf(o1);
+  float q0 = up0 ? g.zl + o0 : g.zl - o0, q1 = up1 ? g.zl + o1 : g.zl - o1;
+  rnd_bf16_pair(q0, q1);
+  c0 = (uint32_t)fminf(fmaxf(q0, 0.f), qmax);
+  c1 = (uint32_t)fminf(fmaxf(q1, 0.f), qmax);
+}
+
 // Min / max over the 8 lanes of a group (lanes 8k..8k+7), NaN-propagating.
 __device__ __forceinline__ float group8_min(float v) {
   v = nmin(v, dpp_sel<DPP_QUAD_XOR1>(v));
@@ -178,8 +216,17 @@ __device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, ui
   const bool finite = QTable<DT, BITS>::IN_LDS && __builtin_isfinite(g.mn) && __builtin_isfinite(g.sc) &&
                       g.sc > 0.f && g.pe > 0.f && g.ne > 0.f;
   if (qfast<DT>(g) && finite) {
+    if constexpr (DT == MZ_BF16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true, true>(x[i], g, lds, table) << (i * BITS);
+      for (int i = 0; i < 8; i += 2) {
+        uint32_t c0, c1;
+        value_code_bf16_pair<BITS>(x[i], x[i + 1], g, lds, c0, c1);
+        w |= ((uint64_t)c0 << (i * BITS)) | ((uint64_t)c1 << ((i + 1) * BITS));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true, true>(x[i], g, lds, table) << (i * BITS);
+    }
   } else if (finite) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false, true>(x[i], g, lds, table) << (i * BITS);
