@@ -140,7 +140,9 @@ __device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const 
     }
     off = rintf(rnd<DT>(y * bins));
   }
-  const float q = rnd<DT>(up ? g.zl + off : g.zl - off);
+  // zl +- off is an integer in [-1, qmax + 1] <= 256 there: exact in every
+  // input dtype, so its rounding is the identity
+  const float q = FINITE ? (up ? g.zl + off : g.zl - off) : rnd<DT>(up ? g.zl + off : g.zl - off);
   // clamp(0, qmax).to(uint8); a NaN code converts to 0 (as on the reference CPU)
   if (!FINITE && !(q == q)) return 0u;
   return (uint32_t)fminf(fmaxf(q, 0.f), qmax);
@@ -178,8 +180,8 @@ __device__ __forceinline__ void value_code_bf16_pair(float v0, float v1, const Q
   float o0 = y0 * (up0 ? g.pb : g.nb), o1 = y1 * (up1 ? g.pb : g.nb);
   rnd_bf16_pair(o0, o1);
   o0 = rintf(o0), o1 = rintf(o1);
-  float q0 = up0 ? g.zl + o0 : g.zl - o0, q1 = up1 ? g.zl + o1 : g.zl - o1;
-  rnd_bf16_pair(q0, q1);
+  // zl +- off: an integer in [-1, qmax + 1], exact in bf16 (its rounding is the identity)
+  const float q0 = up0 ? g.zl + o0 : g.zl - o0, q1 = up1 ? g.zl + o1 : g.zl - o1;
   c0 = (uint32_t)fminf(fmaxf(q0, 0.f), qmax);
   c1 = (uint32_t)fminf(fmaxf(q1, 0.f), qmax);
 }
