@@ -287,9 +287,13 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
     const uint32_t r[4] = {odd ? s0 : w0, odd ? w0 : s0, odd ? s1 : w1, odd ? w1 : s1};
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
-      uint32_t e = grep;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) e |= __builtin_amdgcn_ubfe(r[ii], sh + 3 * jt, 3) << (8 * jt + 2);
+      // 12 bits c3|c2|c1|c0 -> bytes 4*c_jt: split into 6-bit halves 16 bits
+      // apart, then into 3-bit fields 8 bits apart (the masks drop the
+      // overlaps of the shifted copies)
+      const uint32_t f = __builtin_amdgcn_ubfe(r[ii], sh, 12);
+      const uint32_t t = ((f << 10) | f) & 0x003F003Fu;
+      const uint32_t u = ((t << 5) | t) & 0x07070707u;
+      const uint32_t e = (u << 2) | grep;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
         B[jt][ii] = *(const uint32_t*)(smem + TBASE +
