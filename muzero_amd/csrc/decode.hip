@@ -78,17 +78,19 @@ struct DeqG {
   int zl;                    // zero level, an integer in 0..qmax
   int bp, bn;                // <= 6 bits: LDS byte address of code q's expm1 entry is (q >= zl ? bp : bn) + 4q
   float fa, fp, fn;          // fast form: x = fa + (q >= zl ? fp : fn) * Z[zl][q]
+  float fb;                  // fast form, 7/8 bits: x = (q >= zl ? fp : fn) * e + (q >= zl ? fa : fb)
 };
 
 // `ebase`: LDS byte address of the forward expm1 rows E[bins][d]; the reversed
 // rows R[bins][k] = E[bins][bins - k] follow them (same row offsets), so a
 // code below the zero level reads R[nb][q] = E[nb][zl - q] (nb = zl then)
 // and both sides index with +q.
-// `fast` (codes of up to 6 bits): the table at `ebase` is Z[zl][q] =
+// `fast`, codes of up to 6 bits: the table at `ebase` is Z[zl][q] =
 // +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] (q < zl), and the value is
 // a + (s*pe or s*ne) * Z with a = mn + s*za: the reference's value to a few
 // fp32 ulp (its fused CUDA kernels' fp32 codebook form), one table read and
-// about five ops per code.
+// about five ops per code.  `fast`, 7 and 8 bits: the same value with the
+// expm1 term from the hardware exp2, one fma per code after it.
 template <int BITS, bool FAST>
 __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float inv_alpha, int ebase) {
   constexpr float qmax = (float)((1 << BITS) - 1);
@@ -101,7 +103,18 @@ __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float in
   g.pe = r.pe;
   g.mne = -r.ne;
   g.zl = r.zl == r.zl ? (int)r.zl : 0;  // a NaN zero level reads row 1 (pb = nb = 1), never past the table
-  if constexpr (FAST) {
+  if constexpr (FAST && BITS > 6) {
+    // e = 2^(|q - zl| * log2(1 + alpha) / bins) = 1 + alpha * expm1 term:
+    // x = a + (s*pe/alpha) * (e - 1) above the zero level, a - (s*ne/alpha) * (e - 1) below
+    const float fa = r.mn + r.s * r.za;
+    g.cp = lb2 / r.pb;
+    g.cn = lb2 / r.nb;
+    g.fp = r.s * r.pe * inv_alpha;
+    g.fn = -(r.s * r.ne * inv_alpha);
+    g.fa = fa - g.fp;
+    g.fb = fa - g.fn;
+    return g;
+  } else if constexpr (FAST) {
     g.bp = ebase + 4 * (g.zl << BITS);
     g.fa = r.mn + r.s * r.za;
     g.fp = r.s * r.pe;
@@ -134,7 +147,9 @@ __device__ __forceinline__ float lds_load_f32(int addr) {
 template <int BITS, bool FAST>
 __device__ __forceinline__ float deq_fetch(const DeqG& g, int q) {
   const bool pos = q >= g.zl;
-  if constexpr (FAST) {
+  if constexpr (FAST && BITS > 6) {
+    return __builtin_amdgcn_exp2f(fabsf((float)(q - g.zl)) * (pos ? g.cp : g.cn));
+  } else if constexpr (FAST) {
     return lds_load_f32(g.bp + 4 * q);
   } else if constexpr (BITS <= 6) {
     return lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
@@ -148,6 +163,7 @@ __device__ __forceinline__ float deq_fetch(const DeqG& g, int q) {
 template <int BITS, bool FAST>
 __device__ __forceinline__ float deq_apply(const DeqG& g, int q, float z) {
   const bool pos = q >= g.zl;
+  if constexpr (FAST && BITS > 6) return __builtin_fmaf(pos ? g.fp : g.fn, z, pos ? g.fa : g.fb);
   if constexpr (FAST) return __builtin_fmaf(pos ? g.fp : g.fn, z, g.fa);
   const float t = BITS <= 6 ? (pos ? g.pe : g.mne) * z : z;
   const float norm = __builtin_amdgcn_fmed3f(g.za + t, 0.f, 1.f);
@@ -215,7 +231,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int EF = L::e_floats(BITS);
   constexpr int ZF = L::z_floats(BITS);
   constexpr bool kTab = BITS <= 6;
-  static_assert(!FAST || kTab, "the fast form needs the per-zero-level table (codes of up to 6 bits)");
 
   extern __shared__ __align__(16) uint16_t lds[];
   const int lane = threadIdx.x & 63;
@@ -231,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint16_t* pb = kv + L::STAGE;
   constexpr int EK_BASE = L::WAVES_BYTES;                              // key table
   constexpr int EV_BASE = L::WAVES_BYTES + (FAST ? 4 * ZF : 8 * EF);  // value table
-  if constexpr (FAST) {
+  if constexpr (FAST && kTab) {
     // Z[zl][q] = +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] from the expm1 rows
     if (a.n_groups > 0 || a.v_prefix > 0) {
       float* zK = (float*)((uint8_t*)lds + EK_BASE);
@@ -766,7 +781,7 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) 
   switch (a->bits) {
 #define MZ_CASE(BB)                                                                                           \
   case BB: {                                                                                                  \
-    constexpr bool F = FAST && BB <= 6;                                                                       \
+    constexpr bool F = FAST;                                                                                  \
     const size_t lds = Lds<D>::bytes(BB, F);                                                                  \
     static const hipError_t attr = hipFuncSetAttribute(                                                       \
         (const void*)decode_split_kernel<D, BB, IO, F>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
