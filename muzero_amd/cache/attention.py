@@ -85,7 +85,8 @@ def mu_zero_decode_attention_forward(
     key = None
     if attention_mask is None and has_res and value_prefix_length == key_prefix_length:
         key = (id(layer._kstore.packed), id(layer._vstore.packed), layer._kstore.count > 0,
-               id(layer._key_buffer), id(layer._value_buffer), layer._key_buffer is not None,
+               layer._kres.stamp(), layer._vres.stamp(),
+               layer._kres.buf is not None and layer._vres.buf is not None,
                query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key, alpha_value,
                float(scaling))
     if fast is not None and key is not None and fast.key == key:
@@ -105,7 +106,7 @@ def mu_zero_decode_attention_forward(
         )
         out = plan.run()
         # cache the validated arguments only when every pointer they hold is
-        # stable across steps (residual in its capacity buffer, no mask)
+        # stable across steps (residual windows in their decode buffers, no mask)
         layer._hip_decode = _k.StepDecode(plan, key) if key is not None and key[5] else None
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1

@@ -16,6 +16,12 @@ stored differently, for the GPU:
   buffers (strided in the token / group dimension), exactly what the fused
   HIP decode kernel reads; capacity grows geometrically when a flush does not
   fit.
+* The full-precision tail (``keys`` / ``values``) is a sliding window over a
+  decode buffer: a flush advances the window's start instead of copying the
+  remaining tokens to the front (the reference clones and copies them at
+  every flush, ``layer.py:198-217``); the tokens move only when the buffer's
+  end is reached.  The flush policy itself (which tokens leave, when) is the
+  reference's, so the packed prefix holds the same codes.
 
 Everything is computed by the HIP kernels; a CPU tensor is an error.
 """
@@ -82,6 +88,91 @@ class _PackedStore:
         self.count = 0
 
 
+class _ResidualWindow:
+    """The full-precision tail of one kind (keys or values).
+
+    Decode appends go to a capacity buffer ``[B, H, cap, D]`` that holds the
+    window as tokens ``[start, end)``: an append writes at ``end`` and a flush
+    only advances ``start``, so the tail is not copied at every flush.  When an
+    append finds no room at the end, the live tokens move to the front of a
+    buffer (a larger one if needed); that copy happens once per
+    ``cap - len`` appended tokens.  Multi-token appends (prefill) keep the
+    tensor they arrive in, without a buffer, as the dense attention reads it.
+    """
+
+    __slots__ = ("buf", "start", "end", "loose", "align", "view")
+
+    def __init__(self, align: int):
+        self.align = align  # capacities are multiples of this many tokens
+        self.clear()
+
+    def clear(self) -> None:
+        self.buf, self.start, self.end, self.loose, self.view = None, 0, 0, None, None
+
+    def _refresh(self) -> None:
+        # the tokens as one tensor, made once per change (the decode path reads it often)
+        self.view = self.buf[:, :, self.start:self.end] if self.buf is not None else self.loose
+
+    def tokens(self) -> Optional[torch.Tensor]:
+        return self.view
+
+    def __len__(self) -> int:
+        t = self.view
+        return int(t.shape[2]) if t is not None and t.dim() == 4 else 0
+
+    def set(self, t: Optional[torch.Tensor]) -> None:
+        self.clear()
+        self.loose = self.view = t
+
+    def stamp(self):
+        """Identifies the memory the window's tokens start at (changes on a flush or a move)."""
+        return None if self.buf is None else (id(self.buf), self.start)
+
+    def _room_for_one(self, min_cap: int) -> None:
+        live = self.tokens()
+        n = len(self)
+        if self.buf is not None and self.end < int(self.buf.shape[2]):
+            return
+        cap = max(min_cap, n + 1)
+        cap = -(-cap // self.align) * self.align
+        buf = torch.empty((*live.shape[:2], cap, live.shape[3]), dtype=live.dtype, device=live.device)
+        if n:
+            buf[:, :, :n].copy_(live)
+        self.buf, self.start, self.end, self.loose = buf, 0, n, None
+        self._refresh()
+
+    def slot(self, min_cap: int) -> torch.Tensor:
+        """The row the next token goes to (``[B, H, 1, D]``); :meth:`commit` takes it in."""
+        self._room_for_one(min_cap)
+        return self.buf[:, :, self.end:self.end + 1]
+
+    def commit(self) -> None:
+        self.end += 1
+        self._refresh()
+
+    def append(self, t: torch.Tensor, min_cap: int) -> None:
+        if len(self) == 0 and (t.shape[2] != 1 or self.buf is None):
+            self.set(t)
+        elif t.shape[2] == 1:
+            self.slot(min_cap).copy_(t)
+            self.commit()
+        else:
+            self.set(torch.cat([self.tokens(), t], dim=2))
+
+    def drop(self, n: int) -> None:
+        """Forget the oldest ``n`` tokens (they went to the packed prefix)."""
+        if n <= 0:
+            return
+        if self.buf is not None:
+            self.start += n
+            if self.start == self.end:
+                self.start = self.end = 0
+        else:
+            # a copy, so the prefill tensor is not kept alive by the short tail
+            self.loose = self.loose[:, :, n:].contiguous()
+        self._refresh()
+
+
 class MuZeroCacheLayer:
     """Single-layer mu-Zero KV cache: a packed prefix plus a full-precision residual tail.
 
@@ -123,11 +214,27 @@ class MuZeroCacheLayer:
         self.v_head_dim = None
         self.v_head_dim_padded = None
         self.v_num_groups = None
-        self.keys = None
-        self.values = None
-        self._key_buffer = None
-        self._value_buffer = None
-        self._buffer_capacity = 0
+        # decode buffers are sized for the residual plus four groups, in
+        # multiples of four groups
+        self._kres = _ResidualWindow(4 * self.q_group_size)
+        self._vres = _ResidualWindow(4 * self.q_group_size)
+
+        self.keys = self.values = None  # the windows' tokens (reference names), kept in step by _sync
+
+    # ------------------------------------------------------------------
+    # The full-precision tail
+    # ------------------------------------------------------------------
+
+    def _sync(self) -> None:
+        self.keys, self.values = self._kres.tokens(), self._vres.tokens()
+
+    def _set_tail(self, keys: Optional[torch.Tensor], values: Optional[torch.Tensor]) -> None:
+        self._kres.set(keys)
+        self._vres.set(values)
+        self._sync()
+
+    def _decode_capacity(self) -> int:
+        return self.residual_length + 4 * self.q_group_size
 
     # ------------------------------------------------------------------
     # Packed-prefix views (reference attribute names)
@@ -172,8 +279,8 @@ class MuZeroCacheLayer:
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         self.dtype = key_states.dtype
         self.device = key_states.device
-        self.keys = torch.empty(0, dtype=self.dtype, device=self.device)
-        self.values = torch.empty(0, dtype=self.dtype, device=self.device)
+        self._set_tail(torch.empty(0, dtype=self.dtype, device=self.device),
+                       torch.empty(0, dtype=self.dtype, device=self.device))
         self.k_head_dim = key_states.shape[-1]
         self.v_head_dim = value_states.shape[-1]
         self.v_head_dim_padded = ((self.v_head_dim + self.q_group_size - 1) // self.q_group_size) * self.q_group_size
@@ -193,92 +300,30 @@ class MuZeroCacheLayer:
         return (self.q_group_size * self.nbits + 7) // 8
 
     # ------------------------------------------------------------------
-    # Residual buffer (same policy as layer.py:135-217)
+    # Appends (the residual windows)
     # ------------------------------------------------------------------
 
-    def _reserve_residual_buffer(self, min_capacity: int) -> None:
-        """Ensure decode residual storage can grow without per-token cat."""
-        if self.keys is None or self.values is None:
-            return
-        if self._key_buffer is not None and self._buffer_capacity >= min_capacity:
-            return
-        current_key_len = int(self.keys.shape[2]) if self.keys.numel() else 0
-        current_value_len = int(self.values.shape[2]) if self.values.numel() else 0
-        flush_unit = self.q_group_size * 4
-        capacity = max(min_capacity, self.residual_length + flush_unit)
-        capacity = ((capacity + flush_unit - 1) // flush_unit) * flush_unit
-        key_buffer = torch.empty((*self.keys.shape[:2], capacity, self.k_head_dim), dtype=self.dtype,
-                                 device=self.device)
-        value_buffer = torch.empty((*self.values.shape[:2], capacity, self.v_head_dim), dtype=self.dtype,
-                                   device=self.device)
-        if current_key_len > 0:
-            key_buffer[:, :, :current_key_len, :].copy_(self.keys)
-        if current_value_len > 0:
-            value_buffer[:, :, :current_value_len, :].copy_(self.values)
-        self._key_buffer = key_buffer
-        self._value_buffer = value_buffer
-        self._buffer_capacity = capacity
-        self.keys = self._key_buffer[:, :, :current_key_len, :]
-        self.values = self._value_buffer[:, :, :current_value_len, :]
-
-    def _append_dense(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        append_len = int(key_states.shape[2])
-        if self.keys.numel() == 0:
-            self.keys = key_states
-            self.values = value_states
-            self._key_buffer = None
-            self._value_buffer = None
-            self._buffer_capacity = 0
-            return
-        if append_len == 1:
-            old_key_len = int(self.keys.shape[2])
-            old_value_len = int(self.values.shape[2])
-            self._reserve_residual_buffer(max(old_key_len + 1, old_value_len + 1))
-            self._key_buffer[:, :, old_key_len:old_key_len + 1, :].copy_(key_states)
-            self._value_buffer[:, :, old_value_len:old_value_len + 1, :].copy_(value_states)
-            self.keys = self._key_buffer[:, :, :old_key_len + 1, :]
-            self.values = self._value_buffer[:, :, :old_value_len + 1, :]
-            return
-        self.keys = torch.cat([self.keys, key_states], dim=-2)
-        self.values = torch.cat([self.values, value_states], dim=-2)
-        self._key_buffer = None
-        self._value_buffer = None
-        self._buffer_capacity = 0
+    def _append_tokens(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        cap = self._decode_capacity()
+        self._kres.append(key_states, cap)
+        self._vres.append(value_states, cap)
+        self._sync()
 
     def decode_append_slot(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """Reserve the residual rows of one decode token and return them (key and value views
-        ``[B, H, 1, D]``) for the caller to write; :meth:`decode_append_commit` then appends the
-        token as :meth:`update` would (the fused decode prologue writes the rows in place)."""
-        old_k, old_v = int(self.keys.shape[2]), int(self.values.shape[2])
-        self._reserve_residual_buffer(max(old_k + 1, old_v + 1))
-        self._pending_append = (old_k, old_v)
-        return (self._key_buffer[:, :, old_k:old_k + 1, :], self._value_buffer[:, :, old_v:old_v + 1, :])
+        """The residual rows of one decode token (key and value views ``[B, H, 1, D]``) for the
+        caller to write; :meth:`decode_append_commit` then takes the token in as :meth:`update`
+        would (the fused decode prologue writes the rows in place)."""
+        cap = self._decode_capacity()
+        rows = self._kres.slot(cap), self._vres.slot(cap)
+        self._sync()
+        return rows
 
     def decode_append_commit(self) -> None:
-        old_k, old_v = self._pending_append
-        self._pending_append = None
-        self.keys = self._key_buffer[:, :, :old_k + 1, :]
-        self.values = self._value_buffer[:, :, :old_v + 1, :]
+        self._kres.commit()
+        self._vres.commit()
+        self._sync()
         self.cumulative_length += 1
         self.compress_residual_prefix(decode_flush=True)
-
-    def _drop_residual_prefix(self, key_len: int, value_len: int) -> None:
-        if key_len > 0:
-            remaining = int(self.keys.shape[2]) - key_len
-            if self._key_buffer is not None:
-                if remaining > 0:
-                    self._key_buffer[:, :, :remaining, :].copy_(self.keys[:, :, key_len:, :].clone())
-                self.keys = self._key_buffer[:, :, :remaining, :]
-            else:
-                self.keys = self.keys[:, :, key_len:, :].contiguous()
-        if value_len > 0:
-            remaining = int(self.values.shape[2]) - value_len
-            if self._value_buffer is not None:
-                if remaining > 0:
-                    self._value_buffer[:, :, :remaining, :].copy_(self.values[:, :, value_len:, :].clone())
-                self.values = self._value_buffer[:, :, :remaining, :]
-            else:
-                self.values = self.values[:, :, value_len:, :].contiguous()
 
     # ------------------------------------------------------------------
     # Alpha selection (layer.py:223-234)
@@ -391,26 +436,32 @@ class MuZeroCacheLayer:
     # Flush (layer.py:369-396)
     # ------------------------------------------------------------------
 
+    def _flush_lengths(self, decode_flush: bool) -> tuple[int, int]:
+        """Tokens of keys and of values that leave the residual now (layer.py:378-396):
+        whole groups of the key excess over ``residual_length`` (four groups at a time
+        for a decode step unless ``decode_flush_by_group`` or the legacy LogQ layout);
+        values follow the keys, or under the LogQ layout flush their own excess token by
+        token."""
+        nk, nv = len(self._kres), len(self._vres)
+        step = self.q_group_size
+        if decode_flush and not (self.cfg.decode_flush_by_group or self.cfg.logq_compatible_layout):
+            step *= 4
+        k_out = max(nk - self.residual_length, 0) // step * step
+        v_out = max(nv - self.residual_length, 0) if self.cfg.logq_compatible_layout else min(k_out, nv)
+        return k_out, v_out
+
     def compress_residual_prefix(self, *, decode_flush: bool = False) -> None:
-        """Compress the dense residual prefix, preserving the configured tail."""
+        """Move the residual's excess over ``residual_length`` into the packed prefix."""
         if not self.is_initialized or self.keys is None or self.values is None:
             return
-        key_excess = max(self.keys.shape[2] - self.residual_length, 0)
-        key_flush_unit = self.q_group_size
-        if decode_flush and not (self.cfg.logq_compatible_layout or self.cfg.decode_flush_by_group):
-            key_flush_unit = self.q_group_size * 4
-        key_flush_len = (key_excess // key_flush_unit) * key_flush_unit
-        if key_flush_len > 0:
-            self._quantize_key_block(self.keys[:, :, :key_flush_len, :])
-            self._drop_residual_prefix(key_flush_len, 0)
-
-        if self.cfg.logq_compatible_layout:
-            val_flush_len = max(self.values.shape[2] - self.residual_length, 0)
-        else:
-            val_flush_len = min(key_flush_len, self.values.shape[2])
-        if val_flush_len > 0:
-            self._quantize_value_block(self.values[:, :, :val_flush_len, :])
-            self._drop_residual_prefix(0, val_flush_len)
+        k_out, v_out = self._flush_lengths(decode_flush)
+        if k_out:
+            self._quantize_key_block(self.keys[:, :, :k_out])
+            self._kres.drop(k_out)
+        if v_out:
+            self._quantize_value_block(self.values[:, :, :v_out])
+            self._vres.drop(v_out)
+        self._sync()
 
     # ------------------------------------------------------------------
     # Primary update (layer.py:402-459)
@@ -418,31 +469,28 @@ class MuZeroCacheLayer:
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor,
                cache_kwargs: dict[str, Any] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-        """Append key/value states, flush the prefix to quantised storage, return KV for attention.
+        """Take in new key/value tokens, flush the excess to the packed prefix, return the
+        KV the caller's attention reads (reference ``layer.py:402-459``).
 
-        ``materialize_full_kv`` (default True) returns dequantised prefix + residual;
-        the patched decode path passes False and gets only the residual, the fused
-        HIP kernel reading the packed prefix itself.  ``defer_quantize`` skips the
-        flush (prefill, quantised after the dense attention).
+        The first call returns the tokens as given (prefill attention).  Later calls
+        return the dequantised prefix followed by the residual, or only the residual
+        with ``materialize_full_kv=False`` (the fused decode reads the packed prefix
+        itself).  ``defer_quantize`` leaves the flush to a later
+        :meth:`compress_residual_prefix` (prefill quantised after the dense attention).
         """
-        materialize_full_kv = True if cache_kwargs is None else cache_kwargs.get("materialize_full_kv", True)
-        defer_quantize = False if cache_kwargs is None else cache_kwargs.get("defer_quantize", False)
-
-        is_first = not self.is_initialized
-        if is_first:
+        kw = cache_kwargs or {}
+        first = not self.is_initialized
+        if first:
             self.lazy_initialization(key_states, value_states)
-        self._append_dense(key_states, value_states)
+        self._append_tokens(key_states, value_states)
         self.cumulative_length += key_states.shape[-2]
-
-        raw_keys, raw_values = self.keys, self.values
-        if not defer_quantize:
+        # prefill attention reads the tokens before any of them is quantised
+        before_flush = (self.keys, self.values) if first else None
+        if not kw.get("defer_quantize", False):
             self.compress_residual_prefix(decode_flush=key_states.shape[-2] == 1)
-
-        if is_first:
-            return raw_keys, raw_values
-        if not materialize_full_kv:
-            return self.keys, self.values
-        if self._kstore.count == 0 and self._vstore.count == 0:
+        if first:
+            return before_flush
+        if not kw.get("materialize_full_kv", True) or (self._kstore.count == 0 and self._vstore.count == 0):
             return self.keys, self.values
         return (torch.cat([self._dequantize_key_prefix(), self.keys], dim=2),
                 torch.cat([self._dequantize_value_prefix(), self.values], dim=2))
@@ -477,27 +525,30 @@ class MuZeroCacheLayer:
     # ------------------------------------------------------------------
 
     def crop(self, max_length: int) -> None:
-        if max_length < 0:
-            max_length = max(0, self.get_seq_length() + max_length)
-        if max_length >= self.get_seq_length():
+        """Keep the first ``max_length`` tokens (a negative value drops that many from the
+        end), as the reference does (``layer.py:494-506``): the kept tokens, the packed
+        prefix dequantised in the layer dtype followed by the residual, become one dense
+        window that later flushes quantise again."""
+        total = self.get_seq_length()
+        keep = max(0, total + max_length) if max_length < 0 else max_length
+        if keep >= total:
             return
-        full_k = torch.cat([self._dequantize_key_prefix(), self.keys], dim=2)[..., :max_length, :]
-        full_v = torch.cat([self._dequantize_value_prefix(), self.values], dim=2)[..., :max_length, :]
+        dense_k, dense_v = (torch.cat(parts, dim=2)[:, :, :keep] for parts in
+                            ((self._dequantize_key_prefix(), self.keys),
+                             (self._dequantize_value_prefix(), self.values)))
         self.reset()
-        if max_length > 0:
-            self.lazy_initialization(full_k[:, :, :1, :], full_v[:, :, :1, :])
-            self.keys = full_k
-            self.values = full_v
-            self.cumulative_length = max_length
+        if keep:
+            self.lazy_initialization(dense_k, dense_v)
+            self._set_tail(dense_k, dense_v)
+            self.cumulative_length = keep
 
     def _map_tensors(self, fn) -> None:
         """Apply ``fn`` to the residual and to the filled packed prefix (batch dim 0)."""
-        for attr in ("keys", "values"):
-            t = getattr(self, attr, None)
+        for win in (self._kres, self._vres):
+            t = win.tokens()
             if t is not None and t.numel():
-                setattr(self, attr, fn(t))
-        self._key_buffer = self._value_buffer = None
-        self._buffer_capacity = 0
+                win.set(fn(t))
+        self._sync()
         for st in (self._kstore, self._vstore):
             if st.count:
                 st.replace(*(fn(st.view(name)) for name in _STORE_ATTRS))
@@ -529,8 +580,4 @@ class MuZeroCacheLayer:
         # keep pre-calibrated alphas from the config; clear runtime-selected ones
         self._selected_alpha_key = self.cfg.alpha_key
         self._selected_alpha_value = self.cfg.alpha_value
-        self.keys = None
-        self.values = None
-        self._key_buffer = None
-        self._value_buffer = None
-        self._buffer_capacity = 0
+        self._set_tail(None, None)

@@ -115,6 +115,68 @@ def test_step_decode_reuse_matches_fresh_plan():
     assert reused >= steps - 4  # cached arguments served all but the steps after a storage change
 
 
+@pytest.mark.parametrize("keep", [600, 100, -50])
+def test_crop_then_decode(keep):
+    """crop (layer.py:494-506) keeps the first tokens as a dense window (the packed prefix
+    dequantized in the layer dtype, then the residual); the next decode token flushes them again.
+    The stored bytes then equal the oracle's cache for that dense sequence plus the token, and
+    the fused decode matches its attention."""
+    B, hkv, n_rep, d, prefill = 2, 2, 4, 128, 700
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + 1, d, hkv * n_rep, seed=21)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0))
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    _, st = ref.reference_decode(q, k[:, :, :prefill], v[:, :, :prefill], bits=4, alpha_k=2.0, alpha_v=2.0,
+                                 group_size=64, residual=128)
+    n = keep if keep >= 0 else prefill + keep
+    dense_k = torch.cat([st["key_prefix"], st["res_k"]], dim=2)[:, :, :n]
+    dense_v = torch.cat([st["value_prefix"], st["res_v"]], dim=2)[:, :, :n]
+    layer.crop(keep)
+    assert layer.get_seq_length() == n and layer._kstore.count == 0 and layer._vstore.count == 0
+    assert torch.equal(layer.keys.cpu(), dense_k) and torch.equal(layer.values.cpu(), dense_v)
+
+    layer.update(k[:, :, prefill:].to(DEV), v[:, :, prefill:].to(DEV), {"materialize_full_kv": False})
+    seq_k = torch.cat([dense_k, k[:, :, prefill:]], dim=2)
+    seq_v = torch.cat([dense_v, v[:, :, prefill:]], dim=2)
+    exact, st2 = ref.reference_decode(q, seq_k, seq_v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64,
+                                      residual=128, dequant_dtype=torch.float32)
+    state = layer.get_attention_state()
+    assert state["key_prefix_length"] == st2["lq"] == layer.get_seq_length() - layer.keys.shape[2]
+    if st2["lq"]:
+        assert torch.equal(layer._packed_key_q.cpu(), st2["packed_k"])
+        assert torch.equal(layer._packed_value_q.cpu(), st2["packed_v"])
+        assert torch.equal(layer._key_mn.cpu().view(torch.int16), st2["k_mn"].view(torch.int16))
+    assert torch.equal(layer.keys.cpu(), st2["res_k"]) and torch.equal(layer.values.cpu(), st2["res_v"])
+    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
+
+
+def test_batch_select_then_decode():
+    """batch_select_indices / reorder_cache (beam search) keep the selected rows of the packed
+    prefix and the residual; decoding continues on them exactly as on a cache built from those
+    rows alone."""
+    B, hkv, n_rep, d, prefill = 3, 2, 4, 128, 700
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + 1, d, hkv * n_rep, seed=23)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=2, alpha_key=2.0, alpha_value=2.0))
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    idx = torch.tensor([2, 0, 2])
+    layer.reorder_cache(idx.to(DEV))
+    layer.update(k[idx, :, prefill:].to(DEV), v[idx, :, prefill:].to(DEV), {"materialize_full_kv": False})
+    exact, st = ref.reference_decode(q[idx], k[idx], v[idx], bits=2, alpha_k=2.0, alpha_v=2.0, group_size=64,
+                                     residual=128, dequant_dtype=torch.float32)
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q[idx].to(DEV), None, d ** -0.5,
+                                                 layer.get_attention_state())
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
+
+
 @pytest.mark.parametrize("kind", ["key", "value"])
 def test_block_alpha_statistics_on_device(kind):
     """On the GPU the cache's alpha statistics (gathered from the strided block, min / max in
