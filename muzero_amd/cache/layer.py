@@ -196,9 +196,8 @@ class MuZeroCacheLayer:
         self.quant_qmax = float((1 << self.nbits) - 1)
         self.backend = cfg.backend
 
-        # set once from config (None = select at first flush)
-        self._selected_alpha_key = cfg.alpha_key
-        self._selected_alpha_value = cfg.alpha_value
+        # alpha per kind: preset by the config, else chosen at the kind's first flush
+        self._alphas = {"key": cfg.alpha_key, "value": cfg.alpha_value}
 
         self.is_initialized = False
         self.cumulative_length = 0
@@ -237,7 +236,27 @@ class MuZeroCacheLayer:
         return self.residual_length + 4 * self.q_group_size
 
     # ------------------------------------------------------------------
-    # Packed-prefix views (reference attribute names)
+    # Reference attribute names: the alphas and the packed-prefix views
+    # ------------------------------------------------------------------
+
+    @property
+    def _selected_alpha_key(self) -> Optional[float]:
+        return self._alphas["key"]
+
+    @_selected_alpha_key.setter
+    def _selected_alpha_key(self, alpha: Optional[float]) -> None:
+        self._alphas["key"] = alpha
+
+    @property
+    def _selected_alpha_value(self) -> Optional[float]:
+        return self._alphas["value"]
+
+    @_selected_alpha_value.setter
+    def _selected_alpha_value(self, alpha: Optional[float]) -> None:
+        self._alphas["value"] = alpha
+
+    # ------------------------------------------------------------------
+    # Packed-prefix views
     # ------------------------------------------------------------------
 
     @property
@@ -277,14 +296,15 @@ class MuZeroCacheLayer:
     # ------------------------------------------------------------------
 
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        self.dtype = key_states.dtype
-        self.device = key_states.device
-        self._set_tail(torch.empty(0, dtype=self.dtype, device=self.device),
-                       torch.empty(0, dtype=self.dtype, device=self.device))
-        self.k_head_dim = key_states.shape[-1]
-        self.v_head_dim = value_states.shape[-1]
-        self.v_head_dim_padded = ((self.v_head_dim + self.q_group_size - 1) // self.q_group_size) * self.q_group_size
-        self.v_num_groups = self.v_head_dim_padded // self.q_group_size
+        """Take dtype, device and head dims from the first tokens; the residual starts empty.
+        Value rows are cut into whole groups, the last one zero-padded when ``head_dim`` is
+        not a multiple of the group."""
+        self.dtype, self.device = key_states.dtype, key_states.device
+        self.k_head_dim, self.v_head_dim = int(key_states.shape[-1]), int(value_states.shape[-1])
+        self.v_num_groups = -(-self.v_head_dim // self.q_group_size)
+        self.v_head_dim_padded = self.v_num_groups * self.q_group_size
+        empty = torch.empty(0, dtype=self.dtype, device=self.device)
+        self._set_tail(empty, empty)
         self.is_initialized = True
 
     def _can_cuda(self, tensor: torch.Tensor) -> bool:
@@ -330,29 +350,26 @@ class MuZeroCacheLayer:
     # ------------------------------------------------------------------
 
     def _ensure_alpha(self, flat_grouped: torch.Tensor, kind: str) -> float:
-        attr = "_selected_alpha_key" if kind == "key" else "_selected_alpha_value"
-        if getattr(self, attr) is None:
-            alpha = select_alpha(flat_grouped, bits=self.nbits, q_group_size=self.q_group_size, kind=kind,
-                                 max_points=self.cfg.stats_max_points)
-            setattr(self, attr, alpha)
-        return getattr(self, attr)
+        """The kind's alpha, chosen from ``flat_grouped`` (rows of one group) if not yet set."""
+        alpha = self._alphas[kind]
+        if alpha is None:
+            alpha = self._alphas[kind] = select_alpha(flat_grouped, bits=self.nbits, q_group_size=self.q_group_size,
+                                                      kind=kind, max_points=self.cfg.stats_max_points)
+        return alpha
 
     def _alpha_for_block(self, block: torch.Tensor, kind: str) -> float:
-        """The block's alpha; statistics (bits != 4, not preset) see the block grouped
-        exactly as the reference flattens it for ``quantize_rows``."""
-        attr = "_selected_alpha_key" if kind == "key" else "_selected_alpha_value"
-        if getattr(self, attr) is not None or self.nbits == 4:
-            return self._ensure_alpha(block, kind)  # preset, or 4-bit: no statistics
-        bs, nh, sl, hd = block.shape
-        if kind == "key" or self.v_head_dim_padded == hd:
-            # the same statistics gathered from the block itself (no grouped copy)
-            alpha = select_alpha_block(block, bits=self.nbits, q_group_size=self.q_group_size, kind=kind,
-                                       max_points=self.cfg.stats_max_points)
-            setattr(self, attr, alpha)
-            return alpha
-        # values whose head_dim is padded to whole groups: the padded copy, as the reference makes it
-        flat = F.pad(block, (0, self.v_head_dim_padded - hd))
-        return self._ensure_alpha(flat.reshape(-1, self.q_group_size), kind)
+        """The kind's alpha for a ``[B, H, T, D]`` block, chosen (when not yet set) from the
+        same statistics the reference takes over the block's grouped rows."""
+        if self._alphas[kind] is not None or self.nbits == 4:
+            return self._ensure_alpha(block, kind)  # already set, or 4-bit (fixed alpha, no statistics)
+        if kind == "value" and self.v_head_dim_padded != block.shape[-1]:
+            # value rows padded to whole groups: the statistics see the padded rows
+            padded = F.pad(block, (0, self.v_head_dim_padded - block.shape[-1]))
+            return self._ensure_alpha(padded.reshape(-1, self.q_group_size), kind)
+        # read in place from the block (no grouped copy)
+        alpha = self._alphas[kind] = select_alpha_block(block, bits=self.nbits, q_group_size=self.q_group_size,
+                                                        kind=kind, max_points=self.cfg.stats_max_points)
+        return alpha
 
     # ------------------------------------------------------------------
     # Quantise / dequantise
@@ -365,7 +382,7 @@ class MuZeroCacheLayer:
                              backend=self.backend)
 
     def _dequantize_rows(self, packed_q, mn, scale, kind: str) -> torch.Tensor:
-        alpha = self._selected_alpha_key if kind == "key" else self._selected_alpha_value
+        alpha = self._alphas[kind]
         return dequantize_rows(packed_q, mn, scale, self.nbits, float(alpha), self.q_group_size, self.dtype,
                                amax_eps=self.amax_eps)
 
@@ -403,34 +420,39 @@ class MuZeroCacheLayer:
         st.count += t
         return pq, mn, sc
 
+    def _dequantize_span(self, kind: str, start: int, end: int) -> torch.Tensor:
+        """Slots ``[start, end)`` of the kind's packed store as ``[B, H, T, D]`` in the layer
+        dtype.  A key slot is one group of tokens (its rows run along the token axis, one
+        row per channel); a value slot is one token (its rows are the channel groups)."""
+        store, d = (self._kstore, self.k_head_dim) if kind == "key" else (self._vstore, self.v_head_dim)
+        tail = self.keys if kind == "key" else self.values
+        if store.count == 0 or start >= end:
+            return torch.empty((tail.shape[0], tail.shape[1], 0, d), dtype=self.dtype, device=self.device)
+        packed, mn, scale = (store.view(name, start, end).contiguous() for name in _STORE_ATTRS)
+        rows = self._dequantize_rows(packed.flatten(0, -2), mn.flatten(0, -2), scale.flatten(0, -2), kind)
+        b, h, n = packed.shape[:3]
+        if kind == "key":  # [B, H, groups, D, G] -> tokens along dim 2
+            return rows.reshape(b, h, n, d, self.q_group_size).transpose(3, 4).reshape(b, h, n * self.q_group_size, d)
+        return rows.reshape(b, h, n, -1)[..., :d]
+
     def _dequantize_key_range(self, start_group: int, end_group: int) -> torch.Tensor:
-        if self._kstore.count == 0 or start_group >= end_group:
-            return torch.empty((self.keys.shape[0], self.keys.shape[1], 0, self.k_head_dim), dtype=self.dtype,
-                               device=self.device)
-        pq = self._kstore.view("packed", start_group, end_group).contiguous()
-        mn = self._kstore.view("mn", start_group, end_group).contiguous()
-        sc = self._kstore.view("scale", start_group, end_group).contiguous()
-        bs, nh, nsg, hd, _ = pq.shape
-        recon = self._dequantize_rows(pq.reshape(-1, pq.shape[-1]), mn.reshape(-1, 1), sc.reshape(-1, 1), "key")
-        recon = recon.reshape(bs, nh, nsg, hd, self.q_group_size)
-        return recon.permute(0, 1, 2, 4, 3).reshape(bs, nh, nsg * self.q_group_size, hd)
+        return self._dequantize_span("key", start_group, end_group)
 
     def _dequantize_value_range(self, start_token: int, end_token: int) -> torch.Tensor:
-        if self._vstore.count == 0 or start_token >= end_token:
-            return torch.empty((self.values.shape[0], self.values.shape[1], 0, self.v_head_dim), dtype=self.dtype,
-                               device=self.device)
-        pq = self._vstore.view("packed", start_token, end_token).contiguous()
-        mn = self._vstore.view("mn", start_token, end_token).contiguous()
-        sc = self._vstore.view("scale", start_token, end_token).contiguous()
-        recon = self._dequantize_rows(pq.reshape(-1, pq.shape[-1]), mn.reshape(-1, 1), sc.reshape(-1, 1), "value")
-        bs, nh, qt = pq.shape[:3]
-        return recon.reshape(bs, nh, qt, self.v_num_groups * self.q_group_size)[..., :self.v_head_dim]
+        return self._dequantize_span("value", start_token, end_token)
 
     def _dequantize_key_prefix(self) -> torch.Tensor:
         return self._dequantize_key_range(0, self._kstore.count)
 
     def _dequantize_value_prefix(self) -> torch.Tensor:
         return self._dequantize_value_range(0, self._vstore.count)
+
+    def dense_kv(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """Keys and values of every cached token, ``[B, H, T, D]`` in the layer dtype: the
+        packed prefix dequantised, then the residual tail."""
+        k = torch.cat([self._dequantize_key_prefix(), self.keys], dim=2) if self._kstore.count else self.keys
+        v = torch.cat([self._dequantize_value_prefix(), self.values], dim=2) if self._vstore.count else self.values
+        return k, v
 
     # ------------------------------------------------------------------
     # Flush (layer.py:369-396)
@@ -490,10 +512,7 @@ class MuZeroCacheLayer:
             self.compress_residual_prefix(decode_flush=key_states.shape[-2] == 1)
         if first:
             return before_flush
-        if not kw.get("materialize_full_kv", True) or (self._kstore.count == 0 and self._vstore.count == 0):
-            return self.keys, self.values
-        return (torch.cat([self._dequantize_key_prefix(), self.keys], dim=2),
-                torch.cat([self._dequantize_value_prefix(), self.values], dim=2))
+        return self.dense_kv() if kw.get("materialize_full_kv", True) else (self.keys, self.values)
 
     def get_attention_state(self) -> dict[str, Any] | None:
         if not self.is_initialized:
@@ -533,9 +552,7 @@ class MuZeroCacheLayer:
         keep = max(0, total + max_length) if max_length < 0 else max_length
         if keep >= total:
             return
-        dense_k, dense_v = (torch.cat(parts, dim=2)[:, :, :keep] for parts in
-                            ((self._dequantize_key_prefix(), self.keys),
-                             (self._dequantize_value_prefix(), self.values)))
+        dense_k, dense_v = (t[:, :, :keep] for t in self.dense_kv())
         self.reset()
         if keep:
             self.lazy_initialization(dense_k, dense_v)
@@ -577,7 +594,6 @@ class MuZeroCacheLayer:
         self._triton_ok = None
         self._kstore.clear()
         self._vstore.clear()
-        # keep pre-calibrated alphas from the config; clear runtime-selected ones
-        self._selected_alpha_key = self.cfg.alpha_key
-        self._selected_alpha_value = self.cfg.alpha_value
+        # alphas preset by the config stay; chosen ones are chosen again
+        self._alphas = {"key": self.cfg.alpha_key, "value": self.cfg.alpha_value}
         self._set_tail(None, None)
