@@ -18,20 +18,20 @@ GPU_BACKENDS = ("auto", "hip", "cuda")
 
 @dataclass
 class MuZeroConfig:
-    """Configuration for the mu-Zero KV-cache quantizer.
+    """What the cache quantises and when.
 
-    Attributes:
-        bits: Quantization bit-width (1, 2, 3, 4, 7, or 8).
-        q_group_size: Number of values per quantization group (the HIP kernels implement 64).
-        residual_length: Number of most-recent tokens kept at full precision.
-        amax_dtype: Dtype for min/scale metadata ("float16", "bfloat16", "float32").
-        stats_max_points: Maximum sample points used when selecting alpha at runtime.
-        backend: Kernel backend ("auto", "hip"; "cuda" is accepted as the same GPU path).
-        alpha_key: Pre-calibrated alpha for keys.  None = select at first flush.
-        alpha_value: Pre-calibrated alpha for values.  None = select at first flush.
-        logq_compatible_layout: Match legacy LogQ key/value flush boundaries.
-        decode_flush_by_group: Flush decode residuals every q_group_size tokens
-            (default); False restores the 4-group decode flush batch.
+    * ``bits``: code width, one of 1, 2, 3, 4, 7, 8.
+    * ``q_group_size``: values sharing one min / scale pair (64 in the HIP kernels).
+    * ``residual_length``: the newest tokens, held unquantised.
+    * ``amax_dtype``: storage type of min and scale, ``"float16"``, ``"bfloat16"`` or ``"float32"``.
+    * ``stats_max_points``: cap on the values sampled when alpha is chosen from data.
+    * ``backend``: ``"auto"`` or ``"hip"`` (``"cuda"`` names the same GPU path).
+    * ``alpha_key`` / ``alpha_value``: a fixed alpha per kind; ``None`` chooses it from the
+      first block flushed.
+    * ``logq_compatible_layout``: flush boundaries of the legacy LogQ cache (values flush
+      token by token).
+    * ``decode_flush_by_group``: decode flushes one group at a time (default); ``False``
+      waits for four groups.
     """
 
     bits: int = 4

@@ -179,33 +179,27 @@ def _subsample_positions(numel: int, max_points: int, device) -> torch.Tensor:
 
 
 def _subsample(tensor: torch.Tensor, max_points: int) -> torch.Tensor:
-    """Every ``numel // max_points``-th element, at most ``max_points`` (``quantizer.py:86-91``)."""
+    """The elements at :func:`_subsample_positions` of the flattened tensor (``quantizer.py:86-91``)."""
     flat = tensor.reshape(-1)
-    if flat.numel() <= max_points:
-        return flat
-    step = max(1, flat.numel() // max_points)
-    return flat[::step][:max_points]
+    return flat if flat.numel() <= max_points else flat[_subsample_positions(flat.numel(), max_points, flat.device)]
 
 
 def _prepare_groups(tensor: torch.Tensor, *, q_group_size: int, kind: str) -> torch.Tensor:
     """Groups of ``q_group_size`` values as the cache forms them (``quantizer.py:94-112``):
     keys per channel over consecutive tokens, values per token over channels.  Kept in
     the tensor's dtype (the reference converts to fp32 first; min / max are the same values)."""
-    work = tensor
-    if work.dim() == 2:
-        n, gs = work.shape
-        if gs != q_group_size:
-            ng = max(1, gs // q_group_size)
-            work = work[:, :ng * q_group_size].reshape(n, ng, q_group_size)
-            return work.unsqueeze(0).unsqueeze(0)
-        return work.unsqueeze(0).unsqueeze(0).unsqueeze(0)
-    if kind == "key":
-        work = work.transpose(2, 3).contiguous()
-    bs, nh, sl, hd = work.shape
-    hd_pad = ((hd + q_group_size - 1) // q_group_size) * q_group_size
-    if hd_pad != hd:
-        work = F.pad(work, (0, hd_pad - hd), value=0)
-    return work.reshape(bs, nh, sl, hd_pad // q_group_size, q_group_size)
+    g = q_group_size
+    if tensor.dim() == 2:  # rows already; a width other than g is cut into whole groups
+        n, width = tensor.shape
+        if width == g:
+            return tensor.reshape(1, 1, 1, n, g)
+        groups = max(1, width // g)
+        return tensor[:, :groups * g].reshape(1, 1, n, groups, g)
+    rows = tensor.transpose(2, 3) if kind == "key" else tensor  # the group axis last
+    short = -rows.shape[-1] % g
+    if short:
+        rows = F.pad(rows, (0, short))  # zero-fill the last group
+    return rows.reshape(*rows.shape[:3], -1, g)
 
 
 # ---------------------------------------------------------------------------
@@ -298,21 +292,16 @@ def roundtrip(
     if alpha_value is None:
         alpha_value = select_alpha(value, bits=bits, q_group_size=q_group_size, kind="value")
 
-    def _rt(tensor: torch.Tensor, alpha: float, kind: str) -> torch.Tensor:
-        bs, nh, sl, hd = tensor.shape
-        if kind == "key":
-            nsg = sl // q_group_size
-            flat = tensor.reshape(bs, nh, nsg, q_group_size, hd).permute(0, 1, 2, 4, 3).contiguous()
-            flat = flat.reshape(-1, q_group_size)
-            pq, mn, sc = quantize_rows(flat.float(), bits, alpha, amax_eps, amax_dtype)
-            recon = dequantize_rows(pq, mn, sc, bits, alpha, q_group_size, tensor.dtype, amax_eps=amax_eps)
-            recon = recon.reshape(bs, nh, nsg, hd, q_group_size).permute(0, 1, 2, 4, 3)
-            return recon.reshape(bs, nh, sl, hd).contiguous()
-        hd_pad = ((hd + q_group_size - 1) // q_group_size) * q_group_size
-        t = F.pad(tensor, (0, hd_pad - hd)) if hd_pad != hd else tensor
-        flat = t.reshape(bs, nh, sl, hd_pad // q_group_size, q_group_size).reshape(-1, q_group_size)
-        pq, mn, sc = quantize_rows(flat.float(), bits, alpha, amax_eps, amax_dtype)
-        recon = dequantize_rows(pq, mn, sc, bits, alpha, q_group_size, tensor.dtype, amax_eps=amax_eps)
-        return recon.reshape(bs, nh, sl, hd_pad)[..., :hd].contiguous()
+    g = q_group_size
 
-    return _rt(key, alpha_key, "key"), _rt(value, alpha_value, "value")
+    def codec(rows: torch.Tensor, alpha: float, dtype: torch.dtype) -> torch.Tensor:
+        packed, mn, scale = quantize_rows(rows.float(), bits, alpha, amax_eps, amax_dtype)
+        return dequantize_rows(packed, mn, scale, bits, alpha, g, dtype, amax_eps=amax_eps)
+
+    b, h, s, d = key.shape
+    k_rows = key.reshape(b, h, s // g, g, d).transpose(3, 4).reshape(-1, g)  # one channel, g tokens
+    k_out = codec(k_rows, alpha_key, key.dtype).reshape(b, h, s // g, d, g).transpose(3, 4).reshape(b, h, s, d)
+    vd = value.shape[-1]
+    v_rows = F.pad(value, (0, -vd % g)).reshape(-1, g)  # one token, g channels (last group zero-filled)
+    v_out = codec(v_rows, alpha_value, value.dtype).reshape(*value.shape[:3], -1)[..., :vd]
+    return k_out.contiguous(), v_out.contiguous()

@@ -280,3 +280,26 @@ def test_config0_round_trip(dname):
     kx, vx = k[:, :, :896].float(), v[:, :, :896].float()
     key_mse = ((kx - dk.float()) ** 2).mean(dim=2) / (kx ** 2).mean(dim=2)  # per channel: outliers are x10
     assert key_mse.mean().item() < 0.015 and ((vx - dv.float()) ** 2).mean().item() < 0.015
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_roundtrip_matches_oracle(bits):
+    """``muzero_amd.roundtrip`` (rows quantised from fp32, keys per channel over 64 tokens,
+    values per token over 64 channels with a zero-filled last group) equals the oracle's
+    quantise -> dequantise of the same rows, bit for bit."""
+    import muzero_amd as mz
+
+    g = torch.Generator().manual_seed(60 + bits)
+    key = (torch.randn(2, 3, 128, 128, generator=g) * 2).to(torch.bfloat16)
+    value = torch.randn(2, 3, 128, 96, generator=g).to(torch.bfloat16)
+    k_out, v_out = mz.roundtrip(key.to(DEV), value.to(DEV), bits=bits, alpha_key=2.0, alpha_value=4.0)
+    torch.cuda.synchronize()
+
+    def oracle(rows, alpha):
+        pq, mn, sc = ref.quantize_rows(rows, bits, alpha, 1e-8, torch.float16)
+        return ref.dequantize_rows(pq, mn, sc, bits, alpha, 64, torch.bfloat16)
+
+    k_exp = oracle(ref.key_rows(key.float(), 64), 2.0).reshape(2, 3, 2, 128, 64)
+    k_exp = k_exp.transpose(3, 4).reshape(2, 3, 128, 128)
+    v_exp = oracle(ref.value_rows(value.float(), 64), 4.0).reshape(2, 3, 128, 128)[..., :96]
+    assert torch.equal(k_out.cpu(), k_exp) and torch.equal(v_out.cpu(), v_exp)
