@@ -201,8 +201,6 @@ class MuZeroCacheLayer:
 
         self.is_initialized = False
         self.cumulative_length = 0
-        self._cuda_ok = None
-        self._triton_ok = None
 
         self._kstore = _PackedStore()
         self._vstore = _PackedStore()
@@ -306,15 +304,6 @@ class MuZeroCacheLayer:
         empty = torch.empty(0, dtype=self.dtype, device=self.device)
         self._set_tail(empty, empty)
         self.is_initialized = True
-
-    def _can_cuda(self, tensor: torch.Tensor) -> bool:
-        """Whether the HIP path can run on ``tensor`` (reference name, ``layer.py:100-112``)."""
-        if not tensor.is_cuda:
-            return False
-        if self._cuda_ok is None:
-            _k.load_mu_zero_cuda_extension()
-            self._cuda_ok = True
-        return True
 
     def _q_bytes(self) -> int:
         return (self.q_group_size * self.nbits + 7) // 8
@@ -590,8 +579,6 @@ class MuZeroCacheLayer:
     def reset(self) -> None:
         self.is_initialized = False
         self.cumulative_length = 0
-        self._cuda_ok = None
-        self._triton_ok = None
         self._kstore.clear()
         self._vstore.clear()
         # alphas preset by the config stay; chosen ones are chosen again
