@@ -261,3 +261,32 @@ def test_generate_uses_fused_decode_and_matches_dequant_path(arch, monkeypatch):
         scale = b.abs().max().item()
         assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
     assert torch.equal(fused.sequences[:, :301], dense.sequences[:, :301])
+
+
+def test_generate_legacy_request_forms_match():
+    """``cache_implementation="quantized"`` with a legacy ``logq{b}_zeroanchor_stat_cuda[_opt]``
+    backend, and ``mu_zero_{b}bit`` with the ``quant_backend`` alias, build the same cache and
+    produce identical scores and tokens; ``cache[i]`` afterwards gives every token densely."""
+    mz.patch_transformers()
+    model = _tiny_model("qwen3")
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, 512, (2, 260), generator=g).to(DEV)
+    common = dict(max_new_tokens=3, do_sample=False, output_scores=True, return_dict_in_generate=True,
+                  pad_token_id=0)
+    runs = {}
+    for name, impl, cfg in (("legacy", "quantized", {"backend": "logq2_zeroanchor_stat_cuda_opt",
+                                                     "residual_length": 128}),
+                            ("alias", "mu_zero_2bit", {"quant_backend": "auto", "residual_length": 128})):
+        with torch.no_grad():
+            runs[name] = model.generate(ids, cache_implementation=impl, cache_config=cfg, **common)
+    a, b = runs["legacy"], runs["alias"]
+    assert torch.equal(a.sequences, b.sequences)
+    for s in range(3):
+        assert torch.equal(a.scores[s], b.scores[s]), s
+    cache = a.past_key_values
+    assert isinstance(cache, mz.MuZeroCache) and cache.cfg.bits == 2
+    [k], [v] = cache[0]
+    assert k.shape[2] == v.shape[2] == cache.get_seq_length() == 262
+    layer = cache.layers[0]
+    assert layer.get_attention_state()["key_prefix_length"] == 128  # 262 - 128 residual -> 2 whole groups
+    torch.testing.assert_close(k[:, :, 128:], layer.keys, rtol=0, atol=0)
