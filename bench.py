@@ -40,7 +40,7 @@ if ROOT not in sys.path:
 
 
 def algorithmic_bytes(B, hkv, hq, d, lq, r, bits):
-    """Packed codes + fp16 metadata (K and V) + bf16 residual K/V + Q + O."""
+    """Algorithmic bytes of one decode call: packed codes + fp16 metadata (K and V), bf16 residual K/V, Q and O."""
     qb = 8 * bits
     ng = (d + 63) // 64
     k = B * hkv * (lq // 64) * d * (qb + 4)
@@ -398,7 +398,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the packed-KV decode path is sharded by batch or kv-head "
-              "with no exchange inside the path (see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "with no exchange inside the path; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb, args.steps)
