@@ -6,8 +6,11 @@
  * enums and a hipStream_t (0 = the default stream), launches asynchronously
  * and returns an int status (0 = success, negative = argument error, or the
  * positive hipError_t of a failed launch).  Nothing here allocates device
- * memory; callers own every buffer.  Calls are thread-safe: the library keeps
- * no mutable global state.
+ * memory; callers own every buffer.  Calls are thread-safe.  The library's
+ * only mutable state is per device and process: each device's compute-unit
+ * count and whether the general decode kernels' dynamic-LDS limit has been
+ * raised on it, both filled on the first call on that device (idempotent, so
+ * concurrent first calls are harmless).
  *
  * Reference boundary being replaced: the pybind11 module returned by
  * load_mu_zero_cuda_extension() (muzero/kernels/loader.py:37-94, 1862-1880),
@@ -141,10 +144,9 @@ typedef struct mz_decode_args {
   void* workspace; int64_t workspace_bytes;
   int n_split;      /* 0 = let the library choose */
   int kernel_path;  /* MZ_PATH_AUTO, or force MZ_PATH_EXACT / MZ_PATH_FOLD */
-  /* The compander alphas the expm1 tables were built for.  The general
-   * kernel evaluates the 7- and 8-bit expm1 rows from them (those rows do not
-   * fit in LDS); they must be > 0 when bits >= 7 and there is a quantized
-   * prefix, and are not read otherwise. */
+  /* The compander alphas the expm1 and fold tables were built for.  Recorded
+   * for the caller; the kernels read every table value from e_key / e_value /
+   * fold_k / fold_v and do not read these. */
   float alpha_key, alpha_value;
   /* Quantized value tokens when they differ from the 64*n_groups quantized
    * key tokens (logq_compatible_layout flushes values per token,

@@ -13,10 +13,17 @@ kernel does all of it in a single pass over the packed prefix and the
 residual window with an online softmax, split over tokens, followed by a
 small cross-split combine kernel.
 
-Statistics counters (``get_mu_zero_decode_stats``): ``calls``, ``returns``,
-``missing_layer``, ``non_decode_query`` as in the reference, and
-``hip_fused_decode`` for each call served by the fused kernel (the reference
-counts ``fused_qk_success`` / ``fused_av_success`` for its two launches).
+Statistics counters (``get_mu_zero_decode_stats``) keep the reference's names
+(``attention.py:171-177``, ``:209-211``, ``:270-272``), which its throughput
+harness reads (``benchmarks/bench_throughput.py:341-343``): ``calls``,
+``returns``, ``missing_layer``, ``non_decode_query``; per fused call
+``fused_qk_success`` when there is a quantized key prefix, ``fused_av_success``
+when there is a quantized value prefix, and ``fused_prefix_decode_success`` /
+``fused_prefix_decode_chunked_success`` (the one kernel is the split-over-tokens
+prefix decode with the residual merged in); plus ``hip_fused_decode`` for
+every call the kernel serves.  When the launch raises, the matching
+``*_fallback`` counters are incremented as in the reference, and the error
+propagates: this build has no dequantize-then-attend fallback to run instead.
 """
 
 from __future__ import annotations
@@ -84,11 +91,51 @@ def mu_zero_decode_attention_forward(
     fast = getattr(layer, "_hip_decode", None)
     key = None
     if attention_mask is None and has_res and value_prefix_length == key_prefix_length:
-        key = (id(layer._kstore.packed), id(layer._vstore.packed), layer._kstore.count > 0,
-               layer._kres.stamp(), layer._vres.stamp(),
-               layer._kres.buf is not None and layer._vres.buf is not None,
-               query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key, alpha_value,
-               float(scaling))
+        storage = _storage_key(layer)
+        if storage is not None:
+            key = (storage, query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key,
+                   alpha_value, float(scaling))
+    try:
+        out = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
+                      scaling, attention_mask, value_prefix_length)
+    except Exception:
+        _count(key_prefix_length, value_prefix_length, "fallback")
+        raise
+    _count(key_prefix_length, value_prefix_length, "success")
+    _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
+    _MU_ZERO_DECODE_STATS["returns"] += 1
+    return out, None
+
+
+def _count(key_prefix_length: int, value_prefix_length: int, outcome: str) -> None:
+    """The reference's per-launch counters for one fused call (``outcome``: success / fallback)."""
+    if key_prefix_length > 0:
+        _MU_ZERO_DECODE_STATS[f"fused_qk_{outcome}"] += 1
+        _MU_ZERO_DECODE_STATS[f"fused_prefix_decode_{outcome}"] += 1
+        if outcome == "success":
+            _MU_ZERO_DECODE_STATS["fused_prefix_decode_chunked_success"] += 1
+    if value_prefix_length > 0:
+        _MU_ZERO_DECODE_STATS[f"fused_av_{outcome}"] += 1
+
+
+def _storage_key(layer):
+    """Device addresses of every buffer a cached decode launch points into, or None when the
+    residual windows are not in their decode buffers.  The cached launch keeps those
+    buffers alive, so while it is cached no other tensor can be allocated at these
+    addresses: a key match means the same storage (a Python ``id`` would not: a freed
+    tensor object's id is re-used at once)."""
+    ks, vs, kr, vr = layer._kstore, layer._vstore, layer._kres, layer._vres
+    if kr.buf is None or vr.buf is None:
+        return None
+
+    def store(st):
+        return (st.packed.data_ptr(), st.mn.data_ptr(), st.scale.data_ptr()) if st.count else None
+
+    return store(ks), store(vs), kr.buf.data_ptr(), kr.start, vr.buf.data_ptr(), vr.start
+
+
+def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value, scaling,
+            attention_mask, value_prefix_length):
     if fast is not None and key is not None and fast.key == key:
         out = fast.launch(query, n_groups, r)
     else:
@@ -107,7 +154,5 @@ def mu_zero_decode_attention_forward(
         out = plan.run()
         # cache the validated arguments only when every pointer they hold is
         # stable across steps (residual windows in their decode buffers, no mask)
-        layer._hip_decode = _k.StepDecode(plan, key) if key is not None and key[5] else None
-    _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
-    _MU_ZERO_DECODE_STATS["returns"] += 1
-    return out, None
+        layer._hip_decode = _k.StepDecode(plan, key) if key is not None else None
+    return out

@@ -124,10 +124,6 @@ class _ResidualWindow:
         self.clear()
         self.loose = self.view = t
 
-    def stamp(self):
-        """Identifies the memory the window's tokens start at (changes on a flush or a move)."""
-        return None if self.buf is None else (id(self.buf), self.start)
-
     def _room_for_one(self, min_cap: int) -> None:
         live = self.tokens()
         n = len(self)
@@ -217,6 +213,9 @@ class MuZeroCacheLayer:
         self._vres = _ResidualWindow(4 * self.q_group_size)
 
         self.keys = self.values = None  # the windows' tokens (reference names), kept in step by _sync
+        # the decode hook's cached launch arguments (they point into the storage above);
+        # dropped whenever that storage is replaced
+        self._hip_decode = None
 
     # ------------------------------------------------------------------
     # The full-precision tail
@@ -542,7 +541,7 @@ class MuZeroCacheLayer:
         if keep >= total:
             return
         dense_k, dense_v = (t[:, :, :keep] for t in self.dense_kv())
-        self.reset()
+        self.reset()  # also drops the cached decode launch
         if keep:
             self.lazy_initialization(dense_k, dense_v)
             self._set_tail(dense_k, dense_v)
@@ -550,6 +549,7 @@ class MuZeroCacheLayer:
 
     def _map_tensors(self, fn) -> None:
         """Apply ``fn`` to the residual and to the filled packed prefix (batch dim 0)."""
+        self._hip_decode = None
         for win in (self._kres, self._vres):
             t = win.tokens()
             if t is not None and t.numel():
@@ -577,6 +577,7 @@ class MuZeroCacheLayer:
             self._map_tensors(lambda t: t.to(self.device, non_blocking=True) if t.device != self.device else t)
 
     def reset(self) -> None:
+        self._hip_decode = None
         self.is_initialized = False
         self.cumulative_length = 0
         self._kstore.clear()

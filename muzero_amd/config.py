@@ -1,11 +1,12 @@
 """MuZeroConfig: the parameters of the mu-Zero KV-cache path.
 
 Mirrors ``muzero/config.py:7-51`` of the reference: same fields, defaults,
-validation messages and ``from_dict``.  The one difference is the backend
-set: this build runs the HIP kernels only, so ``"auto"``, ``"hip"`` and the
-reference's ``"cuda"`` (accepted as a name for the same GPU path) select it,
-and ``"triton"`` / ``"torch"`` are rejected with an error instead of silently
-running a different implementation.
+validation messages and ``from_dict``.  The backend names are the
+reference's (``"auto"``, ``"cuda"``, ``"triton"``, ``"torch"``) plus
+``"hip"``.  This build has one implementation, the HIP kernels, so every name
+selects it for device tensors (the reference's ``"triton"`` and ``"torch"``
+produce the same bytes there: the kernels are bit-exact to the torch
+quantizer); a CPU tensor is an error whatever the backend.
 """
 
 from __future__ import annotations
@@ -13,7 +14,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Optional
 
-GPU_BACKENDS = ("auto", "hip", "cuda")
+BACKENDS = ("auto", "cuda", "triton", "torch", "hip")
 
 
 @dataclass
@@ -25,7 +26,8 @@ class MuZeroConfig:
     * ``residual_length``: the newest tokens, held unquantised.
     * ``amax_dtype``: storage type of min and scale, ``"float16"``, ``"bfloat16"`` or ``"float32"``.
     * ``stats_max_points``: cap on the values sampled when alpha is chosen from data.
-    * ``backend``: ``"auto"`` or ``"hip"`` (``"cuda"`` names the same GPU path).
+    * ``backend``: ``"auto"``, ``"cuda"``, ``"triton"``, ``"torch"`` or ``"hip"``; all run
+      the HIP kernels on device tensors.
     * ``alpha_key`` / ``alpha_value``: a fixed alpha per kind; ``None`` chooses it from the
       first block flushed.
     * ``logq_compatible_layout``: flush boundaries of the legacy LogQ cache (values flush
@@ -53,12 +55,8 @@ class MuZeroConfig:
         if self.amax_dtype not in {"float16", "bfloat16", "float32"}:
             raise ValueError(
                 f"`amax_dtype` must be one of {{'float16','bfloat16','float32'}}, got {self.amax_dtype}")
-        if self.backend in {"triton", "torch"}:
-            raise ValueError(
-                f"`backend`={self.backend!r} is not provided by this build: the mu-Zero path runs on its HIP "
-                "kernels only (use 'auto' or 'hip')")
-        if self.backend not in GPU_BACKENDS:
-            raise ValueError(f"`backend` must be one of {{'auto','hip','cuda'}}, got {self.backend}")
+        if self.backend not in BACKENDS:
+            raise ValueError(f"`backend` must be one of {{'auto','cuda','triton','torch','hip'}}, got {self.backend}")
         if self.decode_flush_by_group and self.residual_length % self.q_group_size != 0:
             raise ValueError(
                 "`residual_length` must be a multiple of `q_group_size` when `decode_flush_by_group=True`")

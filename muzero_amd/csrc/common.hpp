@@ -8,12 +8,48 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/muzero_hip.h"
 
 namespace mz {
 
 constexpr int kWave = 64;
 constexpr int kGroup = 64;  // q_group_size supported by the HIP path
+
+// ---------------------------------------------------------------- per-device host state
+// The library's only mutable state: facts fetched from the runtime once per
+// device and process.  A slot is written with the same value by whichever
+// thread gets there first, so concurrent first calls are harmless.
+constexpr int kMaxDevices = 64;
+
+// Compute units of the current device (256 if the runtime cannot tell).
+inline int device_cu_count() {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  const bool slot = dev >= 0 && dev < kMaxDevices;
+  if (slot) {
+    const int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  if (slot) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+// Raise kernel `fn`'s dynamic LDS limit to `bytes` on the current device,
+// once per device (`done` holds one bit per device, owned by the caller).
+inline hipError_t set_dynamic_lds(const void* fn, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const uint64_t bit = dev >= 0 && dev < kMaxDevices ? (uint64_t)1 << dev : 0;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_relaxed);
+  return e;
+}
 
 // ---------------------------------------------------------------- rounding
 // torch's float -> bfloat16 conversion: round to nearest even, NaN -> 0x7FC0

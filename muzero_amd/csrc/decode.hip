@@ -23,11 +23,11 @@
 // owns two adjacent channels of a K chunk (two key groups) or two adjacent
 // tokens of a V chunk (two value groups), so a group's parameters are formed
 // once per tile and each code costs one table read and a few branch-free ops.
-// Codes of up to 6 bits read the reference's fp32 expm1 rows from LDS and
-// reproduce its dequantized value bit for bit before the rounding; the 7- and
-// 8-bit rows (32 KB and 128 KB per alpha) do not fit next to the staging
-// buffers, so those widths evaluate expm1 with the hardware exp2 (a few fp32
-// ulp from the reference's value before the same rounding to the layer dtype).
+// Every width reproduces the reference's dequantized value bit for bit before
+// the rounding to the layer dtype (its op order, its fp32 expm1 rows): codes
+// of up to 6 bits read the rows from LDS, the 7- and 8-bit rows (32 KB and
+// 128 KB per alpha, too large to sit next to the staging buffers) are read
+// from the host-built table in global memory (L2-resident).
 // A tile's packed words are loaded one tile ahead: the next tile's key words
 // are issued as soon as this tile's keys are staged, its value words as soon
 // as this tile's values are.
@@ -63,36 +63,26 @@ struct Lds {
   // expm1 rows for bins 1..qmax (codes of up to 6 bits), forward and
   // reversed, one pair of tables per alpha
   static constexpr int e_floats(int bits) { return bits <= 6 ? ((1 << bits) - 1) * ((1 << bits) + 2) / 2 : 0; }
-  // fast form: one signed expm1 value per (zero level, code), (2^bits)^2 floats per alpha
-  static constexpr int z_floats(int bits) { return bits <= 6 ? (1 << bits) * (1 << bits) : 0; }
-  static constexpr size_t bytes(int bits, bool fast) {
-    return (size_t)WAVES_BYTES + (fast ? 2 * (size_t)z_floats(bits) : 4 * (size_t)e_floats(bits)) * 4;
-  }
+  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 4 * (size_t)e_floats(bits) * 4; }
 };
 
 // One group's dequantization parameters (muzero/quantizer.py:241-255, from the
 // stored metadata, scale guarded as in loader.py:201).
 struct DeqG {
-  float za, s, mn, pe, mne;  // mne = -ne (7/8 bits: pe / alpha and -ne / alpha)
-  float cp, cn;              // 7/8 bits: log2(1 + alpha) / pb, / nb
+  float za, s, mn, pe, mne;  // mne = -ne
   int zl;                    // zero level, an integer in 0..qmax
-  int bp, bn;                // <= 6 bits: LDS byte address of code q's expm1 entry is (q >= zl ? bp : bn) + 4q
-  float fa, fp, fn;          // fast form: x = fa + (q >= zl ? fp : fn) * Z[zl][q]
-  float fb;                  // fast form, 7/8 bits: x = (q >= zl ? fp : fn) * e + (q >= zl ? fa : fb)
+  // <= 6 bits: LDS byte address of code q's expm1 entry is (q >= zl ? bp : bn) + 4q;
+  // 7/8 bits: its index in the global table is q >= zl ? bp + q : bn - q
+  int bp, bn;
+  const float* eg;           // 7/8 bits: the global expm1 table
 };
 
 // `ebase`: LDS byte address of the forward expm1 rows E[bins][d]; the reversed
 // rows R[bins][k] = E[bins][bins - k] follow them (same row offsets), so a
 // code below the zero level reads R[nb][q] = E[nb][zl - q] (nb = zl then)
 // and both sides index with +q.
-// `fast`, codes of up to 6 bits: the table at `ebase` is Z[zl][q] =
-// +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] (q < zl), and the value is
-// a + (s*pe or s*ne) * Z with a = mn + s*za: the reference's value to a few
-// fp32 ulp (its fused CUDA kernels' fp32 codebook form), one table read and
-// about five ops per code.  `fast`, 7 and 8 bits: the same value with the
-// expm1 term from the hardware exp2, one fma per code after it.
-template <int BITS, bool FAST>
-__device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float inv_alpha, int ebase) {
+template <int BITS>
+__device__ __forceinline__ DeqG deq_group(float mn, float s, int ebase, const float* eg) {
   constexpr float qmax = (float)((1 << BITS) - 1);
   constexpr int EF = ((1 << BITS) - 1) * ((1 << BITS) + 2) / 2;
   const DeqRow r = deq_row(mn, s, qmax, true);
@@ -103,31 +93,15 @@ __device__ __forceinline__ DeqG deq_group(float mn, float s, float lb2, float in
   g.pe = r.pe;
   g.mne = -r.ne;
   g.zl = r.zl == r.zl ? (int)r.zl : 0;  // a NaN zero level reads row 1 (pb = nb = 1), never past the table
-  if constexpr (FAST && BITS > 6) {
-    // e = 2^(|q - zl| * log2(1 + alpha) / bins) = 1 + alpha * expm1 term:
-    // x = a + (s*pe/alpha) * (e - 1) above the zero level, a - (s*ne/alpha) * (e - 1) below
-    const float fa = r.mn + r.s * r.za;
-    g.cp = lb2 / r.pb;
-    g.cn = lb2 / r.nb;
-    g.fp = r.s * r.pe * inv_alpha;
-    g.fn = -(r.s * r.ne * inv_alpha);
-    g.fa = fa - g.fp;
-    g.fb = fa - g.fn;
-    return g;
-  } else if constexpr (FAST) {
-    g.bp = ebase + 4 * (g.zl << BITS);
-    g.fa = r.mn + r.s * r.za;
-    g.fp = r.s * r.pe;
-    g.fn = r.s * r.ne;
-    return g;
-  }
-  g.bp = ebase + 4 * (r.offp - g.zl);
-  g.bn = ebase + 4 * (EF + r.offn);
-  if constexpr (BITS > 6) {
-    g.cp = lb2 / r.pb;
-    g.cn = lb2 / r.nb;
-    g.pe *= inv_alpha;
-    g.mne *= inv_alpha;
+  if constexpr (BITS <= 6) {
+    g.bp = ebase + 4 * (r.offp - g.zl);
+    g.bn = ebase + 4 * (EF + r.offn);
+  } else {
+    // E[pb][q - zl] and E[nb][zl - q] (row offsets expm1_row(bins)); q and zl
+    // lie in 0..qmax, so the index stays inside the table for any metadata
+    g.bp = r.offp - g.zl;
+    g.bn = r.offn + g.zl;
+    g.eg = eg;
   }
   return g;
 }
@@ -138,40 +112,27 @@ __device__ __forceinline__ float lds_load_f32(int addr) {
   return *(const __attribute__((address_space(3))) float*)(size_t)(uint32_t)addr;
 }
 
-// Dequantized fp32 value of code q.  Up to 6 bits this is the reference's
-// value exactly: norm = za + pe*E[pb][q-zl] or za - ne*E[nb][zl-q] (the sign
-// folded into mne is exact), clamped, times s, plus mn, with no contraction.
-// Split in two so a block of codes can issue all its table reads before
-// using any: deq_fetch returns the table entry (or, for 7/8 bits, evaluates
-// the expm1 term), deq_apply finishes the value.
-template <int BITS, bool FAST>
+// Dequantized fp32 value of code q, the reference's value exactly: norm =
+// za + pe*E[pb][q-zl] or za - ne*E[nb][zl-q] (the sign folded into mne is
+// exact), clamped, times s, plus mn, with no contraction.  Split in two so a
+// block of codes can issue all its table reads before using any: deq_fetch
+// returns the table entry, deq_apply finishes the value.
+template <int BITS>
 __device__ __forceinline__ float deq_fetch(const DeqG& g, int q) {
   const bool pos = q >= g.zl;
-  if constexpr (FAST && BITS > 6) {
-    return __builtin_amdgcn_exp2f(fabsf((float)(q - g.zl)) * (pos ? g.cp : g.cn));
-  } else if constexpr (FAST) {
-    return lds_load_f32(g.bp + 4 * q);
-  } else if constexpr (BITS <= 6) {
-    return lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
-  } else {
-    // pe * expm1(|q - zl| / bins * log1p(alpha)) / alpha, the 1/alpha folded into pe (ne)
-    const float c = pos ? g.pe : g.mne;
-    const float e = __builtin_amdgcn_exp2f(fabsf((float)(q - g.zl)) * (pos ? g.cp : g.cn));
-    return __builtin_fmaf(c, e, -c);
-  }
+  if constexpr (BITS <= 6) return lds_load_f32((pos ? g.bp : g.bn) + 4 * q);
+  else return g.eg[pos ? g.bp + q : g.bn - q];
 }
-template <int BITS, bool FAST>
+template <int BITS>
 __device__ __forceinline__ float deq_apply(const DeqG& g, int q, float z) {
   const bool pos = q >= g.zl;
-  if constexpr (FAST && BITS > 6) return __builtin_fmaf(pos ? g.fp : g.fn, z, pos ? g.fa : g.fb);
-  if constexpr (FAST) return __builtin_fmaf(pos ? g.fp : g.fn, z, g.fa);
-  const float t = BITS <= 6 ? (pos ? g.pe : g.mne) * z : z;
+  const float t = (pos ? g.pe : g.mne) * z;
   const float norm = __builtin_amdgcn_fmed3f(g.za + t, 0.f, 1.f);
   return norm * g.s + g.mn;
 }
-template <int BITS, bool FAST>
+template <int BITS>
 __device__ __forceinline__ float deq_code(const DeqG& g, int q) {
-  return deq_apply<BITS, FAST>(g, q, deq_fetch<BITS, FAST>(g, q));
+  return deq_apply<BITS>(g, q, deq_fetch<BITS>(g, q));
 }
 
 // Code `idx` of an LSB-first bitstream held in registers (idx is a constant
@@ -216,7 +177,7 @@ __device__ __forceinline__ uint32_t io_pair_to_f16(uint16_t h0, uint16_t h1) {
   else return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{bf2f(h0), bf2f(h1)}), f16x2_t));
 }
 
-template <int D, int BITS, int IO, bool FAST>
+template <int D, int BITS, int IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, int direct) {
   using L = Lds<D>;
@@ -229,7 +190,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int KTPL = D == 128 ? 64 : 32;  // K tokens per lane and tile
   constexpr int KWR = KTPL * BITS / 32;  // K words per row and lane
   constexpr int EF = L::e_floats(BITS);
-  constexpr int ZF = L::z_floats(BITS);
   constexpr bool kTab = BITS <= 6;
 
   extern __shared__ __align__(16) uint16_t lds[];
@@ -245,23 +205,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint16_t* kv = lds + wave * L::WAVE_HALVES;
   uint16_t* pb = kv + L::STAGE;
   constexpr int EK_BASE = L::WAVES_BYTES;                              // key table
-  constexpr int EV_BASE = L::WAVES_BYTES + (FAST ? 4 * ZF : 8 * EF);  // value table
-  if constexpr (FAST && kTab) {
-    // Z[zl][q] = +E[pb][q - zl] (q >= zl) or -E[nb][zl - q] from the expm1 rows
-    if (a.n_groups > 0 || a.v_prefix > 0) {
-      float* zK = (float*)((uint8_t*)lds + EK_BASE);
-      float* zV = (float*)((uint8_t*)lds + EV_BASE);
-      constexpr int QM = (1 << BITS) - 1;
-      for (int i = threadIdx.x; i < ZF; i += 256) {
-        const int zl = i >> BITS, q = i & QM;
-        const int bins = q >= zl ? max(QM - zl, 1) : max(zl, 1);
-        const int idx = (bins - 1) * (bins + 2) / 2 + (q >= zl ? q - zl : zl - q);
-        zK[i] = q >= zl ? a.e_key[idx] : -a.e_key[idx];
-        zV[i] = q >= zl ? a.e_value[idx] : -a.e_value[idx];
-      }
-    }
-    __syncthreads();
-  } else if constexpr (kTab) {
+  constexpr int EV_BASE = L::WAVES_BYTES + 8 * EF;  // value table
+  if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
     if (a.n_groups > 0 || a.v_prefix > 0) {
       float* eK = (float*)((uint8_t*)lds + EK_BASE);
@@ -280,11 +225,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     __syncthreads();
   }
-  // 7/8 bits: expm1(d/bins * log1p(alpha)) / alpha = (2^(d * log2(1+alpha)/bins) - 1) / alpha
-  const float lb2k = kTab ? 0.f : __log2f(1.f + a.alpha_key);
-  const float lb2v = kTab ? 0.f : __log2f(1.f + a.alpha_value);
-  const float iak = kTab ? 0.f : 1.f / a.alpha_key;
-  const float iav = kTab ? 0.f : 1.f / a.alpha_value;
 
   // Q rows as the MFMA A operand: lane (m=n, g) holds Q[m][32*ks + 8g .. +7].
   u32x4 qa[D / 32];
@@ -376,7 +316,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     DeqG gk[2];
     if (quant) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS, FAST>(kmeta[r][0], kmeta[r][1], lb2k, iak, EK_BASE);
+      for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], EK_BASE, a.e_key);
     }
 #pragma unroll
     for (int kc = 0; kc < KCH; ++kc) {
@@ -391,15 +331,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int wi = (KCH == 2 ? 32 * kc : 0) + i0 + u;  // code index in the lane's words
             q0[u] = code_at<BITS>(kw[0], wi);
             q1[u] = code_at<BITS>(kw[1], wi);
-            z0[u] = deq_fetch<BITS, FAST>(gk[0], q0[u]);
-            z1[u] = deq_fetch<BITS, FAST>(gk[1], q1[u]);
+            z0[u] = deq_fetch<BITS>(gk[0], q0[u]);
+            z1[u] = deq_fetch<BITS>(gk[1], q1[u]);
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
             const int row = (KCH == 2 ? 0 : 32 * ts) + i0 + u;  // token row of the chunk
             *(uint32_t*)(kv + row * L::K_LD + 2 * cp) =
-                pack_io<IO>(deq_apply<BITS, FAST>(gk[0], q0[u], z0[u]), deq_apply<BITS, FAST>(gk[1], q1[u], z1[u]));
+                pack_io<IO>(deq_apply<BITS>(gk[0], q0[u], z0[u]), deq_apply<BITS>(gk[1], q1[u], z1[u]));
           }
         }
       } else {
@@ -486,7 +426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (quant) {
         DeqG gv[2];
 #pragma unroll
-        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS, FAST>(vmeta[vc][r][0], vmeta[vc][r][1], lb2v, iav, EV_BASE);
+        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], EV_BASE, a.e_value);
 #pragma unroll
         for (int i0 = 0; i0 < 32; i0 += 8) {
           int q0[8], q1[8];
@@ -495,14 +435,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int u = 0; u < 8; ++u) {
             q0[u] = code_at<BITS>(vw[vc][0], i0 + u);
             q1[u] = code_at<BITS>(vw[vc][1], i0 + u);
-            z0[u] = deq_fetch<BITS, FAST>(gv[0], q0[u]);
-            z1[u] = deq_fetch<BITS, FAST>(gv[1], q1[u]);
+            z0[u] = deq_fetch<BITS>(gv[0], q0[u]);
+            z1[u] = deq_fetch<BITS>(gv[1], q1[u]);
           }
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int u = 0; u < 8; ++u)
             *(uint32_t*)(kv + (32 * cs + i0 + u) * L::V_LD + cs * L::V_HI + 2 * tp) =
-                pack_io_f16<IO>(deq_apply<BITS, FAST>(gv[0], q0[u], z0[u]), deq_apply<BITS, FAST>(gv[1], q1[u], z1[u]));
+                pack_io_f16<IO>(deq_apply<BITS>(gv[0], q0[u], z0[u]), deq_apply<BITS>(gv[1], q1[u], z1[u]));
         }
       } else if (dv > 0) {
         // misaligned value prefix (logq_compatible_layout): the first dv
@@ -520,12 +460,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int i = 0; i < BITS; ++i) w[i] = row[i];
             const int64_t mi = vmb + at * NG + vc;
-            const DeqG gq = deq_group<BITS, FAST>(meta_load(a.v_mn, mi, a.meta_dtype), meta_load(a.v_scale, mi, a.meta_dtype),
-                                            lb2v, iav, EV_BASE);
+            const DeqG gq = deq_group<BITS>(meta_load(a.v_mn, mi, a.meta_dtype), meta_load(a.v_scale, mi, a.meta_dtype),
+                                            EV_BASE, a.e_value);
 #pragma unroll
             for (int i = 0; i < 32; i += 2) {
-              const uint32_t h = pack_io_f16<IO>(deq_code<BITS, FAST>(gq, code_at<BITS>(w, i)),
-                                                 deq_code<BITS, FAST>(gq, code_at<BITS>(w, i + 1)));
+              const uint32_t h = pack_io_f16<IO>(deq_code<BITS>(gq, code_at<BITS>(w, i)),
+                                                 deq_code<BITS>(gq, code_at<BITS>(w, i + 1)));
               col[i * L::V_LD] = (uint16_t)h;
               col[(i + 1) * L::V_LD] = (uint16_t)(h >> 16);
             }
@@ -671,18 +611,6 @@ bool fold_supported(const mz_decode_args* a);
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 
-static int decode_cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-      n = cus;
-    else
-      n = 256;
-  }
-  return n;
-}
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + kTile - 1) / kTile;
@@ -692,7 +620,7 @@ static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
     // fill the resident workgroup slots (two per CU) once: each workgroup then
     // loads its tables and query once and runs all its tiles in one pass
     const int64_t units = (int64_t)a->batch * a->kv_heads;
-    const int64_t slots = 2 * (int64_t)decode_cu_count();
+    const int64_t slots = 2 * (int64_t)device_cu_count();
     ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
   }
@@ -721,12 +649,10 @@ static int check_args(const mz_decode_args* a) {
   const int64_t v_dense = (int64_t)a->n_residual - (a->v_prefix ? a->v_prefix - (int64_t)a->n_groups * 64 : 0);
   if (a->n_residual > 0 && !a->k_res) return MZ_EINVAL;
   if (v_dense > 0 && !a->v_res) return MZ_EINVAL;
-  if (a->n_groups > 0 && a->bits >= 7 && !(a->alpha_key > 0.f && a->alpha_value > 0.f)) return MZ_EINVAL;
   if (a->v_prefix != 0) {
     const int64_t lk = (int64_t)a->n_groups * 64;
     if (a->v_prefix < lk || a->v_prefix > lk + a->n_residual) return MZ_EINVAL;
     if (a->v_prefix > lk && (!a->v_packed || !a->v_mn || !a->v_scale || !a->e_value)) return MZ_EINVAL;
-    if (a->v_prefix > lk && a->bits >= 7 && !(a->alpha_value > 0.f)) return MZ_EINVAL;
   }
   // 16-byte vector loads of query rows and residual rows
   if (((uintptr_t)a->query & 15) || (a->q_sh & 7) || (a->q_sb & 7)) return MZ_EINVAL;
@@ -769,7 +695,7 @@ extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
   return use_fold(a) ? 1 : 0;
 }
 
-template <int D, int IO, bool FAST>
+template <int D, int IO>
 static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   int tps;
   const int ns = choose_split(a, &tps);
@@ -781,12 +707,11 @@ static int launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) 
   switch (a->bits) {
 #define MZ_CASE(BB)                                                                                           \
   case BB: {                                                                                                  \
-    constexpr bool F = FAST;                                                                                  \
-    const size_t lds = Lds<D>::bytes(BB, F);                                                                  \
-    static const hipError_t attr = hipFuncSetAttribute(                                                       \
-        (const void*)decode_split_kernel<D, BB, IO, F>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds); \
+    const size_t lds = Lds<D>::bytes(BB);                                                                     \
+    static std::atomic<uint64_t> lds_set{0};                                                                  \
+    const hipError_t attr = set_dynamic_lds((const void*)decode_split_kernel<D, BB, IO>, (int)lds, lds_set);  \
     if (attr != hipSuccess) return (int)attr;                                                                 \
-    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO, F>), grid, dim3(256), lds, s, *a, tps, ns, dir);       \
+    hipLaunchKernelGGL((decode_split_kernel<D, BB, IO>), grid, dim3(256), lds, s, *a, tps, ns, dir);       \
   } break;
     MZ_CASE(1) MZ_CASE(2) MZ_CASE(3) MZ_CASE(4) MZ_CASE(5) MZ_CASE(6) MZ_CASE(7) MZ_CASE(8)
 #undef MZ_CASE
@@ -817,21 +742,14 @@ static int decode_check_launchable(const mz_decode_args* a) {
   return MZ_OK;
 }
 
-template <bool FAST>
-static int launch_general_t(const mz_decode_args* a, hipStream_t s, bool direct) {
+static int launch_general(const mz_decode_args* a, hipStream_t s, bool direct) {
   if (a->head_dim == 128)
-    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16, FAST>(a, s, direct)
-                                  : launch_partials<128, MZ_F16, FAST>(a, s, direct);
-  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16, FAST>(a, s, direct)
-                                : launch_partials<64, MZ_F16, FAST>(a, s, direct);
+    return a->io_dtype == MZ_BF16 ? launch_partials<128, MZ_BF16>(a, s, direct)
+                                  : launch_partials<128, MZ_F16>(a, s, direct);
+  return a->io_dtype == MZ_BF16 ? launch_partials<64, MZ_BF16>(a, s, direct)
+                                : launch_partials<64, MZ_F16>(a, s, direct);
 }
 
-// kernel_path "exact" keeps the bit-exact dequantization; otherwise codes of
-// up to 6 bits take the fast (fp32 codebook) form
-static int launch_general(const mz_decode_args* a, hipStream_t s, bool direct) {
-  return a->kernel_path == MZ_PATH_EXACT ? launch_general_t<false>(a, s, direct)
-                                         : launch_general_t<true>(a, s, direct);
-}
 
 extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t stream) {
   const int st = decode_check_launchable(a);

@@ -11,8 +11,12 @@
 // is an MFMA whose A operand carries the group scalars times the query (for
 // P.V: the softmax weight times the token's scalars) and whose B operand is
 // a table lookup (an fp16 pair) per code, contracting over (channel, side)
-// pairs.  The constant part sum_c Q_c*a_c is one more MFMA against a ones
-// operand.  No element is ever dequantized to memory.  The dequantized
+// pairs.  The constant part sum_c Q_c*a_c is one more MFMA per 16 channels,
+// contracting over (channel, part): A = the fp16 query (exact) twice, B = a
+// as an fp16 hi + lo pair (a is the group's value nearest zero, large for
+// one-signed groups, so one fp16 rounding of it would not do); the values'
+// constant part sum_t p_t*a_t is an fp32 row reduction.  No element is ever
+// dequantized to memory.  The dequantized
 // values are those of the reference's fused CUDA kernels: full precision
 // (their fp32 codebooks, loader.py:197-263), not rounded to the layer dtype.
 //
@@ -56,7 +60,6 @@ constexpr int TILE = 64;  // tokens per tile
 // Waves per workgroup (one per SIMD; two workgroups share a CU).
 template <int NREP>
 constexpr int waves_for() { return 4; }
-constexpr uint32_t ONES_F16X2 = 0x3C003C00u;
 // (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
 // zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
 // level (one channel / one token-group), and each group owns a disjoint bank
@@ -89,7 +92,6 @@ __device__ __forceinline__ uint32_t pair_shift(int n) {
 constexpr int AROW = D + 4;         // uint32 per head row of the key A operand
 constexpr int HROW = D / 2 + 4;     // uint32 per head row of fp16 [D] arrays
 constexpr int LROW = TILE + 4;      // uint32 per head row of per-token arrays
-constexpr int PROW = TILE / 2 + 4;  // uint32 per head row of fp16 per-token arrays
 
 // Static LDS layout (bytes).  Per workgroup: the two (P, N) tables and the
 // query in two forms; per wave: the current tile's operands and weights.
@@ -99,19 +101,20 @@ struct Smem {
   static constexpr int TBL_V = TBL;
   static constexpr int Q16 = 2 * TBL;                 // fp16 [NREP][HROW*2]
   static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
-  static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
+  static constexpr int QD = Q_IO + NREP * HROW * 4;   // uint32 [NREP][AROW]   (q, q) fp16 per channel
+  static constexpr int ZERO = QD + NREP * AROW * 4;   // AROW zero words: A rows that must be 0
   static constexpr int WAVE0 = ZERO + AROW * 4;
   // per-wave region
   static constexpr int KZP = 0;                      // uint32 [4 g][8 kt]    zl of channels 16kt+4g+{0..3}
   static constexpr int AHI = KZP + 4 * 8 * 4;        // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
   static constexpr int ALO = AHI + NREP * AROW * 4;  // uint32 [NREP][AROW]   low part
-  static constexpr int QA = ALO + NREP * AROW * 4;   // fp16 [NREP][HROW*2]   q*a
-  static constexpr int VZP = QA + NREP * HROW * 4;   // uint32 [NG][4 g][4 kt] zl of tokens 16kt+4g+{0..3}
-  static constexpr int VBP = VZP + NG * 4 * 4 * 4;   // uint32 [NG][TILE]     (bp, bn) fp16
-  static constexpr int VA = VBP + NG * TILE * 4;     // fp16 [NG][TILE]       a
-  static constexpr int PA = VA + NG * TILE * 2;         // uint32 [NG][NREP][LROW]   (p*bp, p*bn) fp16
-  static constexpr int PA1 = PA + NG * NREP * LROW * 4;  // fp16 [NG][NREP][PROW*2]   p*a
-  static constexpr int PER_WAVE = (PA1 + NG * NREP * PROW * 4 + 15) / 16 * 16;
+  static constexpr int KA = ALO + NREP * AROW * 4;   // uint32 [D]            (a hi, a lo) fp16 per channel
+  static constexpr int VZP = KA + D * 4;             // uint32 [NG][4 g][4 kt] zl of tokens 16kt+4g+{0..3}
+  static constexpr int VBP = VZP + NG * 4 * 4 * 4;   // float2 [NG][TILE]     (bp, bn)
+  static constexpr int VA = VBP + NG * TILE * 8;     // fp32 [NG][TILE]       a
+  static constexpr int PA = VA + NG * TILE * 4;      // uint32 [NG][NREP][LROW]   (p*bp, p*bn) fp16, high part
+  static constexpr int PALO = PA + NG * NREP * LROW * 4;  // uint32 [NG][NREP][LROW]   low part
+  static constexpr int PER_WAVE = (PALO + NG * NREP * LROW * 4 + 15) / 16 * 16;
   static constexpr int MERGE = (2 * NREP + NREP * D) * 4;  // per wave at the end (aliases the wave area)
   static constexpr int WAVE_AREA = WAVES * (PER_WAVE > MERGE ? PER_WAVE : MERGE);
   static constexpr int TOTAL = WAVE0 + WAVE_AREA;
@@ -121,11 +124,6 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
-}
-
-__device__ __forceinline__ uint32_t pk_mul(uint32_t x, uint32_t y) {
-  const h2 r = __builtin_bit_cast(h2, x) * __builtin_bit_cast(h2, y);
-  return __builtin_bit_cast(uint32_t, r);
 }
 
 // q*b0 and q*b1 as fp16 pairs hi + lo with hi + lo = q*b to about 2^-22
@@ -139,6 +137,13 @@ __device__ __forceinline__ uint2 split_product(_Float16 q, float b0, float b1) {
   const _Float16 l0 = (_Float16)__builtin_fmaf(fq, b0, -(float)h0);
   const _Float16 l1 = (_Float16)__builtin_fmaf(fq, b1, -(float)h1);
   return uint2{__builtin_bit_cast(uint32_t, h2{h0, h1}), __builtin_bit_cast(uint32_t, h2{l0, l1})};
+}
+
+// x as an fp16 pair (hi, lo) with hi + lo = x to about 2^-22 relative.
+__device__ __forceinline__ uint32_t split_value(float x) {
+  const _Float16 h = (_Float16)x;
+  const _Float16 l = (_Float16)(x - (float)h);
+  return __builtin_bit_cast(uint32_t, h2{h, l});
 }
 
 // Exponent k with |v| * 2^k < 2^15 (fp16 operands and products stay finite).
@@ -177,7 +182,10 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
 // (bounded by their filled length, so a load past it reads 0, never faults).
 struct Bufs {
   __amdgpu_buffer_rsrc_t kp, vp, kmn, ksc, vmn, vsc;
-  __amdgpu_buffer_rsrc_t kr, vr;  // residual rows (bounded by the filled rows: padding tokens read 0)
+  // first residual row of this (batch, kv-head); each residual tile bounds its
+  // own buffer by its filled rows (padding tokens read 0)
+  const uint16_t* kr;
+  const uint16_t* vr;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_t bytes) {
@@ -390,9 +398,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * D * meta_es);
     bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NG * meta_es);
     bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NG * meta_es);
-    const int64_t nr = a.n_residual;
-    bf.kr = make_buf((const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh, nr ? ((nr - 1) * a.kr_st + D) * 2 : 0);
-    bf.vr = make_buf((const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh, nr ? ((nr - 1) * a.vr_st + D) * 2 : 0);
+    bf.kr = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
+    bf.vr = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
   }
 
   // The split's tiles in virtual order: residual tiles first (their loads
@@ -443,8 +450,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     if (i >= NREP * D) break;
     const uint16_t raw = qraw[j];
     const float qf = M::load(raw);
-    ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = f2h(qf);
+    const uint32_t qh = f2h(qf);
+    ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = (uint16_t)qh;
     ((uint16_t*)(smem + S::Q_IO))[h * HROW * 2 + c] = raw;
+    ((uint32_t*)(smem + S::QD))[h * AROW + c] = qh | (qh << 16);
     qabs = fmaxf(qabs, fabsf(qf));
   }
   qabs = wave_max_fast(qabs);
@@ -461,17 +470,21 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
   uint32_t* pa = (uint32_t*)(W + S::PA);
-  uint16_t* pa1 = (uint16_t*)(W + S::PA1);
+  uint32_t* pa_lo = (uint32_t*)(W + S::PALO);
 
   // A-operand row n of this lane belongs to query head hA = n / RS.  For
   // QK, row 0 of a head's rows carries the high fp16 part of the key-side
-  // product and row 1 its low part (both against the same codes, summed per
-  // logit); the head's remaining rows are zero.  For PV only row 0 is used.
+  // products (q*bp, q*bn against the codes) and row 1 their low part (summed
+  // per logit), the head's remaining rows are zero; the constant part uses
+  // row 0 only (the query, twice, against a's hi + lo pairs).  For PV row 0
+  // carries the high fp16 part of p*bp, p*bn and row 1 the low part (summed
+  // at the end); the other rows repeat row 1 and are not read.
   const int hA = n / RS;
   const int rA = n % RS;
   const uint8_t* a_hi_row = rA == 0 ? W + S::AHI + hA * AROW * 4
                                     : (rA == 1 ? W + S::ALO + hA * AROW * 4 : smem + S::ZERO);
-  const uint8_t* qa_row = rA == 0 ? W + S::QA + hA * HROW * 4 : smem + S::ZERO;
+  const uint8_t* qd_row = rA == 0 ? smem + S::QD + hA * AROW * 4 : smem + S::ZERO;
+  const uint32_t* pv_row = (rA == 0 ? pa : pa_lo) + hA * LROW;  // PV A operand: this row's head
   const uint8_t* qio_row = rA == 0 ? smem + S::Q_IO + hA * HROW * 4 : smem + S::ZERO;
   const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
   // MFMA output element (g, i) = row 4g+i: head slot s is element i = s*RS
@@ -482,14 +495,18 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   float m_run[HS], l_run[HS];
 #pragma unroll
   for (int s = 0; s < HS; ++s) m_run[s] = -INFINITY, l_run[s] = 0.f;
-  f32x4 acc[NG][4], acc_a[NG];
+  f32x4 acc[NG][4];
+  // the values' constant part sum_t p_t * a_t per head slot and value group
+  // (fp32; the same in the 16 lanes of a head's row)
+  float acc_a[HS][NG];
 #pragma unroll
   for (int vg = 0; vg < NG; ++vg) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[vg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc_a[vg] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sl = 0; sl < HS; ++sl) acc_a[sl][vg] = 0.f;
   }
-  int kacc = 0;  // acc holds sum p * x * 2^kacc
+  int kacc = 0;  // acc and acc_a hold sum p * x * 2^kacc
   bool kacc_init = false;
 
   // ---------------- per-tile scalars, computed for the NEXT tile in 8 chunks
@@ -500,7 +517,6 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   struct ScalState {
     GroupScalars k0, k1, v0, v1;
     float kmx, vmx;
-    uint32_t ka;
   } sc;
   float unscale_n = a.scaling;  // next tile's logit factor: scaling * 2^-kexp
   int kvexp_n = 0;              // next tile's value exponent
@@ -534,17 +550,18 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       unscale_n = ldexpf(a.scaling, -kexp);
       sc.k0.bp = ldexpf(sc.k0.bp, kexp), sc.k0.bn = ldexpf(sc.k0.bn, kexp);
       sc.k1.bp = ldexpf(sc.k1.bp, kexp), sc.k1.bn = ldexpf(sc.k1.bn, kexp);
-      sc.ka = pack_h2(ldexpf(sc.k0.a, kexp), ldexpf(sc.k1.a, kexp));
+      // a of channels 2*lane, 2*lane+1 as (hi, lo) pairs: the constant part's B operand
+      *(uint2*)(W + S::KA + 8 * lane) = uint2{split_value(ldexpf(sc.k0.a, kexp)), split_value(ldexpf(sc.k1.a, kexp))};
       kvexp_n = range_exp(sc.vmx);
     } else if (chunk == 3) {
       // keep the accumulators' exponent unless the tile needs a smaller one
       kvexp_n = min(kacc_init ? kacc : 60, kvexp_n);
-      ((uint32_t*)(W + S::VBP))[lane] = pack_h2(ldexpf(sc.v0.bp, kvexp_n), ldexpf(sc.v0.bn, kvexp_n));
-      ((uint32_t*)(W + S::VBP))[TILE + lane] = pack_h2(ldexpf(sc.v1.bp, kvexp_n), ldexpf(sc.v1.bn, kvexp_n));
-      ((uint16_t*)(W + S::VA))[lane] = f2h(ldexpf(sc.v0.a, kvexp_n));
-      ((uint16_t*)(W + S::VA))[TILE + lane] = f2h(ldexpf(sc.v1.a, kvexp_n));
+      ((float2*)(W + S::VBP))[lane] = float2{ldexpf(sc.v0.bp, kvexp_n), ldexpf(sc.v0.bn, kvexp_n)};
+      ((float2*)(W + S::VBP))[TILE + lane] = float2{ldexpf(sc.v1.bp, kvexp_n), ldexpf(sc.v1.bn, kvexp_n)};
+      ((float*)(W + S::VA))[lane] = ldexpf(sc.v0.a, kvexp_n);
+      ((float*)(W + S::VA))[TILE + lane] = ldexpf(sc.v1.a, kvexp_n);
     } else {
-      // key-side products of heads HPC*(chunk-4) ...: q*bp, q*bn as fp16 hi + lo, and q*a
+      // key-side products of heads HPC*(chunk-4) ...: q*bp, q*bn as fp16 hi + lo
 #pragma unroll
       for (int hh = 0; hh < HPC; ++hh) {
         const int h = HPC * (chunk - 4) + hh;
@@ -555,7 +572,6 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
           const uint2 p1_ = split_product(qh.y, sc.k1.bp, sc.k1.bn);
           *(uint2*)(W + S::AHI + (h * AROW + 2 * lane) * 4) = uint2{p0.x, p1_.x};
           *(uint2*)(W + S::ALO + (h * AROW + 2 * lane) * 4) = uint2{p0.y, p1_.y};
-          *(uint32_t*)(W + S::QA + (h * HROW + lane) * 4) = pk_mul(q01, sc.ka);
         }
       }
     }
@@ -586,12 +602,14 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     float unscale = unscale_n;
     if (quant) {
       wave_lds_sync();  // this tile's scalars were written by other lanes
-      // ---------- S = Q K^T: constant part (ones operand), then the folded codes
+      // ---------- S = Q K^T: constant part (the same for every token: the
+      // query against a's (hi, lo) pairs), then the folded codes
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 A = *(const u32x4*)(qa_row + (32 * kq + 8 * g) * 2);
-        s0 = Mfma<MZ_F16>::run(A, u32x4{ONES_F16X2, ONES_F16X2, ONES_F16X2, ONES_F16X2}, s0);
+      for (int kq = 0; kq < 8; ++kq) {
+        const u32x4 A = *(const u32x4*)(qd_row + (16 * kq + 4 * g) * 4);
+        const u32x4 Bq = *(const u32x4*)(W + S::KA + (16 * kq + 4 * g) * 4);
+        s0 = Mfma<MZ_F16>::run(A, Bq, s0);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = s0;
@@ -622,22 +640,26 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     } else {
       // ---------- residual tile: S = Q K^T with dense operands; the weight
       // products below then use (bp, bn) = (2^kv_exp, 0) and a = 0: A =
-      // (p * 2^kv_exp, 0), so the accumulators keep their exponent (at most
-      // 15: p * 2^15 stays finite in fp16) whatever the tile order
+      // (p * 2^kv_exp, 0), exact in fp16 (low parts 0), so the accumulators
+      // keep their exponent (at most 15: p * 2^15 stays finite in fp16)
+      // whatever the tile order
       kv_exp = min(kacc_init ? kacc : 15, 15);
       unscale = a.scaling;
-      const uint32_t unit_h = (uint32_t)f2h(ldexpf(1.f, kv_exp));
+      const float unit = ldexpf(1.f, kv_exp);
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) {
-        ((uint32_t*)(W + S::VBP))[vg * TILE + lane] = unit_h;
-        ((uint16_t*)(W + S::VA))[vg * TILE + lane] = 0;
+        ((float2*)(W + S::VBP))[vg * TILE + lane] = float2{unit, 0.f};
+        ((float*)(W + S::VA))[vg * TILE + lane] = 0.f;
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      // key vectors in two batches of 8 per lane, each batch in flight at once
-      // (rows past the residual read 0 through the bounded buffer; their
-      // logits are masked)
+      // key vectors in two batches of 8 per lane, each batch in flight at once.
+      // The buffer starts at the tile's first row and ends after its last
+      // filled row, so the per-lane offset (row, lane group's column) carries
+      // every bound: rows past the residual read 0 (their logits are masked);
+      // the 32-column step rides in the scalar offset and never leaves a row.
       const int kst = a.kr_st * 2;
+      const __amdgpu_buffer_rsrc_t krb = make_buf(bf.kr + (int64_t)r0 * a.kr_st, (n_valid - 1) * kst + D * 2);
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         u32x4 kb[2][4];
@@ -647,7 +669,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
           for (int jt = 0; jt < 4; ++jt)
             kb[k2][jt] = __builtin_bit_cast(
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           bf.kr, (4 * n + jt) * kst + (32 * (2 * kh + k2) + 8 * g) * 2, r0 * kst, 0));
+                           krb, (4 * n + jt) * kst + 16 * g, 64 * (2 * kh + k2), 0));
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) {
           const u32x4 qv = *(const u32x4*)(qio_row + (32 * (2 * kh + k2) + 8 * g) * 2);
@@ -663,6 +685,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
     float corr[HS];
     bool moved = false;
+    // factor taking the accumulators from exponent kacc to this tile's kv_exp
+    const float fexp = ldexpf(1.f, kv_exp - kacc);
 #pragma unroll
     for (int sl = 0; sl < HS; ++sl) {
       const int i = sl * RS;  // MFMA output element of this head slot
@@ -683,29 +707,44 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       moved |= corr[sl] != 1.f;
       m_run[sl] = m_new;
       float psum = 0.f;
-      uint32_t pp[4];
       uint16_t ph[4];
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt) {
         const float p = (x[jt] == -INFINITY) ? 0.f : __expf(x[jt] - m_new);
         ph[jt] = f2h(p);
         psum += h2f(ph[jt]);
-        pp[jt] = (uint32_t)ph[jt] | ((uint32_t)ph[jt] << 16);
       }
       psum = group_reduce<16>(psum, OpAdd());
       l_run[sl] = l_run[sl] * corr[sl] + psum;
+      // the values' constant part of this head: the running sum rescaled,
+      // plus sum_t p_t * a_t over the tile, in fp32 with the same (fp16)
+      // weights as the rest of the row
+      const float fa = corr[sl] * fexp;
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg) {
+        const f32x4 av = *(const f32x4*)(W + S::VA + (vg * TILE + 4 * n) * 4);
+        float c = h2f(ph[0]) * av[0];
+        c = __builtin_fmaf(h2f(ph[1]), av[1], c);
+        c = __builtin_fmaf(h2f(ph[2]), av[2], c);
+        c = __builtin_fmaf(h2f(ph[3]), av[3], c);
+        acc_a[sl][vg] = __builtin_fmaf(acc_a[sl][vg], fa, group_reduce<16>(c, OpAdd()));
+      }
       if (owner) {
-        // PV A operands of this head's 4 tokens: p times the token's (bp, bn) and a
+        // PV A operands of this head's 4 tokens: p times the token's (bp, bn),
+        // as fp16 hi + lo pairs
         const int h = h0 + sl;
-        const uint32_t ph01 = (uint32_t)ph[0] | ((uint32_t)ph[1] << 16);
-        const uint32_t ph23 = (uint32_t)ph[2] | ((uint32_t)ph[3] << 16);
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
-          const u32x4 bq = *(const u32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 4);
-          const uint2 av = *(const uint2*)(W + S::VA + (vg * TILE + 4 * n) * 2);
-          *(u32x4*)(pa + (vg * NREP + h) * LROW + 4 * n) =
-              u32x4{pk_mul(pp[0], bq[0]), pk_mul(pp[1], bq[1]), pk_mul(pp[2], bq[2]), pk_mul(pp[3], bq[3])};
-          *(uint2*)(pa1 + (vg * NREP + h) * PROW * 2 + 4 * n) = uint2{pk_mul(ph01, av.x), pk_mul(ph23, av.y)};
+          const f32x4 b01 = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 8);
+          const f32x4 b23 = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 8 + 16);
+          const h2 p01 = __builtin_bit_cast(h2, (uint32_t)ph[0] | ((uint32_t)ph[1] << 16));
+          const h2 p23 = __builtin_bit_cast(h2, (uint32_t)ph[2] | ((uint32_t)ph[3] << 16));
+          const uint2 w0 = split_product(p01.x, b01[0], b01[1]);
+          const uint2 w1 = split_product(p01.y, b01[2], b01[3]);
+          const uint2 w2 = split_product(p23.x, b23[0], b23[1]);
+          const uint2 w3 = split_product(p23.y, b23[2], b23[3]);
+          *(u32x4*)(pa + (vg * NREP + h) * LROW + 4 * n) = u32x4{w0.x, w1.x, w2.x, w3.x};
+          *(u32x4*)(pa_lo + (vg * NREP + h) * LROW + 4 * n) = u32x4{w0.y, w1.y, w2.y, w3.y};
         }
       }
     }
@@ -713,8 +752,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
 
     // ---------- rescale the accumulators (softmax correction and value-tile exponent),
     // skipped when no head's maximum moved and the exponent is unchanged
+    // (acc_a was rescaled above)
     if (__ballot(owner && moved) != 0 || kv_exp != kacc || !kacc_init) {
-      const float fexp = ldexpf(1.f, kv_exp - kacc);
       kacc = kv_exp;
       kacc_init = true;
 #pragma unroll
@@ -724,8 +763,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[vg][j][i] *= f;
-          acc_a[vg][i] *= f;
+          for (int j = 0; j < 4; ++j) acc[vg][j][i] *= f, acc[vg][j][i + 1] *= f;
         }
       }
     }
@@ -736,7 +774,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       u32x4 vz[NG];
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
-      u32x4 Ac = *(const u32x4*)(pa + hA * LROW + 4 * g);
+      u32x4 Ac = *(const u32x4*)(pv_row + 4 * g);
       u32x4 Bc[4], Bn[4];
       lookup_ktile<BITS, S::TBL_V>(smem, VW[0], VW[1], vz[0][0], grep, odd, lsh, Bc);
 #pragma unroll
@@ -745,7 +783,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
         u32x4 An;
         if (st + 1 < 4 * NG) {
           const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
-          An = *(const u32x4*)(pa + (vg1 * NREP + hA) * LROW + 16 * kt1 + 4 * g);
+          An = *(const u32x4*)(pv_row + vg1 * NREP * LROW + 16 * kt1 + 4 * g);
           lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, lsh, Bn);
         }
         scal_chunk(MN, st);  // the next tile's scalars, chunk st
@@ -758,29 +796,26 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
           for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
         }
       }
-      // constant part: sum_t p_t * a_t against a ones operand
-#pragma unroll
-      for (int kq = 0; kq < 2; ++kq) {
-#pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
-          const u32x4 A = *(const u32x4*)(pa1 + (vg * NREP + hA) * PROW * 2 + 32 * kq + 8 * g);
-          acc_a[vg] = Mfma<MZ_F16>::run(A, u32x4{ONES_F16X2, ONES_F16X2, ONES_F16X2, ONES_F16X2}, acc_a[vg]);
-        }
-      }
     } else {
       // residual values: B pairs (v, 0) against A pairs (p, 0); each k-tile's
-      // 8 value vectors are loaded together (padding rows read 0, p = 0 there)
+      // 8 value vectors are loaded together through a buffer that starts at
+      // the k-tile's first row and ends after its last filled row (padding
+      // rows read 0, p = 0 there); the value-group column step rides in the
+      // scalar offset and never leaves a row
       const int vst = a.vr_st * 2;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        const u32x4 pd = *(const u32x4*)(pa + hA * LROW + 16 * kt + 4 * g);  // (p, 0) pairs
+        const u32x4 pd = *(const u32x4*)(pv_row + 16 * kt + 4 * g);  // (p, 0) pairs (row 1: zeros)
+        const int rows = n_valid - 16 * kt;
+        const __amdgpu_buffer_rsrc_t vrb =
+            make_buf(bf.vr + (int64_t)(r0 + 16 * kt) * a.vr_st, rows > 0 ? (rows - 1) * vst + D * 2 : 0);
         uint32_t vv[NG][4][2];
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg)
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
-            const auto raw = __builtin_amdgcn_raw_buffer_load_b64(
-                bf.vr, (16 * kt + 4 * g + ii) * vst + (64 * vg + 4 * n) * 2, r0 * vst, 0);
+            const auto raw =
+                __builtin_amdgcn_raw_buffer_load_b64(vrb, (4 * g + ii) * vst + 8 * n, 128 * vg, 0);
             vv[vg][ii][0] = raw[0];
             vv[vg][ii][1] = raw[1];
           }
@@ -858,8 +893,9 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg)
         *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n) =
-            f32x4{acc[vg][0][i] + acc_a[vg][i], acc[vg][1][i] + acc_a[vg][i], acc[vg][2][i] + acc_a[vg][i],
-                  acc[vg][3][i] + acc_a[vg][i]} * unit;
+            f32x4{acc[vg][0][i] + acc[vg][0][i + 1] + acc_a[sl][vg], acc[vg][1][i] + acc[vg][1][i + 1] + acc_a[sl][vg],
+                  acc[vg][2][i] + acc[vg][2][i + 1] + acc_a[sl][vg], acc[vg][3][i] + acc[vg][3][i + 1] + acc_a[sl][vg]} *
+            unit;
     }
   }
   __syncthreads();
@@ -932,18 +968,6 @@ bool fold_supported(const mz_decode_args* a) {
          fold_meta_aligned(a->v_scale, a->vm_sb, a->vm_sh, a->meta_dtype);
 }
 
-static int fold_cu_count() {
-  static int n = 0;
-  if (n == 0) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-      n = cus;
-    else
-      n = 256;
-  }
-  return n;
-}
 
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + fold::TILE - 1) / fold::TILE;
@@ -952,7 +976,7 @@ int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
     // fill the resident workgroup slots (two per CU) once: every workgroup
     // then runs its tiles in one pass with its tables loaded once
     const int64_t units = (int64_t)a->batch * a->kv_heads;
-    const int64_t slots = 2 * (int64_t)fold_cu_count();
+    const int64_t slots = 2 * (int64_t)device_cu_count();
     ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
   }
@@ -969,7 +993,7 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const uint32_t* fk = (const uint32_t*)a->fold_k;
   const uint32_t* fv = (const uint32_t*)a->fold_v;
   const int dir = direct ? 1 : 0;
-  const int cus = fold_cu_count();
+  const int cus = device_cu_count();
 #define MZ_FOLD(IOV, NR, BB)                                                                            \
   if (a->meta_dtype == MZ_F32)                                                                          \
     hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \

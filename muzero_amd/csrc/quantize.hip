@@ -532,23 +532,13 @@ static inline int launch_status() {
 
 using namespace mz;
 
-static int cu_count() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-  }
-  return cus;
-}
 
 // Persistent grid: enough workgroups to fill the GPU a few times over, each
 // looping over its share of the 64-value groups (table staged once).
 static int quantize_grid(int64_t work_groups) {
   const int64_t per_wg = (int64_t)(QWG / 64) * QGROUPS_PER_WAVE;
   const int64_t need = (work_groups + per_wg - 1) / per_wg;
-  return (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)cu_count() * 8));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)device_cu_count() * 8));
 }
 
 // Alignment the packed rows need: a lane stores its `bits` bytes as one
@@ -615,7 +605,7 @@ extern "C" int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H,
         if (e != hipSuccess) return (int)e;
       }
       const int per_cu = std::max<int>(1, std::min<int>(4, (int)((160 * 1024) / lds)));
-      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ntiles, per_cu * (int64_t)cu_count())));
+      const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ntiles, per_cu * (int64_t)device_cu_count())));
       if (vec) hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, true>), grid, dim3(QWG), lds, s, keys, B, H, T, D,
                                   x_sb, x_sh, x_st, packed, p_sb, p_sh, mn, scale, meta_dtype, m_sb, m_sh, eps, table);
       else hipLaunchKernelGGL((quantize_keys_kernel<D_, B_, false>), grid, dim3(QWG), lds, s, keys, B, H, T, D,

@@ -26,6 +26,7 @@ import torch
 import torch.nn.functional as F
 
 from ._lib import MuZeroHipError
+from .config import BACKENDS
 from .kernels import loader as _k
 
 GROUP = _k.GROUP
@@ -225,11 +226,13 @@ def quantize_rows(
     """Quantise a ``[N, group_size]`` tensor; returns ``(packed_q uint8 [N, qb], mn [N, 1], scale [N, 1])``.
 
     ``backend`` / ``_cuda_ok`` / ``_triton_ok`` are accepted for call
-    compatibility with the reference (``quantizer.py:119-158``); the HIP
-    kernel always runs.
+    compatibility with the reference (``quantizer.py:119-158``).  The reference
+    tries its CUDA extension, then Triton, then torch; all three give these
+    bytes on a device tensor, and here the HIP kernel always runs.  A CPU
+    tensor raises :class:`MuZeroHipError` (there is no CPU path).
     """
-    if backend not in ("auto", "hip", "cuda"):
-        raise MuZeroHipError(f"backend {backend!r} is not provided by this build (HIP kernels only)")
+    if backend not in BACKENDS:
+        raise MuZeroHipError(f"unknown backend {backend!r}; expected one of {BACKENDS}")
     _check_group(flat_grouped.shape[1])
     n = flat_grouped.shape[0]
     q_bytes = (flat_grouped.shape[1] * bits + 7) // 8

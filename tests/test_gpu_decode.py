@@ -11,9 +11,12 @@ values at full precision like the reference's fused CUDA qk/av kernels
 (fp32 codebooks, loader.py:197-263).  The two oracles differ from each other
 by up to ~1.3e-2 at short contexts, so each kernel is held to its own.  Tolerances: 2e-3 max-abs and
 1e-3 mean-abs.  They are checked on the kernel's fp32 output (the kernel's own
-error), and on its bf16 output with half a bf16 ulp of the exact value added
-to the max bound: rounding the exact fp64 answer itself to bf16 already moves
-outputs near 1.0 by up to 3.9e-3, so no bf16 result can meet 2e-3 there.
+error), and on its bf16 output with what rounding the exact answer itself to
+bf16 costs added: half a bf16 ulp of the exact value to the max bound, and
+the mean distance of the exact answer from its bf16 rounding to the mean bound
+(rounding the exact fp64 answer to bf16 already moves outputs near 1.0 by up
+to 3.9e-3, and outputs near 5, where value groups are one-signed, by 7.8e-3 on
+average, so no bf16 result can meet the bare bounds there).
 """
 
 
@@ -34,18 +37,44 @@ def _half_ulp_bf16(x: torch.Tensor) -> torch.Tensor:
     return torch.pow(2.0, e - 8)
 
 
+def _offset_inputs(k, v, q, *, k_offset=0.0, v_offset=0.0, q_scale=1.0, seed=0):
+    """Shift 8 key channels by +k_offset and 8 by -k_offset (their 64-token groups are then
+    one-signed, |min| >> scale, as in low-frequency post-RoPE key channels), every value by
+    +v_offset (one-signed value groups), and scale the query (a peaked softmax)."""
+    dtype = k.dtype
+    if k_offset:
+        g = torch.Generator().manual_seed(1000 + seed)
+        ch = torch.randperm(k.shape[-1], generator=g)[:16]
+        k = k.float()
+        k[..., ch[:8]] += k_offset
+        k[..., ch[8:]] -= k_offset
+    if v_offset:
+        v = v.float() + v_offset
+    if q_scale != 1.0:
+        q = q.float() * q_scale
+    return k.to(dtype), v.to(dtype), q.to(dtype)
+
+
 def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n_split=0,
               dtype=torch.bfloat16, meta=torch.float16, alpha_k=2.0, alpha_v=2.0, outliers=4,
-              kernel_path="auto"):
-    """Returns (fp32-output max err, mean err, io-dtype output, fp64 oracle)."""
+              kernel_path="auto", k_offset=0.0, v_offset=0.0, q_scale=1.0, layer_gap=False):
+    """Returns (fp32-output max err, mean err, io-dtype output, fp64 oracle).
+
+    ``mask``: False, True / "float" (additive, the HF form) or "bool" (keep-mask, converted by
+    the loader).  ``layer_gap``: also return, as a 5th element, the fp32 output's max and
+    mean distance to the layer-dtype dequantize-then-attend oracle and that oracle's own max
+    distance to the fp32-dequant one (the fold kernel's semantics)."""
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=seed, outliers=outliers, dtype=dtype)
-    am = None
+    k, v, q = _offset_inputs(k, v, q, k_offset=k_offset, v_offset=v_offset, q_scale=q_scale, seed=seed)
+    am = am_kernel = None
     if mask:
-        am = torch.zeros(B, 1, 1, length, dtype=dtype)
-        am[0, ..., : length // 3] = torch.finfo(dtype).min
+        keep = torch.ones(B, 1, 1, length, dtype=torch.bool)
+        keep[0, ..., : length // 3] = False
         if B > 1:
-            am[1, ..., 5:9] = torch.finfo(dtype).min
+            keep[1, ..., 5:9] = False
+        am = torch.zeros(B, 1, 1, length, dtype=dtype).masked_fill_(~keep, torch.finfo(dtype).min)
+        am_kernel = keep if mask == "bool" else am
     lq0 = ref.split_prefix(length, residual, 64)
     fold = (kernel_path == "fold" or (kernel_path == "auto" and 1 <= bits <= 4 and d == 128
                                       and n_rep in (1, 2, 4, 8) and lq0 > 0))
@@ -58,7 +87,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
               k_packed=dev(st.get("packed_k")), k_mn=dev(st.get("k_mn")), k_scale=dev(st.get("k_scale")),
               v_packed=dev(st.get("packed_v")), v_mn=dev(st.get("v_mn")), v_scale=dev(st.get("v_scale")),
               k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=alpha_k, alpha_value=alpha_v,
-              scaling=d ** -0.5, attention_mask=dev(am), n_split=n_split, kernel_path=kernel_path)
+              scaling=d ** -0.5, attention_mask=dev(am_kernel), n_split=n_split, kernel_path=kernel_path)
     qd = dev(q)
     out32 = L.DecodePlan(qd, out_dtype=torch.float32, **kw).run()
     out = L.DecodePlan(qd, **kw).run()
@@ -71,7 +100,14 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         err16 = (out.double() - exact).abs()
         bound = MAX_ABS + _half_ulp_bf16(exact)
         assert bool((err16 <= bound).all()), (err16 - bound).max().item()
-        assert err16.mean().item() < MEAN_ABS
+        rounding = (exact.to(torch.bfloat16).double() - exact).abs().mean().item()
+        assert err16.mean().item() < MEAN_ABS + rounding, (err16.mean().item(), rounding)
+    if layer_gap:
+        layer, _ = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
+                                        residual=residual, amax_dtype=meta, attention_mask=am)
+        dl = (out32.double() - layer).abs()
+        gap = (layer - exact).abs().max().item()
+        return err.max().item(), err.mean().item(), out, exact, (dl.max().item(), dl.mean().item(), gap)
     return err.max().item(), err.mean().item(), out, exact
 
 
@@ -99,8 +135,12 @@ def test_decode_matches_oracle(case):
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-def test_decode_with_mask():
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 4, 128, mask=True)
+@pytest.mark.parametrize("mask", ["float", "bool"])
+@pytest.mark.parametrize("bits", [4, 2, 5])
+def test_decode_with_mask(mask, bits):
+    """Additive (HF) and boolean keep-masks (converted by the loader, loader.py's bool handling of
+    attention.py:203-233's mask slices) give the same masked attention as the oracle."""
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, bits, 128, mask=mask)
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
@@ -266,3 +306,98 @@ def test_misaligned_value_prefix(bits, d, length, extra):
     torch.cuda.synchronize()
     err = (out.cpu().double() - exact).abs()
     assert err.max().item() < MAX_ABS and err.mean().item() < MEAN_ABS, (err.max().item(), err.mean().item())
+
+
+# ---------------------------------------------------------------- long contexts (config 3)
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("length", [8192, 16384, 32768])
+def test_long_context_matches_oracle(length, bits):
+    """Config 3's contexts on one (batch, kv-head) pair of rows: the library's split choice and a
+    single split (config 3's B=64 launch: every tile of a row in one workgroup, 128 tiles per
+    wave at 32K) through the online softmax, the accumulators' exponent and the combine."""
+    from muzero_amd.kernels import loader as L
+    B, hkv, n_rep, d, residual = 1, 2, 4, 128, 128
+    k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=length + bits)
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64,
+                                     residual=residual, dequant_dtype=torch.float32)
+    kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5, out_dtype=torch.float32)
+    for n_split in (0, 1):
+        plan = L.DecodePlan(q.to(DEV), n_split=n_split, **kw)
+        assert plan.uses_fold and (n_split == 0 or plan.n_split == 1)
+        out = plan.run()
+        torch.cuda.synchronize()
+        err = (out.cpu().double() - exact).abs()
+        print(f"L={length} bits={bits} n_split={plan.n_split}: max {err.max().item():.2e} "
+              f"mean {err.mean().item():.2e}", flush=True)
+        assert err.max().item() < MAX_ABS and err.mean().item() < MEAN_ABS, (plan.n_split, err.max().item())
+
+
+# ---------------------------------------------------------------- one-signed groups
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8])
+def test_offset_groups(bits):
+    """Key channels offset by +-20 and values offset by +5: groups with |min| >> scale, whose
+    zero-anchored constant term a = mn + s*za is far from zero (the fold kernel carries it at
+    fp32 accuracy: a as an fp16 hi + lo pair against the query, sum_t p_t*a_t in fp32)."""
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 1500, bits, 128, seed=bits, k_offset=20.0, v_offset=5.0)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_offset_groups_split_and_mask(bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, seed=7, k_offset=20.0, v_offset=5.0,
+                               mask="bool", n_split=3)
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+# Peaked rows: the query x4 on top of the offsets and the x10 outlier key channels (logits of
+# std ~8, a few tokens carry each row).  Here the reference's own two semantics part ways: its
+# layer-dtype dequantize-then-attend path (attention.py:179-295) and its fp32-codebook fused
+# kernels (loader.py:197-263) differ by up to 0.09-0.2 max and ~1e-2 mean on these inputs.
+# * The exact kernel rounds each dequantized value to the layer dtype as the former does and
+#   is held to the bare tolerance against it.
+# * The fold kernel follows the latter.  Its one remaining rounding is the (P, N) table entry
+#   in fp16 (B operand): |dx| <= s * 2^-12 per element, s the group's stored range.  On an
+#   outlier key channel (s ~ 50) against a x4 query that moves a logit by up to
+#   ~|q_c| * s * 2^-12 * d^-0.5 per channel, which a peaked row turns into output errors of a
+#   few 1e-3; it is held to 4e-3 max (twice the tolerance) and the bare 1e-3 mean, against
+#   the reference-semantics spread above.
+PEAKED_FOLD_MAX = 4e-3
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8])
+def test_peaked_offset_groups_exact_kernel(bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 1500, bits, 128, seed=bits, k_offset=20.0, v_offset=5.0,
+                               q_scale=4.0, kernel_path="exact")
+    assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+@pytest.mark.parametrize("split_mask", [False, True])
+def test_peaked_offset_groups_fold_kernel(bits, split_mask):
+    kw = dict(mask="bool", n_split=3) if split_mask else {}
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000 if split_mask else 1500, bits, 128,
+                               seed=7 if split_mask else bits, k_offset=20.0, v_offset=5.0, q_scale=4.0,
+                               kernel_path="fold", **kw)
+    print(f"peaked fold bits={bits} split_mask={split_mask}: max {mx:.2e} mean {mean:.2e}", flush=True)
+    assert mx < PEAKED_FOLD_MAX and mean < MEAN_ABS, (mx, mean)
+
+
+# ---------------------------------------------------------------- distance to the layer-dtype path
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_fold_distance_to_layer_dtype_path(bits):
+    """At config 1's row shape (8 kv heads, 4096 tokens) the fold kernel is held to the
+    fp32-dequantized oracle (the reference's fused CUDA semantics).  Its distance to the
+    layer-dtype dequantize-then-attend oracle (attention.py:179-295) is reported; it is bounded
+    by that oracle's own distance from the fp32-dequantized one plus the tolerance, and its mean
+    stays under 1e-3."""
+    mx, mean, _, _, (lmx, lmean, gap) = _run_case(1, 8, 4, 128, 4096, bits, 128, seed=1234, layer_gap=True)
+    print(f"bits={bits}: vs fp32-dequant oracle max {mx:.2e} mean {mean:.2e}; vs layer-dtype oracle "
+          f"max {lmx:.2e} mean {lmean:.2e} (oracle gap {gap:.2e})", flush=True)
+    assert mx < MAX_ABS and mean < MEAN_ABS
+    assert lmx <= gap + MAX_ABS and lmean < MEAN_ABS, (lmx, lmean, gap)

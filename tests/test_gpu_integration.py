@@ -290,3 +290,126 @@ def test_generate_legacy_request_forms_match():
     layer = cache.layers[0]
     assert layer.get_attention_state()["key_prefix_length"] == 128  # 262 - 128 residual -> 2 whole groups
     torch.testing.assert_close(k[:, :, 128:], layer.keys, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("bits", [1, 5])
+def test_decode_stream_with_flushes_matches_oracle(bits):
+    """Config 2's stream on a small batch: a cache layer takes a prefill, then 160 decode tokens
+    one at a time, flushing one group every 64 tokens (decode_flush_by_group=True).  After
+    every 16th token and after every flush the decode hook's output matches the oracle's
+    attention over the same token sequence (the flush policy gives the same prefix length),
+    and at the end the stored bytes equal the oracle's.  1-bit runs the fold kernel, 5-bit the
+    general kernel (5 bits is below the config's validated set, as in the stream benchmark)."""
+    B, hkv, n_rep, d, prefill, steps = 1, 2, 4, 128, 640, 160
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=31 + bits)
+    cfg = mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0)
+    cfg.bits = bits
+    layer = MuZeroCacheLayer(cfg)
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    fold = bits <= 4
+    qd = q.to(DEV)
+    checked = flushes = 0
+    for t in range(prefill, prefill + steps):
+        before = layer._kstore.count
+        layer.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), {"materialize_full_kv": False})
+        flushed = layer._kstore.count != before
+        flushes += flushed
+        if not (flushed or (t + 1 - prefill) % 16 == 0):
+            continue
+        state = layer.get_attention_state()
+        out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), qd, None, d ** -0.5, state)
+        torch.cuda.synchronize()
+        n = t + 1
+        exact, st = ref.reference_decode(q, k[:, :, :n], v[:, :, :n], bits=bits, alpha_k=2.0, alpha_v=2.0,
+                                         group_size=64, residual=128,
+                                         dequant_dtype=torch.float32 if fold else None)
+        assert state["key_prefix_length"] == st["lq"], t
+        err = (out.cpu().double() - exact).abs()
+        half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+        assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (t, err.max().item())
+        checked += 1
+    assert flushes == 2 and checked >= 10
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+
+
+def test_reorder_between_decode_steps_under_inference_mode():
+    """Beam-search reorders between decode steps, under torch.inference_mode (where freed tensor
+    objects are re-used at once): the decode hook's cached launch must never point into
+    replaced storage.  Every step equals a freshly built plan over the layer's current state."""
+    from muzero_amd.kernels import loader as L
+    B, hkv, n_rep, d, prefill, steps = 3, 2, 4, 128, 640, 70
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=41)
+    with torch.inference_mode():
+        layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0))
+        layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+        qd = q.to(DEV)
+        perms = [torch.tensor(p, device=DEV) for p in ([2, 0, 1], [1, 1, 0], [0, 2, 2])]
+        for i, t in enumerate(range(prefill, prefill + steps)):
+            layer.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), {"materialize_full_kv": False})
+            state = layer.get_attention_state()
+            out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), qd, None, d ** -0.5, state)
+            fresh = L.DecodePlan(qd, bits=4, n_groups=state["key_prefix_length"] // 64,
+                                 k_packed=layer._packed_key_q, k_mn=layer._key_mn, k_scale=layer._key_scale,
+                                 v_packed=layer._packed_value_q, v_mn=layer._value_mn,
+                                 v_scale=layer._value_scale, k_res=layer.keys, v_res=layer.values,
+                                 alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5).run()
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), fresh.view(torch.int16)), t
+            if i % 5 == 4:
+                layer.reorder_cache(perms[(i // 5) % 3])
+                assert layer._hip_decode is None
+
+
+@pytest.mark.parametrize("backend", ["triton", "torch"])
+def test_generate_through_muzero_import_name(backend):
+    """``import muzero`` (the reference's package name), patch, and generate with the reference's
+    ``backend`` values: the fused kernel serves every decode step of every layer, counted under
+    the reference's statistics names (bench_throughput.py:341-343 reads them)."""
+    import muzero
+    muzero.patch_transformers()
+    model = _tiny_model("qwen3")
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, 512, (2, 300), generator=g).to(DEV)
+    new_tokens, n_layers = 4, 2
+    muzero.reset_mu_zero_decode_stats()
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=new_tokens, do_sample=False, cache_implementation="mu_zero_4bit",
+                             cache_config={"backend": backend, "residual_length": 128}, pad_token_id=0)
+    stats = muzero.get_mu_zero_decode_stats()
+    steps = new_tokens - 1  # the first token comes from the prefill
+    assert out.shape == (2, 300 + new_tokens)
+    assert stats.get("fused_qk_success", 0) == steps * n_layers, stats
+    assert stats.get("fused_av_success", 0) == steps * n_layers, stats
+    assert stats.get("fused_prefix_decode_success", 0) == steps * n_layers, stats
+    assert not any(k.endswith("_fallback") for k in stats), stats
+
+
+def test_left_padded_generate_matches_dequant_path(monkeypatch):
+    """A left-padded batch (row 1 starts with 40 padding tokens, masked by its attention mask):
+    the decode steps pass the model's mask to the fused kernel, and the scores match the same
+    generate with the prefix dequantised and attended by the model's own attention."""
+    mz.patch_transformers()
+    model = _tiny_model("qwen3")
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(1, 512, (2, 300), generator=g)
+    am = torch.ones(2, 300, dtype=torch.long)
+    ids[1, :40] = 0
+    am[1, :40] = 0
+    ids, am = ids.to(DEV), am.to(DEV)
+    kw = dict(attention_mask=am, max_new_tokens=4, do_sample=False, cache_implementation="mu_zero_4bit",
+              cache_config={"residual_length": 128}, output_scores=True, return_dict_in_generate=True,
+              pad_token_id=0)
+    mz.reset_mu_zero_decode_stats()
+    with torch.no_grad():
+        fused = model.generate(ids, **kw)
+    assert mz.get_mu_zero_decode_stats().get("hip_fused_decode", 0) == 3 * 2
+    monkeypatch.setenv("MUZERO_DISABLE_FUSED_DECODE", "1")
+    with torch.no_grad():
+        dense = model.generate(ids, **kw)
+    for s in (1, 2, 3):
+        a, b = fused.scores[s].float(), dense.scores[s].float()
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
+    assert torch.equal(fused.sequences[:, :301], dense.sequences[:, :301])

@@ -37,12 +37,24 @@ def test_config_defaults_and_validation():
     mz.MuZeroConfig(residual_length=100, decode_flush_by_group=False)
 
 
-def test_config_rejects_non_hip_backends():
-    for b in ("triton", "torch"):
-        with pytest.raises(ValueError, match="HIP"):
-            mz.MuZeroConfig(backend=b)
-    for b in ("auto", "hip", "cuda"):
+def test_config_accepts_reference_backends():
+    """The reference's backend names validate (muzero/config.py:43-44; its own integration test
+    passes backend="torch"); all of them select the HIP kernels here."""
+    for b in ("auto", "cuda", "triton", "torch", "hip"):
         assert mz.MuZeroConfig(backend=b).backend == b
+    with pytest.raises(ValueError, match="backend"):
+        mz.MuZeroConfig(backend="bogus")
+
+
+def test_quantize_rows_backends_reject_cpu_tensors():
+    """Every backend name reaches the HIP kernel; a CPU tensor is an error (no CPU path)."""
+    from muzero_amd._lib import MuZeroHipError
+    x = torch.randn(4, 64)
+    for b in ("auto", "cuda", "triton", "torch", "hip"):
+        with pytest.raises(MuZeroHipError):
+            mz.quantize_rows(x, 4, 2.0, 1e-8, torch.float16, backend=b)
+    with pytest.raises(MuZeroHipError, match="backend"):
+        mz.quantize_rows(x, 4, 2.0, 1e-8, torch.float16, backend="bogus")
 
 
 def test_config_from_dict_ignores_unknown_keys():
@@ -284,3 +296,40 @@ def test_cpu_tensors_are_rejected_by_the_kernels():
     from muzero_amd._lib import MuZeroHipError
     with pytest.raises(MuZeroHipError):
         mz.quantize_rows(torch.randn(4, 64), 4, 2.0, 1e-8, torch.float16)
+
+
+def test_muzero_import_name_is_the_reference_package_surface():
+    """``import muzero`` (the reference's package name, muzero/__init__.py:16-34) exposes the same
+    public names, and its submodules are the very modules muzero_amd uses."""
+    import muzero
+    import muzero_amd
+    assert sorted(muzero.__all__) == sorted(muzero_amd.__all__)
+    for name in muzero.__all__:
+        assert getattr(muzero, name) is getattr(muzero_amd, name), name
+    import muzero.cache.attention
+    import muzero.cache.layer
+    import muzero.config
+    import muzero.kernels.loader
+    import muzero.quantizer
+    assert muzero.cache.attention is muzero_amd.cache.attention
+    assert muzero.cache.layer.MuZeroCacheLayer is muzero_amd.MuZeroCacheLayer
+    assert muzero.kernels.loader.mu_zero_quantize_cuda is muzero_amd.kernels.loader.mu_zero_quantize_cuda
+    assert muzero.config.MuZeroConfig is muzero_amd.MuZeroConfig
+    from muzero.integrations import transformers_patch as tp
+    import muzero_amd.integrations.transformers_patch as tp2
+    assert tp is tp2 and muzero.MuZeroCache is tp2.MuZeroCache
+
+
+def test_decode_stats_counter_names():
+    """The reference's counter names (attention.py:171-177, :209-211, :270-272) for a fused call with
+    a quantized prefix; the fallback names when the launch raises."""
+    from muzero_amd.cache import attention as A
+    A.reset_mu_zero_decode_stats()
+    A._count(128, 128, "success")
+    A._count(0, 0, "success")
+    A._count(64, 64, "fallback")
+    s = A.get_mu_zero_decode_stats()
+    assert s["fused_qk_success"] == s["fused_av_success"] == s["fused_prefix_decode_success"] == 1
+    assert s["fused_prefix_decode_chunked_success"] == 1
+    assert s["fused_qk_fallback"] == s["fused_av_fallback"] == s["fused_prefix_decode_fallback"] == 1
+    A.reset_mu_zero_decode_stats()
