@@ -36,7 +36,8 @@ enum {
   MZ_OK = 0,
   MZ_EINVAL = -1,        /* bad pointer, size, stride or dtype */
   MZ_EUNSUPPORTED = -2,  /* valid for the reference but not built here (e.g. head_dim) */
-  MZ_EWORKSPACE = -3     /* workspace too small */
+  MZ_EWORKSPACE = -3,    /* workspace too small */
+  MZ_ESCRATCH = -4       /* the call needs more than the static decode scratch (muzero_decode_attention_noalloc) */
 };
 
 const char* muzero_version(void);
@@ -187,6 +188,23 @@ int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
  *   residual window and every bit width. */
 int muzero_decode_partials(const mz_decode_args* args, mz_stream_t stream);
 int muzero_decode_combine(const mz_decode_args* args, mz_stream_t stream);
+
+/*
+ * muzero_decode_attention without a caller workspace: a split call keeps its
+ * partial records in a static device array of MZ_DECODE_SCRATCH_BYTES inside
+ * the library (one per device, held until the process ends); args->workspace
+ * and args->workspace_bytes are ignored.  Allocates nothing, so it serves
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation).  Returns MZ_ESCRATCH,
+ * launching nothing, when a split call's muzero_decode_workspace_bytes(args)
+ * exceeds the array (a single-split call uses no workspace).  Every call on a device shares that device's array (the last call's
+ * records stay in it; each call writes every record it reads), so calls that
+ * overlap on one device, on different streams or threads, race.  Same
+ * results as muzero_decode_attention with a workspace, bit for bit.
+ * No counterpart in the reference; it is for callers that cannot allocate.
+ */
+#define MZ_DECODE_SCRATCH_BYTES (8u << 20)
+int muzero_decode_attention_noalloc(const mz_decode_args* args, mz_stream_t stream);
 
 /*
  * Decode-step prologue of one attention layer for a single new token: per

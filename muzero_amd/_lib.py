@@ -72,6 +72,8 @@ class PrologueArgs(ctypes.Structure):
 
 
 MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2
+MZ_ESCRATCH = -4
+MZ_DECODE_SCRATCH_BYTES = 8 << 20  # the static scratch of muzero_decode_attention_noalloc
 
 
 # exported symbol -> (restype, argtypes)
@@ -93,6 +95,7 @@ SIGNATURES = {
     "muzero_decode_uses_fold": (c_int, [ctypes.POINTER(DecodeArgs)]),
     "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_attention_noalloc": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_prologue": (c_int, [ctypes.POINTER(PrologueArgs), c_vp]),
 }
 

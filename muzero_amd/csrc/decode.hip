@@ -788,3 +788,41 @@ extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stre
   if (st != MZ_OK) return st;
   return muzero_decode_combine(a, stream);
 }
+
+// ------------------------------------------------------------ allocation-free entry point
+// muzero_decode_attention_noalloc keeps a split call's partial records in this
+// array instead of a caller workspace: one copy per device, held by each
+// device that runs the library until the process ends.  In host code the
+// name `scratch` is a stand-in, not a device address: the address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static __device__ __align__(256) float scratch[MZ_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+static hipError_t scratch_address(void** out) {
+  static std::atomic<void*> addr[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return hipSuccess;
+}
+
+extern "C" int muzero_decode_attention_noalloc(const mz_decode_args* a, mz_stream_t stream) {
+  if (!a) return MZ_EINVAL;
+  int ns = 0;
+  const int64_t need = muzero_decode_workspace_bytes(a, &ns);
+  if (need < 0) return MZ_EINVAL;
+  // a single split writes the output directly and reads no workspace
+  if (ns > 1 && need > (int64_t)MZ_DECODE_SCRATCH_BYTES) return MZ_ESCRATCH;
+  mz_decode_args b = *a;
+  const hipError_t e = scratch_address(&b.workspace);
+  if (e != hipSuccess) return (int)e;
+  b.workspace_bytes = (int64_t)MZ_DECODE_SCRATCH_BYTES;
+  return muzero_decode_attention(&b, stream);
+}

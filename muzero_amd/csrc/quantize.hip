@@ -676,6 +676,7 @@ extern "C" const char* muzero_strerror(int status) {
     case MZ_EINVAL: return "invalid argument (pointer, size, stride, dtype or bit width)";
     case MZ_EUNSUPPORTED: return "shape not supported by the HIP path";
     case MZ_EWORKSPACE: return "workspace too small";
+    case MZ_ESCRATCH: return "the call needs more than the static decode scratch (MZ_DECODE_SCRATCH_BYTES = 8 MiB)";
     default: return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown error";
   }
 }

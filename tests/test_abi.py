@@ -45,7 +45,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_strerror():
     lib = _lib.load()
     assert lib.muzero_version().decode().startswith("muzero_hip")
-    for code in (0, -1, -2, -3):
+    for code in (0, -1, -2, -3, -4):
         assert lib.muzero_strerror(code)
 
 
@@ -77,3 +77,26 @@ def test_decode_workspace_rejects_bad_args_without_a_device():
     assert lib.muzero_decode_workspace_bytes(ctypes.byref(a), None) == -1
     a.head_dim, a.bits = 128, 9
     assert lib.muzero_decode_workspace_bytes(ctypes.byref(a), None) == -1
+
+
+def test_noalloc_rejects_partials_beyond_the_scratch_without_a_device():
+    """muzero_decode_attention_noalloc checks the split partials' size against its static scratch
+    (MZ_DECODE_SCRATCH_BYTES) on the host and returns MZ_ESCRATCH before any device work: 64 batch
+    rows x 8 kv heads x 4 q heads x 64 forced splits x 130 floats is 17 MB.  The pointers are
+    placeholders: nothing is read."""
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = 64, 8, 4, 128, 4
+    a.n_groups, a.n_residual, a.n_split = 62, 128, 64
+    a.meta_dtype, a.io_dtype, a.out_dtype = _lib.MZ_F16, _lib.MZ_BF16, _lib.MZ_BF16
+    fake = 1 << 20
+    a.query = a.k_packed = a.k_mn = a.k_scale = a.v_packed = a.v_mn = a.v_scale = fake
+    a.k_res = a.v_res = a.e_key = a.e_value = a.out = fake
+    a.q_sb, a.q_sh = 32 * 128, 128
+    a.kr_sb, a.kr_sh, a.kr_st = 8 * 128 * 128, 128 * 128, 128
+    a.vr_sb, a.vr_sh, a.vr_st = a.kr_sb, a.kr_sh, a.kr_st
+    ns = ctypes.c_int(0)
+    need = lib.muzero_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(ns))
+    assert ns.value == 64 and need == 64 * 32 * 64 * 130 * 4 > _lib.MZ_DECODE_SCRATCH_BYTES
+    assert lib.muzero_decode_attention_noalloc(ctypes.byref(a), None) == _lib.MZ_ESCRATCH
+    assert b"scratch" in lib.muzero_strerror(_lib.MZ_ESCRATCH)
