@@ -10,11 +10,20 @@ cache_config={...})`` works unchanged after ``patch_transformers()``:
 * ``patch_transformers()`` (``:207-246``) registers one cache class per width in
   ``CACHE_CLASS_REGISTRY`` (``mu_zero_{1,2,3,4,7,8}bit``), adds those names to the
   generation config's allow-lists, makes ``GenerationMixin`` build a
-  ``MuZeroCache`` with prefill quantisation deferred to the first decode step (also
-  for the legacy ``cache_implementation="quantized"`` with
+  ``MuZeroCache`` (also for the legacy ``cache_implementation="quantized"`` with
   ``backend="logq{b}_zeroanchor_stat_cuda[_opt]"``, ``:289-350``), and sends
   single-token decode of Llama / Qwen3 attention to the fused HIP decode kernel
   (``:402-596``).
+
+Prefill quantisation: the reference defers it for the whole model to the
+first decode step (``:347``, ``:550-555``), so every layer's bf16 prefill K/V
+is held at once.  Here each layer quantises its prefill in its own cache
+update, while its prefill attention still reads the dense tokens (the update
+hands them back), so only one layer's dense K/V is alive at a time.  The
+packed bytes are the same either way: the first flush of every layer is the
+same block.  The reference's whole-model deferral is kept for chunked
+prefill (``generation_config.prefill_chunk_size``: later chunks must attend to
+the earlier chunks' dense tokens) and when ``MUZERO_DEFER_PREFILL_QUANTIZATION=1``.
 
 Differences: the legacy LogQ module aliases (``:249-262``) are not installed (the
 legacy kernels are not part of this build), and the attention hook is written
@@ -279,8 +288,9 @@ def _hook_cache_preparation() -> None:
 
     def wrap(original):
         def _prepare_cache_for_generation(self, generation_config, model_kwargs, *args, **kwargs):
-            """For a mu-Zero request, put a ``MuZeroCache`` (prefill quantisation deferred
-            to the first decode step) in ``model_kwargs["past_key_values"]``."""
+            """For a mu-Zero request, put a ``MuZeroCache`` in ``model_kwargs["past_key_values"]``
+            (each layer quantises its prefill in its own update; the whole-model deferral
+            to the first decode step only for chunked prefill or on request)."""
             options = dict(getattr(generation_config, "cache_config", None) or {})
             bits, legacy = _requested_bits(getattr(generation_config, "cache_implementation", None), options)
             if bits is None:
@@ -288,7 +298,8 @@ def _hook_cache_preparation() -> None:
             if getattr(self.config, "is_encoder_decoder", False):
                 raise ValueError("mu_zero cache currently supports decoder-only models")
             cache = MuZeroCache(_config_for(bits, options, drop=("config", "backend") if legacy else ("config",)))
-            cache.defer_prefill_quantization = True
+            cache.defer_prefill_quantization = (bool(getattr(generation_config, "prefill_chunk_size", None))
+                                                or _env_off("MUZERO_DEFER_PREFILL_QUANTIZATION"))
             model_kwargs["past_key_values"] = cache
             return None
 

@@ -413,3 +413,36 @@ def test_left_padded_generate_matches_dequant_path(monkeypatch):
         scale = b.abs().max().item()
         assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
     assert torch.equal(fused.sequences[:, :301], dense.sequences[:, :301])
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_per_layer_prefill_quantization_matches_whole_model_deferral(bits, monkeypatch):
+    """generate() quantises each layer's prefill in that layer's own cache update (only one
+    layer's dense prefill K/V alive at a time); the reference defers every layer to the first
+    decode step (transformers_patch.py:347, :550-555).  Both give the same tokens and scores
+    and, after generate, byte-identical caches (packed codes, metadata, residual windows,
+    alphas); 3-bit also chooses its alphas from the first flushed block on both paths."""
+    mz.patch_transformers()
+    model = _tiny_model("qwen3")
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 512, (2, 330), generator=g).to(DEV)
+    kw = dict(max_new_tokens=4, do_sample=False, cache_implementation=f"mu_zero_{bits}bit",
+              cache_config={"residual_length": 128}, output_scores=True, return_dict_in_generate=True,
+              pad_token_id=0)
+    runs = {}
+    for mode in ("per_layer", "deferred"):
+        if mode == "deferred":
+            monkeypatch.setenv("MUZERO_DEFER_PREFILL_QUANTIZATION", "1")
+        with torch.no_grad():
+            runs[mode] = model.generate(ids, **kw)
+    a, b = runs["per_layer"], runs["deferred"]
+    assert torch.equal(a.sequences, b.sequences)
+    for s in range(4):
+        assert torch.equal(a.scores[s], b.scores[s]), s
+    for la, lb in zip(a.past_key_values.layers, b.past_key_values.layers):
+        assert la._kstore.count == lb._kstore.count > 0 and la._vstore.count == lb._vstore.count
+        for x, y in ((la._packed_key_q, lb._packed_key_q), (la._packed_value_q, lb._packed_value_q),
+                     (la._key_mn, lb._key_mn), (la._key_scale, lb._key_scale), (la._value_mn, lb._value_mn),
+                     (la._value_scale, lb._value_scale), (la.keys, lb.keys), (la.values, lb.values)):
+            assert torch.equal(x.contiguous().view(torch.uint8), y.contiguous().view(torch.uint8))
+        assert la._alphas == lb._alphas
