@@ -91,8 +91,34 @@ def time_region(fn, steps, stream):
     return start.elapsed_time(end) / steps
 
 
+def host_cpu():
+    """(threads, host_cores, model): the CPU baseline runs on every core this process may use
+    (its affinity mask, capped by a cgroup CPU quota when one is set), out of the host's
+    `host_cores`; `model` is /proc/cpuinfo's model name."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            avail = min(avail, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    model = platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return avail, os.cpu_count() or avail, model
+
+
 def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alpha_v=2.0):
-    """The reference's CPU decode path (oracle restatement) on `sample_batch` batch rows."""
+    """The reference's CPU decode path (oracle restatement) on `sample_batch` batch rows:
+    (seconds per call, its output for those rows)."""
     from oracle import reference_torch as ref
     torch.set_num_threads(threads)
     sl = slice(0, sample_batch)
@@ -109,7 +135,7 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alph
             vq = c["v_res"][:, :, :0]
         return ref.decode_attention_literal(qc, kq, vq, c["k_res"], c["v_res"], None, d ** -0.5)
 
-    run()  # warm
+    out = run()  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
         run()
@@ -117,7 +143,7 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alph
         el = time.perf_counter() - t0
         if el > 8.0 or reps >= 3:
             break
-    return el / reps
+    return el / reps, out
 
 
 def quantize_bytes(B, hkv, d, tokens, bits, in_bytes=2):
@@ -204,17 +230,17 @@ def run_stream(args):
 
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
+        threads, host_cores, cpu_model = host_cpu()
         lq_last, r_last, _ = shapes[-1]
         c = dict(k_packed=layer._packed_key_q, k_mn=layer._key_mn, k_scale=layer._key_scale,
                  v_packed=layer._packed_value_q, v_mn=layer._value_mn, v_scale=layer._value_scale,
                  k_res=layer.keys, v_res=layer.values)
-        sec = cpu_baseline(c, qs[0], bits, lq_last, d, args.cpu_sample_batch, threads,
-                           alpha_k=layer._selected_alpha_key, alpha_v=layer._selected_alpha_value)
+        sec, _ = cpu_baseline(c, qs[0], bits, lq_last, d, args.cpu_sample_batch, threads,
+                              alpha_k=layer._selected_alpha_key, alpha_v=layer._selected_alpha_value)
         sec_stream = sec * B / args.cpu_sample_batch * steps
-        cpu = {"value": round(decode_bytes / sec_stream / 1e9, 3), "unit": "GB/s", "cores": threads,
+        cpu = {"value": round(decode_bytes / sec_stream / 1e9, 3), "unit": "GB/s", "cores": threads, "host_cores": host_cores,
                "kind": "port", "seconds_per_stream_full_batch": round(sec_stream, 1),
-               "cpu": platform.processor() or platform.machine(),
+               "cpu": cpu_model,
                "sample": f"the last step's decode (Lq={lq_last}, R={r_last}) on batch rows "
                          f"0..{args.cpu_sample_batch - 1} of {B} (dequantize prefix + attend, oracle restatement "
                          f"of attention.py:179-295), time x {B // args.cpu_sample_batch} x {steps} steps "
@@ -309,7 +335,7 @@ def run_codec(args):
     cpu = None
     if not args.no_cpu:
         from oracle import reference_torch as ref
-        threads = min(os.cpu_count() or 1, 16)
+        threads, host_cores, cpu_model = host_cpu()
         torch.set_num_threads(threads)
         kc, vc = k[:, :, :T], v[:, :, :T]
 
@@ -328,9 +354,9 @@ def run_codec(args):
             if el > 10.0 or reps >= 20:
                 break
         sec = el / reps
-        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        cpu = {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "host_cores": host_cores, "kind": "port",
                "seconds_per_round_trip": round(sec, 5), "speedup_gpu_over_cpu": round(sec / (ms * 1e-3), 1),
-               "cpu": platform.processor() or platform.machine(),
+               "cpu": cpu_model,
                "sample": f"the whole config-0 round trip ({reps} repetitions), oracle restatement of "
                          "quantizer.py:161-255 and layer.py:271-345"}
 
@@ -454,15 +480,24 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        threads = min(os.cpu_count() or 1, 16)
-        sec = cpu_baseline(caches[0], q, bits, lq, d, args.cpu_sample_batch, threads)
+        threads, host_cores, cpu_model = host_cpu()
+        sec, cpu_out = cpu_baseline(caches[0], q, bits, lq, d, args.cpu_sample_batch, threads)
         sec_full = sec * B / args.cpu_sample_batch
-        cpu = {"value": round(nbytes / sec_full / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        # the timed calls' output against the reference CPU path's on the sampled rows
+        plans[0].run()
+        torch.cuda.synchronize()
+        diff = (plans[0].out[:args.cpu_sample_batch].cpu().double() - cpu_out.double()).abs()
+        cpu = {"value": round(nbytes / sec_full / 1e9, 3), "unit": "GB/s", "cores": threads, "host_cores": host_cores, "kind": "port",
                "seconds_per_call_full_batch": round(sec_full, 3),
                "speedup_gpu_over_cpu": round(sec_full / (ms_step * 1e-3), 1),
-               "cpu": platform.processor() or platform.machine(),
+               "cpu": cpu_model,
                "sample": f"batch rows 0..{args.cpu_sample_batch - 1} of {B} (dequantize prefix + "
-                         f"attend, oracle restatement of attention.py:179-295), time x {B // args.cpu_sample_batch}"}
+                         f"attend, oracle restatement of attention.py:179-295), time x {B // args.cpu_sample_batch}",
+               "gpu_vs_cpu_path": {"max_abs": round(diff.max().item(), 6), "mean_abs": round(diff.mean().item(), 7),
+                                   "note": "bf16 outputs of the sampled rows; the CPU path rounds dequantized "
+                                           "values, logits and weights to bf16 (the reference's dequantize-then-"
+                                           "attend), the fold kernel keeps fp32 codebook values (its fused "
+                                           "kernels' semantics)"}}
 
     line = {
         "metric": "packed-KV decode attn HBM GB/s (% of peak); decode tokens/sec at B=64 ctx 4096",
