@@ -167,7 +167,10 @@ def test_patch_transformers_registers_cache_classes():
     transformers.GenerationConfig(cache_implementation="mu_zero_2bit").validate()
 
 
-def test_prepare_cache_builds_mu_zero_cache():
+def test_prepare_cache_builds_mu_zero_cache(monkeypatch):
+    """generate()'s cache preparation builds a MuZeroCache whose layers quantize their prefill in
+    their own update (not deferred); the reference's whole-model deferral comes back for chunked
+    prefill and under MUZERO_DEFER_PREFILL_QUANTIZATION=1."""
     transformers = pytest.importorskip("transformers")
     mz.patch_transformers()
     from transformers.generation.utils import GenerationMixin
@@ -184,9 +187,19 @@ def test_prepare_cache_builds_mu_zero_cache():
         kw = {}
         GenerationMixin._prepare_cache_for_generation(_Model(), gc, kw, None, 1, 4096)
         cache = kw["past_key_values"]
-        assert isinstance(cache, mz.MuZeroCache) and cache.defer_prefill_quantization
+        assert isinstance(cache, mz.MuZeroCache) and not cache.defer_prefill_quantization
         assert cache.cfg.bits == (2 if impl == "mu_zero_2bit" else 4)
         assert cache.cfg.residual_length == cfg["residual_length"]
+    gc = transformers.GenerationConfig(cache_implementation="mu_zero_4bit")
+    gc.prefill_chunk_size = 512
+    kw = {}
+    GenerationMixin._prepare_cache_for_generation(_Model(), gc, kw, None, 1, 4096)
+    assert kw["past_key_values"].defer_prefill_quantization
+    monkeypatch.setenv("MUZERO_DEFER_PREFILL_QUANTIZATION", "1")
+    kw = {}
+    GenerationMixin._prepare_cache_for_generation(_Model(), transformers.GenerationConfig(
+        cache_implementation="mu_zero_4bit"), kw, None, 1, 4096)
+    assert kw["past_key_values"].defer_prefill_quantization
 
 
 # --------------------------------------------------------------------------- flush bookkeeping
