@@ -11,12 +11,11 @@
 // is an MFMA whose A operand carries the group scalars times the query (for
 // P.V: the softmax weight times the token's scalars) and whose B operand is
 // a table lookup (an fp16 pair) per code, contracting over (channel, side)
-// pairs.  The constant part sum_c Q_c*a_c is one more MFMA per 16 channels,
-// contracting over (channel, part): A = the fp16 query (exact) twice, B = a
-// as an fp16 hi + lo pair (a is the group's value nearest zero, large for
-// one-signed groups, so one fp16 rounding of it would not do); the values'
-// constant part sum_t p_t*a_t is an fp32 row reduction.  No element is ever
-// dequantized to memory.  The dequantized
+// pairs.  The constant part sum_c Q_c*a_c is two more MFMAs per 32 channels:
+// A = the fp16 query (exact), B = a's high fp16 part, then its low part (a
+// is the group's value nearest zero, large for one-signed groups, so one fp16
+// rounding of it would not do); the values' constant part sum_t p_t*a_t is
+// an fp32 row reduction.  No element is ever dequantized to memory.  The dequantized
 // values are those of the reference's fused CUDA kernels: full precision
 // (their fp32 codebooks, loader.py:197-263), not rounded to the layer dtype.
 //
@@ -48,6 +47,8 @@
 // (m, l, acc) goes to the workspace and the shared combine kernel merges
 // splits.  With a single split (the grid already fills the GPU) the kernel
 // writes the output itself.
+#include <type_traits>
+
 #include "decode_common.hpp"
 
 namespace mz {
@@ -56,10 +57,17 @@ namespace fold {
 
 constexpr int D = 128;
 constexpr int NG = 2;     // value groups per token
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kLn2 = 0.693147180559945309f;
 constexpr int TILE = 64;  // tokens per tile
-// Waves per workgroup (one per SIMD; two workgroups share a CU).
+// Waves per workgroup (one per SIMD; two workgroups share a CU).  Six-wave
+// workgroups (three waves per SIMD; they fit the registers and LDS for up to
+// 4 query heads) measured 13 % slower at config 1: more waves per CU contend
+// for its LDS rather than hide more latency.
 template <int NREP>
 constexpr int waves_for() { return 4; }
+template <int NREP>
+constexpr int waves_per_simd() { return 2; }
 // (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
 // zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
 // level (one channel / one token-group), and each group owns a disjoint bank
@@ -101,17 +109,17 @@ struct Smem {
   static constexpr int TBL_V = TBL;
   static constexpr int Q16 = 2 * TBL;                 // fp16 [NREP][HROW*2]
   static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
-  static constexpr int QD = Q_IO + NREP * HROW * 4;   // uint32 [NREP][AROW]   (q, q) fp16 per channel
-  static constexpr int ZERO = QD + NREP * AROW * 4;   // AROW zero words: A rows that must be 0
+  static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
   static constexpr int WAVE0 = ZERO + AROW * 4;
   // per-wave region
   static constexpr int KZP = 0;                      // uint32 [4 g][8 kt]    zl of channels 16kt+4g+{0..3}
   static constexpr int AHI = KZP + 4 * 8 * 4;        // uint32 [NREP][AROW]   (q*bp, q*bn) fp16, high part
   static constexpr int ALO = AHI + NREP * AROW * 4;  // uint32 [NREP][AROW]   low part
-  static constexpr int KA = ALO + NREP * AROW * 4;   // uint32 [D]            (a hi, a lo) fp16 per channel
-  static constexpr int VZP = KA + D * 4;             // uint32 [NG][4 g][4 kt] zl of tokens 16kt+4g+{0..3}
-  static constexpr int VBP = VZP + NG * 4 * 4 * 4;   // float2 [NG][TILE]     (bp, bn)
-  static constexpr int VA = VBP + NG * TILE * 8;     // fp32 [NG][TILE]       a
+  static constexpr int KA = ALO + NREP * AROW * 4;   // fp16 [2][D]           a per channel: high part, low part
+  static constexpr int VZP = KA + 2 * D * 2;         // uint32 [NG][4 g][4 kt] zl of tokens 16kt+4g+{0..3}
+  static constexpr int VBP = VZP + NG * 4 * 4 * 4;   // fp32 [NG][TILE]       bp
+  static constexpr int VBN = VBP + NG * TILE * 4;    // fp32 [NG][TILE]       bn
+  static constexpr int VA = VBN + NG * TILE * 4;     // fp32 [NG][TILE]       a
   static constexpr int PA = VA + NG * TILE * 4;      // uint32 [NG][NREP][LROW]   (p*bp, p*bn) fp16, high part
   static constexpr int PALO = PA + NG * NREP * LROW * 4;  // uint32 [NG][NREP][LROW]   low part
   static constexpr int PER_WAVE = (PALO + NG * NREP * LROW * 4 + 15) / 16 * 16;
@@ -139,11 +147,12 @@ __device__ __forceinline__ uint2 split_product(_Float16 q, float b0, float b1) {
   return uint2{__builtin_bit_cast(uint32_t, h2{h0, h1}), __builtin_bit_cast(uint32_t, h2{l0, l1})};
 }
 
-// x as an fp16 pair (hi, lo) with hi + lo = x to about 2^-22 relative.
-__device__ __forceinline__ uint32_t split_value(float x) {
-  const _Float16 h = (_Float16)x;
-  const _Float16 l = (_Float16)(x - (float)h);
-  return __builtin_bit_cast(uint32_t, h2{h, l});
+// x0, x1 as fp16 pairs hi = (hi0, hi1), lo = (lo0, lo1) with hi + lo = x to
+// about 2^-22 relative.
+__device__ __forceinline__ uint2 split_values(float x0, float x1) {
+  const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+  const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+  return uint2{__builtin_bit_cast(uint32_t, h2{h0, h1}), __builtin_bit_cast(uint32_t, h2{l0, l1})};
 }
 
 // Exponent k with |v| * 2^k < 2^15 (fp16 operands and products stay finite).
@@ -161,20 +170,24 @@ struct GroupScalars {
 
 // (a, bp, bn, zl) of one stored group (mn, s); the scale is guarded like the
 // reference CUDA extension (loader.py:201), so an all-zero group gives x = mn.
+// The clamps are single max / med3 ops: for any finite metadata they are
+// torch's clamp / clamp_min; a NaN in the metadata cannot carry the zero level
+// outside 0..QMAX (med3 returns one of its bounds), so the table reads stay in
+// range.
 template <int QMAX>
 __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   constexpr float qmax = (float)QMAX;
   const float eps = 1e-8f;
-  if (!(s >= eps)) s = eps;
-  const float za = clamp01((0.f - mn) / s);  // IEEE division: zl must match the reference
+  s = fmaxf(s, eps);
+  const float za = __builtin_amdgcn_fmed3f((0.f - mn) / s, 0.f, 1.f);  // IEEE division: zl must match the reference
   const float zl = rintf(za * qmax);
-  const float pe = clamp_min(1.f - za, eps);
-  const float ne = clamp_min(za, eps);
+  const float pe = fmaxf(1.f - za, eps);
+  const float ne = fmaxf(za, eps);
   GroupScalars r;
   r.a = mn + s * za;
   r.bp = s * pe;
   r.bn = -(s * ne);
-  r.zl = (uint32_t)(zl == zl ? (int)zl : 0);
+  r.zl = (uint32_t)zl;
   return r;
 }
 
@@ -194,7 +207,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_
 
 // Global data of one quantized tile.  Code words: lanes 2m and 2m+1 of a
 // lane group read the same 2*LB bytes of two rows of a pair (key: channels,
-// value: tokens); lookup_ktile() later swaps halves between them so each lane
+// value: tokens); addr_ktile() later swaps halves between them so each lane
 // ends with the bytes of both rows that hold ITS codes.
 //   4-bit: kw[kt*2+p] = 32 bits of row 16kt+4g+2p+(n&1)
 //   2-bit: kw[kt*2+h] = 16 bits of row 16kt+4g+2h+(n&1)
@@ -222,11 +235,14 @@ __device__ __forceinline__ void load_meta(uint32_t (&w)[MW], const __amdgpu_buff
   if constexpr (MW == 2) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4, soff, 0);
 }
 
+// `imm` (a compile-time offset within the tile) rides in the scalar offset
+// with the tile's own; the tile index is always a quantized tile, so the
+// address stays inside the buffer whatever the range check counts.
 template <int BITS>
 __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int imm) {
-  if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff + imm, soff, 0);
-  else if constexpr (BITS == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff + imm, soff, 0);
-  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff + imm, soff, 0);
+  if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff + imm, 0);
+  else if constexpr (BITS == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff + imm, 0);
+  else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff + imm, 0);
 }
 
 // All metadata of a tile (loaded one tile ahead of its use).
@@ -277,16 +293,16 @@ __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_XOR1, 0xF, 0xF, true);
 }
 
-// The B operands of one k-tile (4 rows ii of this lane's k-slice x its 4
-// codes, jt = code index) from the two raw words w0, w1 of the k-tile.  The
-// codes are spread to bytes as table offsets 4*q + 64*group (two ops per 4
-// codes); one v_perm per code then joins the offset (low byte) with row ii's
-// zero level (byte ii of zp, as the high byte: the table row zl*256) and one
-// ds_read_b32 fetches the (P, N) pair straight into the operand register.
-// `odd` = lane n is odd.
-template <int BITS, int TBASE>
-__device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, uint32_t w1, uint32_t zp,
-                                             uint32_t grep, bool odd, uint32_t sh, u32x4 B[4]) {
+// The table addresses of one k-tile's B operands (4 rows ii of this lane's
+// k-slice x its 4 codes, jt = code index) from the two raw words w0, w1 of
+// the k-tile.  The codes are spread to bytes as table offsets 4*q + 64*group
+// (two ops per 4 codes); one v_perm per code then joins the offset (low byte)
+// with row ii's zero level (byte ii of zp, as the high byte: the table row
+// zl*256).  read_ktile() then fetches each (P, N) pair with one ds_read_b32
+// straight into the operand register.  `odd` = lane n is odd.
+template <int BITS>
+__device__ __forceinline__ void addr_ktile(uint32_t w0, uint32_t w1, uint32_t zp, uint32_t grep, bool odd,
+                                           uint32_t sh, uint32_t (&ad)[4][4]) {
   if constexpr (BITS == 3) {
     // w0 / w1: the pair's dword of rows (0 | 1) / (2 | 3); after the swap the
     // lane holds all four rows and takes its 12 bits (4 codes) from each at
@@ -304,8 +320,7 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
       const uint32_t e = (u << 2) | grep;
 #pragma unroll
       for (int jt = 0; jt < 4; ++jt)
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
-                                       __builtin_amdgcn_perm(zp, e, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | jt));
+        ad[jt][ii] = __builtin_amdgcn_perm(zp, e, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | jt);
     }
   } else if constexpr (BITS == 1) {
     // w0 / w1: byte m of rows (0 | 1) / (2 | 3) (even / odd lane); gather the
@@ -319,8 +334,7 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
       const uint32_t ej = ((w4 >> jt) & 0x04040404u) | grep;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
-                                       __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii));
+        ad[jt][ii] = __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii);
     }
   } else if constexpr (BITS == 4) {
     // w0 / w1: rows (0,1) / (2,3) of the pair, 32 bits = codes of lanes 2m, 2m+1;
@@ -337,7 +351,7 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
       for (int jt = 0; jt < 4; ++jt) {
         const uint32_t e = (jt & 1) ? od[ii >> 1] : ev[ii >> 1];
         const uint32_t s = 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | (uint32_t)((ii & 1) * 2 + (jt >> 1));
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE + __builtin_amdgcn_perm(zp, e, s));
+        ad[jt][ii] = __builtin_amdgcn_perm(zp, e, s);
       }
   } else {
     // w0 / w1: 16 bits of rows (0 | 1) / (2 | 3) (even / odd lane), one byte per
@@ -351,14 +365,22 @@ __device__ __forceinline__ void lookup_ktile(const uint8_t* smem, uint32_t w0, u
       const uint32_t ej = e | grep;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
-        B[jt][ii] = *(const uint32_t*)(smem + TBASE +
-                                       __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii));
+        ad[jt][ii] = __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii);
     }
   }
 }
 
+template <int TBASE>
+__device__ __forceinline__ void read_ktile(const uint8_t* smem, const uint32_t (&ad)[4][4], u32x4 B[4]) {
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) B[jt][ii] = *(const uint32_t*)(smem + TBASE + ad[jt][ii]);
+}
+
 template <int IO, int NREP, int BITS, int MW>
-__global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves_per_eu(2, 2))) void fold_kernel(
+__global__ __launch_bounds__(64 * waves_for<NREP>())
+__attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>()))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
     const uint32_t* __restrict__ ftab_v, int direct, int cus) {
   constexpr int WAVES = waves_for<NREP>();
@@ -418,13 +440,13 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
 
   // ---------------- workgroup setup: tables and query in LDS.  Their loads
   // are issued before the first tile's, so the setup waits for them only.
-  constexpr int TW = TBL / 4 / NT;                // table words per thread (each table)
+  constexpr int TW = (TBL / 4 + NT - 1) / NT;     // table words per thread (each table)
   constexpr int QW = (NREP * D + NT - 1) / NT;    // query elements per thread
   uint32_t tk[TW], tv[TW];
   uint16_t qraw[QW];
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
-    const int i = threadIdx.x + j * NT, zl = i >> 6, q = i & 15;
+    const int i = min(threadIdx.x + j * NT, TBL / 4 - 1), zl = i >> 6, q = i & 15;
     tk[j] = ftab_k[zl * 16 + q];
     tv[j] = ftab_v[zl * 16 + q];
   }
@@ -439,8 +461,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   load_kw<BITS>(KW, bf, min(tile_of(v0), q_last), lane);
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
-    ((uint32_t*)(smem + S::TBL_K))[threadIdx.x + j * NT] = tk[j];
-    ((uint32_t*)(smem + S::TBL_V))[threadIdx.x + j * NT] = tv[j];
+    if (threadIdx.x + j * NT < TBL / 4) {
+      ((uint32_t*)(smem + S::TBL_K))[threadIdx.x + j * NT] = tk[j];
+      ((uint32_t*)(smem + S::TBL_V))[threadIdx.x + j * NT] = tv[j];
+    }
   }
   for (int i = threadIdx.x; i < AROW; i += NT) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
   float qabs = 0.f;
@@ -450,10 +474,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     if (i >= NREP * D) break;
     const uint16_t raw = qraw[j];
     const float qf = M::load(raw);
-    const uint32_t qh = f2h(qf);
-    ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = (uint16_t)qh;
+    ((uint16_t*)(smem + S::Q16))[h * HROW * 2 + c] = f2h(qf);
     ((uint16_t*)(smem + S::Q_IO))[h * HROW * 2 + c] = raw;
-    ((uint32_t*)(smem + S::QD))[h * AROW + c] = qh | (qh << 16);
     qabs = fmaxf(qabs, fabsf(qf));
   }
   qabs = wave_max_fast(qabs);
@@ -469,6 +491,12 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   __syncthreads();
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
+  // fp16 query of channels 2*lane, 2*lane+1 per head (the key-side products'
+  // left factor), kept in registers: an LDS read in the scalar chunks would
+  // make their wait take the table reads in flight with it
+  uint32_t q16_pair[NREP];
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) q16_pair[h] = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
   uint32_t* pa = (uint32_t*)(W + S::PA);
   uint32_t* pa_lo = (uint32_t*)(W + S::PALO);
 
@@ -476,14 +504,14 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   // QK, row 0 of a head's rows carries the high fp16 part of the key-side
   // products (q*bp, q*bn against the codes) and row 1 their low part (summed
   // per logit), the head's remaining rows are zero; the constant part uses
-  // row 0 only (the query, twice, against a's hi + lo pairs).  For PV row 0
+  // row 0 only (the query against a's high, then low parts).  For PV row 0
   // carries the high fp16 part of p*bp, p*bn and row 1 the low part (summed
   // at the end); the other rows repeat row 1 and are not read.
   const int hA = n / RS;
   const int rA = n % RS;
   const uint8_t* a_hi_row = rA == 0 ? W + S::AHI + hA * AROW * 4
                                     : (rA == 1 ? W + S::ALO + hA * AROW * 4 : smem + S::ZERO);
-  const uint8_t* qd_row = rA == 0 ? smem + S::QD + hA * AROW * 4 : smem + S::ZERO;
+  const uint8_t* q16_row = rA == 0 ? smem + S::Q16 + hA * HROW * 4 : smem + S::ZERO;
   const uint32_t* pv_row = (rA == 0 ? pa : pa_lo) + hA * LROW;  // PV A operand: this row's head
   const uint8_t* qio_row = rA == 0 ? smem + S::Q_IO + hA * HROW * 4 : smem + S::ZERO;
   const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
@@ -518,7 +546,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     GroupScalars k0, k1, v0, v1;
     float kmx, vmx;
   } sc;
-  float unscale_n = a.scaling;  // next tile's logit factor: scaling * 2^-kexp
+  // logits are kept in base-2 units (times log2(e)): the softmax exponentials
+  // are then single v_exp_f32 ops
+  const float scaling2 = a.scaling * kLog2e;
+  float unscale_n = scaling2;  // next tile's logit factor: scaling * log2(e) * 2^-kexp
   int kvexp_n = 0;              // next tile's value exponent
   auto scal_chunk = [&](const MetaWords<MW>& Mw, const int chunk) __attribute__((always_inline)) {
     constexpr int HPC = (NREP + 3) / 4;  // heads per chunk 4..7
@@ -547,17 +578,21 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       // power-of-two scales keeping the fp16 operands in range (one reduction for both)
       wave_max2_bound(sc.kmx, sc.vmx);
       const int kexp = min(range_exp(sc.kmx * fmaxf(qabs, 1.f)), range_exp(sc.kmx));
-      unscale_n = ldexpf(a.scaling, -kexp);
+      unscale_n = ldexpf(scaling2, -kexp);
       sc.k0.bp = ldexpf(sc.k0.bp, kexp), sc.k0.bn = ldexpf(sc.k0.bn, kexp);
       sc.k1.bp = ldexpf(sc.k1.bp, kexp), sc.k1.bn = ldexpf(sc.k1.bn, kexp);
-      // a of channels 2*lane, 2*lane+1 as (hi, lo) pairs: the constant part's B operand
-      *(uint2*)(W + S::KA + 8 * lane) = uint2{split_value(ldexpf(sc.k0.a, kexp)), split_value(ldexpf(sc.k1.a, kexp))};
+      // a of channels 2*lane, 2*lane+1 in high and low parts: the constant part's B operands
+      const uint2 ka = split_values(ldexpf(sc.k0.a, kexp), ldexpf(sc.k1.a, kexp));
+      ((uint32_t*)(W + S::KA))[lane] = ka.x;
+      ((uint32_t*)(W + S::KA))[D / 2 + lane] = ka.y;
       kvexp_n = range_exp(sc.vmx);
     } else if (chunk == 3) {
       // keep the accumulators' exponent unless the tile needs a smaller one
       kvexp_n = min(kacc_init ? kacc : 60, kvexp_n);
-      ((float2*)(W + S::VBP))[lane] = float2{ldexpf(sc.v0.bp, kvexp_n), ldexpf(sc.v0.bn, kvexp_n)};
-      ((float2*)(W + S::VBP))[TILE + lane] = float2{ldexpf(sc.v1.bp, kvexp_n), ldexpf(sc.v1.bn, kvexp_n)};
+      ((float*)(W + S::VBP))[lane] = ldexpf(sc.v0.bp, kvexp_n);
+      ((float*)(W + S::VBN))[lane] = ldexpf(sc.v0.bn, kvexp_n);
+      ((float*)(W + S::VBP))[TILE + lane] = ldexpf(sc.v1.bp, kvexp_n);
+      ((float*)(W + S::VBN))[TILE + lane] = ldexpf(sc.v1.bn, kvexp_n);
       ((float*)(W + S::VA))[lane] = ldexpf(sc.v0.a, kvexp_n);
       ((float*)(W + S::VA))[TILE + lane] = ldexpf(sc.v1.a, kvexp_n);
     } else {
@@ -566,8 +601,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       for (int hh = 0; hh < HPC; ++hh) {
         const int h = HPC * (chunk - 4) + hh;
         if (h < NREP) {
-          const uint32_t q01 = *(const uint32_t*)(smem + S::Q16 + (h * HROW + lane) * 4);
-          const h2 qh = __builtin_bit_cast(h2, q01);
+          const h2 qh = __builtin_bit_cast(h2, q16_pair[h]);
           const uint2 p0 = split_product(qh.x, sc.k0.bp, sc.k0.bn);
           const uint2 p1_ = split_product(qh.y, sc.k1.bp, sc.k1.bn);
           *(uint2*)(W + S::AHI + (h * AROW + 2 * lane) * 4) = uint2{p0.x, p1_.x};
@@ -581,14 +615,16 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   // its P.V), the next tile tn's metadata (issued here, used by the scalars
   // computed during this tile's P.V) and the next tile's key words (issued
   // after this tile's Q.K).
-  auto process = [&](const int tile, const int tn) {
+  // `quant` (a compile-time tag): a quantized tile, or a residual tile; the two
+  // kinds run in separate loops, so neither carries the other's branches
+  auto process = [&](auto quant_tag, const int tile, const int tn) {
+    constexpr bool quant = decltype(quant_tag)::value;
     const int tl = min(tn, q_last);
     load_vw<BITS>(VW, bf, min(tile, q_last), lane);
     MetaWords<MW> MN;
     load_meta_tile<MW>(MN, bf, tl, lane);
-    const bool quant = tile < a.n_groups;
     int n_valid, pos0, r0 = 0;
-    if (quant) {
+    if constexpr (quant) {
       n_valid = TILE;
       pos0 = TILE * tile;
     } else {
@@ -598,36 +634,62 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     }
 
     f32x4 s[4];
+    // this lane's value scalars (a, bp, bn of tokens 4n..4n+3, per value
+    // group), read once the tile's scalars are in LDS: at the start of a
+    // quantized tile, so the reads complete behind its Q.K
+    f32x4 va_r[NG], vbp_r[NG], vbn_r[NG];
+    auto read_value_scalars = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg) {
+        va_r[vg] = *(const f32x4*)(W + S::VA + (vg * TILE + 4 * n) * 4);
+        vbp_r[vg] = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 4);
+        vbn_r[vg] = *(const f32x4*)(W + S::VBN + (vg * TILE + 4 * n) * 4);
+      }
+    };
     int kv_exp = kvexp_n;
     float unscale = unscale_n;
-    if (quant) {
+    if constexpr (quant) {
       wave_lds_sync();  // this tile's scalars were written by other lanes
+      read_value_scalars();
       // ---------- S = Q K^T: constant part (the same for every token: the
-      // query against a's (hi, lo) pairs), then the folded codes
+      // query against a's high part, then its low part), then the folded codes
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kq = 0; kq < 8; ++kq) {
-        const u32x4 A = *(const u32x4*)(qd_row + (16 * kq + 4 * g) * 4);
-        const u32x4 Bq = *(const u32x4*)(W + S::KA + (16 * kq + 4 * g) * 4);
-        s0 = Mfma<MZ_F16>::run(A, Bq, s0);
+      for (int kq = 0; kq < 4; ++kq) {
+        const u32x4 A = *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2);
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const u32x4 Bq = *(const u32x4*)(W + S::KA + (part * D + 32 * kq + 8 * g) * 2);
+          s0 = Mfma<MZ_F16>::run(A, Bq, s0);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[j] = s0;
-      // k-tiles software-pipelined: the lookups of k-tile kt+1 are issued
-      // before the MFMAs of k-tile kt, so the LDS latency overlaps the MFMAs
+      // k-tiles software-pipelined in three stages: the table reads of
+      // k-tile kt+1 are issued, then the addresses of k-tile kt+2 computed,
+      // then the MFMAs of k-tile kt run.  The address work sits between the
+      // reads and the wait for them: a k-tile has 16 reads and the LDS
+      // counter can leave at most 15 outstanding, so the wait before the
+      // MFMAs also takes the oldest reads of the next k-tile.
       const u32x4 kz0 = *(const u32x4*)(W + S::KZP + g * 32);
       const u32x4 kz1 = *(const u32x4*)(W + S::KZP + g * 32 + 16);
+      auto kzp = [&](int kt) { return kt < 4 ? kz0[kt] : kz1[kt - 4]; };
       u32x4 Ac = *(const u32x4*)(a_hi_row + (4 * g) * 4);
       u32x4 Bc[4], Bn[4];
-      lookup_ktile<BITS, S::TBL_K>(smem, KW[0], KW[1], kz0[0], grep, odd, lsh, Bc);
+      uint32_t adc[4][4], adn[4][4];
+      addr_ktile<BITS>(KW[0], KW[1], kzp(0), grep, odd, lsh, adc);
+      read_ktile<S::TBL_K>(smem, adc, Bc);
+      addr_ktile<BITS>(KW[2], KW[3], kzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         u32x4 An;
         if (kt < 7) {
           An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
-          lookup_ktile<BITS, S::TBL_K>(smem, KW[2 * kt + 2], KW[2 * kt + 3], kt + 1 < 4 ? kz0[kt + 1] : kz1[kt - 3],
-                                       grep, odd, lsh, Bn);
+          read_ktile<S::TBL_K>(smem, adn, Bn);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt < 6) addr_ktile<BITS>(KW[2 * kt + 4], KW[2 * kt + 5], kzp(kt + 2), grep, odd, lsh, adn);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], s[jt]);
         __builtin_amdgcn_sched_barrier(0);
@@ -644,11 +706,12 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       // keep their exponent (at most 15: p * 2^15 stays finite in fp16)
       // whatever the tile order
       kv_exp = min(kacc_init ? kacc : 15, 15);
-      unscale = a.scaling;
+      unscale = scaling2;
       const float unit = ldexpf(1.f, kv_exp);
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) {
-        ((float2*)(W + S::VBP))[vg * TILE + lane] = float2{unit, 0.f};
+        ((float*)(W + S::VBP))[vg * TILE + lane] = unit;
+        ((float*)(W + S::VBN))[vg * TILE + lane] = 0.f;
         ((float*)(W + S::VA))[vg * TILE + lane] = 0.f;
       }
 #pragma unroll
@@ -678,13 +741,13 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
         }
       }
       wave_lds_sync();  // the (1, 0) / 0 scalars above are read by other lanes below
+      read_value_scalars();
     }
     load_kw<BITS>(KW, bf, tl, lane);
 
     // ---------- online softmax in registers: head slot s of this lane group
     // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
     float corr[HS];
-    bool moved = false;
     // factor taking the accumulators from exponent kacc to this tile's kv_exp
     const float fexp = ldexpf(1.f, kv_exp - kacc);
 #pragma unroll
@@ -697,23 +760,24 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
         const int tt = 4 * n + jt;
         float v = (s[jt][i] + s[jt][i + 1]) * unscale;
         if (tt >= n_valid) v = -INFINITY;
-        else if (a.mask) v += a.mask[b * a.mask_sb + pos0 + tt];
+        else if (a.mask) v = __builtin_fmaf(a.mask[b * a.mask_sb + pos0 + tt], kLog2e, v);
         x[jt] = v;
         tmax = fmaxf(tmax, v);
       }
       tmax = group_reduce<16>(tmax, OpMax());
       const float m_new = fmaxf(m_run[sl], tmax);
-      corr[sl] = (m_new == -INFINITY) ? 1.f : __expf(m_run[sl] - m_new);
-      moved |= corr[sl] != 1.f;
+      // while a row is fully masked its maximum stays -inf; 0 stands in for
+      // it, so exp2(-inf - 0) gives the zero weights, and a zero correction
+      // of the still all-zero sums, with no per-element test
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      corr[sl] = __builtin_amdgcn_exp2f(m_run[sl] - m_use);
       m_run[sl] = m_new;
-      float psum = 0.f;
-      uint16_t ph[4];
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        const float p = (x[jt] == -INFINITY) ? 0.f : __expf(x[jt] - m_new);
-        ph[jt] = f2h(p);
-        psum += h2f(ph[jt]);
-      }
+      // weights rounded to fp16 (the P.V operand precision); the row sum uses
+      // the same rounded weights
+      const h2 p01 = h2{(_Float16)__builtin_amdgcn_exp2f(x[0] - m_use), (_Float16)__builtin_amdgcn_exp2f(x[1] - m_use)};
+      const h2 p23 = h2{(_Float16)__builtin_amdgcn_exp2f(x[2] - m_use), (_Float16)__builtin_amdgcn_exp2f(x[3] - m_use)};
+      const h2 one2 = h2{(_Float16)1.f, (_Float16)1.f};
+      float psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
       psum = group_reduce<16>(psum, OpAdd());
       l_run[sl] = l_run[sl] * corr[sl] + psum;
       // the values' constant part of this head: the running sum rescaled,
@@ -722,11 +786,11 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       const float fa = corr[sl] * fexp;
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) {
-        const f32x4 av = *(const f32x4*)(W + S::VA + (vg * TILE + 4 * n) * 4);
-        float c = h2f(ph[0]) * av[0];
-        c = __builtin_fmaf(h2f(ph[1]), av[1], c);
-        c = __builtin_fmaf(h2f(ph[2]), av[2], c);
-        c = __builtin_fmaf(h2f(ph[3]), av[3], c);
+        const f32x4 av = va_r[vg];
+        float c = (float)p01.x * av[0];
+        c = __builtin_fmaf((float)p01.y, av[1], c);
+        c = __builtin_fmaf((float)p23.x, av[2], c);
+        c = __builtin_fmaf((float)p23.y, av[3], c);
         acc_a[sl][vg] = __builtin_fmaf(acc_a[sl][vg], fa, group_reduce<16>(c, OpAdd()));
       }
       if (owner) {
@@ -735,14 +799,12 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
         const int h = h0 + sl;
 #pragma unroll
         for (int vg = 0; vg < NG; ++vg) {
-          const f32x4 b01 = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 8);
-          const f32x4 b23 = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 8 + 16);
-          const h2 p01 = __builtin_bit_cast(h2, (uint32_t)ph[0] | ((uint32_t)ph[1] << 16));
-          const h2 p23 = __builtin_bit_cast(h2, (uint32_t)ph[2] | ((uint32_t)ph[3] << 16));
-          const uint2 w0 = split_product(p01.x, b01[0], b01[1]);
-          const uint2 w1 = split_product(p01.y, b01[2], b01[3]);
-          const uint2 w2 = split_product(p23.x, b23[0], b23[1]);
-          const uint2 w3 = split_product(p23.y, b23[2], b23[3]);
+          const f32x4 bp = vbp_r[vg];
+          const f32x4 bn = vbn_r[vg];
+          const uint2 w0 = split_product(p01.x, bp[0], bn[0]);
+          const uint2 w1 = split_product(p01.y, bp[1], bn[1]);
+          const uint2 w2 = split_product(p23.x, bp[2], bn[2]);
+          const uint2 w3 = split_product(p23.y, bp[3], bn[3]);
           *(u32x4*)(pa + (vg * NREP + h) * LROW + 4 * n) = u32x4{w0.x, w1.x, w2.x, w3.x};
           *(u32x4*)(pa_lo + (vg * NREP + h) * LROW + 4 * n) = u32x4{w0.y, w1.y, w2.y, w3.y};
         }
@@ -750,42 +812,46 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     }
     wave_lds_sync();
 
-    // ---------- rescale the accumulators (softmax correction and value-tile exponent),
-    // skipped when no head's maximum moved and the exponent is unchanged
-    // (acc_a was rescaled above)
-    if (__ballot(owner && moved) != 0 || kv_exp != kacc || !kacc_init) {
-      kacc = kv_exp;
-      kacc_init = true;
+    // ---------- rescale the accumulators (softmax correction and value-tile
+    // exponent; acc_a was rescaled above).  Unconditional: a branch around it
+    // costs the accumulators a register copy on every tile.
+    kacc = kv_exp;
+    kacc_init = true;
 #pragma unroll
-      for (int sl = 0; sl < HS; ++sl) {
-        const int i = sl * RS;
-        const float f = corr[sl] * fexp;
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS;
+      const float f = corr[sl] * fexp;
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
+      for (int vg = 0; vg < NG; ++vg) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[vg][j][i] *= f, acc[vg][j][i + 1] *= f;
-        }
+        for (int j = 0; j < 4; ++j) acc[vg][j][i] *= f, acc[vg][j][i + 1] *= f;
       }
     }
 
     // ---------- acc += P V
-    if (quant) {
+    if constexpr (quant) {
       // steps st = (kt, vg), software-pipelined like Q.K
       u32x4 vz[NG];
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
+      auto vzp = [&](int st) { return vz[st % NG][st / NG]; };
       u32x4 Ac = *(const u32x4*)(pv_row + 4 * g);
       u32x4 Bc[4], Bn[4];
-      lookup_ktile<BITS, S::TBL_V>(smem, VW[0], VW[1], vz[0][0], grep, odd, lsh, Bc);
+      uint32_t adc[4][4], adn[4][4];
+      addr_ktile<BITS>(VW[0], VW[1], vzp(0), grep, odd, lsh, adc);
+      read_ktile<S::TBL_V>(smem, adc, Bc);
+      addr_ktile<BITS>(VW[2], VW[3], vzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int st = 0; st < 4 * NG; ++st) {
-        const int kt = st / NG, vg = st % NG;
+        const int vg = st % NG;
         u32x4 An;
         if (st + 1 < 4 * NG) {
           const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
           An = *(const u32x4*)(pv_row + vg1 * NREP * LROW + 16 * kt1 + 4 * g);
-          lookup_ktile<BITS, S::TBL_V>(smem, VW[2 * st + 2], VW[2 * st + 3], vz[vg1][kt1], grep, odd, lsh, Bn);
+          read_ktile<S::TBL_V>(smem, adn, Bn);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 2 < 4 * NG) addr_ktile<BITS>(VW[2 * st + 4], VW[2 * st + 5], vzp(st + 2), grep, odd, lsh, adn);
         scal_chunk(MN, st);  // the next tile's scalars, chunk st
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], acc[vg][jt]);
@@ -858,8 +924,8 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
   int done = 0;
   if (older) __builtin_amdgcn_s_setprio(2);
   else __builtin_amdgcn_s_setprio(3);
-  for (int v = v0; v < n_virt; v += WAVES) {
-    process(tile_of(v), v + WAVES < n_virt ? tile_of(v + WAVES) : q_last);
+  auto step = [&](auto quant_tag, const int v) {
+    process(quant_tag, tile_of(v), v + WAVES < n_virt ? tile_of(v + WAVES) : q_last);
     ++done;
     switch ((4 * done) / max(n_mine, 1) + older) {  // wave-uniform
       case 0: break;
@@ -867,7 +933,10 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       case 2: __builtin_amdgcn_s_setprio(1); break;
       default: __builtin_amdgcn_s_setprio(0); break;
     }
-  }
+  };
+  int v = v0;
+  for (; v < n_res; v += WAVES) step(std::false_type{}, v);  // residual tiles come first
+  for (; v < n_virt; v += WAVES) step(std::true_type{}, v);
   __builtin_amdgcn_s_setprio(0);
 
   // ---------------- merge the waves and write this split's partial records
@@ -911,7 +980,7 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
       if (M_ != -INFINITY) {
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
-          const float f = __expf(red[w * RED + h] - M_);
+          const float f = __builtin_amdgcn_exp2f(red[w * RED + h] - M_);
           num += f * red[w * RED + 2 * NREP + h * D + c];
           den += f * red[w * RED + NREP + h];
         }
@@ -929,11 +998,11 @@ __global__ __launch_bounds__(64 * waves_for<NREP>()) __attribute__((amdgpu_waves
     for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
     float val = 0.f;
     if (c == D) {
-      val = M_;
+      val = M_ * kLn2;  // the record's maximum in natural-log units
     } else if (M_ != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) {
-        const float f = __expf(red[w * RED + h] - M_);
+        const float f = __builtin_amdgcn_exp2f(red[w * RED + h] - M_);
         val += f * (c == D + 1 ? red[w * RED + NREP + h] : red[w * RED + 2 * NREP + h * D + c]);
       }
     }
