@@ -73,7 +73,13 @@ template <> __device__ __forceinline__ float rnd<MZ_F32>(float x) { return x; }
 // gfx950 converts to bf16 in hardware (v_cvt_pk_bf16_f32, round to nearest
 // even, the same as f2bf for every non-NaN input; a NaN stays a NaN but its
 // payload is not canonicalised, so stores go through f2bf).
-template <> __device__ __forceinline__ float rnd<MZ_BF16>(float x) { return (float)(__bf16)x; }
+// The value goes to the high half of the converted pair with 0 in the low
+// half, so the pair's bits are already the fp32 value: one instruction.
+template <> __device__ __forceinline__ float rnd<MZ_BF16>(float x) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(float, __builtin_convertvector(f32x2_t{0.f, x}, bf16x2_t));
+}
 template <> __device__ __forceinline__ float rnd<MZ_F16>(float x) { return h2f(f2h(x)); }
 
 template <int DT> __device__ __forceinline__ float load_val(const void* p, int64_t i);

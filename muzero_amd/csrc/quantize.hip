@@ -19,8 +19,13 @@
 
 namespace mz {
 
-constexpr int QWG = 256;           // threads per quantize workgroup
-constexpr int QGROUPS_PER_WAVE = 8;
+constexpr int QWG = 256;  // threads per quantize workgroup
+// Values per lane: each lane quantizes 32 values of a 64-value group (two
+// lanes per group), so a wave quantizes 32 groups and a group's parameters
+// are formed once per 32 values.  Key groups read their column from an LDS
+// tile.
+constexpr int QN_ROWS = 32;
+constexpr int QN_KEYS = 32;
 
 // Compander parameters of one group (quantizer.py:169-181), every op rounded
 // to the input dtype DT.
@@ -65,14 +70,28 @@ __device__ __forceinline__ QParams qparams(float mn, float mx, float eps_in) {
   g.eps = rnd<DT>(eps_in);
   g.mn = mn;
   g.sc = clamp_min(rnd<DT>(mx - mn), g.eps);
-  g.za = clamp01(rnd<DT>(rnd<DT>(0.f - mn) / g.sc));
+  if constexpr (DT == MZ_BF16) {
+    // the reciprocal form of the division (exact for bf16 operands, see
+    // qdiv) unless the scale's reciprocal would be denormal; the IEEE
+    // division runs only in a wave that holds such a group
+    g.rsc = __builtin_amdgcn_rcpf(g.sc);
+    const float a = rnd<DT>(0.f - mn);
+    float zq = rnd<DT>(a * g.rsc);
+    const bool slow = g.sc > 0x1p126f && g.sc < __builtin_inff();
+    if (__ballot(slow) != 0) {
+      if (slow) zq = rnd<DT>(a / g.sc);
+    }
+    g.za = clamp01(zq);
+  } else {
+    g.za = clamp01(rnd<DT>(rnd<DT>(0.f - mn) / g.sc));
+  }
   g.zl = rintf(rnd<DT>(g.za * qmax));
   g.pb = clamp_min(rnd<DT>(qmax - g.zl), 1.f);
   g.nb = clamp_min(g.zl, 1.f);
   g.pe = clamp_min(rnd<DT>(1.f - g.za), g.eps);
   g.ne = clamp_min(g.za, g.eps);
   if constexpr (DT != MZ_F32) {
-    g.rsc = __builtin_amdgcn_rcpf(g.sc);
+    if constexpr (DT != MZ_BF16) g.rsc = __builtin_amdgcn_rcpf(g.sc);
     g.rpe = __builtin_amdgcn_rcpf(g.pe);
     g.rne = __builtin_amdgcn_rcpf(g.ne);
   }
@@ -148,75 +167,93 @@ __device__ __forceinline__ uint32_t value_code(float v, const QParams& g, const 
   return (uint32_t)fminf(fmaxf(q, 0.f), qmax);
 }
 
-// value_code<MZ_BF16, BITS, true, true> of two values at once: each of the
-// chain's roundings to bf16 converts the pair with one v_cvt_pk_bf16_f32.
+// value_code<MZ_BF16, BITS, true, true> of two values at once (the two
+// chains interleave; each rounding to bf16 is one v_cvt_pk_bf16_f32).
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void rnd_bf16_pair(float& a, float& b) {
-  const bf16x2v r = __builtin_convertvector(f32x2v{a, b}, bf16x2v);
-  a = (float)r.x;
-  b = (float)r.y;
+  a = rnd<MZ_BF16>(a);
+  b = rnd<MZ_BF16>(b);
 }
 
+//
+// The same values as the op-by-op chain, in fewer ops (every rewrite below is
+// exact for a finite group: mn and the scale finite, the divisors positive):
+//  - min(rnd(x), 1) = rnd(min(x, 1)) (1 is a bf16 value and rounding is
+//    monotone), and x >= 0, so the clamp rides on the multiply (med3 = the
+//    VOP3 clamp bit);
+//  - the selected side's difference, za - n below za and n - za above, is
+//    |n - za| (fp32 negation is exact, and bf16 rounding is symmetric);
+//  - the down side's offset is subtracted: zl - rint(rnd(y * nb)) =
+//    zl + rint(rnd(y * -nb)) (both roundings are symmetric);
+//  - p is a bf16 value >= +0 with a zero low half, so its ratio-table byte
+//    address, pattern * 2, is its bit pattern >> 15.
 template <int BITS>
 __device__ __forceinline__ void value_code_bf16_pair(float v0, float v1, const QParams& g, const uint8_t* lds,
                                                      uint32_t& c0, uint32_t& c1) {
   constexpr float qmax = (float)((1 << BITS) - 1);
   float a0 = v0 - g.mn, a1 = v1 - g.mn;
   rnd_bf16_pair(a0, a1);
-  float n0 = a0 * g.rsc, n1 = a1 * g.rsc;
+  float n0 = __builtin_amdgcn_fmed3f(a0 * g.rsc, 0.f, 1.f), n1 = __builtin_amdgcn_fmed3f(a1 * g.rsc, 0.f, 1.f);
   rnd_bf16_pair(n0, n1);
-  n0 = fminf(n0, 1.f), n1 = fminf(n1, 1.f);
   const bool up0 = n0 >= g.za, up1 = n1 >= g.za;
-  float d0 = up0 ? n0 - g.za : g.za - n0, d1 = up1 ? n1 - g.za : g.za - n1;
-  rnd_bf16_pair(d0, d1);
-  float p0 = d0 * (up0 ? g.rpe : g.rne), p1 = d1 * (up1 ? g.rpe : g.rne);
+  float d0 = n0 - g.za, d1 = n1 - g.za;
+  rnd_bf16_pair(d0, d1);  // |rnd(x)| = rnd(|x|): the absolute value rides on the multiply's operand
+  float p0 = __builtin_amdgcn_fmed3f(__builtin_fabsf(d0) * (up0 ? g.rpe : g.rne), 0.f, 1.f);
+  float p1 = __builtin_amdgcn_fmed3f(__builtin_fabsf(d1) * (up1 ? g.rpe : g.rne), 0.f, 1.f);
   rnd_bf16_pair(p0, p1);
-  p0 = fminf(p0, 1.f), p1 = fminf(p1, 1.f);
-  // p0, p1 are bf16 values >= 0: their pattern is the high half of the fp32 bits
-  const uint16_t* Y = (const uint16_t*)lds;
-  const float y0 = bf2f(Y[(__float_as_uint(p0) >> 16) & 0x7FFFu]);
-  const float y1 = bf2f(Y[(__float_as_uint(p1) >> 16) & 0x7FFFu]);
-  float o0 = y0 * (up0 ? g.pb : g.nb), o1 = y1 * (up1 ? g.pb : g.nb);
+  const float y0 = bf2f(*(const uint16_t*)(lds + (__float_as_uint(p0) >> 15)));
+  const float y1 = bf2f(*(const uint16_t*)(lds + (__float_as_uint(p1) >> 15)));
+  float o0 = y0 * (up0 ? g.pb : -g.nb), o1 = y1 * (up1 ? g.pb : -g.nb);
   rnd_bf16_pair(o0, o1);
-  o0 = rintf(o0), o1 = rintf(o1);
-  // zl +- off: an integer in [-1, qmax + 1], exact in bf16 (its rounding is the identity)
-  const float q0 = up0 ? g.zl + o0 : g.zl - o0, q1 = up1 ? g.zl + o1 : g.zl - o1;
-  c0 = (uint32_t)fminf(fmaxf(q0, 0.f), qmax);
-  c1 = (uint32_t)fminf(fmaxf(q1, 0.f), qmax);
+  // zl + off: an integer in [-1, qmax + 1], exact in bf16 (its rounding is the identity)
+  const float q0 = g.zl + rintf(o0), q1 = g.zl + rintf(o1);
+  c0 = (uint32_t)__builtin_amdgcn_fmed3f(q0, 0.f, qmax);
+  c1 = (uint32_t)__builtin_amdgcn_fmed3f(q1, 0.f, qmax);
 }
 
-// Min / max over the 8 lanes of a group (lanes 8k..8k+7), NaN-propagating.
-__device__ __forceinline__ float group8_min(float v) {
-  v = nmin(v, dpp_sel<DPP_QUAD_XOR1>(v));
-  v = nmin(v, dpp_sel<DPP_QUAD_XOR2>(v));
-  return nmin(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+// Min / max over the 8 lanes of a group (lanes 8k..8k+7), NaN-propagating:
+// IEEE 754-2019 minimum / maximum (v_minimum3_f32 / v_maximum3_f32), which
+// return NaN when either operand is NaN, as torch's amin / amax do.  (Between
+// -0 and +0 they pick -0 / +0; torch's choice there depends on its
+// vectorisation.  The codes are the same either way: only the sign of a zero
+// minimum or maximum in the metadata can differ.)
+__device__ __forceinline__ float fmin_nan(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+__device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// Over the L lanes of a group (aligned runs of L = 2, 4 or 8 lanes).
+template <int L>
+__device__ __forceinline__ float group_min(float v) {
+  if constexpr (L >= 2) v = fmin_nan(v, dpp_sel<DPP_QUAD_XOR1>(v));
+  if constexpr (L >= 4) v = fmin_nan(v, dpp_sel<DPP_QUAD_XOR2>(v));
+  if constexpr (L >= 8) v = fmin_nan(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+  return v;
 }
-__device__ __forceinline__ float group8_max(float v) {
-  v = nmax(v, dpp_sel<DPP_QUAD_XOR1>(v));
-  v = nmax(v, dpp_sel<DPP_QUAD_XOR2>(v));
-  return nmax(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+template <int L>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (L >= 2) v = fmax_nan(v, dpp_sel<DPP_QUAD_XOR1>(v));
+  if constexpr (L >= 4) v = fmax_nan(v, dpp_sel<DPP_QUAD_XOR2>(v));
+  if constexpr (L >= 8) v = fmax_nan(v, dpp_sel<DPP_ROW_HALF_MIRROR>(v));
+  return v;
 }
 
-// Quantize this lane's 8 values x[0..7] (positions 8*part .. 8*part+7 of its
-// group) and store its BITS packed bytes at prow + part*BITS; lane part 0
-// stores the group's metadata at index midx.
+// NaN-propagating min / max of x[0..N) (a balanced tree).
+template <int N, int S = 0>
+__device__ __forceinline__ float tree_min(const float* x) {
+  if constexpr (N == 1) return x[S];
+  else return fmin_nan(tree_min<N / 2, S>(x), tree_min<N / 2, S + N / 2>(x));
+}
+template <int N, int S = 0>
+__device__ __forceinline__ float tree_max(const float* x) {
+  if constexpr (N == 1) return x[S];
+  else return fmax_nan(tree_max<N / 2, S>(x), tree_max<N / 2, S + N / 2>(x));
+}
+
+// Quantize the 8 values x[0..7] of a chunk with the group's parameters and
+// store their BITS packed bytes at dst.
 template <int DT, int BITS>
-__device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, uint8_t* prow, void* mn_out,
-                                               void* sc_out, int64_t midx, int meta_dtype, float eps,
-                                               const uint8_t* lds, const void* table) {
-  float mn = x[0], mx = x[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) mn = nmin(mn, x[i]), mx = nmax(mx, x[i]);
-  mn = group8_min(mn);
-  mx = group8_max(mx);
-  const QParams g = qparams<DT, BITS>(mn, mx, eps);
+__device__ __forceinline__ void quantize_chunk8(const float* x, const QParams& g, bool finite, uint8_t* dst,
+                                                const uint8_t* lds, const void* table) {
   uint64_t w = 0;
-  // (fp16 rounds eps to 0: a constant group, or za at 0 or 1, then divides by 0).
-  // The fp32 8-bit thresholds stay in global memory, where the plain form's
-  // binary search measured faster.
-  const bool finite = QTable<DT, BITS>::IN_LDS && __builtin_isfinite(g.mn) && __builtin_isfinite(g.sc) &&
-                      g.sc > 0.f && g.pe > 0.f && g.ne > 0.f;
   if (qfast<DT>(g) && finite) {
     if constexpr (DT == MZ_BF16) {
 #pragma unroll
@@ -239,7 +276,6 @@ __device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, ui
 #pragma unroll
     for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, false, false>(x[i], g, lds, table) << (i * BITS);
   }
-  uint8_t* dst = prow + part * BITS;
   if constexpr (BITS == 8) *(uint64_t*)dst = w;
   else if constexpr (BITS == 4) *(uint32_t*)dst = (uint32_t)w;
   else if constexpr (BITS == 2) *(uint16_t*)dst = (uint16_t)w;
@@ -248,6 +284,29 @@ __device__ __forceinline__ void quantize_lane8(const float (&x)[8], int part, ui
 #pragma unroll
     for (int k = 0; k < BITS; ++k) dst[k] = (uint8_t)(w >> (8 * k));
   }
+}
+
+// Quantize this lane's N values x[0..N) (positions N*part .. N*part+N-1 of
+// its group, which 64 / N lanes share) and store its N*BITS/8 packed bytes
+// at prow + part*N*BITS/8; lane part 0 stores the group's metadata at index
+// midx.  The group's parameters are formed once per lane, so a larger N
+// spreads them over more values.
+template <int DT, int BITS, int N>
+__device__ __forceinline__ void quantize_lane(const float (&x)[N], int part, uint8_t* prow, void* mn_out,
+                                              void* sc_out, int64_t midx, int meta_dtype, float eps,
+                                              const uint8_t* lds, const void* table) {
+  constexpr int L = 64 / N;
+  const float mn = group_min<L>(tree_min<N>(x));
+  const float mx = group_max<L>(tree_max<N>(x));
+  const QParams g = qparams<DT, BITS>(mn, mx, eps);
+  // (fp16 rounds eps to 0: a constant group, or za at 0 or 1, then divides by 0).
+  // The fp32 8-bit thresholds stay in global memory, where the plain form's
+  // binary search measured faster.
+  const bool finite = QTable<DT, BITS>::IN_LDS && __builtin_isfinite(g.mn) && __builtin_isfinite(g.sc) &&
+                      g.sc > 0.f && g.pe > 0.f && g.ne > 0.f;
+  uint8_t* dst = prow + part * (N / 8) * BITS;
+#pragma unroll
+  for (int c = 0; c < N / 8; ++c) quantize_chunk8<DT, BITS>(x + 8 * c, g, finite, dst + c * BITS, lds, table);
   if (part == 0) {
     store_val(mn_out, midx, mn, meta_dtype);
     store_val(sc_out, midx, g.sc, meta_dtype);
@@ -283,15 +342,17 @@ __global__ __launch_bounds__(QWG) void quantize_rows_kernel(const void* __restri
                                                             float eps, const void* __restrict__ table) {
   __shared__ __align__(16) uint8_t lds[QTable<DT, BITS>::LDS_BYTES];
   stage_table<DT, BITS>(lds, table);
+  constexpr int N = QN_ROWS, L = 64 / N;
   const int lane = threadIdx.x & 63;
-  const int part = lane & 7;
-  const int64_t stride = (int64_t)gridDim.x * (QWG / 64) * QGROUPS_PER_WAVE;
-  for (int64_t row = ((int64_t)blockIdx.x * (QWG / 64) + (threadIdx.x >> 6)) * QGROUPS_PER_WAVE + (lane >> 3);
-       row - (lane >> 3) < nrows; row += stride) {
+  const int part = lane % L;
+  const int64_t stride = (int64_t)gridDim.x * (QWG / 64) * N;
+  for (int64_t row = ((int64_t)blockIdx.x * (QWG / 64) + (threadIdx.x >> 6)) * N + lane / L;
+       row - lane / L < nrows; row += stride) {
     if (row < nrows) {  // lanes of a group share `row`: the whole group takes this branch
-      float v[8];
-      load8<DT, VEC>(v, x, row * xs + 8 * part);
-      quantize_lane8<DT, BITS>(v, part, packed + row * ps, mn, sc, row * ms, meta_dtype, eps, lds, table);
+      float v[N];
+#pragma unroll
+      for (int c = 0; c < N / 8; ++c) load8<DT, VEC>(*(float(*)[8])(v + 8 * c), x, row * xs + N * part + 8 * c);
+      quantize_lane<DT, BITS, N>(v, part, packed + row * ps, mn, sc, row * ms, meta_dtype, eps, lds, table);
     }
   }
 }
@@ -315,7 +376,7 @@ static FastDiv make_fastdiv(uint32_t d) {
 // Row (b, h, t, j): channels 64j..64j+63 of token t, zero beyond D.  Rows
 // are numbered b-major with j fastest; nrows < 2^31 per launch (the host
 // splits the batch).
-template <int DT, int BITS, bool VEC>
+template <int DT, int BITS, bool VEC, bool NARROW>
 __global__ __launch_bounds__(QWG) void quantize_values_kernel(const void* __restrict__ x, int nrows, FastDiv fng,
                                                               FastDiv fT, FastDiv fH, int D, int64_t sb, int64_t sh,
                                                               int64_t st, uint8_t* __restrict__ packed, int64_t psb,
@@ -325,32 +386,61 @@ __global__ __launch_bounds__(QWG) void quantize_values_kernel(const void* __rest
   __shared__ __align__(16) uint8_t lds[QTable<DT, BITS>::LDS_BYTES];
   stage_table<DT, BITS>(lds, table);
   constexpr int QB = 8 * BITS;
+  constexpr int N = QN_ROWS, L = 64 / N;  // values per lane, lanes per group
   const int ng = (int)fng.d, T = (int)fT.d, H = (int)fH.d;
+  const int TN = T * ng;  // rows per (b, h)
   const int lane = threadIdx.x & 63;
-  const int part = lane & 7;
-  const int stride = gridDim.x * (QWG / 64) * QGROUPS_PER_WAVE;
-  for (int row = (blockIdx.x * (QWG / 64) + (threadIdx.x >> 6)) * QGROUPS_PER_WAVE + (lane >> 3);
-       row - (lane >> 3) < nrows; row += stride) {
-    if (row < nrows) {  // lanes of a group share `row`: the whole group takes this branch
-      const int r1 = (int)fng.div((uint32_t)row);
-      const int j = row - r1 * ng;
-      const int r2 = (int)fT.div((uint32_t)r1);
-      const int t = r1 - r2 * T;
-      const int b = (int)fH.div((uint32_t)r2);
-      const int h = r2 - b * H;
-      const int c = 64 * j + 8 * part;
-      const int64_t src = b * sb + h * sh + t * st + c;
-      float v[8];
-      if (c + 8 <= D) {  // VEC only picks the load width; lanes past D (D % 64 != 0) read nothing
-        load8<DT, VEC>(v, x, src);
+  const int part = lane % L;
+  const int k = lane / L;  // the lane's row within its wave's N
+  // wave-uniform (the compiler cannot see that threadIdx.x >> 6 is): the
+  // (b, h) decomposition of a wave's first row then runs on the scalar unit
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int stride = gridDim.x * (QWG / 64) * N;
+  for (int w0 = (blockIdx.x * (QWG / 64) + wave) * N; w0 < nrows; w0 += stride) {
+    const int row = w0 + k;
+    if (row >= nrows) continue;  // lanes of a group share `row`: the whole group takes this branch
+    int64_t xo, po, mo;
+    int i;
+    if (TN >= N) {
+      // the wave's N rows lie in (b, h) slices o0 and o0 + 1 at most (rows
+      // are b-major, (t, j) fastest): their offsets are scalar
+      const int o0 = (int)fT.div((uint32_t)fng.div((uint32_t)w0));  // w0 / (T*ng)
+      const int b0 = (int)fH.div((uint32_t)o0), h0 = o0 - b0 * H;
+      const int b1 = h0 + 1 == H ? b0 + 1 : b0, h1 = h0 + 1 == H ? 0 : h0 + 1;
+      i = w0 - o0 * TN + k;
+      const bool next = i >= TN;
+      if (next) i -= TN;
+      xo = next ? b1 * sb + h1 * sh : b0 * sb + h0 * sh;
+      po = next ? b1 * psb + h1 * psh : b0 * psb + h0 * psh;
+      mo = next ? b1 * msb + h1 * msh : b0 * msb + h0 * msh;
+    } else {
+      // short slices (few tokens): each row decomposed on its own
+      const int o = (int)fT.div((uint32_t)fng.div((uint32_t)row));
+      const int b = (int)fH.div((uint32_t)o), h = o - b * H;
+      i = row - o * TN;
+      xo = b * sb + h * sh;
+      po = b * psb + h * psh;
+      mo = b * msb + h * msh;
+    }
+    const int t = (int)fng.div((uint32_t)i);
+    const int j = i - t * ng;
+    const int c = 64 * j + N * part;
+    // NARROW: every offset within a slice fits 31 bits (checked on the host)
+    const int64_t src = xo + (NARROW ? (int64_t)(t * (int)st + c) : (int64_t)t * st + c);
+    float v[N];
+#pragma unroll
+    for (int e8 = 0; e8 < N / 8; ++e8) {
+      float (&v8)[8] = *(float(*)[8])(v + 8 * e8);
+      const int c8 = c + 8 * e8;
+      if (c8 + 8 <= D) {  // VEC only picks the load width; lanes past D (D % 64 != 0) read nothing
+        load8<DT, VEC>(v8, x, src + 8 * e8);
       } else {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = c + k < D ? load_val<DT>(x, src + k) : 0.f;
+        for (int e = 0; e < 8; ++e) v8[e] = c8 + e < D ? load_val<DT>(x, src + 8 * e8 + e) : 0.f;
       }
-      uint8_t* prow = packed + b * psb + h * psh + ((int64_t)t * ng + j) * QB;
-      const int64_t midx = b * msb + h * msh + (int64_t)t * ng + j;
-      quantize_lane8<DT, BITS>(v, part, prow, mn, sc, midx, meta_dtype, eps, lds, table);
     }
+    uint8_t* prow = packed + po + (NARROW ? (int64_t)(i * QB) : (int64_t)i * QB);
+    quantize_lane<DT, BITS, N>(v, part, prow, mn, sc, mo + i, meta_dtype, eps, lds, table);
   }
 }
 
@@ -399,6 +489,22 @@ struct KeyStage {
     else if constexpr (DT == MZ_BF16) return bf2f(*p);
     else return h2f(*p);
   }
+  static __device__ __forceinline__ float load16(uint16_t u) { return DT == MZ_BF16 ? bf2f(u) : h2f(u); }
+};
+
+// 16-bit inputs arriving as vectors are staged transposed instead: one row
+// of KT_PITCH dwords per channel, dword m = tokens 2m (low half) and 2m + 1
+// (high half), so a lane reads its 32 tokens of a column as four 16-byte
+// LDS reads.  A staging thread loads the same 8 channels of two adjacent
+// tokens and pairs them with v_perm; threads of a wave take consecutive
+// token pairs, so their stores fill consecutive dwords of a row.  The pitch
+// (36 dwords, a multiple of 4) keeps the 16-byte reads aligned, and the 8
+// lanes served in one cycle (4 columns x 2 halves) cover distinct banks.
+constexpr int KT_PITCH = 36;
+template <int DT, bool VEC>
+struct KeyTrans {
+  static constexpr bool ON = VEC && DT != MZ_F32;
+  static constexpr size_t bytes(int D) { return (size_t)D * KT_PITCH * 4; }
 };
 
 template <int DT, int BITS, bool VEC>
@@ -418,7 +524,7 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
   const int ld = D + KS::PAD;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int part = lane & 7;
+  const int part = lane % (64 / QN_KEYS);
   constexpr int QB = 8 * BITS;
   constexpr int NE = Vec16<DT>::N;
   const int vpr = D / NE;             // vectors per token row (VEC)
@@ -427,9 +533,25 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
     const int s = ti % nsg, h = (ti / nsg) % H, b = ti / (nsg * H);
     return b * sb + h * sh + (int64_t)(64 * s) * st;
   };
+  constexpr bool TRANS = KeyTrans<DT, VEC>::ON;
+  uint32_t* tileT = (uint32_t*)tile;  // TRANS: [D][KT_PITCH] token-pair dwords
+  const int npair = 32 * vpr;         // TRANS: (token pair, 8-channel block) items per tile
   uint4 nxt[KEY_MAX_VEC];
   auto fetch = [&](int ti) {
-    if constexpr (VEC) {
+    if constexpr (TRANS) {
+      const int64_t base = tile_base(ti);
+      const uint16_t* xb = (const uint16_t*)x;
+#pragma unroll
+      for (int k = 0; k < KEY_MAX_VEC / 2; ++k) {
+        const int e = threadIdx.x + k * QWG;
+        if (e < npair) {
+          const int tp = e & 31, cb = e >> 5;
+          const int64_t a = base + (int64_t)(2 * tp) * st + NE * cb;
+          nxt[2 * k] = *(const uint4*)(xb + a);
+          nxt[2 * k + 1] = *(const uint4*)(xb + a + st);
+        }
+      }
+    } else if constexpr (VEC) {
       const int64_t base = tile_base(ti);
       const char* xb = (const char*)x;
 #pragma unroll
@@ -446,7 +568,24 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
   for (int ti = blockIdx.x; ti < ntiles; ti += gridDim.x) {
     const int s = ti % nsg, h = (ti / nsg) % H, b = ti / (nsg * H);
     __syncthreads();  // the previous tile's columns are consumed
-    if constexpr (VEC) {
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int k = 0; k < KEY_MAX_VEC / 2; ++k) {
+        const int e = threadIdx.x + k * QWG;
+        if (e < npair) {
+          const int tp = e & 31, cb = e >> 5;
+          const uint32_t a4[4] = {nxt[2 * k].x, nxt[2 * k].y, nxt[2 * k].z, nxt[2 * k].w};
+          const uint32_t b4[4] = {nxt[2 * k + 1].x, nxt[2 * k + 1].y, nxt[2 * k + 1].z, nxt[2 * k + 1].w};
+          uint32_t* col = tileT + (NE * cb) * KT_PITCH + tp;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            col[(2 * q) * KT_PITCH] = __builtin_amdgcn_perm(b4[q], a4[q], 0x05040100u);      // channel 2q
+            col[(2 * q + 1) * KT_PITCH] = __builtin_amdgcn_perm(b4[q], a4[q], 0x07060302u);  // channel 2q+1
+          }
+        }
+      }
+      if (ti + (int)gridDim.x < ntiles) fetch(ti + gridDim.x);  // lands while this tile is quantized
+    } else if constexpr (VEC) {
 #pragma unroll
       for (int k = 0; k < KEY_MAX_VEC; ++k) {
         const int e = threadIdx.x + k * QWG;
@@ -472,13 +611,29 @@ __global__ __launch_bounds__(QWG) void quantize_keys_kernel(const void* __restri
     __syncthreads();
     uint8_t* gbase = packed + b * psb + h * psh + (int64_t)s * D * QB;
     const int64_t mbase = b * msb + h * msh + (int64_t)s * D;
-    for (int c0 = 8 * wave; c0 < D; c0 += 8 * (QWG / 64)) {
-      const int c = c0 + (lane >> 3);
-      if (c < D) {  // a group's 8 lanes share c
-        float v[8];
+    constexpr int N = QN_KEYS, L = 64 / N;  // values per lane, lanes per group (one column)
+    for (int c0 = (64 / L) * wave; c0 < D; c0 += (64 / L) * (QWG / 64)) {
+      const int c = c0 + lane / L;
+      if (c < D) {  // a group's lanes share c
+        float v[N];
+        if constexpr (TRANS) {
+          static_assert(N == 32, "a lane reads 16 token-pair dwords");
+          const uint4* src = (const uint4*)(tileT + c * KT_PITCH + 16 * part);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = KS::load(tile + (8 * part + k) * ld + c);
-        quantize_lane8<DT, BITS>(v, part, gbase + (int64_t)c * QB, mn, sc, mbase + c, meta_dtype, eps, lds, table);
+          for (int m4 = 0; m4 < 4; ++m4) {
+            const uint4 u = src[m4];
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              v[8 * m4 + 2 * q] = KS::load16((uint16_t)w[q]);
+              v[8 * m4 + 2 * q + 1] = KS::load16((uint16_t)(w[q] >> 16));
+            }
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < N; ++k) v[k] = KS::load(tile + (N * part + k) * ld + c);
+        }
+        quantize_lane<DT, BITS, N>(v, part, gbase + (int64_t)c * QB, mn, sc, mbase + c, meta_dtype, eps, lds, table);
       }
     }
   }
@@ -535,8 +690,8 @@ using namespace mz;
 
 // Persistent grid: enough workgroups to fill the GPU a few times over, each
 // looping over its share of the 64-value groups (table staged once).
-static int quantize_grid(int64_t work_groups) {
-  const int64_t per_wg = (int64_t)(QWG / 64) * QGROUPS_PER_WAVE;
+static int quantize_grid(int64_t work_groups, int groups_per_wave) {
+  const int64_t per_wg = (int64_t)(QWG / 64) * groups_per_wave;
   const int64_t need = (work_groups + per_wg - 1) / per_wg;
   return (int)std::max<int64_t>(1, std::min<int64_t>(need, (int64_t)device_cu_count() * 8));
 }
@@ -559,7 +714,7 @@ extern "C" int muzero_quantize_rows(const void* x, int x_dtype, int64_t nrows, i
   // packed bytes are stored 1/2/4/8 at a time at offsets part*bits: rows must keep that alignment
   if (((uintptr_t)packed | (uintptr_t)packed_row_stride) % packed_align(bits) != 0) return MZ_EINVAL;
   const bool vec = aligned16(x) && x_row_stride % 8 == 0;
-  const dim3 grid((unsigned)quantize_grid(nrows));
+  const dim3 grid((unsigned)quantize_grid(nrows, QN_ROWS));
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
       if (vec) hipLaunchKernelGGL((quantize_rows_kernel<D_, B_, true>), grid, dim3(QWG), 0, s, x, nrows,
@@ -597,7 +752,8 @@ extern "C" int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H,
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
       const size_t lds = (size_t)QTable<D_, B_>::LDS_BYTES +
-                         (size_t)64 * (D + KeyStage<D_>::PAD) * sizeof(typename KeyStage<D_>::T);
+                         (vec && D_ != MZ_F32 ? KeyTrans<D_, true>::bytes(D)
+                                              : (size_t)64 * (D + KeyStage<D_>::PAD) * sizeof(typename KeyStage<D_>::T));
       if (lds > 160 * 1024) return MZ_EUNSUPPORTED;
       const void* fn = vec ? (const void*)quantize_keys_kernel<D_, B_, true> : (const void*)quantize_keys_kernel<D_, B_, false>;
       if (lds > 64 * 1024) {
@@ -628,6 +784,9 @@ extern "C" int muzero_quantize_values(const void* values, int x_dtype, int B, in
   const bool vec = aligned16(values) && D % 8 == 0 && (x_sb * es) % 16 == 0 && (x_sh * es) % 16 == 0 &&
                    (x_st * es) % 16 == 0;
   const FastDiv fng = make_fastdiv((uint32_t)ng), fT = make_fastdiv((uint32_t)T), fH = make_fastdiv((uint32_t)H);
+  // offsets within one (b, h) slice in 32-bit arithmetic when they all fit
+  const bool narrow = x_st >= 0 && (int64_t)(T - 1) * x_st + D < ((int64_t)1 << 31) &&
+                      (int64_t)T * ng * 8 * bits < ((int64_t)1 << 31);
   hipStream_t s = (hipStream_t)stream;
   // row numbers stay below 2^31 per launch: batches go in slices of bstep
   const int bstep = (int)std::min<int64_t>(B, (((int64_t)1 << 31) - 1) / rows_per_b);
@@ -638,14 +797,16 @@ extern "C" int muzero_quantize_values(const void* values, int x_dtype, int B, in
     uint8_t* ps = packed + b0 * p_sb;
     void* mns = (char*)mn + b0 * m_sb * (int64_t)dtype_size(meta_dtype);
     void* scs = (char*)scale + b0 * m_sb * (int64_t)dtype_size(meta_dtype);
-    const dim3 grid((unsigned)quantize_grid(nrows));
+    const dim3 grid((unsigned)quantize_grid(nrows, QN_ROWS));
+#define MZ_QV(VECV, NARV)                                                                                     \
+  hipLaunchKernelGGL((quantize_values_kernel<D_, B_, VECV, NARV>), grid, dim3(QWG), 0, s, xs, nrows, fng, fT, fH, D, \
+                     x_sb, x_sh, x_st, ps, p_sb, p_sh, mns, scs, meta_dtype, m_sb, m_sh, eps, table)
     MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
-        if (vec) hipLaunchKernelGGL((quantize_values_kernel<D_, B_, true>), grid, dim3(QWG), 0, s, xs, nrows, fng, fT,
-                                    fH, D, x_sb, x_sh, x_st, ps, p_sb, p_sh, mns, scs, meta_dtype, m_sb, m_sh, eps,
-                                    table);
-        else hipLaunchKernelGGL((quantize_values_kernel<D_, B_, false>), grid, dim3(QWG), 0, s, xs, nrows, fng, fT,
-                                fH, D, x_sb, x_sh, x_st, ps, p_sb, p_sh, mns, scs, meta_dtype, m_sb, m_sh, eps,
-                                table)));
+        if (vec && narrow) MZ_QV(true, true);
+        else if (vec) MZ_QV(true, false);
+        else if (narrow) MZ_QV(false, true);
+        else MZ_QV(false, false)));
+#undef MZ_QV
     const int st2 = launch_status();
     if (st2 != MZ_OK) return st2;
   }
