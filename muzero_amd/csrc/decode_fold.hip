@@ -68,17 +68,29 @@ template <int NREP>
 constexpr int waves_for() { return 4; }
 template <int NREP>
 constexpr int waves_per_simd() { return 2; }
-// (P, N) table in LDS: entry (zl, q) replicated for the 4 lane groups at byte
-// zl*256 + 64*group + 4*q.  The 16 lanes of a group always read one zero
-// level (one channel / one token-group), and each group owns a disjoint bank
-// range, so the per-code lookups are free of bank conflicts.
-constexpr int TBL = 16 * 4 * 16 * 4;  // 4 KB
-
+// (P, N) table in LDS.  Up to 4 bits: entry (zl, q) replicated for the 4
+// lane groups at byte zl*256 + 64*group + 4*q; the 16 lanes of a group always
+// read one zero level (one channel / one token-group) and each group owns a
+// disjoint bank range, so the per-code lookups are free of bank conflicts.
+// 5 and 6 bits ("wide"): one copy, entry (zl, q) at byte zl*256 + 4*q (a
+// group's 32 or 64 codes span every bank anyway, so copies would not help;
+// two lane groups of a half-wave can meet on a bank).
 template <int BITS>
 struct Fmt {
   static constexpr int QMAX = (1 << BITS) - 1;
   static constexpr int QB = 8 * BITS;  // bytes per packed 64-code row
+  static constexpr bool WIDE = BITS >= 5;
+  static constexpr int WPK = WIDE ? 4 : 2;  // code words per lane and k-tile
+  static constexpr int TBL = WIDE ? (1 << BITS) * 256 : 16 * 4 * 16 * 4;  // bytes per table
 };
+
+// Wide codes: each lane loads, per row of its k-tile, the dword holding its 4
+// codes (4*BITS bits at bit 4*BITS*n, read unaligned; the last lane's dword
+// is moved back inside the row), then extracts them with bit-field ops.
+template <int BITS>
+__device__ __forceinline__ int wide_byte(int n) {
+  return min((4 * BITS * n) >> 3, Fmt<BITS>::QB - 4);
+}
 
 // Lanes 2m and 2m+1 of a lane group need the codes of tokens 8m..8m+7 of a
 // row: 8*BITS bits starting at byte BITS*m.  The pair's word (1-bit: a byte,
@@ -91,6 +103,7 @@ __device__ __forceinline__ int pair_byte(int m) {
 }
 template <int BITS>
 __device__ __forceinline__ uint32_t pair_shift(int n) {
+  if constexpr (Fmt<BITS>::WIDE) return (uint32_t)(4 * BITS * n - 8 * wide_byte<BITS>(n));
   const int m = n >> 1;
   return (uint32_t)(8 * (BITS * m - pair_byte<BITS>(m)) + 4 * BITS * (n & 1));
 }
@@ -103,11 +116,11 @@ constexpr int LROW = TILE + 4;      // uint32 per head row of per-token arrays
 
 // Static LDS layout (bytes).  Per workgroup: the two (P, N) tables and the
 // query in two forms; per wave: the current tile's operands and weights.
-template <int NREP, int WAVES>
+template <int NREP, int WAVES, int TBLB>
 struct Smem {
   static constexpr int TBL_K = 0;
-  static constexpr int TBL_V = TBL;
-  static constexpr int Q16 = 2 * TBL;                 // fp16 [NREP][HROW*2]
+  static constexpr int TBL_V = TBLB;
+  static constexpr int Q16 = 2 * TBLB;                // fp16 [NREP][HROW*2]
   static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
   static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
   static constexpr int WAVE0 = ZERO + AROW * 4;
@@ -260,11 +273,21 @@ __device__ __forceinline__ void load_meta_tile(MetaWords<MW>& t, const Bufs& bf,
 // Key code words of a tile (issued once the previous tile's key words are
 // consumed: they land while the previous tile's P.V runs).
 template <int BITS>
-__device__ __forceinline__ void load_kw(uint32_t (&kw)[16], const Bufs& bf, int tile, int lane) {
+__device__ __forceinline__ void load_kw(uint32_t (&kw)[8 * Fmt<BITS>::WPK], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const int voff = (4 * g + (n & 1)) * F::QB + pair_byte<BITS>(n >> 1);
   const int soff = tile * D * F::QB;
+  if constexpr (F::WIDE) {
+    // kw[kt*4+ii] = the lane's dword of row 16kt+4g+ii
+    const int voff = 4 * g * F::QB + wide_byte<BITS>(n);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        kw[kt * 4 + ii] = __builtin_amdgcn_raw_buffer_load_b32(bf.kp, voff, soff + (16 * kt + ii) * F::QB, 0);
+    return;
+  }
+  const int voff = (4 * g + (n & 1)) * F::QB + pair_byte<BITS>(n >> 1);
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
@@ -274,11 +297,24 @@ __device__ __forceinline__ void load_kw(uint32_t (&kw)[16], const Bufs& bf, int 
 // Value code words of a tile (issued at the start of the tile: they land
 // while its Q.K runs).
 template <int BITS>
-__device__ __forceinline__ void load_vw(uint32_t (&vw)[16], const Bufs& bf, int tile, int lane) {
+__device__ __forceinline__ void load_vw(uint32_t (&vw)[8 * Fmt<BITS>::WPK], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + pair_byte<BITS>(n >> 1);
   const int soff = tile * TILE * NG * F::QB;
+  if constexpr (F::WIDE) {
+    // vw[(kt*NG+vg)*4+ii] = the lane's dword of token row 16kt+4g+ii, value group vg
+    const int voff = 4 * g * (NG * F::QB) + wide_byte<BITS>(n);
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          vw[(kt * NG + vg) * 4 + ii] = __builtin_amdgcn_raw_buffer_load_b32(
+              bf.vp, voff, soff + (16 * kt + ii) * (NG * F::QB) + F::QB * vg, 0);
+    return;
+  }
+  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + pair_byte<BITS>(n >> 1);
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -295,15 +331,27 @@ __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
 
 // The table addresses of one k-tile's B operands (4 rows ii of this lane's
 // k-slice x its 4 codes, jt = code index) from the two raw words w0, w1 of
-// the k-tile.  The codes are spread to bytes as table offsets 4*q + 64*group
-// (two ops per 4 codes); one v_perm per code then joins the offset (low byte)
-// with row ii's zero level (byte ii of zp, as the high byte: the table row
-// zl*256).  read_ktile() then fetches each (P, N) pair with one ds_read_b32
+// the k-tile (1-4 bits; wide codes: one dword per row).  The codes are spread
+// to bytes as table offsets 4*q + 64*group (two ops per 4 codes); one v_perm
+// per code then joins the offset (low byte) with row ii's zero level (byte ii
+// of zp, as the high byte: the table row zl*256).  read_ktile() then fetches each (P, N) pair with one ds_read_b32
 // straight into the operand register.  `odd` = lane n is odd.
 template <int BITS>
-__device__ __forceinline__ void addr_ktile(uint32_t w0, uint32_t w1, uint32_t zp, uint32_t grep, bool odd,
-                                           uint32_t sh, uint32_t (&ad)[4][4]) {
-  if constexpr (BITS == 3) {
+__device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint32_t grep, bool odd, uint32_t sh,
+                                           uint32_t (&ad)[4][4]) {
+  const uint32_t w0 = w[0], w1 = w[1];
+  if constexpr (Fmt<BITS>::WIDE) {
+    // w[ii]: the lane's dword of row ii; code jt at bit sh + BITS*jt; the
+    // table row of row ii's zero level starts at byte zl*256 (byte ii of zp
+    // moved to byte 1)
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const uint32_t row = __builtin_amdgcn_perm(zp, 0u, 0x0C0C000Cu | ((uint32_t)(4 + ii) << 8));
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt)
+        ad[jt][ii] = (__builtin_amdgcn_ubfe(w[ii], sh + BITS * jt, BITS) << 2) + row;
+    }
+  } else if constexpr (BITS == 3) {
     // w0 / w1: the pair's dword of rows (0 | 1) / (2 | 3); after the swap the
     // lane holds all four rows and takes its 12 bits (4 codes) from each at
     // bit sh, spread to bytes as table offsets 4*q + 64*group
@@ -386,8 +434,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   constexpr int WAVES = waves_for<NREP>();
   constexpr int NT = 64 * WAVES;  // threads per workgroup
   using M = Mfma<IO>;
-  using S = Smem<NREP, WAVES>;
   using F = Fmt<BITS>;
+  using S = Smem<NREP, WAVES, F::TBL>;
+  constexpr int TBL = F::TBL;
   constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
   static_assert(RS >= 2, "QK needs a second row per head for the low part of the key product");
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;   // head slots per lane of the MFMA output
@@ -446,9 +495,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   uint16_t qraw[QW];
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
-    const int i = min(threadIdx.x + j * NT, TBL / 4 - 1), zl = i >> 6, q = i & 15;
-    tk[j] = ftab_k[zl * 16 + q];
-    tv[j] = ftab_v[zl * 16 + q];
+    const int i = min(threadIdx.x + j * NT, TBL / 4 - 1);
+    // narrow: word i = (zl, group, q) of the 16 x 16 host table; wide: the
+    // host table's [zl][64] words as they are
+    const int src = F::WIDE ? i : (i >> 6) * 16 + (i & 15);
+    tk[j] = ftab_k[src];
+    tv[j] = ftab_v[src];
   }
 #pragma unroll
   for (int j = 0; j < QW; ++j) {
@@ -456,7 +508,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
     qraw[j] = i < NREP * D ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c] : 0;
   }
   MetaWords<MW> MT;              // metadata of the current tile
-  uint32_t KW[16], VW[16];       // key / value code words of the current tile
+  uint32_t KW[8 * F::WPK], VW[8 * F::WPK];  // key / value code words of the current tile
   load_meta_tile<MW>(MT, bf, min(tile_of(v0), q_last), lane);
   load_kw<BITS>(KW, bf, min(tile_of(v0), q_last), lane);
 #pragma unroll
@@ -677,9 +729,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Ac = *(const u32x4*)(a_hi_row + (4 * g) * 4);
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
-      addr_ktile<BITS>(KW[0], KW[1], kzp(0), grep, odd, lsh, adc);
+      addr_ktile<BITS>(KW, kzp(0), grep, odd, lsh, adc);
       read_ktile<S::TBL_K>(smem, adc, Bc);
-      addr_ktile<BITS>(KW[2], KW[3], kzp(1), grep, odd, lsh, adn);
+      addr_ktile<BITS>(KW + F::WPK, kzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         u32x4 An;
@@ -688,7 +740,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
           read_ktile<S::TBL_K>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (kt < 6) addr_ktile<BITS>(KW[2 * kt + 4], KW[2 * kt + 5], kzp(kt + 2), grep, odd, lsh, adn);
+        if (kt < 6) addr_ktile<BITS>(KW + F::WPK * (kt + 2), kzp(kt + 2), grep, odd, lsh, adn);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], s[jt]);
@@ -838,9 +890,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Ac = *(const u32x4*)(pv_row + 4 * g);
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
-      addr_ktile<BITS>(VW[0], VW[1], vzp(0), grep, odd, lsh, adc);
+      addr_ktile<BITS>(VW, vzp(0), grep, odd, lsh, adc);
       read_ktile<S::TBL_V>(smem, adc, Bc);
-      addr_ktile<BITS>(VW[2], VW[3], vzp(1), grep, odd, lsh, adn);
+      addr_ktile<BITS>(VW + F::WPK, vzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int st = 0; st < 4 * NG; ++st) {
         const int vg = st % NG;
@@ -851,7 +903,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
           read_ktile<S::TBL_V>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (st + 2 < 4 * NG) addr_ktile<BITS>(VW[2 * st + 4], VW[2 * st + 5], vzp(st + 2), grep, odd, lsh, adn);
+        if (st + 2 < 4 * NG) addr_ktile<BITS>(VW + F::WPK * (st + 2), vzp(st + 2), grep, odd, lsh, adn);
         scal_chunk(MN, st);  // the next tile's scalars, chunk st
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], acc[vg][jt]);
@@ -1026,8 +1078,11 @@ bool fold_supported(const mz_decode_args* a) {
   const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
-  return a->bits >= 1 && a->bits <= 4 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned &&
-         (a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || a->n_rep == 8) && a->fold_k && a->fold_v &&
+  // 5- and 6-bit tables (8 and 16 KB each) leave room for two workgroups per
+  // CU up to 4 query heads per kv-head; 8 heads take the general kernel there
+  const bool nrep_ok = a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || (a->n_rep == 8 && a->bits <= 4);
+  return a->bits >= 1 && a->bits <= 6 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
+         a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
          ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&
          a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 && a->vp_sh % 4 == 0 &&
@@ -1076,14 +1131,24 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
     case 8: MZ_FOLD(IOV, 8, BB); break;  \
     default: return MZ_EUNSUPPORTED;     \
   }
+#define MZ_FOLD_NREP_WIDE(IOV, BB)       \
+  switch (a->n_rep) {                    \
+    case 1: MZ_FOLD(IOV, 1, BB); break;  \
+    case 2: MZ_FOLD(IOV, 2, BB); break;  \
+    case 4: MZ_FOLD(IOV, 4, BB); break;  \
+    default: return MZ_EUNSUPPORTED;     \
+  }
 #define MZ_FOLD_BITS(IOV)                              \
   if (a->bits == 4) { MZ_FOLD_NREP(IOV, 4) }           \
   else if (a->bits == 3) { MZ_FOLD_NREP(IOV, 3) }      \
   else if (a->bits == 2) { MZ_FOLD_NREP(IOV, 2) }      \
   else if (a->bits == 1) { MZ_FOLD_NREP(IOV, 1) }      \
+  else if (a->bits == 5) { MZ_FOLD_NREP_WIDE(IOV, 5) } \
+  else if (a->bits == 6) { MZ_FOLD_NREP_WIDE(IOV, 6) } \
   else return MZ_EUNSUPPORTED;
   if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
 #undef MZ_FOLD_BITS
+#undef MZ_FOLD_NREP_WIDE
 #undef MZ_FOLD_NREP
 #undef MZ_FOLD
   const hipError_t e = hipGetLastError();

@@ -29,14 +29,15 @@ the reference:
     1..255, ``d`` in 0..bins (``muzero/quantizer.py:250-253``).
     Layout: ``E[(bins-1)*(bins+2)/2 + d]``.
 
-``fold4`` / ``fold2`` (4-bit / 2-bit decode attention)
+``fold1`` .. ``fold6`` (decode attention, 1- to 6-bit codes)
     For zero level ``zl`` and code ``q`` (``qmax = 2^bits - 1``), the pair
     ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
     as two fp16 packed in one uint32 (P in the low half), with
-    ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; a 16 x 16 array (row zl,
-    column q, zero beyond qmax).  The decode kernel rewrites the reference's
-    dequantization as ``a + bp*P + bn*N`` per group and looks these pairs up
-    per code.
+    ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; row zl, column q, zero
+    beyond qmax: 16 x 16 for 1-4 bits, (qmax+1) x 64 for 5 and 6 bits (the
+    layout the kernel keeps in LDS).  The decode kernel rewrites the
+    reference's dequantization as ``a + bp*P + bn*N`` per group and looks
+    these pairs up per code.
 
 These are constants of the format, the way the reference's own
 ``MU_ZERO_ALPHA2_COMPAND`` table is (``muzero/kernels/loader.py:133-150``);
@@ -140,11 +141,13 @@ def _expm1_row(bins: int) -> int:
 
 
 def _build_fold(alpha: float, bits: int) -> torch.Tensor:
-    """(P, N) pairs of the ``bits``-bit codes, zero-padded to 16 x 16 (row zl, column q)."""
+    """(P, N) pairs of the ``bits``-bit codes, zero-padded to 16 x 16 (1-4 bits) or
+    (qmax+1) x 64 (5 and 6 bits); row zl, column q."""
     e = host_table("expm1", alpha)
     qmax = (1 << bits) - 1
-    p = torch.zeros(16, 16, dtype=torch.float32)
-    nq = torch.zeros(16, 16, dtype=torch.float32)
+    rows, cols = (16, 16) if bits <= 4 else (qmax + 1, 64)
+    p = torch.zeros(rows, cols, dtype=torch.float32)
+    nq = torch.zeros(rows, cols, dtype=torch.float32)
     for zl in range(qmax + 1):
         pb, nb = max(qmax - zl, 1), max(zl, 1)
         for q in range(qmax + 1):
@@ -174,7 +177,7 @@ def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> tor
                 t = _build_expm1(alpha)
             elif kind == "fold4":
                 t = _build_fold(alpha, 4)
-            elif kind in ("fold1", "fold2", "fold3"):
+            elif kind in ("fold1", "fold2", "fold3", "fold5", "fold6"):
                 t = _build_fold(alpha, int(kind[-1]))
             else:
                 raise ValueError(kind)

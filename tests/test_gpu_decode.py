@@ -76,8 +76,9 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         am = torch.zeros(B, 1, 1, length, dtype=dtype).masked_fill_(~keep, torch.finfo(dtype).min)
         am_kernel = keep if mask == "bool" else am
     lq0 = ref.split_prefix(length, residual, 64)
-    fold = (kernel_path == "fold" or (kernel_path == "auto" and 1 <= bits <= 4 and d == 128
-                                      and n_rep in (1, 2, 4, 8) and lq0 > 0))
+    fold = (kernel_path == "fold" or (kernel_path == "auto" and d == 128 and lq0 > 0
+                                      and ((1 <= bits <= 4 and n_rep in (1, 2, 4, 8))
+                                           or (bits in (5, 6) and n_rep in (1, 2, 4)))))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
                                      dequant_dtype=torch.float32 if fold else None)
@@ -169,9 +170,9 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 4-bit and 2-bit, head_dim 128, n_rep in {1, 2, 4, 8}: the fold kernel (AUTO
-# picks it); the same cases through the exact-dequantize kernel keep that path
-# covered too.
+# 1- to 4-bit codes, head_dim 128, n_rep in {1, 2, 4, 8}, and 5- and 6-bit codes
+# with n_rep in {1, 2, 4}: the fold kernel (AUTO picks it); the same cases
+# through the exact-dequantize kernel keep that path covered too.
 FOLD_CASES = [
     # B, hkv, n_rep, d, length, bits, residual
     (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
@@ -198,6 +199,18 @@ FOLD_CASES = [
     (1, 2, 2, 128, 700, 1, 128),
     (1, 1, 8, 128, 700, 1, 128),
     (1, 2, 4, 128, 4096, 1, 128),
+    (2, 2, 4, 128, 1024, 5, 128),
+    (1, 2, 1, 128, 700, 5, 128),
+    (1, 2, 2, 128, 700, 5, 128),
+    (1, 2, 4, 128, 4096, 5, 128),
+    (2, 1, 4, 128, 300, 5, 0),
+    (1, 2, 4, 128, 900, 5, 191),
+    (2, 2, 4, 128, 1024, 6, 128),
+    (1, 2, 1, 128, 700, 6, 128),
+    (1, 2, 2, 128, 700, 6, 128),
+    (1, 2, 4, 128, 4096, 6, 128),
+    (2, 1, 4, 128, 300, 6, 0),
+    (1, 2, 4, 128, 900, 6, 191),
     (2, 1, 4, 128, 300, 1, 0),
 ]
 
@@ -262,14 +275,14 @@ def test_single_split_direct_output_matches_two_kernel_path(bits):
 @pytest.mark.parametrize("bits,d", [(5, 128), (8, 128), (4, 64), (7, 64)])
 def test_general_single_split_direct_output_matches_two_kernel_path(bits, d):
     """The general kernel with one split writes the output itself, bit-identical to its workspace +
-    combine path; 5-8 bits and head_dim 64 always take this kernel."""
+    combine path (7-8 bits and head_dim 64 always take this kernel; 5 bits through the exact path)."""
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(2, 2, 900, d, 8, seed=5)
     _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=3.0, group_size=64, residual=128)
     kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
               k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
               v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
-              alpha_key=2.0, alpha_value=3.0, scaling=d ** -0.5, n_split=1)
+              alpha_key=2.0, alpha_value=3.0, scaling=d ** -0.5, n_split=1, kernel_path="exact")
     plan = L.DecodePlan(q.to(DEV), **kw)
     assert plan.n_split == 1 and not plan.uses_fold
     direct = plan.run().clone()
