@@ -564,6 +564,13 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   const uint8_t* a_hi_row = rA == 0 ? W + S::AHI + hA * AROW * 4
                                     : (rA == 1 ? W + S::ALO + hA * AROW * 4 : smem + S::ZERO);
   const uint8_t* q16_row = rA == 0 ? smem + S::Q16 + hA * HROW * 4 : smem + S::ZERO;
+  // the constant part's A operand (the fp16 query on row 0 of each head's
+  // rows, zero elsewhere) is the same for every tile: kept in registers
+  // (wide codes, whose code words take twice the registers, re-read it)
+  u32x4 q16_op[4];
+#pragma unroll
+  for (int kq = 0; kq < 4; ++kq)
+    q16_op[kq] = F::WIDE ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2);
   const uint32_t* pv_row = (rA == 0 ? pa : pa_lo) + hA * LROW;  // PV A operand: this row's head
   const uint8_t* qio_row = rA == 0 ? smem + S::Q_IO + hA * HROW * 4 : smem + S::ZERO;
   const uint32_t grep = 0x40404040u * (uint32_t)g;  // this lane group's table copy
@@ -708,7 +715,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 A = *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2);
+        const u32x4 A = F::WIDE ? *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2) : q16_op[kq];
 #pragma unroll
         for (int part = 0; part < 2; ++part) {
           const u32x4 Bq = *(const u32x4*)(W + S::KA + (part * D + 32 * kq + 8 * g) * 2);
