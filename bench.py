@@ -387,6 +387,89 @@ def run_codec(args):
     print(json.dumps(line), flush=True)
 
 
+def run_split_launches(args):
+    """Config 1 through the reference's default decode path: the separate qk and av launches.
+
+    With MUZERO_FUSED_PREFIX_DECODE unset the reference decodes a layer as qk
+    over the packed key prefix (logits in the query dtype), torch logits of the
+    bf16 residual, an fp32 softmax cast to the query dtype, av over the packed
+    value prefix, and the residual's weighted sum (muzero/cache/attention.py:
+    179-295).  One step runs those steps with this library's muzero_qk /
+    muzero_av; qk and av are also timed alone, against their own algorithmic
+    bytes.  Same inputs as the default bench line (three rotating cache copies).
+    """
+    from muzero_amd.kernels import loader as Lo
+    dev = torch.device("cuda:0")
+    B, hkv, hq, d = args.batch, 8, 32, 128
+    n_rep = hq // hkv
+    L, R, bits = args.context, args.residual, args.bits
+    lq = max(L - R, 0) // 64 * 64
+    r = L - lq
+    k, v, q = make_inputs(B, hkv, hq, L, d, 1234, dev)
+    caches = [quantize_cache(k, v, bits, lq)]
+    for _ in range(args.copies - 1):
+        caches.append({k_: t.clone() for k_, t in caches[0].items()})
+    del k, v
+    scaling = d ** -0.5
+    logits = torch.empty(B, hq, lq, dtype=q.dtype, device=dev)
+    pre = torch.empty(B, hq, d, dtype=q.dtype, device=dev)
+    weights = torch.softmax(torch.randn(B, hq, lq, device=dev), -1).to(q.dtype)
+
+    def qk(i):
+        c = caches[i % len(caches)]
+        Lo.mu_zero_qk_cuda(q, c["k_packed"], c["k_mn"], c["k_scale"], logits, bits, 2.0, n_rep, scaling)
+
+    def av(i, w=None):
+        c = caches[i % len(caches)]
+        Lo.mu_zero_av_cuda(weights if w is None else w, c["v_packed"], c["v_mn"], c["v_scale"], pre, bits, 2.0,
+                           n_rep, 64)
+
+    def step(i):
+        c = caches[i % len(caches)]
+        qk(i)
+        dk = c["k_res"].repeat_interleave(n_rep, dim=1)
+        dense = (torch.matmul(q, dk.transpose(2, 3)) * scaling)[:, :, 0]
+        w = torch.softmax(torch.cat([logits, dense], -1), -1, dtype=torch.float32).to(q.dtype)
+        av(i, w[..., :lq].contiguous())
+        return pre + torch.matmul(w[..., lq:].unsqueeze(2), c["v_res"].repeat_interleave(n_rep, dim=1))[:, :, 0]
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        step(i)
+    ms_step = time_region(step, args.steps, stream)
+    ms_qk = time_region(qk, args.steps, stream)
+    ms_av = time_region(av, args.steps, stream)
+    qb = 8 * bits
+    qk_bytes = B * hkv * (lq // 64) * d * (qb + 4) + B * hq * d * 2 + B * hq * lq * 2
+    av_bytes = B * hkv * lq * ((d + 63) // 64) * (qb + 4) + B * hq * lq * 2 + B * hq * d * 2
+    nbytes = algorithmic_bytes(B, hkv, hq, d, lq, r, bits)
+    gbs = nbytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "packed-KV decode attn HBM GB/s (% of peak); decode tokens/sec at B=64 ctx 4096",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"cfg1 through the reference's default decode path (qk -> softmax -> av, separate "
+                               f"launches): B={B} Hq=32 Hkv=8 hd=128 ctx={L} mu_zero {bits}-bit G64 R={r}",
+                   "batch": B, "context": L, "bits": bits, "residual": r, "quantized_tokens": lq},
+        "kernels": {"qk": {"ms": round(ms_qk, 5), "algorithmic_bytes": qk_bytes,
+                           "frac_of_8TBs": round(qk_bytes / (ms_qk * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+                    "av": {"ms": round(ms_av, 5), "algorithmic_bytes": av_bytes,
+                           "frac_of_8TBs": round(av_bytes / (ms_av * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}},
+        "note": "value = the default bench line's algorithmic bytes over this path's step time; the step also "
+                "runs torch ops (residual logits, concatenation, softmax, casts, residual weighted sum)",
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration(mib, steps):
     """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
     calibrates the same counters on the decode kernel."""
@@ -420,6 +503,8 @@ def main():
                          "with per-group flushes (use with --batch 128 --bits 1|2|3|5)")
     ap.add_argument("--codec", action="store_true",
                     help="config 0: the quantize + dequantize round trip of one [1, 8, 1024, 128] K and V")
+    ap.add_argument("--split-launches", action="store_true",
+                    help="config 1 through the reference's default decode path: separate qk and av launches")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -434,6 +519,9 @@ def main():
         return
     if args.codec:
         run_codec(args)
+        return
+    if args.split_launches:
+        run_split_launches(args)
         return
 
     from muzero_amd.kernels.loader import DecodePlan

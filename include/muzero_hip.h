@@ -8,9 +8,10 @@
  * positive hipError_t of a failed launch).  Nothing here allocates device
  * memory; callers own every buffer.  Calls are thread-safe.  The library's
  * only mutable state is per device and process: each device's compute-unit
- * count and whether the general decode kernels' dynamic-LDS limit has been
- * raised on it, both filled on the first call on that device (idempotent, so
- * concurrent first calls are harmless).
+ * count and whether a kernel's dynamic-LDS limit has been raised on it (the
+ * general decode kernels, the qk / av kernels with more than 64 KB of LDS),
+ * filled on the first call on that device (idempotent, so concurrent first
+ * calls are harmless).
  *
  * Reference boundary being replaced: the pybind11 module returned by
  * load_mu_zero_cuda_extension() (muzero/kernels/loader.py:37-94, 1862-1880),
@@ -105,6 +106,58 @@ int muzero_dequantize_rows(const uint8_t* packed, int64_t nrows, int64_t packed_
                            int bits, const float* e_table, mz_stream_t stream);
 
 /*
+ * Logits of one query token per (batch, q-head) against a packed key prefix.
+ * Replaces: qk(query, packed_q, mn, scale, output, bits, alpha,
+ *   num_key_value_groups, scaling) (muzero/kernels/loader.py:46-49, host
+ *   :1360-1503, kernel :389-450), the first step of the reference's default
+ *   decode path (muzero/cache/attention.py:186-211).
+ * query [B, Hq, 1, D] (q_sb, q_sh; Hq = kv_heads * n_rep), packed_K
+ * [B, Hkv, >=n_groups, D, qb] (kp_sb, kp_sh in bytes, multiples of 8; the
+ * pointer 8-byte aligned), K_mn / K_scale [B, Hkv, >=n_groups, D] (km_sb,
+ * km_sh) -> logits [B, Hq, 64*n_groups] (o_sb, o_sh; last dim contiguous):
+ * logit = (sum_d q[d] * x[d]) * scaling, x the fp32 dequantized key (the
+ * reference's value exactly, muzero/quantizer.py:229-255, from the host-built
+ * expm1 table e_key), summed in fp32, rounded once to io_dtype.
+ * head_dim <= 256, n_rep <= 16 (else MZ_EUNSUPPORTED).
+ */
+typedef struct mz_qk_args {
+  int batch, kv_heads, n_rep, head_dim, bits, n_groups;
+  int meta_dtype, io_dtype;
+  float scaling;
+  const void* query; int64_t q_sb, q_sh;
+  const uint8_t* k_packed; int64_t kp_sb, kp_sh;
+  const void* k_mn; const void* k_scale; int64_t km_sb, km_sh;
+  const float* e_key;
+  void* logits; int64_t o_sb, o_sh;
+} mz_qk_args;
+int muzero_qk(const mz_qk_args* args, mz_stream_t stream);
+
+/*
+ * Attention-weighted sum of a packed value prefix.
+ * Replaces: av(attn_weights, packed_q, mn, scale, output, bits, alpha,
+ *   num_key_value_groups, group_size) (muzero/kernels/loader.py:50-53, host
+ *   :1505-1687, kernel :677-751), the third step of the reference's default
+ *   decode path (muzero/cache/attention.py:248-272).
+ * weights [B, Hq, n_tokens] (w_sb, w_sh; last dim contiguous; io_dtype),
+ * packed_V [B, Hkv, >=n_tokens, ng, qb] (vp_sb, vp_sh in bytes, multiples of
+ * 8; the pointer 8-byte aligned; ng = ceil(head_dim / 64)), V_mn / V_scale
+ * [B, Hkv, >=n_tokens, ng] (vm_sb, vm_sh) -> out [B, Hq, head_dim] (o_sb,
+ * o_sh): out = sum_t w[t] * x[t], x the fp32 dequantized value, summed in
+ * fp32 (deterministically: no atomics), rounded once to io_dtype.
+ * head_dim <= 256, n_rep <= 16 (else MZ_EUNSUPPORTED).
+ */
+typedef struct mz_av_args {
+  int batch, kv_heads, n_rep, head_dim, bits, n_tokens;
+  int meta_dtype, io_dtype;
+  const void* weights; int64_t w_sb, w_sh;
+  const uint8_t* v_packed; int64_t vp_sb, vp_sh;
+  const void* v_mn; const void* v_scale; int64_t vm_sb, vm_sh;
+  const float* e_value;
+  void* out; int64_t o_sb, o_sh;
+} mz_av_args;
+int muzero_av(const mz_av_args* args, mz_stream_t stream);
+
+/*
  * Decode attention of one query token per (batch, q-head) over a packed
  * key/value prefix of 64*n_groups tokens followed by n_residual dense tokens.
  * Replaces the decode hook's quantized path: qk + softmax + av + dense
@@ -135,11 +188,12 @@ typedef struct mz_decode_args {
   const void* v_res; int64_t vr_sb, vr_sh, vr_st;
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
-  /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 4): 16 x 16
-   * pairs of fp16 (P, N) packed in uint32 (P in the low half), row = zero
-   * level, column = code, zero beyond 2^bits - 1; see muzero_amd/tables.py
-   * ("fold1" .. "fold4").  Needed by the fold fast path; may be null (the
-   * generic path is used then). */
+  /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 6): pairs of
+   * fp16 (P, N) packed in uint32 (P in the low half), row = zero level,
+   * column = code; 16 x 16 for bits 1 to 4 (zero beyond 2^bits - 1),
+   * 2^bits x 64 for 5 and 6 bits; see muzero_amd/tables.py ("fold1" ..
+   * "fold6").  Needed by the fold fast path; may be null (the generic path
+   * is used then). */
   const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;
@@ -160,8 +214,9 @@ typedef struct mz_decode_args {
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 1 to 4, head_dim 128, n_rep in {1,2,4,8}, fold tables given)
- * and the exact-dequantize kernel otherwise. */
+ * applies (bits 1 to 6, head_dim 128, aligned prefixes, n_rep in {1,2,4,8}
+ * for 1 to 4 bits and {1,2,4} for 5 and 6, fold tables given) and the
+ * exact-dequantize kernel otherwise. */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments

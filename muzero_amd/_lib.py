@@ -55,6 +55,35 @@ class DecodeArgs(ctypes.Structure):
         ("v_prefix", c_int),
     ]
 
+class QkArgs(ctypes.Structure):
+    """Mirror of ``mz_qk_args`` (include/muzero_hip.h)."""
+
+    _fields_ = [
+        ("batch", c_int), ("kv_heads", c_int), ("n_rep", c_int), ("head_dim", c_int), ("bits", c_int),
+        ("n_groups", c_int), ("meta_dtype", c_int), ("io_dtype", c_int),
+        ("scaling", c_float),
+        ("query", c_vp), ("q_sb", c_i64), ("q_sh", c_i64),
+        ("k_packed", c_vp), ("kp_sb", c_i64), ("kp_sh", c_i64),
+        ("k_mn", c_vp), ("k_scale", c_vp), ("km_sb", c_i64), ("km_sh", c_i64),
+        ("e_key", c_vp),
+        ("logits", c_vp), ("o_sb", c_i64), ("o_sh", c_i64),
+    ]
+
+
+class AvArgs(ctypes.Structure):
+    """Mirror of ``mz_av_args`` (include/muzero_hip.h)."""
+
+    _fields_ = [
+        ("batch", c_int), ("kv_heads", c_int), ("n_rep", c_int), ("head_dim", c_int), ("bits", c_int),
+        ("n_tokens", c_int), ("meta_dtype", c_int), ("io_dtype", c_int),
+        ("weights", c_vp), ("w_sb", c_i64), ("w_sh", c_i64),
+        ("v_packed", c_vp), ("vp_sb", c_i64), ("vp_sh", c_i64),
+        ("v_mn", c_vp), ("v_scale", c_vp), ("vm_sb", c_i64), ("vm_sh", c_i64),
+        ("e_value", c_vp),
+        ("out", c_vp), ("o_sb", c_i64), ("o_sh", c_i64),
+    ]
+
+
 class PrologueArgs(ctypes.Structure):
     """Mirror of ``mz_prologue_args`` (include/muzero_hip.h)."""
 
@@ -90,6 +119,8 @@ SIGNATURES = {
                                        c_int, c_float, c_vp, c_vp]),
     "muzero_dequantize_rows": (c_int, [c_vp, c_i64, c_i64, c_vp, c_vp, c_int, c_i64, c_vp, c_int, c_i64,
                                        c_int, c_vp, c_vp]),
+    "muzero_qk": (c_int, [ctypes.POINTER(QkArgs), c_vp]),
+    "muzero_av": (c_int, [ctypes.POINTER(AvArgs), c_vp]),
     "muzero_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(c_int)]),
     "muzero_decode_attention": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_uses_fold": (c_int, [ctypes.POINTER(DecodeArgs)]),

@@ -1,4 +1,4 @@
-// Packed-KV decode attention, fast path for 1- to 4-bit codes (gfx950, wave64).
+// Packed-KV decode attention, fast path for 1- to 6-bit codes (gfx950, wave64).
 //
 // Dequantization folded into the MFMA operands.  For a group with stored
 // (mn, s) the reference dequantizes code q as (muzero/quantizer.py:241-255)

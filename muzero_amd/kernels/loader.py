@@ -5,8 +5,9 @@ Reference: ``muzero/kernels/loader.py`` exposes a pybind11 extension built with
 ``mu_zero_dequantize_cuda``, ``mu_zero_qk_cuda``, ``mu_zero_av_cuda``
 (``:1883-1911``).  Here the same names call ``libmuzero_hip.so`` through its C
 ABI (``include/muzero_hip.h``) on torch's current HIP stream.  The separate
-qk/softmax/av launches of the reference are replaced by one fused decode
-(:func:`mu_zero_decode_attention_hip`), which the cache's attention hook uses.
+qk and av launches are kept for callers of the reference's API; the cache's
+attention hook runs qk + softmax + av + the residual merge as one fused
+decode (:func:`mu_zero_decode_attention_hip`).
 
 Every function validates shapes, dtypes, devices and strides on the host
 before launching and raises :class:`MuZeroHipError` on any problem; there is
@@ -407,11 +408,104 @@ def mu_zero_decode_attention_hip(query: torch.Tensor, **kwargs) -> torch.Tensor:
     return DecodePlan(query, **kwargs).run()
 
 
-def mu_zero_qk_cuda(*args, **kwargs):  # pragma: no cover - documented gap
-    raise MuZeroHipError("separate qk launch is not built: the decode hook uses the fused "
-                         "mu_zero_decode_attention_hip (qk+softmax+av in one pass)")
+# --------------------------------------------------------------------------- separate qk / av
+
+def _meta4(t: torch.Tensor, name: str) -> torch.Tensor:
+    """Metadata as the 4-d view the ABI takes: the cache's ``[..., 1]`` form loses its last dim."""
+    if t.dim() == 5:
+        _require(t.shape[4] == 1, f"{name} must be [B, H, N, K] or [B, H, N, K, 1]")
+        t = t[..., 0]
+    _require(t.dim() == 4 and t.dtype in DTYPE_ENUM, f"{name} must be a 4-d (or [..., 1]) float tensor")
+    return t
 
 
-def mu_zero_av_cuda(*args, **kwargs):  # pragma: no cover - documented gap
-    raise MuZeroHipError("separate av launch is not built: the decode hook uses the fused "
-                         "mu_zero_decode_attention_hip (qk+softmax+av in one pass)")
+def mu_zero_qk_cuda(query: torch.Tensor, packed_q: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor,
+                    output: torch.Tensor, bits: int, alpha: float, num_key_value_groups: int,
+                    scaling: float) -> None:
+    """Logits of ``query [B, Hq, 1, D]`` against a packed key prefix, in place into ``output [B, Hq, 64*G]``.
+
+    Reference ``loader.py:1891`` (host ``:1360-1503``, kernel ``:389-450``):
+    ``packed_q [B, Hkv, G, D, 8*bits]``, ``mn / scale [B, Hkv, G, D(, 1)]``;
+    ``output = (query . dequantized keys) * scaling`` in the query dtype, the
+    keys dequantized in fp32.  Tensors may be views into larger storage along
+    the batch / head / group axes (the group axis may hold more than G groups,
+    G = ``output.shape[2] / 64``); the last axes are contiguous.
+    """
+    dev = _on_gpu(query, packed_q, mn, scale, output)
+    _require(query.dim() == 4 and query.shape[2] == 1 and query.dtype in DTYPE_ENUM and query.stride(3) == 1,
+             "query must be [B, Hq, 1, D] with a contiguous last dim")
+    b, hq, _, d = query.shape
+    qb = _qbytes(bits)
+    _require(packed_q.dtype == torch.uint8 and packed_q.dim() == 5 and packed_q.shape[0] == b
+             and tuple(packed_q.shape[3:]) == (d, qb), "packed_q must be uint8 [B, Hkv, G, D, 8*bits]")
+    _require(packed_q.stride(4) == 1 and packed_q.stride(3) == qb and packed_q.stride(2) == d * qb,
+             "packed_q: each head's groups must be contiguous [G, D, 8*bits]")
+    hkv = packed_q.shape[1]
+    _require(int(num_key_value_groups) >= 1 and hq == hkv * int(num_key_value_groups),
+             "query heads must equal kv heads * num_key_value_groups")
+    mn_, sc_ = _meta4(mn, "mn"), _meta4(scale, "scale")
+    _require(mn_.shape == sc_.shape and mn_.shape[:2] == (b, hkv) and mn_.shape[3] == d
+             and mn_.dtype == sc_.dtype and mn_.stride() == sc_.stride()
+             and mn_.stride(3) == 1 and mn_.stride(2) == d, "mn / scale must be [B, Hkv, G, D] alike")
+    _require(output.dim() == 3 and output.shape[:2] == (b, hq) and output.shape[2] % GROUP == 0
+             and output.dtype == query.dtype and output.stride(2) == 1,
+             "output must be [B, Hq, 64*G] in the query dtype with a contiguous last dim")
+    n_groups = output.shape[2] // GROUP
+    _require(n_groups <= packed_q.shape[2] and n_groups <= mn_.shape[2], "output covers more groups than stored")
+    e = tables.device_table("expm1", alpha, dev)
+    a = _lib.QkArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = b, hkv, int(num_key_value_groups), d, int(bits)
+    a.n_groups, a.meta_dtype, a.io_dtype, a.scaling = n_groups, DTYPE_ENUM[mn_.dtype], DTYPE_ENUM[query.dtype], \
+        float(scaling)
+    a.query, a.q_sb, a.q_sh = ptr(query), query.stride(0), query.stride(1)
+    a.k_packed, a.kp_sb, a.kp_sh = ptr(packed_q), packed_q.stride(0), packed_q.stride(1)
+    a.k_mn, a.k_scale, a.km_sb, a.km_sh = ptr(mn_), ptr(sc_), mn_.stride(0), mn_.stride(1)
+    a.e_key = ptr(e)
+    a.logits, a.o_sb, a.o_sh = ptr(output), output.stride(0), output.stride(1)
+    check(load().muzero_qk(ctypes.byref(a), stream_ptr(dev)), "muzero_qk")
+
+
+def mu_zero_av_cuda(attn_weights: torch.Tensor, packed_q: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor,
+                    output: torch.Tensor, bits: int, alpha: float, num_key_value_groups: int,
+                    group_size: int) -> None:
+    """Weighted sum of a packed value prefix, in place into ``output [B, Hq, D]``.
+
+    Reference ``loader.py:1910`` (host ``:1505-1687``, kernel ``:677-751``):
+    ``attn_weights [B, Hq, T]``, ``packed_q [B, Hkv, T, ng, 8*bits]``,
+    ``mn / scale [B, Hkv, T, ng(, 1)]`` with ``ng = ceil(D / 64)``;
+    ``output = attn_weights @ dequantized values`` in the weights' dtype, the
+    values dequantized in fp32 and the sum kept in fp32.  The token axis of
+    the packed tensors may be longer than T (preallocated storage).
+    """
+    dev = _on_gpu(attn_weights, packed_q, mn, scale, output)
+    _require(int(group_size) == GROUP, "the HIP path is built for q_group_size 64")
+    _require(attn_weights.dim() == 3 and attn_weights.dtype in DTYPE_ENUM and attn_weights.stride(2) == 1,
+             "attn_weights must be [B, Hq, T] with a contiguous last dim")
+    b, hq, t = attn_weights.shape
+    _require(output.dim() == 3 and output.shape[:2] == (b, hq) and output.dtype == attn_weights.dtype
+             and output.stride(2) == 1, "output must be [B, Hq, D] in the weights' dtype")
+    d = output.shape[2]
+    ng = (d + GROUP - 1) // GROUP
+    qb = _qbytes(bits)
+    _require(packed_q.dtype == torch.uint8 and packed_q.dim() == 5 and packed_q.shape[0] == b
+             and packed_q.shape[2] >= t and tuple(packed_q.shape[3:]) == (ng, qb),
+             "packed_q must be uint8 [B, Hkv, >=T, ceil(D/64), 8*bits]")
+    _require(packed_q.stride(4) == 1 and packed_q.stride(3) == qb and packed_q.stride(2) == ng * qb,
+             "packed_q: each head's tokens must be contiguous [T, ng, 8*bits]")
+    hkv = packed_q.shape[1]
+    _require(int(num_key_value_groups) >= 1 and hq == hkv * int(num_key_value_groups),
+             "query heads must equal kv heads * num_key_value_groups")
+    mn_, sc_ = _meta4(mn, "mn"), _meta4(scale, "scale")
+    _require(mn_.shape == sc_.shape and mn_.shape[:2] == (b, hkv) and mn_.shape[2] >= t and mn_.shape[3] == ng
+             and mn_.dtype == sc_.dtype and mn_.stride() == sc_.stride()
+             and mn_.stride(3) == 1 and mn_.stride(2) == ng, "mn / scale must be [B, Hkv, >=T, ng] alike")
+    e = tables.device_table("expm1", alpha, dev)
+    a = _lib.AvArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = b, hkv, int(num_key_value_groups), d, int(bits)
+    a.n_tokens, a.meta_dtype, a.io_dtype = t, DTYPE_ENUM[mn_.dtype], DTYPE_ENUM[attn_weights.dtype]
+    a.weights, a.w_sb, a.w_sh = ptr(attn_weights), attn_weights.stride(0), attn_weights.stride(1)
+    a.v_packed, a.vp_sb, a.vp_sh = ptr(packed_q), packed_q.stride(0), packed_q.stride(1)
+    a.v_mn, a.v_scale, a.vm_sb, a.vm_sh = ptr(mn_), ptr(sc_), mn_.stride(0), mn_.stride(1)
+    a.e_value = ptr(e)
+    a.out, a.o_sb, a.o_sh = ptr(output), output.stride(0), output.stride(1)
+    check(load().muzero_av(ctypes.byref(a), stream_ptr(dev)), "muzero_av")

@@ -317,6 +317,42 @@ def decode_attention_literal(query: torch.Tensor, key_prefix: torch.Tensor, valu
     return out.transpose(1, 2).contiguous()
 
 
+def prefix_logits(query: torch.Tensor, pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor, bits: int,
+                  alpha: float, n_rep: int, scaling: float, group_size: int = 64) -> torch.Tensor:
+    """The reference's qk launch (loader.py:46-49, kernel :389-450), before its output rounding.
+
+    ``query [B,Hq,1,hd]``, packed keys ``[B,Hkv,nsg,hd,qb]`` with ``mn/scale
+    [B,Hkv,nsg,hd(,1)]``.  Query head ``h`` reads kv-head ``h // n_rep``
+    (:409); the logit of token ``64*g + t`` is ``sum_d q[d] * x[g][d][t] *
+    scaling`` (:414-441) with ``x`` the fp32 dequantized key (its codebook is
+    fp32, :197-263).  Returns ``[B,Hq,nsg*G]`` float64; the kernel rounds it to
+    the query dtype (:440-441).
+    """
+    keys = dequantize_key_block(pq, mn.reshape(pq.shape[:4]), sc.reshape(pq.shape[:4]), bits, alpha,
+                                group_size, torch.float32)
+    k = repeat_kv(keys.double(), n_rep)
+    return torch.matmul(query.double(), k.transpose(2, 3))[:, :, 0, :] * scaling
+
+
+def prefix_weighted_values(weights: torch.Tensor, pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor,
+                           bits: int, alpha: float, n_rep: int, head_dim: int,
+                           group_size: int = 64) -> torch.Tensor:
+    """The reference's av launch (loader.py:50-53, kernel :677-751), before its output rounding.
+
+    ``weights [B,Hq,T]``, packed values ``[B,Hkv,T,ng,qb]`` with ``mn/scale
+    [B,Hkv,T,ng(,1)]``.  Output channel ``c`` of query head ``h`` is ``sum_t
+    w[h][t] * x[t][c]`` (:705-737) over kv-head ``h // n_rep`` (:700) with
+    ``x`` the fp32 dequantized value; channels past ``head_dim`` (the value
+    groups' zero padding) are not written (:696).  Returns ``[B,Hq,hd]``
+    float64; the kernel rounds it to the weights' dtype (:742).
+    """
+    b, h, t, ng, qb = pq.shape
+    vals = dequantize_value_block(pq, mn.reshape(b, h, t, ng), sc.reshape(b, h, t, ng), bits, alpha,
+                                  group_size, head_dim, torch.float32)
+    v = repeat_kv(vals.double(), n_rep)
+    return torch.matmul(weights.double().unsqueeze(2), v)[:, :, 0, :]
+
+
 # ---------------------------------------------------------------------------
 # Cache-level convenience used by the parity tests and the CPU baseline
 # ---------------------------------------------------------------------------

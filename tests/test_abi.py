@@ -50,7 +50,8 @@ def test_version_and_strerror():
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-@pytest.mark.parametrize("cls,cname", [(_lib.DecodeArgs, "mz_decode_args"), (_lib.PrologueArgs, "mz_prologue_args")])
+@pytest.mark.parametrize("cls,cname", [(_lib.DecodeArgs, "mz_decode_args"), (_lib.PrologueArgs, "mz_prologue_args"),
+                                       (_lib.QkArgs, "mz_qk_args"), (_lib.AvArgs, "mz_av_args")])
 def test_args_layout_matches_c(tmp_path, cls, cname):
     fields = [f for f, _ in cls._fields_]
     src = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {",
@@ -100,3 +101,27 @@ def test_noalloc_rejects_partials_beyond_the_scratch_without_a_device():
     assert ns.value == 64 and need == 64 * 32 * 64 * 130 * 4 > _lib.MZ_DECODE_SCRATCH_BYTES
     assert lib.muzero_decode_attention_noalloc(ctypes.byref(a), None) == _lib.MZ_ESCRATCH
     assert b"scratch" in lib.muzero_strerror(_lib.MZ_ESCRATCH)
+
+
+def test_qk_av_reject_bad_args_without_a_device():
+    """muzero_qk / muzero_av validate on the host: bad bits, n_rep and head_dim are rejected
+    before any launch, and an empty call returns 0 without touching a device."""
+    lib = _lib.load()
+    a = _lib.QkArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits, a.n_groups = 1, 1, 4, 128, 9, 1
+    assert lib.muzero_qk(ctypes.byref(a), None) == -1
+    a.bits, a.n_rep = 4, 17
+    assert lib.muzero_qk(ctypes.byref(a), None) == -2
+    a.n_rep, a.head_dim = 4, 512
+    assert lib.muzero_qk(ctypes.byref(a), None) == -2
+    a.head_dim, a.n_groups = 128, 0
+    assert lib.muzero_qk(ctypes.byref(a), None) == 0
+    a.n_groups = 1  # null pointers with work to do
+    assert lib.muzero_qk(ctypes.byref(a), None) == -1
+    v = _lib.AvArgs()
+    v.batch, v.kv_heads, v.n_rep, v.head_dim, v.bits, v.n_tokens = 1, 1, 4, 128, 0, 5
+    assert lib.muzero_av(ctypes.byref(v), None) == -1
+    v.bits, v.head_dim = 4, 300
+    assert lib.muzero_av(ctypes.byref(v), None) == -2
+    v.head_dim, v.batch = 128, 0
+    assert lib.muzero_av(ctypes.byref(v), None) == 0

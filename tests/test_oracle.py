@@ -302,3 +302,68 @@ def test_attention_oracle_brute_force():
             z = sum(w)
             o = sum(wi / z * v[b, kv, t].double() for t, wi in enumerate(w))
             assert torch.allclose(out[b, 0, h], o, atol=1e-12)
+
+
+# ------------------------------------------------------- separate qk / av launches
+
+def _rows_fp32(pq, mn, sc, bits, alpha):
+    """Dequantize a block of rows one row at a time through the fixture-pinned row dequantizer."""
+    flat = pq.reshape(-1, pq.shape[-1])
+    out = [ref.dequantize_rows(flat[i:i + 1], mn.reshape(-1, 1)[i:i + 1], sc.reshape(-1, 1)[i:i + 1], bits,
+                               alpha, 64, torch.float32)[0] for i in range(flat.shape[0])]
+    return torch.stack(out).reshape(*pq.shape[:-1], 64)
+
+
+@pytest.mark.parametrize("bits,n_rep,hd", [(4, 2, 6), (3, 1, 5), (7, 3, 4)])
+def test_prefix_logits_brute_force(bits, n_rep, hd):
+    """prefix_logits against an explicit loop: query head h reads kv-head h // n_rep, token
+    64*g + t of group g is column t of channel rows (g, 0..hd-1)."""
+    g = torch.Generator().manual_seed(bits)
+    hkv, nsg = 2, 2
+    keys = torch.randn(1, hkv, 64 * nsg, hd, generator=g) + 0.3
+    q = torch.randn(1, hkv * n_rep, 1, hd, generator=g)
+    pk, kmn, ksc = ref.quantize_key_block(keys, bits, 2.0)
+    got = ref.prefix_logits(q, pk, kmn, ksc, bits, 2.0, n_rep, 0.5)
+    rows = _rows_fp32(pk, kmn, ksc, bits, 2.0)  # [1, hkv, nsg, hd, 64]
+    assert got.shape == (1, hkv * n_rep, 64 * nsg)
+    for h in range(hkv * n_rep):
+        for gi in range(nsg):
+            for t in range(64):
+                s = sum(float(q[0, h, 0, d]) * float(rows[0, h // n_rep, gi, d, t]) for d in range(hd))
+                assert abs(float(got[0, h, 64 * gi + t]) - 0.5 * s) < 1e-12 * (1 + abs(s))
+
+
+@pytest.mark.parametrize("bits,n_rep,hd,t", [(2, 2, 70, 5), (5, 1, 64, 3), (8, 4, 20, 4)])
+def test_prefix_weighted_values_brute_force(bits, n_rep, hd, t):
+    """prefix_weighted_values against an explicit loop: channel c of token s is code c - 64*j
+    of value row (s, j = c // 64); padding channels past hd are dropped."""
+    g = torch.Generator().manual_seed(10 + bits)
+    hkv = 2
+    vals = torch.randn(1, hkv, t, hd, generator=g) - 0.2
+    w = torch.rand(1, hkv * n_rep, t, generator=g)
+    pv, vmn, vsc = ref.quantize_value_block(vals, bits, 2.0)
+    got = ref.prefix_weighted_values(w, pv, vmn, vsc, bits, 2.0, n_rep, hd)
+    rows = _rows_fp32(pv, vmn, vsc, bits, 2.0)  # [1, hkv, t, ng, 64]
+    assert got.shape == (1, hkv * n_rep, hd)
+    for h in range(hkv * n_rep):
+        for c in range(hd):
+            s = sum(float(w[0, h, s_]) * float(rows[0, h // n_rep, s_, c // 64, c % 64]) for s_ in range(t))
+            assert abs(float(got[0, h, c]) - s) < 1e-12 * (1 + abs(s))
+
+
+def test_qk_softmax_av_composes_to_decode_attention():
+    """softmax(prefix_logits) through prefix_weighted_values is the brute-force-pinned
+    decode_attention_exact over the fp32-dequantized prefix (no residual)."""
+    g = torch.Generator().manual_seed(77)
+    b, hkv, n_rep, length, hd = 2, 2, 4, 192, 64
+    keys = torch.randn(b, hkv, length, hd, generator=g)
+    vals = torch.randn(b, hkv, length, hd, generator=g)
+    q = torch.randn(b, hkv * n_rep, 1, hd, generator=g)
+    pk, kmn, ksc = ref.quantize_key_block(keys, 3, 2.0)
+    pv, vmn, vsc = ref.quantize_value_block(vals, 3, 2.0)
+    logits = ref.prefix_logits(q, pk, kmn, ksc, 3, 2.0, n_rep, hd ** -0.5)
+    out = ref.prefix_weighted_values(torch.softmax(logits, -1), pv, vmn, vsc, 3, 2.0, n_rep, hd)
+    kq = ref.dequantize_key_block(pk, kmn, ksc, 3, 2.0, 64, torch.float32)
+    vq = ref.dequantize_value_block(pv, vmn, vsc, 3, 2.0, 64, hd, torch.float32)
+    exact = ref.decode_attention_exact(q, kq, vq, None, hd ** -0.5)[:, 0]
+    assert torch.allclose(out, exact, atol=1e-12, rtol=0)
