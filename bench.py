@@ -470,6 +470,19 @@ def run_split_launches(args):
     print(json.dumps(line), flush=True)
 
 
+def measured_copy_gbs(mib, steps):
+    """Bytes read + written per second by a plain device-to-device copy of `mib` MiB (a
+    streaming kernel's attainable HBM rate on this box, reported beside the 8 TB/s peak)."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    dst.copy_(src)
+    ms = time_region(lambda i: dst.copy_(src), steps, stream)
+    del src, dst
+    return 2 * n / (ms * 1e-3) / 1e9
+
+
 def copy_calibration(mib, steps):
     """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
     calibrates the same counters on the decode kernel."""
@@ -558,6 +571,7 @@ def main():
     nbytes = algorithmic_bytes(B, hkv, hq, d, lq, r, bits)
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     gbs_split = nbytes / (ms_kernel * 1e-3) / 1e9
+    copy_gbs = measured_copy_gbs(1024, 10)
 
     traffic = None
     if os.path.exists(args.traffic_json):
@@ -610,7 +624,9 @@ def main():
         "n_split": plans[0].n_split,
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes": nbytes},
+                     "algorithmic_bytes": nbytes,
+                     "measured_copy_GBps": round(copy_gbs, 1),
+                     "frac_of_measured_copy": round(gbs_split / copy_gbs, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
