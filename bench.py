@@ -427,8 +427,8 @@ def run_split_launches(args):
     def step(i):
         c = caches[i % len(caches)]
         qk(i)
-        dk = c["k_res"].repeat_interleave(n_rep, dim=1)
-        dense = (torch.matmul(q, dk.transpose(2, 3)) * scaling)[:, :, 0]
+        dkt = c["k_res"].repeat_interleave(n_rep, dim=1).transpose(2, 3).contiguous()
+        dense = (torch.matmul(q, dkt) * scaling)[:, :, 0]
         w = torch.softmax(torch.cat([logits, dense], -1), -1, dtype=torch.float32).to(q.dtype)
         av(i, w[..., :lq].contiguous())
         return pre + torch.matmul(w[..., lq:].unsqueeze(2), c["v_res"].repeat_interleave(n_rep, dim=1))[:, :, 0]

@@ -24,6 +24,11 @@ prefix decode with the residual merged in); plus ``hip_fused_decode`` for
 every call the kernel serves.  When the launch raises, the matching
 ``*_fallback`` counters are incremented as in the reference, and the error
 propagates: this build has no dequantize-then-attend fallback to run instead.
+
+Shapes the fused kernels do not take (head_dim other than 64 / 128, fp32
+queries) run the reference's default path itself: the separate ``qk`` / ``av``
+launches (``muzero_qk`` / ``muzero_av``) around a torch softmax and the
+residual matmuls, counted as ``fused_qk_success`` / ``fused_av_success``.
 """
 
 from __future__ import annotations
@@ -85,6 +90,17 @@ def mu_zero_decode_attention_forward(
     alpha_key = float(layer._selected_alpha_key if layer._selected_alpha_key is not None else 2.0)
     alpha_value = float(layer._selected_alpha_value if layer._selected_alpha_value is not None else 2.0)
     r = int(keys.shape[2]) if has_res else 0
+    if not _fused_shape(query, module):
+        try:
+            out = _split_launches(layer, module, query, attention_mask, float(scaling), key_prefix_length,
+                                  value_prefix_length, keys if has_res else None, values if has_res else None,
+                                  alpha_key, alpha_value)
+        except Exception:
+            _count_split(key_prefix_length, value_prefix_length, "fallback")
+            raise
+        _count_split(key_prefix_length, value_prefix_length, "success")
+        _MU_ZERO_DECODE_STATS["returns"] += 1
+        return out, None
     # Decode steps of one layer differ only in the query, the prefix and
     # residual lengths and the output: once the arguments have been built and
     # validated for a layer's storage, later steps only patch those fields.
@@ -116,6 +132,61 @@ def _count(key_prefix_length: int, value_prefix_length: int, outcome: str) -> No
             _MU_ZERO_DECODE_STATS["fused_prefix_decode_chunked_success"] += 1
     if value_prefix_length > 0:
         _MU_ZERO_DECODE_STATS[f"fused_av_{outcome}"] += 1
+
+
+def _fused_shape(query: torch.Tensor, module) -> bool:
+    """Whether the fused decode kernels take this call: head_dim 64 or 128, bf16 / fp16
+    queries, at most 16 query heads per kv-head.  Other shapes run the separate launches."""
+    n_rep = int(getattr(module, "num_key_value_groups", 1))
+    return query.shape[-1] in (64, 128) and query.dtype in (torch.bfloat16, torch.float16) and n_rep <= 16
+
+
+def _count_split(key_prefix_length: int, value_prefix_length: int, outcome: str) -> None:
+    """The reference's counters for its default path: one qk and one av launch."""
+    if key_prefix_length > 0:
+        _MU_ZERO_DECODE_STATS[f"fused_qk_{outcome}"] += 1
+    if value_prefix_length > 0:
+        _MU_ZERO_DECODE_STATS[f"fused_av_{outcome}"] += 1
+
+
+def _split_launches(layer, module, query, attention_mask, scaling, key_prefix_length, value_prefix_length,
+                    keys, values, alpha_key, alpha_value):
+    """The reference's default decode (``attention.py:179-295``) for shapes the fused kernels
+    do not take (head_dim other than 64 / 128, fp32 queries): ``muzero_qk`` writes the packed
+    prefix's logits in the query dtype, the residual's logits are a torch matmul, the softmax
+    runs in fp32 and is cast to the query dtype, ``muzero_av`` sums the packed values and a
+    torch matmul the residual's.  head_dim up to 256, up to 16 query heads per kv-head."""
+    b, hq, _, d = query.shape
+    n_rep = int(module.num_key_value_groups)
+    r_k = 0 if keys is None else int(keys.shape[2])
+    length = key_prefix_length + r_k
+    mask = _k.prepare_mask(attention_mask, b, length)
+    parts = []
+    if key_prefix_length > 0:
+        logits = torch.empty((b, hq, key_prefix_length), dtype=query.dtype, device=query.device)
+        _k.mu_zero_qk_cuda(query, layer._packed_key_q, layer._key_mn, layer._key_scale, logits, layer.nbits,
+                           alpha_key, n_rep, scaling)
+        parts.append(logits)
+    if r_k > 0:
+        # the right operand is made contiguous: batched half-precision products over a
+        # transposed view are avoided
+        dense_kt = keys.repeat_interleave(n_rep, dim=1).transpose(2, 3).contiguous()
+        parts.append((torch.matmul(query, dense_kt) * scaling)[:, :, 0])
+    logits = torch.cat(parts, dim=-1)
+    if mask is not None:
+        logits = logits + mask[:, None, :].to(logits.dtype)
+    weights = torch.softmax(logits, dim=-1, dtype=torch.float32).to(query.dtype)
+    out = None
+    if value_prefix_length > 0:
+        out = torch.empty((b, hq, d), dtype=query.dtype, device=query.device)
+        _k.mu_zero_av_cuda(weights[..., :value_prefix_length].contiguous(), layer._packed_value_q,
+                           layer._value_mn, layer._value_scale, out, layer.nbits, alpha_value, n_rep,
+                           layer.q_group_size)
+    if length > value_prefix_length:
+        dense_v = values.repeat_interleave(n_rep, dim=1)
+        dense = torch.matmul(weights[..., value_prefix_length:].unsqueeze(2), dense_v)[:, :, 0]
+        out = dense if out is None else out + dense
+    return out.unsqueeze(1)
 
 
 def _storage_key(layer):

@@ -836,8 +836,10 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       const h2 p01 = h2{(_Float16)__builtin_amdgcn_exp2f(x[0] - m_use), (_Float16)__builtin_amdgcn_exp2f(x[1] - m_use)};
       const h2 p23 = h2{(_Float16)__builtin_amdgcn_exp2f(x[2] - m_use), (_Float16)__builtin_amdgcn_exp2f(x[3] - m_use)};
       const h2 one2 = h2{(_Float16)1.f, (_Float16)1.f};
-      float psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
-      psum = group_reduce<16>(psum, OpAdd());
+      // l_run and acc_a are per-lane partial sums (this lane's 4 tokens of
+      // every tile; the rescale factors are the same in the 16 lanes of the
+      // row): they are summed over the row once, at the end
+      const float psum = __builtin_amdgcn_fdot2(p23, one2, __builtin_amdgcn_fdot2(p01, one2, 0.f, false), false);
       l_run[sl] = l_run[sl] * corr[sl] + psum;
       // the values' constant part of this head: the running sum rescaled,
       // plus sum_t p_t * a_t over the tile, in fp32 with the same (fp16)
@@ -850,7 +852,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         c = __builtin_fmaf((float)p01.y, av[1], c);
         c = __builtin_fmaf((float)p23.x, av[2], c);
         c = __builtin_fmaf((float)p23.y, av[3], c);
-        acc_a[sl][vg] = __builtin_fmaf(acc_a[sl][vg], fa, group_reduce<16>(c, OpAdd()));
+        acc_a[sl][vg] = __builtin_fmaf(acc_a[sl][vg], fa, c);
       }
       if (owner) {
         // PV A operands of this head's 4 tokens: p times the token's (bp, bn),
@@ -1014,9 +1016,13 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
 #pragma unroll
     for (int sl = 0; sl < HS; ++sl) {
       const int i = sl * RS, h = h0 + sl;
+      // the row's partial sums (the 16 lanes of lane group g_e)
+      const float l_row = group_reduce<16>(l_run[sl], OpAdd());
+#pragma unroll
+      for (int vg = 0; vg < NG; ++vg) acc_a[sl][vg] = group_reduce<16>(acc_a[sl][vg], OpAdd());
       if (n == 0) {
         w[h] = m_run[sl];
-        w[NREP + h] = l_run[sl];
+        w[NREP + h] = l_row;
       }
 #pragma unroll
       for (int vg = 0; vg < NG; ++vg)

@@ -447,3 +447,92 @@ def test_per_layer_prefill_quantization_matches_whole_model_deferral(bits, monke
                      (la._value_scale, lb._value_scale), (la.keys, lb.keys), (la.values, lb.values)):
             assert torch.equal(x.contiguous().view(torch.uint8), y.contiguous().view(torch.uint8))
         assert la._alphas == lb._alphas
+
+
+def _default_path_emulation(q, st, bits, n_rep, scaling):
+    """The reference's default decode (attention.py:179-295) restated on the CPU with its
+    roundings: prefix logits from the qk launch's semantics rounded to the query dtype, the
+    residual's logits and the scaling each rounded to it, an fp32 softmax cast back, the av
+    launch's sum rounded, the residual's weighted sum rounded, and their sum rounded."""
+    dt = q.dtype
+    parts = []
+    if st["lq"]:
+        parts.append(ref.prefix_logits(q, st["packed_k"], st["k_mn"], st["k_scale"], bits, 2.0, n_rep,
+                                       scaling).to(dt))
+    dk = ref.repeat_kv(st["res_k"], n_rep)
+    if dk.shape[2]:
+        lg = torch.matmul(q.double(), dk.double().transpose(2, 3)).to(dt)
+        parts.append((lg.double() * scaling).to(dt)[:, :, 0])
+    w = torch.softmax(torch.cat(parts, -1), -1, dtype=torch.float32).to(dt)
+    lv = st["lv"]
+    out = ref.prefix_weighted_values(w[..., :lv], st["packed_v"], st["v_mn"], st["v_scale"], bits, 2.0, n_rep,
+                                     q.shape[-1]).to(dt)
+    dv = ref.repeat_kv(st["res_v"], n_rep)
+    dense = torch.matmul(w[..., lv:].unsqueeze(2).double(), dv.double())[:, :, 0].to(dt)
+    return (out.double() + dense.double()).to(dt).float()
+
+
+@pytest.mark.parametrize("d,bits,dtype", [(96, 4, torch.bfloat16), (256, 3, torch.bfloat16),
+                                          (80, 2, torch.float16), (128, 4, torch.float32)])
+def test_decode_hook_runs_split_launches_for_other_shapes(d, bits, dtype):
+    """head_dim other than 64 / 128 (and fp32 queries) run the reference's default path through
+    muzero_qk / muzero_av: same bytes in the cache as the oracle, output within the io dtype's
+    rounding of the oracle's restatement of that path, counted as qk / av launches."""
+    B, hkv, n_rep, prefill, steps = 2, 2, 4, 600, 40
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=d + bits, dtype=dtype)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=bits, alpha_key=2.0, alpha_value=2.0))
+    _feed(layer, k, v, prefill)
+    state = layer.get_attention_state()
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     dequant_dtype=torch.float32)
+    assert state["key_prefix_length"] == st["lq"] > 0
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    mz.reset_mu_zero_decode_stats()
+    out, w = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    stats = mz.get_mu_zero_decode_stats()
+    assert w is None and out.shape == (B, 1, hkv * n_rep, d) and out.dtype == dtype
+    assert stats.get("fused_qk_success") == 1 and stats.get("fused_av_success") == 1
+    assert stats.get("hip_fused_decode", 0) == 0
+    st["lv"] = st["lq"]
+    emu = _default_path_emulation(q, st, bits, n_rep, d ** -0.5)
+    to_emu = (out[:, 0].cpu().float() - emu).abs()
+    # a logit or weight rounding to the neighbouring io-dtype value moves the output by a few 1e-3
+    lim, lim_mean = (2e-4, 1e-5) if dtype == torch.float32 else (1.5e-2, 3e-4)
+    assert to_emu.max().item() < lim and to_emu.mean().item() < lim_mean, (to_emu.max().item(), to_emu.mean().item())
+    to_exact = (out[:, 0].cpu().double() - exact[:, 0]).abs()
+    assert to_exact.mean().item() < (1e-4 if dtype == torch.float32 else 3e-3), to_exact.mean().item()
+
+
+def test_generate_with_head_dim_96(monkeypatch):
+    """A model whose head_dim the fused kernels do not take (96) generates through the cache with
+    the separate launches; its decode-step logits match the dequantize-and-attend run."""
+    transformers = pytest.importorskip("transformers")
+    mz.patch_transformers()
+    torch.manual_seed(0)
+    cfg = transformers.Qwen3Config(vocab_size=512, hidden_size=384, intermediate_size=1024, num_hidden_layers=2,
+                                   num_attention_heads=8, num_key_value_heads=2, head_dim=96,
+                                   max_position_embeddings=4096, rms_norm_eps=1e-6, rope_theta=1e6,
+                                   attn_implementation="eager")
+    model = transformers.Qwen3ForCausalLM(cfg)
+    for p in model.parameters():
+        torch.nn.init.normal_(p, std=0.02)
+    model = model.to(DEV, torch.bfloat16).eval()
+    ids = torch.randint(0, 512, (2, 300), generator=torch.Generator().manual_seed(3)).to(DEV)
+    kw = dict(max_new_tokens=3, do_sample=False, cache_implementation="mu_zero_4bit",
+              cache_config={"residual_length": 128}, output_scores=True, return_dict_in_generate=True,
+              pad_token_id=0)
+    mz.reset_mu_zero_decode_stats()
+    with torch.no_grad():
+        split = model.generate(ids, **kw)
+    stats = mz.get_mu_zero_decode_stats()
+    assert stats.get("fused_qk_success", 0) == 2 * 2 and stats.get("hip_fused_decode", 0) == 0
+    monkeypatch.setenv("MUZERO_DISABLE_FUSED_DECODE", "1")
+    with torch.no_grad():
+        dense = model.generate(ids, **kw)
+    for s in (1, 2):
+        a, b = split.scores[s].float(), dense.scores[s].float()
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
+    assert torch.equal(split.sequences[:, :301], dense.sequences[:, :301])

@@ -188,7 +188,7 @@ def test_reference_default_decode_path():
                            bits, 2.0, n_rep, d ** -0.5)
     dense_k = ref.repeat_kv(st["res_k"].to(DEV), n_rep)
     dense_v = ref.repeat_kv(st["res_v"].to(DEV), n_rep)
-    dense = (torch.matmul(qd.float(), dense_k.float().transpose(2, 3)) * d ** -0.5).to(q.dtype)[:, :, 0]
+    dense = (torch.matmul(qd.float(), dense_k.float().transpose(2, 3).contiguous()) * d ** -0.5).to(q.dtype)[:, :, 0]
     w = torch.softmax(torch.cat([logits, dense], -1), -1, dtype=torch.float32).to(q.dtype)
     pre = torch.empty(b, hkv * n_rep, d, dtype=q.dtype, device=DEV)
     loader.mu_zero_av_cuda(w[..., :lq].contiguous(), st["packed_v"].to(DEV), st["v_mn"].to(DEV),
