@@ -75,13 +75,20 @@ constexpr int waves_per_simd() { return 2; }
 // 5 and 6 bits ("wide"): one copy, entry (zl, q) at byte zl*256 + 4*q (a
 // group's 32 or 64 codes span every bank anyway, so copies would not help;
 // two lane groups of a half-wave can meet on a bank).
+// 2 bits ("pair"): entry (z, e) = the (P, N) pairs of two codes q0 = e & 3,
+// q1 = e >> 2 of two rows with zero levels z & 3, z >> 2, as two words at
+// byte z*128 + 8*e: one ds_read_b64 fills two B registers.  A 64-bit read
+// serves 16 lanes (one lane group, one row pair, so one 128-byte block) per
+// cycle: no conflicts and no copies.
 template <int BITS>
 struct Fmt {
   static constexpr int QMAX = (1 << BITS) - 1;
   static constexpr int QB = 8 * BITS;  // bytes per packed 64-code row
   static constexpr bool WIDE = BITS >= 5;
+  // 2 bits: one lookup serves two codes (rows 2p, 2p+1 of a k-slice at one token)
+  static constexpr bool PAIR = BITS == 2;
   static constexpr int WPK = WIDE ? 4 : 2;  // code words per lane and k-tile
-  static constexpr int TBL = WIDE ? (1 << BITS) * 256 : 16 * 4 * 16 * 4;  // bytes per table
+  static constexpr int TBL = WIDE ? (1 << BITS) * 256 : (PAIR ? 16 * 16 * 8 : 16 * 4 * 16 * 4);  // bytes per table
 };
 
 // Wide codes: each lane loads, per row of its k-tile, the dword holding its 4
@@ -401,6 +408,24 @@ __device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint3
         const uint32_t s = 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | (uint32_t)((ii & 1) * 2 + (jt >> 1));
         ad[jt][ii] = __builtin_amdgcn_perm(zp, e, s);
       }
+  } else if constexpr (Fmt<BITS>::PAIR) {
+    // w0 / w1 as below; byte ii of w = this lane's codes of row ii (token jt
+    // at bits 2jt).  zp = the two row pairs' block offsets (z*128, 16 bits
+    // each).  One dot product per pair and token forms the entry offset
+    // 8*q0 + 32*q1 from the two rows' codes (masked in place) plus the block:
+    // ad[jt][p] is the byte address of rows (2p, 2p+1) at token jt.
+    const uint32_t own = w0 | (w1 << 16);
+    const uint32_t sel = odd ? 0x03070105u : 0x06020400u;
+    const uint32_t w = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, sel);
+    const uint32_t w2 = w >> 4;  // tokens 2, 3 at bits 0 / 2 of each byte
+    const uint32_t c0 = zp & 0xFFFFu, c1 = zp >> 16;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const int s2 = 2 * (jt & 1);
+      const uint32_t t = (jt < 2 ? w : w2) & (0x03030303u << s2);
+      ad[jt][0] = __builtin_amdgcn_udot4(t, s2 ? 0x00000802u : 0x00002008u, c0, false);
+      ad[jt][1] = __builtin_amdgcn_udot4(t, s2 ? 0x08020000u : 0x20080000u, c1, false);
+    }
   } else {
     // w0 / w1: 16 bits of rows (0 | 1) / (2 | 3) (even / odd lane), one byte per
     // lane of the pair; gather this lane's byte of rows 0..3 into one word
@@ -418,12 +443,19 @@ __device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint3
   }
 }
 
-template <int TBASE>
+template <int TBASE, bool PAIR = false>
 __device__ __forceinline__ void read_ktile(const uint8_t* smem, const uint32_t (&ad)[4][4], u32x4 B[4]) {
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int jt = 0; jt < 4; ++jt) {
+    if constexpr (PAIR) {
+      const uint2 r0 = *(const uint2*)(smem + TBASE + ad[jt][0]);
+      const uint2 r1 = *(const uint2*)(smem + TBASE + ad[jt][1]);
+      B[jt] = u32x4{r0.x, r0.y, r1.x, r1.y};
+    } else {
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) B[jt][ii] = *(const uint32_t*)(smem + TBASE + ad[jt][ii]);
+      for (int ii = 0; ii < 4; ++ii) B[jt][ii] = *(const uint32_t*)(smem + TBASE + ad[jt][ii]);
+    }
+  }
 }
 
 template <int IO, int NREP, int BITS, int MW>
@@ -497,8 +529,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   for (int j = 0; j < TW; ++j) {
     const int i = min(threadIdx.x + j * NT, TBL / 4 - 1);
     // narrow: word i = (zl, group, q) of the 16 x 16 host table; wide: the
-    // host table's [zl][64] words as they are
-    const int src = F::WIDE ? i : (i >> 6) * 16 + (i & 15);
+    // host table's [zl][64] words as they are; pair: two of its words
+    // pair: word i = half (i & 1) of entry ((i >> 1) & 15) of block z = i >> 5
+    const int e = (i >> 1) & 15, z = i >> 5;
+    const int src = F::WIDE ? i
+                    : F::PAIR ? ((i & 1) ? (z >> 2) * 16 + (e >> 2) : (z & 3) * 16 + (e & 3))
+                              : (i >> 6) * 16 + (i & 15);
     tk[j] = ftab_k[src];
     tv[j] = ftab_v[src];
   }
@@ -620,8 +656,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       sc.kmx = fmaxf(fmaxf(fabsf(sc.k0.a), fmaxf(sc.k0.bp, -sc.k0.bn)),
                      fmaxf(fabsf(sc.k1.a), fmaxf(sc.k1.bp, -sc.k1.bn)));
       // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
+      // (pair codes: the row pair's block offset in the table)
       *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
-          (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
+          F::PAIR ? (uint16_t)((sc.k0.zl + 4 * sc.k1.zl) * 128) : (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
     } else if (chunk == 1) {
       // value group scalars (lane: token lane, both value groups)
       const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
@@ -631,8 +668,17 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
                      fmaxf(fabsf(sc.v1.a), fmaxf(sc.v1.bp, -sc.v1.bn)));
       // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
       const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
-      W[S::VZP + vzo] = (uint8_t)sc.v0.zl;
-      W[S::VZP + 64 + vzo] = (uint8_t)sc.v1.zl;
+      if constexpr (F::PAIR) {
+        // tokens (2p, 2p+1) are lanes (2m, 2m+1): the even lane writes the pair's block offset
+        const uint32_t z0n = dpp_swap_pairs(sc.v0.zl), z1n = dpp_swap_pairs(sc.v1.zl);
+        if (!(lane & 1)) {
+          *(uint16_t*)(W + S::VZP + vzo) = (uint16_t)((sc.v0.zl + 4 * z0n) * 128);
+          *(uint16_t*)(W + S::VZP + 64 + vzo) = (uint16_t)((sc.v1.zl + 4 * z1n) * 128);
+        }
+      } else {
+        W[S::VZP + vzo] = (uint8_t)sc.v0.zl;
+        W[S::VZP + 64 + vzo] = (uint8_t)sc.v1.zl;
+      }
     } else if (chunk == 2) {
       // power-of-two scales keeping the fp16 operands in range (one reduction for both)
       wave_max2_bound(sc.kmx, sc.vmx);
@@ -737,14 +783,14 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
       addr_ktile<BITS>(KW, kzp(0), grep, odd, lsh, adc);
-      read_ktile<S::TBL_K>(smem, adc, Bc);
+      read_ktile<S::TBL_K, F::PAIR>(smem, adc, Bc);
       addr_ktile<BITS>(KW + F::WPK, kzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         u32x4 An;
         if (kt < 7) {
           An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
-          read_ktile<S::TBL_K>(smem, adn, Bn);
+          read_ktile<S::TBL_K, F::PAIR>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (kt < 6) addr_ktile<BITS>(KW + F::WPK * (kt + 2), kzp(kt + 2), grep, odd, lsh, adn);
@@ -900,7 +946,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
       addr_ktile<BITS>(VW, vzp(0), grep, odd, lsh, adc);
-      read_ktile<S::TBL_V>(smem, adc, Bc);
+      read_ktile<S::TBL_V, F::PAIR>(smem, adc, Bc);
       addr_ktile<BITS>(VW + F::WPK, vzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int st = 0; st < 4 * NG; ++st) {
@@ -909,7 +955,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         if (st + 1 < 4 * NG) {
           const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
           An = *(const u32x4*)(pv_row + vg1 * NREP * LROW + 16 * kt1 + 4 * g);
-          read_ktile<S::TBL_V>(smem, adn, Bn);
+          read_ktile<S::TBL_V, F::PAIR>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (st + 2 < 4 * NG) addr_ktile<BITS>(VW + F::WPK * (st + 2), vzp(st + 2), grep, odd, lsh, adn);
