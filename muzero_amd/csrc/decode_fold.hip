@@ -80,13 +80,18 @@ constexpr int waves_per_simd() { return 2; }
 // byte z*128 + 8*e: one ds_read_b64 fills two B registers.  A 64-bit read
 // serves 16 lanes (one lane group, one row pair, so one 128-byte block) per
 // cycle: no conflicts and no copies.
+// 1 bit ("quad"): entry (z, e) = the (P, N) pairs of the 4 rows' codes
+// (e >> ii) & 1 at zero levels (z >> ii) & 1, as four words at byte
+// z*256 + 16*e: one ds_read_b128 is a whole B operand.
 template <int BITS>
 struct Fmt {
   static constexpr int QMAX = (1 << BITS) - 1;
   static constexpr int QB = 8 * BITS;  // bytes per packed 64-code row
   static constexpr bool WIDE = BITS >= 5;
-  // 2 bits: one lookup serves two codes (rows 2p, 2p+1 of a k-slice at one token)
+  // 2 bits: one lookup serves two codes (rows 2p, 2p+1 of a k-slice at one
+  // token); 1 bit: four (the k-slice's 4 rows), a whole B operand
   static constexpr bool PAIR = BITS == 2;
+  static constexpr bool QUAD = BITS == 1;
   static constexpr int WPK = WIDE ? 4 : 2;  // code words per lane and k-tile
   static constexpr int TBL = WIDE ? (1 << BITS) * 256 : (PAIR ? 16 * 16 * 8 : 16 * 4 * 16 * 4);  // bytes per table
 };
@@ -379,18 +384,16 @@ __device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint3
     }
   } else if constexpr (BITS == 1) {
     // w0 / w1: byte m of rows (0 | 1) / (2 | 3) (even / odd lane); gather the
-    // byte of rows 0..3 into one word, then this lane's nibble (bit jt = code
-    // jt) of each byte
+    // byte of rows 0..3 into one word; shifted by sh, bit jt of byte ii is
+    // this lane's code jt of row ii.  zp = the row quad's block offset
+    // (z*256).  One dot product per token forms 16*e (e = the 4 rows' codes
+    // as bits 0..3) plus the block: ad[jt][0] addresses token jt's B operand.
     const uint32_t own = w0 | (w1 << 16);
     const uint32_t w = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, odd ? 0x02060004u : 0x06020400u);
-    const uint32_t w4 = sh ? (w >> (sh - 2)) : (w << 2);  // byte ii: the nibble's code jt at bit 2 + jt
+    const uint32_t ws = w >> sh;
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      const uint32_t ej = ((w4 >> jt) & 0x04040404u) | grep;
-#pragma unroll
-      for (int ii = 0; ii < 4; ++ii)
-        ad[jt][ii] = __builtin_amdgcn_perm(zp, ej, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | ii);
-    }
+    for (int jt = 0; jt < 4; ++jt)
+      ad[jt][0] = __builtin_amdgcn_udot4(ws & (0x01010101u << jt), 0x80402010u >> jt, zp, false);
   } else if constexpr (BITS == 4) {
     // w0 / w1: rows (0,1) / (2,3) of the pair, 32 bits = codes of lanes 2m, 2m+1;
     // this lane keeps 16 bits of each row: low half = row 2p, high half = row 2p+1
@@ -443,11 +446,13 @@ __device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint3
   }
 }
 
-template <int TBASE, bool PAIR = false>
+template <int TBASE, bool PAIR = false, bool QUAD = false>
 __device__ __forceinline__ void read_ktile(const uint8_t* smem, const uint32_t (&ad)[4][4], u32x4 B[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt) {
-    if constexpr (PAIR) {
+    if constexpr (QUAD) {
+      B[jt] = *(const u32x4*)(smem + TBASE + ad[jt][0]);
+    } else if constexpr (PAIR) {
       const uint2 r0 = *(const uint2*)(smem + TBASE + ad[jt][0]);
       const uint2 r1 = *(const uint2*)(smem + TBASE + ad[jt][1]);
       B[jt] = u32x4{r0.x, r0.y, r1.x, r1.y};
@@ -529,11 +534,14 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   for (int j = 0; j < TW; ++j) {
     const int i = min(threadIdx.x + j * NT, TBL / 4 - 1);
     // narrow: word i = (zl, group, q) of the 16 x 16 host table; wide: the
-    // host table's [zl][64] words as they are; pair: two of its words
+    // host table's [zl][64] words as they are; pair / quad: two / four of its words
     // pair: word i = half (i & 1) of entry ((i >> 1) & 15) of block z = i >> 5
+    // quad: word i = row (i & 3) of entry ((i >> 2) & 15) of block z = i >> 6
     const int e = (i >> 1) & 15, z = i >> 5;
+    const int e4 = (i >> 2) & 15, z4 = i >> 6, r4 = i & 3;
     const int src = F::WIDE ? i
                     : F::PAIR ? ((i & 1) ? (z >> 2) * 16 + (e >> 2) : (z & 3) * 16 + (e & 3))
+                    : F::QUAD ? ((z4 >> r4) & 1) * 16 + ((e4 >> r4) & 1)
                               : (i >> 6) * 16 + (i & 15);
     tk[j] = ftab_k[src];
     tv[j] = ftab_v[src];
@@ -656,9 +664,17 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       sc.kmx = fmaxf(fmaxf(fabsf(sc.k0.a), fmaxf(sc.k0.bp, -sc.k0.bn)),
                      fmaxf(fabsf(sc.k1.a), fmaxf(sc.k1.bp, -sc.k1.bn)));
       // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
-      // (pair codes: the row pair's block offset in the table)
-      *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
-          F::PAIR ? (uint16_t)((sc.k0.zl + 4 * sc.k1.zl) * 128) : (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
+      // (pair codes: the row pair's block offset in the table; quad codes: the
+      // row quad's, from this lane's rows and its partner's)
+      if constexpr (F::QUAD) {
+        const uint32_t zpair = sc.k0.zl + 2 * sc.k1.zl;
+        const uint32_t other = dpp_swap_pairs(zpair);
+        if (!(lane & 1))
+          *(uint32_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4) = (zpair + 4 * other) * 256;
+      } else {
+        *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
+            F::PAIR ? (uint16_t)((sc.k0.zl + 4 * sc.k1.zl) * 128) : (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
+      }
     } else if (chunk == 1) {
       // value group scalars (lane: token lane, both value groups)
       const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
@@ -668,7 +684,20 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
                      fmaxf(fabsf(sc.v1.a), fmaxf(sc.v1.bp, -sc.v1.bn)));
       // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
       const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
-      if constexpr (F::PAIR) {
+      if constexpr (F::QUAD) {
+        // tokens 0..3 of a k-slice are lanes 4m..4m+3: their zero levels as
+        // bits of the quad index, summed over the quad; its first lane writes
+        // the block offset
+        uint32_t q0 = sc.v0.zl << (lane & 3), q1 = sc.v1.zl << (lane & 3);
+        q0 += dpp_sel_u<DPP_QUAD_XOR1>(q0);
+        q1 += dpp_sel_u<DPP_QUAD_XOR1>(q1);
+        q0 += dpp_sel_u<DPP_QUAD_XOR2>(q0);
+        q1 += dpp_sel_u<DPP_QUAD_XOR2>(q1);
+        if (!(lane & 3)) {
+          *(uint32_t*)(W + S::VZP + vzo) = q0 * 256;
+          *(uint32_t*)(W + S::VZP + 64 + vzo) = q1 * 256;
+        }
+      } else if constexpr (F::PAIR) {
         // tokens (2p, 2p+1) are lanes (2m, 2m+1): the even lane writes the pair's block offset
         const uint32_t z0n = dpp_swap_pairs(sc.v0.zl), z1n = dpp_swap_pairs(sc.v1.zl);
         if (!(lane & 1)) {
@@ -783,14 +812,14 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
       addr_ktile<BITS>(KW, kzp(0), grep, odd, lsh, adc);
-      read_ktile<S::TBL_K, F::PAIR>(smem, adc, Bc);
+      read_ktile<S::TBL_K, F::PAIR, F::QUAD>(smem, adc, Bc);
       addr_ktile<BITS>(KW + F::WPK, kzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         u32x4 An;
         if (kt < 7) {
           An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
-          read_ktile<S::TBL_K, F::PAIR>(smem, adn, Bn);
+          read_ktile<S::TBL_K, F::PAIR, F::QUAD>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (kt < 6) addr_ktile<BITS>(KW + F::WPK * (kt + 2), kzp(kt + 2), grep, odd, lsh, adn);
@@ -946,7 +975,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
       addr_ktile<BITS>(VW, vzp(0), grep, odd, lsh, adc);
-      read_ktile<S::TBL_V, F::PAIR>(smem, adc, Bc);
+      read_ktile<S::TBL_V, F::PAIR, F::QUAD>(smem, adc, Bc);
       addr_ktile<BITS>(VW + F::WPK, vzp(1), grep, odd, lsh, adn);
 #pragma unroll
       for (int st = 0; st < 4 * NG; ++st) {
@@ -955,7 +984,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         if (st + 1 < 4 * NG) {
           const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
           An = *(const u32x4*)(pv_row + vg1 * NREP * LROW + 16 * kt1 + 4 * g);
-          read_ktile<S::TBL_V, F::PAIR>(smem, adn, Bn);
+          read_ktile<S::TBL_V, F::PAIR, F::QUAD>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
         if (st + 2 < 4 * NG) addr_ktile<BITS>(VW + F::WPK * (st + 2), vzp(st + 2), grep, odd, lsh, adn);
