@@ -365,22 +365,16 @@ __device__ __forceinline__ void addr_ktile(const uint32_t* w, uint32_t zp, uint3
     }
   } else if constexpr (BITS == 3) {
     // w0 / w1: the pair's dword of rows (0 | 1) / (2 | 3); after the swap the
-    // lane holds all four rows and takes its 12 bits (4 codes) from each at
-    // bit sh, spread to bytes as table offsets 4*q + 64*group
+    // lane holds all four rows, its code jt of row ii at bit sh + 3*jt; the
+    // row's table copy for this lane group starts at byte zl*256 + 64*group
+    // (the zero level, byte ii of zp, moved to byte 1 over grep's byte 0)
     const uint32_t s0 = dpp_swap_pairs(w0), s1 = dpp_swap_pairs(w1);
     const uint32_t r[4] = {odd ? s0 : w0, odd ? w0 : s0, odd ? s1 : w1, odd ? w1 : s1};
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) {
-      // 12 bits c3|c2|c1|c0 -> bytes 4*c_jt: split into 6-bit halves 16 bits
-      // apart, then into 3-bit fields 8 bits apart (the masks drop the
-      // overlaps of the shifted copies)
-      const uint32_t f = __builtin_amdgcn_ubfe(r[ii], sh, 12);
-      const uint32_t t = ((f << 10) | f) & 0x003F003Fu;
-      const uint32_t u = ((t << 5) | t) & 0x07070707u;
-      const uint32_t e = (u << 2) | grep;
+      const uint32_t row = __builtin_amdgcn_perm(zp, grep, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8));
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-        ad[jt][ii] = __builtin_amdgcn_perm(zp, e, 0x0C0C0000u | ((uint32_t)(4 + ii) << 8) | jt);
+      for (int jt = 0; jt < 4; ++jt) ad[jt][ii] = (__builtin_amdgcn_ubfe(r[ii], sh + 3 * jt, 3) << 2) + row;
     }
   } else if constexpr (BITS == 1) {
     // w0 / w1: byte m of rows (0 | 1) / (2 | 3) (even / odd lane); gather the
