@@ -30,10 +30,14 @@
 //   MFMA rows = query heads of the kv-head, spread to rows h*16/NREP: every
 //   lane group of the MFMA output then holds real logits, so the softmax
 //   runs in registers (row reductions on DPP) with no LDS round trip.
-// Each code is one conflict-free ds_read_b32 from a per-lane-group copy of
-// the (P, N) table in LDS, addressed by one v_perm (plus about 0.75 VALU ops
-// of code extraction), read straight into the MFMA B register; the lookups of
-// the next k-tile are issued before the MFMAs of the current one.  The
+// Each 3- or 4-bit code is one conflict-free ds_read_b32 from a per-lane-
+// group copy of the (P, N) table in LDS, addressed by one v_perm (plus about
+// 0.75 VALU ops of code extraction), read straight into the MFMA B register;
+// 2-bit codes go two to a ds_read_b64 and 1-bit codes four to a ds_read_b128
+// (a B operand's rows at one token), the address one v_dot4_u32_u8 of the
+// codes; 5- and 6-bit codes are bit-field extracts onto one table copy.  The
+// lookups of the next k-tile are issued before the MFMAs of the current one.
+// The
 // key-side products q*bp, q*bn are formed per (head, channel) per tile as
 // fp16 hi + lo pairs, on two rows of the same MFMA (fp32 accuracy at no extra
 // MFMA); the PV operands p*bp, p*bn, p*a are formed per (head, token) by the
