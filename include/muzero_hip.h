@@ -188,12 +188,13 @@ typedef struct mz_decode_args {
   const void* v_res; int64_t vr_sb, vr_sh, vr_st;
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
-  /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 6): pairs of
+  /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 7): pairs of
    * fp16 (P, N) packed in uint32 (P in the low half), row = zero level,
    * column = code; 16 x 16 for bits 1 to 4 (zero beyond 2^bits - 1),
-   * 2^bits x 64 for 5 and 6 bits; see muzero_amd/tables.py ("fold1" ..
-   * "fold6").  Needed by the fold fast path; may be null (the generic path
-   * is used then). */
+   * 2^bits x 64 for 5 and 6 bits, 128 x 128 for 7 bits; see
+   * muzero_amd/tables.py ("fold1" .. "fold7").  Needed by the fold fast path;
+   * may be null (the generic path is used then).  7 bits: the fold path
+   * needs fold_k == fold_v (one alpha for keys and values). */
   const void* fold_k; const void* fold_v;
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;
@@ -214,9 +215,9 @@ typedef struct mz_decode_args {
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 1 to 6, head_dim 128, aligned prefixes, n_rep in {1,2,4,8}
- * for 1 to 4 bits and {1,2,4} for 5 and 6, fold tables given) and the
- * exact-dequantize kernel otherwise. */
+ * applies (bits 1 to 7, head_dim 128, aligned prefixes, n_rep in {1,2,4,8}
+ * for 1 to 4 bits and {1,2,4} for 5 to 7, fold tables given, at 7 bits one
+ * table for keys and values) and the exact-dequantize kernel otherwise. */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments

@@ -1,4 +1,4 @@
-// Packed-KV decode attention, fast path for 1- to 6-bit codes (gfx950, wave64).
+// Packed-KV decode attention, fast path for 1- to 7-bit codes (gfx950, wave64).
 //
 // Dequantization folded into the MFMA operands.  For a group with stored
 // (mn, s) the reference dequantizes code q as (muzero/quantizer.py:241-255)
@@ -35,7 +35,7 @@
 // 0.75 VALU ops of code extraction), read straight into the MFMA B register;
 // 2-bit codes go two to a ds_read_b64 and 1-bit codes four to a ds_read_b128
 // (a B operand's rows at one token), the address one v_dot4_u32_u8 of the
-// codes; 5- and 6-bit codes are bit-field extracts onto one table copy.  The
+// codes; 5- to 7-bit codes are bit-field extracts onto one table copy.  The
 // lookups of the next k-tile are issued before the MFMAs of the current one.
 // The
 // key-side products q*bp, q*bn are formed per (head, channel) per tile as
@@ -46,7 +46,7 @@
 // a power-of-two scale per key group and an accumulator exponent for the
 // values, folded into the logits and into the online-softmax rescale.
 //
-// Launch: one workgroup of 4 waves per (batch, kv-head, split); a split is a
+// Launch: one workgroup of 4 waves (7 bits: 8) per (batch, kv-head, split); a split is a
 // run of tiles (residual tiles first), waves take every 4th; the split's
 // (m, l, acc) goes to the workspace and the shared combine kernel merges
 // splits.  With a single split (the grid already fills the GPU) the kernel
@@ -68,8 +68,10 @@ constexpr int TILE = 64;  // tokens per tile
 // workgroups (three waves per SIMD; they fit the registers and LDS for up to
 // 4 query heads) measured 13 % slower at config 1: more waves per CU contend
 // for its LDS rather than hide more latency.
-template <int NREP>
-constexpr int waves_for() { return 4; }
+// 7-bit codes: one workgroup of 8 waves per CU (its 64 KB table then serves
+// the CU's two waves per SIMD).
+template <int NREP, int BITS>
+constexpr int waves_for() { return BITS >= 7 ? 8 : 4; }
 template <int NREP>
 constexpr int waves_per_simd() { return 2; }
 // (P, N) table in LDS.  Up to 4 bits: entry (zl, q) replicated for the 4
@@ -78,7 +80,8 @@ constexpr int waves_per_simd() { return 2; }
 // disjoint bank range, so the per-code lookups are free of bank conflicts.
 // 5 and 6 bits ("wide"): one copy, entry (zl, q) at byte zl*256 + 4*q (a
 // group's 32 or 64 codes span every bank anyway, so copies would not help;
-// two lane groups of a half-wave can meet on a bank).
+// two lane groups of a half-wave can meet on a bank).  7 bits: zl*512 + 4*q,
+// one 64 KB table for keys and values (the launcher requires one alpha).
 // 2 bits ("pair"): entry (z, e) = the (P, N) pairs of two codes q0 = e & 3,
 // q1 = e >> 2 of two rows with zero levels z & 3, z >> 2, as two words at
 // byte z*128 + 8*e: one ds_read_b64 fills two B registers.  A 64-bit read
@@ -97,7 +100,12 @@ struct Fmt {
   static constexpr bool PAIR = BITS == 2;
   static constexpr bool QUAD = BITS == 1;
   static constexpr int WPK = WIDE ? 4 : 2;  // code words per lane and k-tile
-  static constexpr int TBL = WIDE ? (1 << BITS) * 256 : (PAIR ? 16 * 16 * 8 : 16 * 4 * 16 * 4);  // bytes per table
+  // wide: bytes per zero level of the table, and the byte that stands for a
+  // zero level in the zero-level words (the table row is that byte * 256)
+  static constexpr int ZROW = (4 << BITS) > 256 ? (4 << BITS) : 256;
+  static constexpr int ZS = ZROW / 256;
+  static constexpr int TBL = WIDE ? (1 << BITS) * ZROW : (PAIR ? 16 * 16 * 8 : 16 * 4 * 16 * 4);  // bytes per table
+  static constexpr bool SHARED = TBL > 16384;  // one table for keys and values
 };
 
 // Wide codes: each lane loads, per row of its k-tile, the dword holding its 4
@@ -132,11 +140,11 @@ constexpr int LROW = TILE + 4;      // uint32 per head row of per-token arrays
 
 // Static LDS layout (bytes).  Per workgroup: the two (P, N) tables and the
 // query in two forms; per wave: the current tile's operands and weights.
-template <int NREP, int WAVES, int TBLB>
+template <int NREP, int WAVES, int TBLB, bool SHARED>
 struct Smem {
   static constexpr int TBL_K = 0;
-  static constexpr int TBL_V = TBLB;
-  static constexpr int Q16 = 2 * TBLB;                // fp16 [NREP][HROW*2]
+  static constexpr int TBL_V = SHARED ? 0 : TBLB;
+  static constexpr int Q16 = (SHARED ? 1 : 2) * TBLB;  // fp16 [NREP][HROW*2]
   static constexpr int Q_IO = Q16 + NREP * HROW * 4;  // io dtype [NREP][HROW*2]
   static constexpr int ZERO = Q_IO + NREP * HROW * 4;  // AROW zero words: A rows that must be 0
   static constexpr int WAVE0 = ZERO + AROW * 4;
@@ -462,15 +470,16 @@ __device__ __forceinline__ void read_ktile(const uint8_t* smem, const uint32_t (
 }
 
 template <int IO, int NREP, int BITS, int MW>
-__global__ __launch_bounds__(64 * waves_for<NREP>())
+__global__ __launch_bounds__((64 * waves_for<NREP, BITS>()))
 __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>()))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
     const uint32_t* __restrict__ ftab_v, int direct, int cus) {
-  constexpr int WAVES = waves_for<NREP>();
+  constexpr int WAVES = waves_for<NREP, BITS>();
   constexpr int NT = 64 * WAVES;  // threads per workgroup
   using M = Mfma<IO>;
   using F = Fmt<BITS>;
-  using S = Smem<NREP, WAVES, F::TBL>;
+  using S = Smem<NREP, WAVES, F::TBL, F::SHARED>;
+  static_assert(S::TOTAL <= 160 * 1024, "LDS of one workgroup");
   constexpr int TBL = F::TBL;
   constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
   static_assert(RS >= 2, "QK needs a second row per head for the low part of the key product");
@@ -542,7 +551,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
                     : F::QUAD ? ((z4 >> r4) & 1) * 16 + ((e4 >> r4) & 1)
                               : (i >> 6) * 16 + (i & 15);
     tk[j] = ftab_k[src];
-    tv[j] = ftab_v[src];
+    if constexpr (!F::SHARED) tv[j] = ftab_v[src];
   }
 #pragma unroll
   for (int j = 0; j < QW; ++j) {
@@ -557,7 +566,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   for (int j = 0; j < TW; ++j) {
     if (threadIdx.x + j * NT < TBL / 4) {
       ((uint32_t*)(smem + S::TBL_K))[threadIdx.x + j * NT] = tk[j];
-      ((uint32_t*)(smem + S::TBL_V))[threadIdx.x + j * NT] = tv[j];
+      if constexpr (!F::SHARED) ((uint32_t*)(smem + S::TBL_V))[threadIdx.x + j * NT] = tv[j];
     }
   }
   for (int i = threadIdx.x; i < AROW; i += NT) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
@@ -671,7 +680,8 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
           *(uint32_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4) = (zpair + 4 * other) * 256;
       } else {
         *(uint16_t*)(W + S::KZP + (((lane >> 1) & 3) * 8 + (lane >> 3)) * 4 + (lane & 1) * 2) =
-            F::PAIR ? (uint16_t)((sc.k0.zl + 4 * sc.k1.zl) * 128) : (uint16_t)(sc.k0.zl | (sc.k1.zl << 8));
+            F::PAIR ? (uint16_t)((sc.k0.zl + 4 * sc.k1.zl) * 128)
+                    : (uint16_t)(sc.k0.zl * F::ZS | (sc.k1.zl * F::ZS << 8));
       }
     } else if (chunk == 1) {
       // value group scalars (lane: token lane, both value groups)
@@ -703,8 +713,8 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
           *(uint16_t*)(W + S::VZP + 64 + vzo) = (uint16_t)((sc.v1.zl + 4 * z1n) * 128);
         }
       } else {
-        W[S::VZP + vzo] = (uint8_t)sc.v0.zl;
-        W[S::VZP + 64 + vzo] = (uint8_t)sc.v1.zl;
+        W[S::VZP + vzo] = (uint8_t)(sc.v0.zl * F::ZS);
+        W[S::VZP + 64 + vzo] = (uint8_t)(sc.v1.zl * F::ZS);
       }
     } else if (chunk == 2) {
       // power-of-two scales keeping the fp16 operands in range (one reduction for both)
@@ -1165,10 +1175,12 @@ bool fold_supported(const mz_decode_args* a) {
                     (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
   // 5- and 6-bit tables (8 and 16 KB each) leave room for two workgroups per
-  // CU up to 4 query heads per kv-head; 8 heads take the general kernel there
+  // CU up to 4 query heads per kv-head, the 7-bit table (64 KB, one for keys
+  // and values) for one 8-wave workgroup; 8 heads take the general kernel there
   const bool nrep_ok = a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || (a->n_rep == 8 && a->bits <= 4);
-  return a->bits >= 1 && a->bits <= 6 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
-         a->fold_k && a->fold_v &&
+  const bool one_table = a->bits < 7 || a->fold_k == a->fold_v;
+  return a->bits >= 1 && a->bits <= 7 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
+         one_table && a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
          ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&
          a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 && a->vp_sh % 4 == 0 &&
@@ -1206,9 +1218,9 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const int cus = device_cu_count();
 #define MZ_FOLD(IOV, NR, BB)                                                                            \
   if (a->meta_dtype == MZ_F32)                                                                          \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
   else                                                                                                       \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(64 * fold::waves_for<NR>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
 #define MZ_FOLD_NREP(IOV, BB)            \
   switch (a->n_rep) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
@@ -1231,6 +1243,7 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   else if (a->bits == 1) { MZ_FOLD_NREP(IOV, 1) }      \
   else if (a->bits == 5) { MZ_FOLD_NREP_WIDE(IOV, 5) } \
   else if (a->bits == 6) { MZ_FOLD_NREP_WIDE(IOV, 6) } \
+  else if (a->bits == 7) { MZ_FOLD_NREP_WIDE(IOV, 7) } \
   else return MZ_EUNSUPPORTED;
   if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
 #undef MZ_FOLD_BITS

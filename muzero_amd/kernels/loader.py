@@ -252,7 +252,7 @@ class DecodePlan:
         a.e_key, a.e_value = ptr(ek), ptr(ev)
         a.alpha_key, a.alpha_value = float(alpha_key), float(alpha_value)
         keep += [ek, ev]
-        if 1 <= int(bits) <= 6:
+        if 1 <= int(bits) <= 7:
             fk = tables.device_table(f"fold{int(bits)}", alpha_key, dev)
             fv = tables.device_table(f"fold{int(bits)}", alpha_value, dev)
             a.fold_k, a.fold_v = ptr(fk), ptr(fv)

@@ -29,7 +29,7 @@ the reference:
     1..255, ``d`` in 0..bins (``muzero/quantizer.py:250-253``).
     Layout: ``E[(bins-1)*(bins+2)/2 + d]``.
 
-``fold1`` .. ``fold6`` (decode attention, 1- to 6-bit codes)
+``fold1`` .. ``fold7`` (decode attention, 1- to 7-bit codes)
     For zero level ``zl`` and code ``q`` (``qmax = 2^bits - 1``), the pair
     ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
     as two fp16 packed in one uint32 (P in the low half), with
@@ -141,11 +141,11 @@ def _expm1_row(bins: int) -> int:
 
 
 def _build_fold(alpha: float, bits: int) -> torch.Tensor:
-    """(P, N) pairs of the ``bits``-bit codes, zero-padded to 16 x 16 (1-4 bits) or
-    (qmax+1) x 64 (5 and 6 bits); row zl, column q."""
+    """(P, N) pairs of the ``bits``-bit codes, zero-padded to 16 x 16 (1-4 bits),
+    (qmax+1) x 64 (5 and 6 bits) or 128 x 128 (7 bits); row zl, column q."""
     e = host_table("expm1", alpha)
     qmax = (1 << bits) - 1
-    rows, cols = (16, 16) if bits <= 4 else (qmax + 1, 64)
+    rows, cols = (16, 16) if bits <= 4 else (qmax + 1, max(64, qmax + 1))
     p = torch.zeros(rows, cols, dtype=torch.float32)
     nq = torch.zeros(rows, cols, dtype=torch.float32)
     for zl in range(qmax + 1):
@@ -177,7 +177,7 @@ def host_table(kind: str, alpha: float, dtype: torch.dtype | None = None) -> tor
                 t = _build_expm1(alpha)
             elif kind == "fold4":
                 t = _build_fold(alpha, 4)
-            elif kind in ("fold1", "fold2", "fold3", "fold5", "fold6"):
+            elif kind in ("fold1", "fold2", "fold3", "fold5", "fold6", "fold7"):
                 t = _build_fold(alpha, int(kind[-1]))
             else:
                 raise ValueError(kind)

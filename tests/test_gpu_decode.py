@@ -78,7 +78,8 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
     lq0 = ref.split_prefix(length, residual, 64)
     fold = (kernel_path == "fold" or (kernel_path == "auto" and d == 128 and lq0 > 0
                                       and ((1 <= bits <= 4 and n_rep in (1, 2, 4, 8))
-                                           or (bits in (5, 6) and n_rep in (1, 2, 4)))))
+                                           or (bits in (5, 6) and n_rep in (1, 2, 4))
+                                           or (bits == 7 and n_rep in (1, 2, 4) and alpha_k == alpha_v))))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
                                      dequant_dtype=torch.float32 if fold else None)
@@ -170,9 +171,10 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 1- to 4-bit codes, head_dim 128, n_rep in {1, 2, 4, 8}, and 5- and 6-bit codes
-# with n_rep in {1, 2, 4}: the fold kernel (AUTO picks it); the same cases
-# through the exact-dequantize kernel keep that path covered too.
+# 1- to 4-bit codes, head_dim 128, n_rep in {1, 2, 4, 8}, and 5- to 7-bit codes
+# with n_rep in {1, 2, 4} (7 bits: one alpha for keys and values): the fold
+# kernel (AUTO picks it); the same cases through the exact-dequantize kernel
+# keep that path covered too.
 FOLD_CASES = [
     # B, hkv, n_rep, d, length, bits, residual
     (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
@@ -212,6 +214,12 @@ FOLD_CASES = [
     (2, 1, 4, 128, 300, 6, 0),
     (1, 2, 4, 128, 900, 6, 191),
     (2, 1, 4, 128, 300, 1, 0),
+    (2, 2, 4, 128, 1024, 7, 128),
+    (1, 2, 1, 128, 700, 7, 128),
+    (1, 2, 2, 128, 700, 7, 128),
+    (1, 2, 4, 128, 4096, 7, 128),
+    (2, 1, 4, 128, 300, 7, 0),
+    (1, 2, 4, 128, 900, 7, 191),
 ]
 
 

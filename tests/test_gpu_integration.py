@@ -42,7 +42,7 @@ def test_cache_layer_matches_oracle_cache(bits, dtype, meta):
     cfg = mz.MuZeroConfig(bits=bits, amax_dtype=meta, alpha_key=2.0, alpha_value=2.0)
     layer = MuZeroCacheLayer(cfg)
     _feed(layer, k, v, prefill)
-    fold = 1 <= bits <= 6  # the fold kernel (fp32 dequantized values) serves 1- to 6-bit (n_rep 4)
+    fold = 1 <= bits <= 7  # the fold kernel (fp32 dequantized values) serves 1- to 7-bit (n_rep 4)
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
                                      amax_dtype=getattr(torch, meta),
                                      dequant_dtype=torch.float32 if fold else None)
@@ -298,16 +298,15 @@ def test_decode_stream_with_flushes_matches_oracle(bits):
     one at a time, flushing one group every 64 tokens (decode_flush_by_group=True).  After
     every 16th token and after every flush the decode hook's output matches the oracle's
     attention over the same token sequence (the flush policy gives the same prefix length),
-    and at the end the stored bytes equal the oracle's.  1- and 5-bit run the fold kernel, 7-bit
-    the general kernel (5 and 7 bits are outside the config's validated set, as in the stream
-    benchmark)."""
+    and at the end the stored bytes equal the oracle's.  All three widths run the fold kernel
+    (5 bits is outside the config's validated set, as in the stream benchmark)."""
     B, hkv, n_rep, d, prefill, steps = 1, 2, 4, 128, 640, 160
     k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=31 + bits)
     cfg = mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0)
     cfg.bits = bits
     layer = MuZeroCacheLayer(cfg)
     layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
-    fold = bits <= 6
+    fold = bits <= 7
     qd = q.to(DEV)
     checked = flushes = 0
     for t in range(prefill, prefill + steps):
