@@ -182,22 +182,30 @@ __device__ __forceinline__ void chunk(uint8_t* area, const Fetch<BITS, NR>& f, c
   const float* cb = (const float*)(area + A::CB_OFF);
   // lane's code: bits [lane*BITS, lane*BITS + BITS) of the row
   const int bit = lane * BITS;
-  const int wofs = (bit >> 5) * 4;
+  const uint8_t* lrow = area + (bit >> 5) * 4;
   const uint32_t sh = bit & 31;
   constexpr uint32_t mask = (1u << BITS) - 1u;
   constexpr bool straddle = (32 % BITS) != 0;
-#pragma unroll 4
-  for (int r = 0; r < nrows; ++r) {
-    const uint8_t* rp = area + r * A::PITCH + wofs;
+  auto row = [&](const int r) __attribute__((always_inline)) {
+    const uint8_t* rp = lrow + r * A::PITCH;
     const uint32_t d0 = *(const uint32_t*)rp;
     uint32_t code;
     if constexpr (straddle) code = __builtin_amdgcn_alignbit(*(const uint32_t*)(rp + 4), d0, sh) & mask;
-    else code = (d0 >> sh) & mask;
+    else code = __builtin_amdgcn_ubfe(d0, sh, BITS);
     float x;
     if constexpr (A::CB) x = cb[r * A::CBP + code];
     else x = deq_select(get_row(area + A::PAR_OFF + 48 * r), code, E);
 #pragma unroll
     for (int h = 0; h < NR; ++h) acc[h] = __builtin_fmaf(coef[r * NR + h], x, acc[h]);
+  };
+  if (nrows == kRows) {
+    // a full chunk: every row's offsets are compile-time constants (immediate
+    // offsets of the LDS reads), so a row costs its extract and multiply-adds
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) row(r);
+  } else {
+#pragma unroll 4
+    for (int r = 0; r < nrows; ++r) row(r);
   }
 }
 
