@@ -483,6 +483,24 @@ def measured_copy_gbs(mib, steps):
     return 2 * n / (ms * 1e-3) / 1e9
 
 
+def measured_read_gbs(mib, steps):
+    """Bytes read per second by the library's streaming-read probe (muzero_stream_read) over a
+    `mib` MiB buffer: the read bandwidth a streaming kernel attains on this box (a decode call
+    is almost all reads), the best of three grid sizes."""
+    from muzero_amd.kernels.loader import stream_read
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    best = 0.0
+    for n_out in (1024, 2048, 4096):
+        out = torch.empty(n_out, dtype=torch.int32, device="cuda:0")
+        stream_read(src, out)
+        ms = time_region(lambda i: stream_read(src, out), steps, stream)
+        best = max(best, n / (ms * 1e-3) / 1e9)
+    del src
+    return best
+
+
 def copy_calibration(mib, steps):
     """A plain device-to-device copy of known size: what FETCH_SIZE / WRITE_SIZE read for it
     calibrates the same counters on the decode kernel."""
@@ -572,6 +590,7 @@ def main():
     gbs = nbytes / (ms_step * 1e-3) / 1e9
     gbs_split = nbytes / (ms_kernel * 1e-3) / 1e9
     copy_gbs = measured_copy_gbs(1024, 10)
+    read_gbs = measured_read_gbs(1024, 10)
 
     traffic = None
     if os.path.exists(args.traffic_json):
@@ -626,7 +645,9 @@ def main():
                      "frac": round(gbs_split / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": nbytes,
                      "measured_copy_GBps": round(copy_gbs, 1),
-                     "frac_of_measured_copy": round(gbs_split / copy_gbs, 4)},
+                     "frac_of_measured_copy": round(gbs_split / copy_gbs, 4),
+                     "measured_stream_read_GBps": round(read_gbs, 1),
+                     "frac_of_measured_stream_read": round(gbs_split / read_gbs, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

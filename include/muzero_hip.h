@@ -292,6 +292,17 @@ typedef struct mz_prologue_args {
 } mz_prologue_args;
 int muzero_decode_prologue(const mz_prologue_args* args, mz_stream_t stream);
 
+/*
+ * Streaming-read probe: reads bytes [0, bytes) of src once (16-byte aligned,
+ * bytes a multiple of 16; src may be null when bytes is 0) and XOR-folds them, 32-bit word by word, into
+ * out[0 .. n_out) (one word per workgroup, n_out workgroups, 1..65535; the
+ * XOR of all n_out words is the XOR of every 32-bit word of the buffer).
+ * Measures the read bandwidth a streaming kernel attains on the device, the
+ * figure the decode kernels' rates are reported against beside the published
+ * peak.  No counterpart in the reference: a measurement utility.
+ */
+int muzero_stream_read(const void* src, int64_t bytes, uint32_t* out, int n_out, mz_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

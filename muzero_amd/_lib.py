@@ -128,6 +128,7 @@ SIGNATURES = {
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_attention_noalloc": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_prologue": (c_int, [ctypes.POINTER(PrologueArgs), c_vp]),
+    "muzero_stream_read": (c_int, [c_vp, c_i64, c_vp, c_int, c_vp]),
 }
 
 _lib = None

@@ -395,6 +395,20 @@ def decode_prologue(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torc
     return out
 
 
+def stream_read(buf: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """Read ``buf`` once on the device (``muzero_stream_read``) and XOR-fold its 32-bit words
+    into ``out`` (int32, one word per workgroup; the XOR of ``out`` is the XOR of every word).
+    A measurement utility: the read bandwidth a streaming kernel attains on this device."""
+    _require(buf.is_cuda and buf.is_contiguous() and buf.data_ptr() % 16 == 0
+             and (buf.numel() * buf.element_size()) % 16 == 0, "stream_read needs a contiguous, 16-byte "
+             "aligned device buffer of a multiple of 16 bytes")
+    _require(out.dtype == torch.int32 and out.is_contiguous() and out.device == buf.device
+             and 1 <= out.numel() <= 65535, "stream_read output: 1..65535 int32 words on the same device")
+    check(load().muzero_stream_read(buf.data_ptr(), buf.numel() * buf.element_size(), out.data_ptr(),
+                                    out.numel(), stream_ptr(buf.device)), "muzero_stream_read")
+    return out
+
+
 def mu_zero_decode_attention_hip(query: torch.Tensor, **kwargs) -> torch.Tensor:
     """Fused decode attention; returns ``[B, 1, Hq, D]`` in the query dtype.
 

@@ -125,3 +125,16 @@ def test_qk_av_reject_bad_args_without_a_device():
     assert lib.muzero_av(ctypes.byref(v), None) == -2
     v.head_dim, v.batch = 128, 0
     assert lib.muzero_av(ctypes.byref(v), None) == 0
+
+
+def test_stream_read_rejects_bad_args_without_a_device():
+    """muzero_stream_read checks pointers, alignment, size and the output count on the host."""
+    lib = _lib.load()
+    src, out = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert lib.muzero_stream_read(None, 16, out, 1, None) == -1
+    assert lib.muzero_stream_read(src, 16, None, 1, None) == -1
+    assert lib.muzero_stream_read(src, 15, out, 1, None) == -1
+    assert lib.muzero_stream_read(ctypes.c_void_p(4100), 16, out, 1, None) == -1
+    assert lib.muzero_stream_read(src, 16, out, 0, None) == -1
+    assert lib.muzero_stream_read(src, 16, out, 65536, None) == -1
+    assert lib.muzero_stream_read(src, -16, out, 1, None) == -1
