@@ -556,7 +556,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
 #pragma unroll
   for (int j = 0; j < QW; ++j) {
     const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
-    qraw[j] = i < NREP * D ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * NREP + h) * a.q_sh + c] : 0;
+    // heads past n_rep (a kernel built for more heads) get a zero query; their
+    // outputs are not written
+    qraw[j] = h < a.n_rep ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * a.n_rep + h) * a.q_sh + c] : 0;
   }
   MetaWords<MW> MT;              // metadata of the current tile
   uint32_t KW[8 * F::WPK], VW[8 * F::WPK];  // key / value code words of the current tile
@@ -1118,7 +1120,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   __syncthreads();
   if (direct) {
     // one split: the final output, exactly as the combine kernel would form it
-    for (int e = tid_e; e < NREP * D; e += NT) {
+    for (int e = tid_e; e < a.n_rep * D; e += NT) {
       const int h = e / D;
       const int c = e - h * D;
       float M_ = -INFINITY;
@@ -1133,12 +1135,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
           den += f * red[w * RED + NREP + h];
         }
       }
-      store_val(a.out, b * a.out_sb + (int64_t)(kvh * NREP + h) * a.out_sh + c, den > 0.f ? num / den : 0.f,
+      store_val(a.out, b * a.out_sb + (int64_t)(kvh * a.n_rep + h) * a.out_sh + c, den > 0.f ? num / den : 0.f,
                 a.out_dtype);
     }
     return;
   }
-  for (int e = tid_e; e < NREP * (D + 2); e += NT) {
+  for (int e = tid_e; e < a.n_rep * (D + 2); e += NT) {
     const int h = e / (D + 2);
     const int c = e - h * (D + 2);
     float M_ = -INFINITY;
@@ -1154,7 +1156,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         val += f * (c == D + 1 ? red[w * RED + NREP + h] : red[w * RED + 2 * NREP + h * D + c]);
       }
     }
-    ws_record<D>(a, b, kvh * NREP + h, split, n_split)[c] = val;
+    ws_record<D>(a, b, kvh * a.n_rep + h, split, n_split)[c] = val;
   }
 }
 
@@ -1177,7 +1179,9 @@ bool fold_supported(const mz_decode_args* a) {
   // 5- and 6-bit tables (8 and 16 KB each) leave room for two workgroups per
   // CU up to 4 query heads per kv-head, the 7-bit table (64 KB, one for keys
   // and values) for one 8-wave workgroup; 8 heads take the general kernel there
-  const bool nrep_ok = a->n_rep == 1 || a->n_rep == 2 || a->n_rep == 4 || (a->n_rep == 8 && a->bits <= 4);
+  // other head counts run the kernel built for the next larger count (3 -> 4,
+  // 5..7 -> 8) with the extra heads' queries zero and their outputs unwritten
+  const bool nrep_ok = (a->n_rep >= 1 && a->n_rep <= 4) || (a->n_rep <= 8 && a->bits <= 4);
   const bool one_table = a->bits < 7 || a->fold_k == a->fold_v;
   return a->bits >= 1 && a->bits <= 7 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
          one_table && a->fold_k && a->fold_v &&
@@ -1216,13 +1220,15 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const uint32_t* fv = (const uint32_t*)a->fold_v;
   const int dir = direct ? 1 : 0;
   const int cus = device_cu_count();
+  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
+  const int nrep_pad = a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0;
 #define MZ_FOLD(IOV, NR, BB)                                                                            \
   if (a->meta_dtype == MZ_F32)                                                                          \
     hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
   else                                                                                                       \
     hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
 #define MZ_FOLD_NREP(IOV, BB)            \
-  switch (a->n_rep) {                    \
+  switch (nrep_pad) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
     case 2: MZ_FOLD(IOV, 2, BB); break;  \
     case 4: MZ_FOLD(IOV, 4, BB); break;  \
@@ -1230,7 +1236,7 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
     default: return MZ_EUNSUPPORTED;     \
   }
 #define MZ_FOLD_NREP_WIDE(IOV, BB)       \
-  switch (a->n_rep) {                    \
+  switch (nrep_pad) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
     case 2: MZ_FOLD(IOV, 2, BB); break;  \
     case 4: MZ_FOLD(IOV, 4, BB); break;  \

@@ -77,9 +77,9 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         am_kernel = keep if mask == "bool" else am
     lq0 = ref.split_prefix(length, residual, 64)
     fold = (kernel_path == "fold" or (kernel_path == "auto" and d == 128 and lq0 > 0
-                                      and ((1 <= bits <= 4 and n_rep in (1, 2, 4, 8))
-                                           or (bits in (5, 6) and n_rep in (1, 2, 4))
-                                           or (bits == 7 and n_rep in (1, 2, 4) and alpha_k == alpha_v))))
+                                      and ((1 <= bits <= 4 and 1 <= n_rep <= 8)
+                                           or (bits in (5, 6) and 1 <= n_rep <= 4)
+                                           or (bits == 7 and 1 <= n_rep <= 4 and alpha_k == alpha_v))))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
                                      dequant_dtype=torch.float32 if fold else None)
@@ -171,10 +171,11 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 1- to 4-bit codes, head_dim 128, n_rep in {1, 2, 4, 8}, and 5- to 7-bit codes
-# with n_rep in {1, 2, 4} (7 bits: one alpha for keys and values): the fold
-# kernel (AUTO picks it); the same cases through the exact-dequantize kernel
-# keep that path covered too.
+# 1- to 4-bit codes, head_dim 128, n_rep 1..8, and 5- to 7-bit codes with
+# n_rep 1..4 (7 bits: one alpha for keys and values): the fold kernel (AUTO
+# picks it; n_rep 3 and 5..7 run the kernel built for 4 / 8 heads with the
+# extra heads unused); the same cases through the exact-dequantize kernel keep
+# that path covered too.
 FOLD_CASES = [
     # B, hkv, n_rep, d, length, bits, residual
     (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
@@ -220,6 +221,14 @@ FOLD_CASES = [
     (1, 2, 4, 128, 4096, 7, 128),
     (2, 1, 4, 128, 300, 7, 0),
     (1, 2, 4, 128, 900, 7, 191),
+    # head counts between the built ones (Qwen2.5-7B: 7, Qwen2.5-14B/32B: 5)
+    (2, 2, 3, 128, 1024, 4, 128),
+    (1, 2, 5, 128, 900, 4, 191),
+    (1, 1, 6, 128, 700, 2, 128),
+    (2, 2, 7, 128, 1024, 4, 128),
+    (1, 2, 7, 128, 700, 1, 128),
+    (1, 2, 3, 128, 700, 5, 128),
+    (1, 2, 3, 128, 700, 7, 128),
 ]
 
 
@@ -235,6 +244,15 @@ def test_decode_fold_and_exact_paths(case, path):
 def test_fold_split_and_mask(n_split, bits):
     mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("n_rep,bits", [(3, 4), (7, 4), (5, 2), (3, 6)])
+def test_fold_padded_heads_split_and_mask(n_rep, bits):
+    """Head counts run on a kernel built for more heads: the split records and the direct
+    output of the real heads only (their indices use the call's n_rep), masked, split."""
+    for n_split in (0, 1, 3):  # 1: one split, the kernel writes the output itself
+        mx, mean, _, _ = _run_case(2, 2, n_rep, 128, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
+        assert mx < MAX_ABS and mean < MEAN_ABS, (n_split, mx, mean)
 
 
 @pytest.mark.parametrize("bits", [4, 3, 2, 1])
