@@ -1176,12 +1176,13 @@ bool fold_supported(const mz_decode_args* a) {
   const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
-  // 5- and 6-bit tables (8 and 16 KB each) leave room for two workgroups per
-  // CU up to 4 query heads per kv-head, the 7-bit table (64 KB, one for keys
-  // and values) for one 8-wave workgroup; 8 heads take the general kernel there
-  // other head counts run the kernel built for the next larger count (3 -> 4,
+  // 8 query heads per kv-head (1 to 6 bits) take one workgroup per CU (their
+  // per-wave operand staging is twice that of 4 heads); the 7-bit table
+  // (64 KB, one for keys and values) leaves room for its 8-wave workgroup up
+  // to 4 heads, so 7-bit codes with more heads take the general kernel.
+  // Other head counts run the kernel built for the next larger count (3 -> 4,
   // 5..7 -> 8) with the extra heads' queries zero and their outputs unwritten
-  const bool nrep_ok = (a->n_rep >= 1 && a->n_rep <= 4) || (a->n_rep <= 8 && a->bits <= 4);
+  const bool nrep_ok = (a->n_rep >= 1 && a->n_rep <= 4) || (a->n_rep <= 8 && a->bits <= 6);
   const bool one_table = a->bits < 7 || a->fold_k == a->fold_v;
   return a->bits >= 1 && a->bits <= 7 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
          one_table && a->fold_k && a->fold_v &&
@@ -1235,7 +1236,7 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
     case 8: MZ_FOLD(IOV, 8, BB); break;  \
     default: return MZ_EUNSUPPORTED;     \
   }
-#define MZ_FOLD_NREP_WIDE(IOV, BB)       \
+#define MZ_FOLD_NREP4(IOV, BB)           \
   switch (nrep_pad) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
     case 2: MZ_FOLD(IOV, 2, BB); break;  \
@@ -1247,13 +1248,13 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   else if (a->bits == 3) { MZ_FOLD_NREP(IOV, 3) }      \
   else if (a->bits == 2) { MZ_FOLD_NREP(IOV, 2) }      \
   else if (a->bits == 1) { MZ_FOLD_NREP(IOV, 1) }      \
-  else if (a->bits == 5) { MZ_FOLD_NREP_WIDE(IOV, 5) } \
-  else if (a->bits == 6) { MZ_FOLD_NREP_WIDE(IOV, 6) } \
-  else if (a->bits == 7) { MZ_FOLD_NREP_WIDE(IOV, 7) } \
+  else if (a->bits == 5) { MZ_FOLD_NREP(IOV, 5) }      \
+  else if (a->bits == 6) { MZ_FOLD_NREP(IOV, 6) }      \
+  else if (a->bits == 7) { MZ_FOLD_NREP4(IOV, 7) }     \
   else return MZ_EUNSUPPORTED;
   if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
 #undef MZ_FOLD_BITS
-#undef MZ_FOLD_NREP_WIDE
+#undef MZ_FOLD_NREP4
 #undef MZ_FOLD_NREP
 #undef MZ_FOLD
   const hipError_t e = hipGetLastError();

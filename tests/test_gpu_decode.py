@@ -78,7 +78,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
     lq0 = ref.split_prefix(length, residual, 64)
     fold = (kernel_path == "fold" or (kernel_path == "auto" and d == 128 and lq0 > 0
                                       and ((1 <= bits <= 4 and 1 <= n_rep <= 8)
-                                           or (bits in (5, 6) and 1 <= n_rep <= 4)
+                                           or (bits in (5, 6) and 1 <= n_rep <= 8)
                                            or (bits == 7 and 1 <= n_rep <= 4 and alpha_k == alpha_v))))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
@@ -171,8 +171,8 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 1- to 4-bit codes, head_dim 128, n_rep 1..8, and 5- to 7-bit codes with
-# n_rep 1..4 (7 bits: one alpha for keys and values): the fold kernel (AUTO
+# 1- to 6-bit codes, head_dim 128, n_rep 1..8, and 7-bit codes with n_rep
+# 1..4 (and one alpha for keys and values): the fold kernel (AUTO
 # picks it; n_rep 3 and 5..7 run the kernel built for 4 / 8 heads with the
 # extra heads unused); the same cases through the exact-dequantize kernel keep
 # that path covered too.
@@ -229,6 +229,10 @@ FOLD_CASES = [
     (1, 2, 7, 128, 700, 1, 128),
     (1, 2, 3, 128, 700, 5, 128),
     (1, 2, 3, 128, 700, 7, 128),
+    (1, 1, 8, 128, 700, 5, 128),
+    (1, 2, 8, 128, 1024, 6, 128),
+    (2, 2, 7, 128, 900, 5, 191),
+    (1, 2, 5, 128, 700, 6, 128),
 ]
 
 
@@ -246,7 +250,7 @@ def test_fold_split_and_mask(n_split, bits):
     assert mx < MAX_ABS and mean < MEAN_ABS, (mx, mean)
 
 
-@pytest.mark.parametrize("n_rep,bits", [(3, 4), (7, 4), (5, 2), (3, 6)])
+@pytest.mark.parametrize("n_rep,bits", [(3, 4), (7, 4), (5, 2), (3, 6), (8, 5), (6, 6)])
 def test_fold_padded_heads_split_and_mask(n_rep, bits):
     """Head counts run on a kernel built for more heads: the split records and the direct
     output of the real heads only (their indices use the call's n_rep), masked, split."""
