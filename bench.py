@@ -1,6 +1,6 @@
-"""Benchmark: packed-KV decode attention on one MI355X (BASELINE.json metric).
+"""Benchmark: packed-KV decode attention on one MI355X (HBM GB/s of the decode call).
 
-Default workload = BASELINE config 1: Qwen3-8B layer shape, query [64, 32, 1,
+Default workload = benchmark config 1: Qwen3-8B layer shape, query [64, 32, 1,
 128] bf16, KV cache [64, 8, 4096, 128] of which the oldest 3968 tokens are
 mu_zero 4-bit packed (group 64, fp16 min/scale) and the last 128 are the bf16
 residual window.  One step = one decode-attention call of one layer as the

@@ -243,7 +243,7 @@ def test_quantize_blocks_aligned_vector_path(dname, bits):
 
 
 def _config0_inputs():
-    """K, V [1, 8, 1024, 128] ~ N(0, 1) from a CPU generator seeded 1234
+    """Benchmark config 0: K, V [1, 8, 1024, 128] ~ N(0, 1) from a CPU generator seeded 1234
     (drawn K, V, Q), 4 of 128 key channels scaled x10."""
     g = torch.Generator().manual_seed(1234)
     k = torch.randn(1, 8, 1024, 128, generator=g)

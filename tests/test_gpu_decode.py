@@ -9,7 +9,7 @@ dtype like the reference's dequantize-then-attend fallback
 (attention.py:213-226, layer.py:263); the 4-/2-bit fold kernel keeps dequantized
 values at full precision like the reference's fused CUDA qk/av kernels
 (fp32 codebooks, loader.py:197-263).  The two oracles differ from each other
-by up to ~1.3e-2 at short contexts, so each kernel is held to its own.  Tolerances: 2e-3 max-abs and
+by up to ~1.3e-2 at short contexts, so each kernel is held to its own.  Tolerances (the target of this path): 2e-3 max-abs and
 1e-3 mean-abs.  They are checked on the kernel's fp32 output (the kernel's own
 error), and on its bf16 output with what rounding the exact answer itself to
 bf16 costs added: half a bf16 ulp of the exact value to the max bound, and
