@@ -215,7 +215,7 @@ typedef struct mz_decode_args {
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 1 to 7, head_dim 128, aligned prefixes, n_rep 1 to 8 for 1 to
+ * applies (bits 1 to 7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8 for 1 to
  * 6 bits and 1 to 4 for 7 (other counts than 1, 2, 4, 8 run the kernel built
  * for the next larger one), fold tables given, at 7 bits one table for keys
  * and values) and the exact-dequantize kernel otherwise. */

@@ -46,6 +46,9 @@
 // a power-of-two scale per key group and an accumulator exponent for the
 // values, folded into the logits and into the online-softmax rescale.
 //
+// head_dim 64 runs the same layout with the k-tiles of channels 64..127 and
+// the second value group absent.
+//
 // Launch: one workgroup of 4 waves (7 bits: 8) per (batch, kv-head, split); a split is a
 // run of tiles (residual tiles first), waves take every 4th; the split's
 // (m, l, acc) goes to the workspace and the shared combine kernel merges
@@ -282,30 +285,40 @@ __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t&
   else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff + imm, 0);
 }
 
-// All metadata of a tile (loaded one tile ahead of its use).
-template <int MW>
+// All metadata of a tile (loaded one tile ahead of its use).  HD = head_dim
+// (64 or 128): HD / 64 value groups per token; with HD = 64 the key entries
+// of lanes 32..63 lie past the tile's own (they are not used).
+template <int MW, int HD>
 __device__ __forceinline__ void load_meta_tile(MetaWords<MW>& t, const Bufs& bf, int tile, int lane) {
   constexpr int ES = 2 * MW;  // bytes per metadata entry
-  const int kmo = 2 * lane * ES, kms = tile * D * ES;
+  constexpr int NGH = HD / 64;
+  const int kmo = 2 * lane * ES, kms = tile * HD * ES;
   load_meta<MW>(t.kmn, bf.kmn, kmo, kms);
   load_meta<MW>(t.ksc, bf.ksc, kmo, kms);
-  const int vmo = NG * lane * ES, vms = tile * TILE * NG * ES;
-  load_meta<MW>(t.vmn, bf.vmn, vmo, vms);
-  load_meta<MW>(t.vsc, bf.vsc, vmo, vms);
+  const int vmo = NGH * lane * ES, vms = tile * TILE * NGH * ES;
+  if constexpr (NGH == 1 && MW == 1) {
+    // one 16-bit entry per token: a 32-bit read would reach past the buffer's
+    // end at the last token of the last tile (and then read 0 as a whole)
+    t.vmn[0] = __builtin_amdgcn_raw_buffer_load_b16(bf.vmn, vmo, vms, 0);
+    t.vsc[0] = __builtin_amdgcn_raw_buffer_load_b16(bf.vsc, vmo, vms, 0);
+  } else {
+    load_meta<MW>(t.vmn, bf.vmn, vmo, vms);
+    load_meta<MW>(t.vsc, bf.vsc, vmo, vms);
+  }
 }
 
 // Key code words of a tile (issued once the previous tile's key words are
 // consumed: they land while the previous tile's P.V runs).
-template <int BITS>
+template <int BITS, int HD>
 __device__ __forceinline__ void load_kw(uint32_t (&kw)[8 * Fmt<BITS>::WPK], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
   const int n = lane & 15, g = lane >> 4;
-  const int soff = tile * D * F::QB;
+  const int soff = tile * HD * F::QB;
   if constexpr (F::WIDE) {
     // kw[kt*4+ii] = the lane's dword of row 16kt+4g+ii
     const int voff = 4 * g * F::QB + wide_byte<BITS>(n);
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
+    for (int kt = 0; kt < HD / 16; ++kt)
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
         kw[kt * 4 + ii] = __builtin_amdgcn_raw_buffer_load_b32(bf.kp, voff, soff + (16 * kt + ii) * F::QB, 0);
@@ -313,40 +326,41 @@ __device__ __forceinline__ void load_kw(uint32_t (&kw)[8 * Fmt<BITS>::WPK], cons
   }
   const int voff = (4 * g + (n & 1)) * F::QB + pair_byte<BITS>(n >> 1);
 #pragma unroll
-  for (int kt = 0; kt < 8; ++kt)
+  for (int kt = 0; kt < HD / 16; ++kt)
 #pragma unroll
     for (int p = 0; p < 2; ++p) kw[kt * 2 + p] = load_code_word<BITS>(bf.kp, voff, soff, (16 * kt + 2 * p) * F::QB);
 }
 
 // Value code words of a tile (issued at the start of the tile: they land
 // while its Q.K runs).
-template <int BITS>
+template <int BITS, int HD>
 __device__ __forceinline__ void load_vw(uint32_t (&vw)[8 * Fmt<BITS>::WPK], const Bufs& bf, int tile, int lane) {
   using F = Fmt<BITS>;
+  constexpr int NGH = HD / 64;
   const int n = lane & 15, g = lane >> 4;
-  const int soff = tile * TILE * NG * F::QB;
+  const int soff = tile * TILE * NGH * F::QB;
   if constexpr (F::WIDE) {
-    // vw[(kt*NG+vg)*4+ii] = the lane's dword of token row 16kt+4g+ii, value group vg
-    const int voff = 4 * g * (NG * F::QB) + wide_byte<BITS>(n);
+    // vw[(kt*NGH+vg)*4+ii] = the lane's dword of token row 16kt+4g+ii, value group vg
+    const int voff = 4 * g * (NGH * F::QB) + wide_byte<BITS>(n);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg)
+      for (int vg = 0; vg < NGH; ++vg)
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
-          vw[(kt * NG + vg) * 4 + ii] = __builtin_amdgcn_raw_buffer_load_b32(
-              bf.vp, voff, soff + (16 * kt + ii) * (NG * F::QB) + F::QB * vg, 0);
+          vw[(kt * NGH + vg) * 4 + ii] = __builtin_amdgcn_raw_buffer_load_b32(
+              bf.vp, voff, soff + (16 * kt + ii) * (NGH * F::QB) + F::QB * vg, 0);
     return;
   }
-  const int voff = (4 * g + (n & 1)) * (NG * F::QB) + pair_byte<BITS>(n >> 1);
+  const int voff = (4 * g + (n & 1)) * (NGH * F::QB) + pair_byte<BITS>(n >> 1);
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int vg = 0; vg < NG; ++vg)
+    for (int vg = 0; vg < NGH; ++vg)
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        vw[(kt * NG + vg) * 2 + p] =
-            load_code_word<BITS>(bf.vp, voff, soff, (16 * kt + 2 * p) * (NG * F::QB) + F::QB * vg);
+        vw[(kt * NGH + vg) * 2 + p] =
+            load_code_word<BITS>(bf.vp, voff, soff, (16 * kt + 2 * p) * (NGH * F::QB) + F::QB * vg);
 }
 
 __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
@@ -469,7 +483,10 @@ __device__ __forceinline__ void read_ktile(const uint8_t* smem, const uint32_t (
   }
 }
 
-template <int IO, int NREP, int BITS, int MW>
+// HD: head_dim, 64 or 128.  The LDS layout is the 128-channel one either way;
+// with 64 channels the k-tiles of channels 64..127 and the second value group
+// are simply absent (lanes 32..63 compute no key scalar of the tile).
+template <int IO, int NREP, int BITS, int MW, int HD>
 __global__ __launch_bounds__((64 * waves_for<NREP, BITS>()))
 __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>()))) void fold_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, const uint32_t* __restrict__ ftab_k,
@@ -484,6 +501,8 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   constexpr int RS = 16 / NREP;                 // MFMA row stride between query heads
   static_assert(RS >= 2, "QK needs a second row per head for the low part of the key product");
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;   // head slots per lane of the MFMA output
+  static_assert(HD == 64 || HD == 128, "head_dim");
+  constexpr int NGH = HD / 64;                  // value groups per token
   __shared__ __align__(16) uint8_t smem[S::TOTAL];
 
   const int lane = threadIdx.x & 63;
@@ -506,13 +525,13 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   Bufs bf;
   {
     const int64_t ng = a.n_groups;
-    bf.kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * F::QB);
-    bf.vp = make_buf(a.v_packed + b * a.vp_sb + kvh * a.vp_sh, ng * TILE * NG * F::QB);
+    bf.kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * HD * F::QB);
+    bf.vp = make_buf(a.v_packed + b * a.vp_sb + kvh * a.vp_sh, ng * TILE * NGH * F::QB);
     const int64_t km = b * a.km_sb + kvh * a.km_sh, vm = b * a.vm_sb + kvh * a.vm_sh;
-    bf.kmn = make_buf((const uint8_t*)a.k_mn + km * meta_es, ng * D * meta_es);
-    bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * D * meta_es);
-    bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NG * meta_es);
-    bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NG * meta_es);
+    bf.kmn = make_buf((const uint8_t*)a.k_mn + km * meta_es, ng * HD * meta_es);
+    bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * HD * meta_es);
+    bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NGH * meta_es);
+    bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NGH * meta_es);
     bf.kr = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
     bf.vr = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
   }
@@ -557,13 +576,16 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   for (int j = 0; j < QW; ++j) {
     const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
     // heads past n_rep (a kernel built for more heads) get a zero query; their
-    // outputs are not written
-    qraw[j] = h < a.n_rep ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * a.n_rep + h) * a.q_sh + c] : 0;
+    // outputs are not written.  Channels past HD (head_dim 64 in the
+    // 128-channel layout) are zero too.
+    qraw[j] = h < a.n_rep && c < HD
+                  ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * a.n_rep + h) * a.q_sh + c]
+                  : 0;
   }
   MetaWords<MW> MT;              // metadata of the current tile
   uint32_t KW[8 * F::WPK], VW[8 * F::WPK];  // key / value code words of the current tile
-  load_meta_tile<MW>(MT, bf, min(tile_of(v0), q_last), lane);
-  load_kw<BITS>(KW, bf, min(tile_of(v0), q_last), lane);
+  load_meta_tile<MW, HD>(MT, bf, min(tile_of(v0), q_last), lane);
+  load_kw<BITS, HD>(KW, bf, min(tile_of(v0), q_last), lane);
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
     if (threadIdx.x + j * NT < TBL / 4) {
@@ -622,7 +644,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   // (wide codes, whose code words take twice the registers, re-read it)
   u32x4 q16_op[4];
 #pragma unroll
-  for (int kq = 0; kq < 4; ++kq)
+  for (int kq = 0; kq < HD / 32; ++kq)
     q16_op[kq] = F::WIDE ? u32x4{0u, 0u, 0u, 0u} : *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2);
   const uint32_t* pv_row = (rA == 0 ? pa : pa_lo) + hA * LROW;  // PV A operand: this row's head
   const uint8_t* qio_row = rA == 0 ? smem + S::Q_IO + hA * HROW * 4 : smem + S::ZERO;
@@ -635,12 +657,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   float m_run[HS], l_run[HS];
 #pragma unroll
   for (int s = 0; s < HS; ++s) m_run[s] = -INFINITY, l_run[s] = 0.f;
-  f32x4 acc[NG][4];
+  f32x4 acc[NGH][4];
   // the values' constant part sum_t p_t * a_t per head slot and value group
   // (fp32; the same in the 16 lanes of a head's row)
-  float acc_a[HS][NG];
+  float acc_a[HS][NGH];
 #pragma unroll
-  for (int vg = 0; vg < NG; ++vg) {
+  for (int vg = 0; vg < NGH; ++vg) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[vg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -672,6 +694,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       sc.k1 = group_scalars<F::QMAX>(kmn.y, ksc.y);
       sc.kmx = fmaxf(fmaxf(fabsf(sc.k0.a), fmaxf(sc.k0.bp, -sc.k0.bn)),
                      fmaxf(fabsf(sc.k1.a), fmaxf(sc.k1.bp, -sc.k1.bn)));
+      // head_dim 64: lanes 32..63 hold no channel of the tile (their stores
+      // below land in layout slots the tile does not read)
+      if constexpr (HD < D) sc.kmx = 2 * lane < HD ? sc.kmx : 0.f;
       // zero levels of channels 2*lane, 2*lane+1 = (kt, g, ii) = (lane/8, lane/2 % 4, 2*(lane%2) + {0,1})
       // (pair codes: the row pair's block offset in the table; quad codes: the
       // row quad's, from this lane's rows and its partner's)
@@ -690,8 +715,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
       sc.v0 = group_scalars<F::QMAX>(vmn.x, vsc.x);
       sc.v1 = group_scalars<F::QMAX>(vmn.y, vsc.y);
-      sc.vmx = fmaxf(fmaxf(fabsf(sc.v0.a), fmaxf(sc.v0.bp, -sc.v0.bn)),
-                     fmaxf(fabsf(sc.v1.a), fmaxf(sc.v1.bp, -sc.v1.bn)));
+      sc.vmx = fmaxf(fabsf(sc.v0.a), fmaxf(sc.v0.bp, -sc.v0.bn));
+      // one value group (head_dim 64): the second entry is the next token's
+      if constexpr (NGH > 1) sc.vmx = fmaxf(sc.vmx, fmaxf(fabsf(sc.v1.a), fmaxf(sc.v1.bp, -sc.v1.bn)));
       // zero levels of token lane = (kt, g, ii) = (lane/16, lane/4 % 4, lane % 4), both value groups
       const int vzo = (((lane >> 2) & 3) * 4 + (lane >> 4)) * 4 + (lane & 3);
       if constexpr (F::QUAD) {
@@ -764,9 +790,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   auto process = [&](auto quant_tag, const int tile, const int tn) {
     constexpr bool quant = decltype(quant_tag)::value;
     const int tl = min(tn, q_last);
-    load_vw<BITS>(VW, bf, min(tile, q_last), lane);
+    load_vw<BITS, HD>(VW, bf, min(tile, q_last), lane);
     MetaWords<MW> MN;
-    load_meta_tile<MW>(MN, bf, tl, lane);
+    load_meta_tile<MW, HD>(MN, bf, tl, lane);
     int n_valid, pos0, r0 = 0;
     if constexpr (quant) {
       n_valid = TILE;
@@ -781,10 +807,10 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
     // this lane's value scalars (a, bp, bn of tokens 4n..4n+3, per value
     // group), read once the tile's scalars are in LDS: at the start of a
     // quantized tile, so the reads complete behind its Q.K
-    f32x4 va_r[NG], vbp_r[NG], vbn_r[NG];
+    f32x4 va_r[NGH], vbp_r[NGH], vbn_r[NGH];
     auto read_value_scalars = [&]() __attribute__((always_inline)) {
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
+      for (int vg = 0; vg < NGH; ++vg) {
         va_r[vg] = *(const f32x4*)(W + S::VA + (vg * TILE + 4 * n) * 4);
         vbp_r[vg] = *(const f32x4*)(W + S::VBP + (vg * TILE + 4 * n) * 4);
         vbn_r[vg] = *(const f32x4*)(W + S::VBN + (vg * TILE + 4 * n) * 4);
@@ -799,7 +825,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       // query against a's high part, then its low part), then the folded codes
       f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kq = 0; kq < 4; ++kq) {
+      for (int kq = 0; kq < HD / 32; ++kq) {
         const u32x4 A = F::WIDE ? *(const u32x4*)(q16_row + (32 * kq + 8 * g) * 2) : q16_op[kq];
 #pragma unroll
         for (int part = 0; part < 2; ++part) {
@@ -824,20 +850,21 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       addr_ktile<BITS>(KW, kzp(0), grep, odd, lsh, adc);
       read_ktile<S::TBL_K, F::PAIR, F::QUAD>(smem, adc, Bc);
       addr_ktile<BITS>(KW + F::WPK, kzp(1), grep, odd, lsh, adn);
+      constexpr int KT = HD / 16;  // k-tiles of 16 channels
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) {
         u32x4 An;
-        if (kt < 7) {
+        if (kt < KT - 1) {
           An = *(const u32x4*)(a_hi_row + (16 * (kt + 1) + 4 * g) * 4);
           read_ktile<S::TBL_K, F::PAIR, F::QUAD>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (kt < 6) addr_ktile<BITS>(KW + F::WPK * (kt + 2), kzp(kt + 2), grep, odd, lsh, adn);
+        if (kt < KT - 2) addr_ktile<BITS>(KW + F::WPK * (kt + 2), kzp(kt + 2), grep, odd, lsh, adn);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], s[jt]);
         __builtin_amdgcn_sched_barrier(0);
-        if (kt < 7) {
+        if (kt < KT - 1) {
           Ac = An;
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
@@ -853,7 +880,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       unscale = scaling2;
       const float unit = ldexpf(1.f, kv_exp);
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
+      for (int vg = 0; vg < NGH; ++vg) {
         ((float*)(W + S::VBP))[vg * TILE + lane] = unit;
         ((float*)(W + S::VBN))[vg * TILE + lane] = 0.f;
         ((float*)(W + S::VA))[vg * TILE + lane] = 0.f;
@@ -866,9 +893,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       // every bound: rows past the residual read 0 (their logits are masked);
       // the 32-column step rides in the scalar offset and never leaves a row.
       const int kst = a.kr_st * 2;
-      const __amdgpu_buffer_rsrc_t krb = make_buf(bf.kr + (int64_t)r0 * a.kr_st, (n_valid - 1) * kst + D * 2);
+      const __amdgpu_buffer_rsrc_t krb = make_buf(bf.kr + (int64_t)r0 * a.kr_st, (n_valid - 1) * kst + HD * 2);
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
+      for (int kh = 0; kh < HD / 64; ++kh) {
         u32x4 kb[2][4];
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2)
@@ -887,7 +914,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       wave_lds_sync();  // the (1, 0) / 0 scalars above are read by other lanes below
       read_value_scalars();
     }
-    load_kw<BITS>(KW, bf, tl, lane);
+    load_kw<BITS, HD>(KW, bf, tl, lane);
 
     // ---------- online softmax in registers: head slot s of this lane group
     // owns tokens 4n+jt (jt = 0..3) of the 16 lanes of its row
@@ -931,7 +958,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       // weights as the rest of the row
       const float fa = corr[sl] * fexp;
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
+      for (int vg = 0; vg < NGH; ++vg) {
         const f32x4 av = va_r[vg];
         float c = (float)p01.x * av[0];
         c = __builtin_fmaf((float)p01.y, av[1], c);
@@ -944,7 +971,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         // as fp16 hi + lo pairs
         const int h = h0 + sl;
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
+        for (int vg = 0; vg < NGH; ++vg) {
           const f32x4 bp = vbp_r[vg];
           const f32x4 bn = vbn_r[vg];
           const uint2 w0 = split_product(p01.x, bp[0], bn[0]);
@@ -968,7 +995,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       const int i = sl * RS;
       const float f = corr[sl] * fexp;
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) {
+      for (int vg = 0; vg < NGH; ++vg) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[vg][j][i] *= f, acc[vg][j][i + 1] *= f;
       }
@@ -977,10 +1004,12 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
     // ---------- acc += P V
     if constexpr (quant) {
       // steps st = (kt, vg), software-pipelined like Q.K
-      u32x4 vz[NG];
+      u32x4 vz[NGH];
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
-      auto vzp = [&](int st) { return vz[st % NG][st / NG]; };
+      for (int vg = 0; vg < NGH; ++vg) vz[vg] = *(const u32x4*)(W + S::VZP + vg * 64 + g * 16);
+      auto vzp = [&](int st) { return vz[st % NGH][st / NGH]; };
+      constexpr int NST = 4 * NGH;  // P.V steps (k-tile, value group)
+      constexpr int CPS = 8 / NST;  // scalar chunks per step
       u32x4 Ac = *(const u32x4*)(pv_row + 4 * g);
       u32x4 Bc[4], Bn[4];
       uint32_t adc[4][4], adn[4][4];
@@ -988,21 +1017,22 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       read_ktile<S::TBL_V, F::PAIR, F::QUAD>(smem, adc, Bc);
       addr_ktile<BITS>(VW + F::WPK, vzp(1), grep, odd, lsh, adn);
 #pragma unroll
-      for (int st = 0; st < 4 * NG; ++st) {
-        const int vg = st % NG;
+      for (int st = 0; st < NST; ++st) {
+        const int vg = st % NGH;
         u32x4 An;
-        if (st + 1 < 4 * NG) {
-          const int kt1 = (st + 1) / NG, vg1 = (st + 1) % NG;
+        if (st + 1 < NST) {
+          const int kt1 = (st + 1) / NGH, vg1 = (st + 1) % NGH;
           An = *(const u32x4*)(pv_row + vg1 * NREP * LROW + 16 * kt1 + 4 * g);
           read_ktile<S::TBL_V, F::PAIR, F::QUAD>(smem, adn, Bn);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (st + 2 < 4 * NG) addr_ktile<BITS>(VW + F::WPK * (st + 2), vzp(st + 2), grep, odd, lsh, adn);
-        scal_chunk(MN, st);  // the next tile's scalars, chunk st
+        if (st + 2 < NST) addr_ktile<BITS>(VW + F::WPK * (st + 2), vzp(st + 2), grep, odd, lsh, adn);
+#pragma unroll
+        for (int c = 0; c < CPS; ++c) scal_chunk(MN, CPS * st + c);  // the next tile's scalars
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = Mfma<MZ_F16>::run(Ac, Bc[jt], acc[vg][jt]);
         __builtin_amdgcn_sched_barrier(0);
-        if (st + 1 < 4 * NG) {
+        if (st + 1 < NST) {
           Ac = An;
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
@@ -1020,10 +1050,10 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         const u32x4 pd = *(const u32x4*)(pv_row + 16 * kt + 4 * g);  // (p, 0) pairs (row 1: zeros)
         const int rows = n_valid - 16 * kt;
         const __amdgpu_buffer_rsrc_t vrb =
-            make_buf(bf.vr + (int64_t)(r0 + 16 * kt) * a.vr_st, rows > 0 ? (rows - 1) * vst + D * 2 : 0);
-        uint32_t vv[NG][4][2];
+            make_buf(bf.vr + (int64_t)(r0 + 16 * kt) * a.vr_st, rows > 0 ? (rows - 1) * vst + HD * 2 : 0);
+        uint32_t vv[NGH][4][2];
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg)
+        for (int vg = 0; vg < NGH; ++vg)
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) {
             const auto raw =
@@ -1032,7 +1062,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
             vv[vg][ii][1] = raw[1];
           }
 #pragma unroll
-        for (int vg = 0; vg < NG; ++vg) {
+        for (int vg = 0; vg < NGH; ++vg) {
           uint32_t (&v4)[4][2] = vv[vg];
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) {  // channel 64vg + 4n + jt
@@ -1088,7 +1118,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   // ---------------- merge the waves and write this split's partial records
   __syncthreads();
   float* red = (float*)(smem + S::WAVE0);
-  constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D]
+  constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D] (first HD used)
   // lane-derived indices recomputed from the lane id (mbcnt) instead of kept
   // live across the tile loop, where every register is taken
   const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
@@ -1104,13 +1134,13 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
       // the row's partial sums (the 16 lanes of lane group g_e)
       const float l_row = group_reduce<16>(l_run[sl], OpAdd());
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg) acc_a[sl][vg] = group_reduce<16>(acc_a[sl][vg], OpAdd());
+      for (int vg = 0; vg < NGH; ++vg) acc_a[sl][vg] = group_reduce<16>(acc_a[sl][vg], OpAdd());
       if (n == 0) {
         w[h] = m_run[sl];
         w[NREP + h] = l_row;
       }
 #pragma unroll
-      for (int vg = 0; vg < NG; ++vg)
+      for (int vg = 0; vg < NGH; ++vg)
         *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n) =
             f32x4{acc[vg][0][i] + acc[vg][0][i + 1] + acc_a[sl][vg], acc[vg][1][i] + acc[vg][1][i + 1] + acc_a[sl][vg],
                   acc[vg][2][i] + acc[vg][2][i + 1] + acc_a[sl][vg], acc[vg][3][i] + acc[vg][3][i + 1] + acc_a[sl][vg]} *
@@ -1120,9 +1150,9 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
   __syncthreads();
   if (direct) {
     // one split: the final output, exactly as the combine kernel would form it
-    for (int e = tid_e; e < a.n_rep * D; e += NT) {
-      const int h = e / D;
-      const int c = e - h * D;
+    for (int e = tid_e; e < a.n_rep * HD; e += NT) {
+      const int h = e / HD;
+      const int c = e - h * HD;
       float M_ = -INFINITY;
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
@@ -1140,23 +1170,23 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
     }
     return;
   }
-  for (int e = tid_e; e < a.n_rep * (D + 2); e += NT) {
-    const int h = e / (D + 2);
-    const int c = e - h * (D + 2);
+  for (int e = tid_e; e < a.n_rep * (HD + 2); e += NT) {
+    const int h = e / (HD + 2);
+    const int c = e - h * (HD + 2);
     float M_ = -INFINITY;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
     float val = 0.f;
-    if (c == D) {
+    if (c == HD) {
       val = M_ * kLn2;  // the record's maximum in natural-log units
     } else if (M_ != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) {
         const float f = __builtin_amdgcn_exp2f(red[w * RED + h] - M_);
-        val += f * (c == D + 1 ? red[w * RED + NREP + h] : red[w * RED + 2 * NREP + h * D + c]);
+        val += f * (c == HD + 1 ? red[w * RED + NREP + h] : red[w * RED + 2 * NREP + h * D + c]);
       }
     }
-    ws_record<D>(a, b, kvh * a.n_rep + h, split, n_split)[c] = val;
+    ws_record<HD>(a, b, kvh * a.n_rep + h, split, n_split)[c] = val;
   }
 }
 
@@ -1173,8 +1203,9 @@ bool fold_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   const int64_t qb = 8 * (int64_t)a->bits;
   // buffer-resource ranges are 32-bit
-  const bool fits = (int64_t)a->n_groups * fold::TILE * fold::NG * qb < ((int64_t)1 << 31) &&
-                    (int64_t)a->n_groups * fold::D * es < ((int64_t)1 << 31);
+  const int64_t ngv = a->head_dim / 64;  // value groups per token
+  const bool fits = (int64_t)a->n_groups * fold::TILE * ngv * qb < ((int64_t)1 << 31) &&
+                    (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
   // 8 query heads per kv-head (1 to 6 bits) take one workgroup per CU (their
   // per-wave operand staging is twice that of 4 heads); the 7-bit table
@@ -1184,7 +1215,7 @@ bool fold_supported(const mz_decode_args* a) {
   // 5..7 -> 8) with the extra heads' queries zero and their outputs unwritten
   const bool nrep_ok = (a->n_rep >= 1 && a->n_rep <= 4) || (a->n_rep <= 8 && a->bits <= 6);
   const bool one_table = a->bits < 7 || a->fold_k == a->fold_v;
-  return a->bits >= 1 && a->bits <= 7 && a->head_dim == 128 && a->n_groups > 0 && fits && aligned && nrep_ok &&
+  return a->bits >= 1 && a->bits <= 7 && (a->head_dim == 128 || a->head_dim == 64) && a->n_groups > 0 && fits && aligned && nrep_ok &&
          one_table && a->fold_k && a->fold_v &&
          ((uintptr_t)a->fold_k % 4) == 0 && ((uintptr_t)a->fold_v % 4) == 0 &&
          ((uintptr_t)a->k_packed % 4) == 0 && ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 &&
@@ -1223,11 +1254,14 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const int cus = device_cu_count();
   // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
   const int nrep_pad = a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0;
-#define MZ_FOLD(IOV, NR, BB)                                                                            \
+#define MZ_FOLD_HD(IOV, NR, BB, HD)                                                                     \
   if (a->meta_dtype == MZ_F32)                                                                          \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 2, HD>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus); \
   else                                                                                                       \
-    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
+    hipLaunchKernelGGL((fold::fold_kernel<IOV, NR, BB, 1, HD>), grid, dim3(64 * fold::waves_for<NR, BB>()), 0, s, *a, tps, ns, fk, fv, dir, cus)
+#define MZ_FOLD(IOV, NR, BB)                                        \
+  if (a->head_dim == 128) { MZ_FOLD_HD(IOV, NR, BB, 128); } \
+  else { MZ_FOLD_HD(IOV, NR, BB, 64); }
 #define MZ_FOLD_NREP(IOV, BB)            \
   switch (nrep_pad) {                    \
     case 1: MZ_FOLD(IOV, 1, BB); break;  \
@@ -1257,6 +1291,7 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
 #undef MZ_FOLD_NREP4
 #undef MZ_FOLD_NREP
 #undef MZ_FOLD
+#undef MZ_FOLD_HD
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MZ_OK : (int)e;
 }

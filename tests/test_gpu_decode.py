@@ -76,7 +76,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         am = torch.zeros(B, 1, 1, length, dtype=dtype).masked_fill_(~keep, torch.finfo(dtype).min)
         am_kernel = keep if mask == "bool" else am
     lq0 = ref.split_prefix(length, residual, 64)
-    fold = (kernel_path == "fold" or (kernel_path == "auto" and d == 128 and lq0 > 0
+    fold = (kernel_path == "fold" or (kernel_path == "auto" and d in (64, 128) and lq0 > 0
                                       and ((1 <= bits <= 4 and 1 <= n_rep <= 8)
                                            or (bits in (5, 6) and 1 <= n_rep <= 8)
                                            or (bits == 7 and 1 <= n_rep <= 4 and alpha_k == alpha_v))))
@@ -171,7 +171,7 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 1- to 6-bit codes, head_dim 128, n_rep 1..8, and 7-bit codes with n_rep
+# 1- to 6-bit codes, head_dim 64 or 128, n_rep 1..8, and 7-bit codes with n_rep
 # 1..4 (and one alpha for keys and values): the fold kernel (AUTO
 # picks it; n_rep 3 and 5..7 run the kernel built for 4 / 8 heads with the
 # extra heads unused); the same cases through the exact-dequantize kernel keep
@@ -233,6 +233,17 @@ FOLD_CASES = [
     (1, 2, 8, 128, 1024, 6, 128),
     (2, 2, 7, 128, 900, 5, 191),
     (1, 2, 5, 128, 700, 6, 128),
+    # head_dim 64 (one value group; k-tiles of channels 64..127 absent)
+    (2, 2, 4, 64, 1024, 4, 128),
+    (1, 2, 4, 64, 4096, 4, 128),
+    (2, 1, 4, 64, 300, 4, 0),
+    (1, 2, 4, 64, 900, 2, 191),
+    (1, 2, 1, 64, 700, 1, 128),
+    (1, 2, 8, 64, 700, 3, 128),
+    (1, 2, 7, 64, 700, 4, 128),
+    (1, 2, 4, 64, 700, 5, 128),
+    (1, 2, 2, 64, 700, 6, 128),
+    (1, 2, 4, 64, 700, 7, 128),
 ]
 
 
@@ -257,6 +268,18 @@ def test_fold_padded_heads_split_and_mask(n_rep, bits):
     for n_split in (0, 1, 3):  # 1: one split, the kernel writes the output itself
         mx, mean, _, _ = _run_case(2, 2, n_rep, 128, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
         assert mx < MAX_ABS and mean < MEAN_ABS, (n_split, mx, mean)
+
+
+@pytest.mark.parametrize("bits", [4, 2, 6])
+def test_fold_head_dim_64_split_and_mask(bits):
+    """head_dim 64 on the fold kernel: split records, direct output and masks; fp16 io with
+    fp32 and bf16 metadata (the value entries one per token)."""
+    for n_split in (0, 1, 3):
+        mx, mean, _, _ = _run_case(2, 2, 4, 64, 2000, bits, 128, mask=True, n_split=n_split, kernel_path="fold")
+        assert mx < MAX_ABS and mean < MEAN_ABS, (n_split, mx, mean)
+    for dtype, meta in ((torch.float16, torch.float32), (torch.bfloat16, torch.bfloat16)):
+        mx, mean, _, _ = _run_case(1, 2, 4, 64, 900, bits, 128, dtype=dtype, meta=meta, kernel_path="fold")
+        assert mx < MAX_ABS and mean < MEAN_ABS, (dtype, meta, mx, mean)
 
 
 @pytest.mark.parametrize("bits", [4, 3, 2, 1])
@@ -305,7 +328,7 @@ def test_single_split_direct_output_matches_two_kernel_path(bits):
 @pytest.mark.parametrize("bits,d", [(5, 128), (8, 128), (4, 64), (7, 64)])
 def test_general_single_split_direct_output_matches_two_kernel_path(bits, d):
     """The general kernel with one split writes the output itself, bit-identical to its workspace +
-    combine path (7-8 bits and head_dim 64 always take this kernel; 5 bits through the exact path)."""
+    combine path (8 bits always takes this kernel; the others through the exact path)."""
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(2, 2, 900, d, 8, seed=5)
     _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=3.0, group_size=64, residual=128)
