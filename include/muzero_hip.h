@@ -215,10 +215,10 @@ typedef struct mz_decode_args {
 } mz_decode_args;
 
 /* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 1 to 7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8 for 1 to
- * 6 bits and 1 to 4 for 7 (other counts than 1, 2, 4, 8 run the kernel built
- * for the next larger one), fold tables given, at 7 bits one table for keys
- * and values) and the exact-dequantize kernel otherwise. */
+ * applies (bits 1 to 7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8
+ * (other counts than 1, 2, 4, 8 run the kernel built for the next larger
+ * one), fold tables given, at 7 bits one table for keys and values) and the
+ * exact-dequantize kernel otherwise. */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments

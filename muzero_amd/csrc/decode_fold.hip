@@ -72,9 +72,10 @@ constexpr int TILE = 64;  // tokens per tile
 // 4 query heads) measured 13 % slower at config 1: more waves per CU contend
 // for its LDS rather than hide more latency.
 // 7-bit codes: one workgroup of 8 waves per CU (its 64 KB table then serves
-// the CU's two waves per SIMD).
+// the CU's two waves per SIMD); with 8 query heads (one wave per SIMD by
+// registers) one workgroup of 4.
 template <int NREP, int BITS>
-constexpr int waves_for() { return BITS >= 7 ? 8 : 4; }
+constexpr int waves_for() { return BITS >= 7 && NREP <= 4 ? 8 : 4; }
 template <int NREP>
 constexpr int waves_per_simd() { return 2; }
 // (P, N) table in LDS.  Up to 4 bits: entry (zl, q) replicated for the 4
@@ -1207,13 +1208,12 @@ bool fold_supported(const mz_decode_args* a) {
   const bool fits = (int64_t)a->n_groups * fold::TILE * ngv * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * fold::TILE;
-  // 8 query heads per kv-head (1 to 6 bits) take one workgroup per CU (their
-  // per-wave operand staging is twice that of 4 heads); the 7-bit table
-  // (64 KB, one for keys and values) leaves room for its 8-wave workgroup up
-  // to 4 heads, so 7-bit codes with more heads take the general kernel.
-  // Other head counts run the kernel built for the next larger count (3 -> 4,
-  // 5..7 -> 8) with the extra heads' queries zero and their outputs unwritten
-  const bool nrep_ok = (a->n_rep >= 1 && a->n_rep <= 4) || (a->n_rep <= 8 && a->bits <= 6);
+  // 8 query heads per kv-head take one workgroup per CU (their per-wave
+  // operand staging is twice that of 4 heads; at 7 bits a workgroup of 4
+  // waves beside the 64 KB table).  Other head counts run the kernel built
+  // for the next larger count (3 -> 4, 5..7 -> 8) with the extra heads'
+  // queries zero and their outputs unwritten
+  const bool nrep_ok = a->n_rep >= 1 && a->n_rep <= 8;
   const bool one_table = a->bits < 7 || a->fold_k == a->fold_v;
   return a->bits >= 1 && a->bits <= 7 && (a->head_dim == 128 || a->head_dim == 64) && a->n_groups > 0 && fits && aligned && nrep_ok &&
          one_table && a->fold_k && a->fold_v &&
@@ -1270,13 +1270,6 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
     case 8: MZ_FOLD(IOV, 8, BB); break;  \
     default: return MZ_EUNSUPPORTED;     \
   }
-#define MZ_FOLD_NREP4(IOV, BB)           \
-  switch (nrep_pad) {                    \
-    case 1: MZ_FOLD(IOV, 1, BB); break;  \
-    case 2: MZ_FOLD(IOV, 2, BB); break;  \
-    case 4: MZ_FOLD(IOV, 4, BB); break;  \
-    default: return MZ_EUNSUPPORTED;     \
-  }
 #define MZ_FOLD_BITS(IOV)                              \
   if (a->bits == 4) { MZ_FOLD_NREP(IOV, 4) }           \
   else if (a->bits == 3) { MZ_FOLD_NREP(IOV, 3) }      \
@@ -1284,11 +1277,10 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   else if (a->bits == 1) { MZ_FOLD_NREP(IOV, 1) }      \
   else if (a->bits == 5) { MZ_FOLD_NREP(IOV, 5) }      \
   else if (a->bits == 6) { MZ_FOLD_NREP(IOV, 6) }      \
-  else if (a->bits == 7) { MZ_FOLD_NREP4(IOV, 7) }     \
+  else if (a->bits == 7) { MZ_FOLD_NREP(IOV, 7) }      \
   else return MZ_EUNSUPPORTED;
   if (a->io_dtype == MZ_BF16) { MZ_FOLD_BITS(MZ_BF16) } else { MZ_FOLD_BITS(MZ_F16) }
 #undef MZ_FOLD_BITS
-#undef MZ_FOLD_NREP4
 #undef MZ_FOLD_NREP
 #undef MZ_FOLD
 #undef MZ_FOLD_HD

@@ -79,7 +79,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
     fold = (kernel_path == "fold" or (kernel_path == "auto" and d in (64, 128) and lq0 > 0
                                       and ((1 <= bits <= 4 and 1 <= n_rep <= 8)
                                            or (bits in (5, 6) and 1 <= n_rep <= 8)
-                                           or (bits == 7 and 1 <= n_rep <= 4 and alpha_k == alpha_v))))
+                                           or (bits == 7 and 1 <= n_rep <= 8 and alpha_k == alpha_v))))
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
                                      dequant_dtype=torch.float32 if fold else None)
@@ -171,8 +171,8 @@ def test_decode_deterministic():
     assert torch.equal(o1, o2)
 
 
-# 1- to 6-bit codes, head_dim 64 or 128, n_rep 1..8, and 7-bit codes with n_rep
-# 1..4 (and one alpha for keys and values): the fold kernel (AUTO
+# 1- to 7-bit codes, head_dim 64 or 128, n_rep 1..8 (7 bits: one alpha for
+# keys and values): the fold kernel (AUTO
 # picks it; n_rep 3 and 5..7 run the kernel built for 4 / 8 heads with the
 # extra heads unused); the same cases through the exact-dequantize kernel keep
 # that path covered too.
@@ -244,6 +244,8 @@ FOLD_CASES = [
     (1, 2, 4, 64, 700, 5, 128),
     (1, 2, 2, 64, 700, 6, 128),
     (1, 2, 4, 64, 700, 7, 128),
+    (1, 1, 8, 128, 700, 7, 128),
+    (2, 2, 6, 64, 900, 7, 191),
 ]
 
 
