@@ -522,6 +522,9 @@ def main():
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--residual", type=int, default=128)
+    ap.add_argument("--head-dim", type=int, default=128, help="decode mode: head_dim (other models' shapes)")
+    ap.add_argument("--kv-heads", type=int, default=8, help="decode mode: kv heads")
+    ap.add_argument("--q-heads", type=int, default=32, help="decode mode: query heads (a multiple of --kv-heads)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
     ap.add_argument("--no-cpu", action="store_true")
@@ -557,7 +560,7 @@ def main():
 
     from muzero_amd.kernels.loader import DecodePlan
     dev = torch.device("cuda:0")
-    B, hkv, hq, d = args.batch, 8, 32, 128
+    B, hkv, hq, d = args.batch, args.kv_heads, args.q_heads, args.head_dim
     L, R, bits = args.context, args.residual, args.bits
     lq = max(L - R, 0) // 64 * 64
     r = L - lq
@@ -593,7 +596,7 @@ def main():
     read_gbs = measured_read_gbs(1024, 10)
 
     traffic = None
-    if os.path.exists(args.traffic_json):
+    if os.path.exists(args.traffic_json) and (hq, hkv, d) == (32, 8, 128):  # measured for this shape only
         with open(args.traffic_json) as f:
             tj = json.load(f)
         key = f"B{B}_L{L}_b{bits}_R{R}"
@@ -633,8 +636,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"cfg1 decode attention: Qwen3-8B layer B={B} Hq=32 Hkv=8 hd=128 ctx={L} "
-                               f"mu_zero {bits}-bit G64 R={r} fp16 meta",
+        "config": {"workload": (f"cfg1 decode attention: Qwen3-8B layer B={B} Hq=32 Hkv=8 hd=128 ctx={L} "
+                                if (hq, hkv, d) == (32, 8, 128) else
+                                f"decode attention (not a benchmark config shape): B={B} Hq={hq} Hkv={hkv} hd={d} ctx={L} ")
+                               + f"mu_zero {bits}-bit G64 R={r} fp16 meta",
                    "batch": B, "context": L, "bits": bits, "residual": r, "quantized_tokens": lq,
                    "cache_copies": args.copies},
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
