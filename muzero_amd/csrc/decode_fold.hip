@@ -1231,10 +1231,13 @@ int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
   const int n_tiles = a->n_groups + (a->n_residual + fold::TILE - 1) / fold::TILE;
   int ns = a->n_split;
   if (ns <= 0) {
-    // fill the resident workgroup slots (two per CU) once: every workgroup
-    // then runs its tiles in one pass with its tables loaded once
+    // fill the resident workgroup slots once: every workgroup then runs its
+    // tiles in one pass with its tables loaded once.  Two workgroups fit a
+    // CU up to 4 query heads per kv-head and 6 bits; the 8-head kernels and
+    // the 7-bit workgroups take a CU alone.
     const int64_t units = (int64_t)a->batch * a->kv_heads;
-    const int64_t slots = 2 * (int64_t)device_cu_count();
+    const int per_cu = (a->n_rep > 4 || a->bits >= 7) ? 1 : 2;
+    const int64_t slots = per_cu * (int64_t)device_cu_count();
     ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
   }
