@@ -212,6 +212,29 @@ __device__ __forceinline__ void value_code_bf16_pair(float v0, float v1, const Q
   c1 = (uint32_t)__builtin_amdgcn_fmed3f(q1, 0.f, qmax);
 }
 
+// value_code<MZ_F16, BITS, true, true> with the rewrites of the bf16 pair
+// form, which hold for fp16 as well (they use only that 1 is an fp16 value,
+// that rounding is monotone and symmetric, and that in a finite group every
+// quotient is >= +0).  Each division is a * rcp(b) plus one residual
+// correction (qdiv; b is positive and finite here), the clamp riding on the
+// correction's FMA; p's fp16 pattern addresses the ratio table directly.
+template <int BITS>
+__device__ __forceinline__ uint32_t value_code_f16(float v, const QParams& g, const uint8_t* lds) {
+  constexpr float qmax = (float)((1 << BITS) - 1);
+  const float a = rnd<MZ_F16>(v - g.mn);
+  const float n0 = a * g.rsc;
+  const float n = rnd<MZ_F16>(__builtin_amdgcn_fmed3f(__builtin_fmaf(__builtin_fmaf(-g.sc, n0, a), g.rsc, n0), 0.f, 1.f));
+  const bool up = n >= g.za;
+  const float d = __builtin_fabsf(rnd<MZ_F16>(n - g.za));
+  const float b = up ? g.pe : g.ne, r = up ? g.rpe : g.rne;
+  const float p0 = d * r;
+  const uint32_t pat = f2h(__builtin_amdgcn_fmed3f(__builtin_fmaf(__builtin_fmaf(-b, p0, d), r, p0), 0.f, 1.f));
+  const float y = h2f(*(const uint16_t*)(lds + 2 * (pat & 0x7FFFu)));
+  const float o = rnd<MZ_F16>(y * (up ? g.pb : -g.nb));
+  // zl + off: an integer in [-1, qmax + 1], exact in fp16
+  return (uint32_t)__builtin_amdgcn_fmed3f(g.zl + rintf(o), 0.f, qmax);
+}
+
 // Min / max over the 8 lanes of a group (lanes 8k..8k+7), NaN-propagating:
 // IEEE 754-2019 minimum / maximum (v_minimum3_f32 / v_maximum3_f32), which
 // return NaN when either operand is NaN, as torch's amin / amax do.  (Between
@@ -262,6 +285,9 @@ __device__ __forceinline__ void quantize_chunk8(const float* x, const QParams& g
         value_code_bf16_pair<BITS>(x[i], x[i + 1], g, lds, c0, c1);
         w |= ((uint64_t)c0 << (i * BITS)) | ((uint64_t)c1 << ((i + 1) * BITS));
       }
+    } else if constexpr (DT == MZ_F16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code_f16<BITS>(x[i], g, lds) << (i * BITS);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) w |= (uint64_t)value_code<DT, BITS, true, true>(x[i], g, lds, table) << (i * BITS);
