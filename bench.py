@@ -50,14 +50,14 @@ def algorithmic_bytes(B, hkv, hq, d, lq, r, bits):
     return k + v + res + qo
 
 
-def make_inputs(B, hkv, hq, L, d, seed, device):
+def make_inputs(B, hkv, hq, L, d, seed, device, dtype=torch.bfloat16):
     g = torch.Generator(device=device).manual_seed(seed)
     k = torch.randn(B, hkv, L, d, generator=g, device=device)
     v = torch.randn(B, hkv, L, d, generator=g, device=device)
     q = torch.randn(B, hq, 1, d, generator=g, device=device)
     idx = torch.randperm(d, generator=g, device=device)[:4]
     k[..., idx] *= 10.0
-    return k.to(torch.bfloat16), v.to(torch.bfloat16), q.to(torch.bfloat16)
+    return k.to(dtype), v.to(dtype), q.to(dtype)
 
 
 def quantize_cache(k, v, bits, lq, alpha=2.0):
@@ -116,7 +116,7 @@ def host_cpu():
     return avail, os.cpu_count() or avail, model
 
 
-def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alpha_v=2.0):
+def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alpha_v=2.0, dtype=torch.bfloat16):
     """The reference's CPU decode path (oracle restatement) on `sample_batch` batch rows:
     (seconds per call, its output for those rows)."""
     from oracle import reference_torch as ref
@@ -127,9 +127,8 @@ def cpu_baseline(cache, q, bits, lq, d, sample_batch, threads, alpha_k=2.0, alph
 
     def run():
         if lq:
-            kq = ref.dequantize_key_block(c["k_packed"], c["k_mn"], c["k_scale"], bits, alpha_k, 64, torch.bfloat16)
-            vq = ref.dequantize_value_block(c["v_packed"], c["v_mn"], c["v_scale"], bits, alpha_v, 64, d,
-                                            torch.bfloat16)
+            kq = ref.dequantize_key_block(c["k_packed"], c["k_mn"], c["k_scale"], bits, alpha_k, 64, dtype)
+            vq = ref.dequantize_value_block(c["v_packed"], c["v_mn"], c["v_scale"], bits, alpha_v, 64, d, dtype)
         else:
             kq = c["k_res"][:, :, :0]
             vq = c["v_res"][:, :, :0]
@@ -525,6 +524,8 @@ def main():
     ap.add_argument("--head-dim", type=int, default=128, help="decode mode: head_dim (other models' shapes)")
     ap.add_argument("--kv-heads", type=int, default=8, help="decode mode: kv heads")
     ap.add_argument("--q-heads", type=int, default=32, help="decode mode: query heads (a multiple of --kv-heads)")
+    ap.add_argument("--kv-dtype", choices=("bf16", "f16"), default="bf16",
+                    help="decode mode: dtype of the query and the K/V the cache is quantized from (the residual's)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
     ap.add_argument("--no-cpu", action="store_true")
@@ -564,7 +565,8 @@ def main():
     L, R, bits = args.context, args.residual, args.bits
     lq = max(L - R, 0) // 64 * 64
     r = L - lq
-    k, v, q = make_inputs(B, hkv, hq, L, d, 1234, dev)
+    io = {"bf16": torch.bfloat16, "f16": torch.float16}[args.kv_dtype]
+    k, v, q = make_inputs(B, hkv, hq, L, d, 1234, dev, io)
     caches = [quantize_cache(k, v, bits, lq)]
     for _ in range(args.copies - 1):
         caches.append({k_: t.clone() for k_, t in caches[0].items()})
@@ -596,7 +598,7 @@ def main():
     read_gbs = measured_read_gbs(1024, 10)
 
     traffic = None
-    if os.path.exists(args.traffic_json) and (hq, hkv, d) == (32, 8, 128):  # measured for this shape only
+    if os.path.exists(args.traffic_json) and (hq, hkv, d) == (32, 8, 128) and args.kv_dtype == "bf16":  # measured for this case only
         with open(args.traffic_json) as f:
             tj = json.load(f)
         key = f"B{B}_L{L}_b{bits}_R{R}"
@@ -605,7 +607,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         threads, host_cores, cpu_model = host_cpu()
-        sec, cpu_out = cpu_baseline(caches[0], q, bits, lq, d, args.cpu_sample_batch, threads)
+        sec, cpu_out = cpu_baseline(caches[0], q, bits, lq, d, args.cpu_sample_batch, threads, dtype=io)
         sec_full = sec * B / args.cpu_sample_batch
         # the timed calls' output against the reference CPU path's on the sampled rows
         plans[0].run()
@@ -618,8 +620,8 @@ def main():
                "sample": f"batch rows 0..{args.cpu_sample_batch - 1} of {B} (dequantize prefix + "
                          f"attend, oracle restatement of attention.py:179-295), time x {B // args.cpu_sample_batch}",
                "gpu_vs_cpu_path": {"max_abs": round(diff.max().item(), 6), "mean_abs": round(diff.mean().item(), 7),
-                                   "note": "bf16 outputs of the sampled rows; the CPU path rounds dequantized "
-                                           "values, logits and weights to bf16 (the reference's dequantize-then-"
+                                   "note": f"{args.kv_dtype} outputs of the sampled rows; the CPU path rounds dequantized "
+                                           f"values, logits and weights to {args.kv_dtype} (the reference's dequantize-then-"
                                            "attend), the fold kernel keeps fp32 codebook values (its fused "
                                            "kernels' semantics)"}}
 
@@ -634,11 +636,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.kv_dtype,
         "data": "synthetic",
         "config": {"workload": (f"cfg1 decode attention: Qwen3-8B layer B={B} Hq=32 Hkv=8 hd=128 ctx={L} "
-                                if (hq, hkv, d) == (32, 8, 128) else
-                                f"decode attention (not a benchmark config shape): B={B} Hq={hq} Hkv={hkv} hd={d} ctx={L} ")
+                                if (hq, hkv, d) == (32, 8, 128) and args.kv_dtype == "bf16" else
+                                f"decode attention (not a benchmark config shape): B={B} Hq={hq} Hkv={hkv} hd={d} ctx={L} "
+                                f"{args.kv_dtype} ")
                                + f"mu_zero {bits}-bit G64 R={r} fp16 meta",
                    "batch": B, "context": L, "bits": bits, "residual": r, "quantized_tokens": lq,
                    "cache_copies": args.copies},
