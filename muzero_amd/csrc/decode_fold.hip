@@ -49,7 +49,7 @@
 // head_dim 64 runs the same layout with the k-tiles of channels 64..127 and
 // the second value group absent.
 //
-// Launch: one workgroup of 4 waves (7 bits: 8) per (batch, kv-head, split); a split is a
+// Launch: one workgroup of 4 waves (7 bits with up to 4 heads: 8) per (batch, kv-head, split); a split is a
 // run of tiles (residual tiles first), waves take every 4th; the split's
 // (m, l, acc) goes to the workspace and the shared combine kernel merges
 // splits.  With a single split (the grid already fills the GPU) the kernel
@@ -72,8 +72,9 @@ constexpr int TILE = 64;  // tokens per tile
 // 4 query heads) measured 13 % slower at config 1: more waves per CU contend
 // for its LDS rather than hide more latency.
 // 7-bit codes: one workgroup of 8 waves per CU (its 64 KB table then serves
-// the CU's two waves per SIMD); with 8 query heads (one wave per SIMD by
-// registers) one workgroup of 4.
+// the CU's two waves per SIMD); with 8 query heads one workgroup of 4 (the
+// per-wave operand staging of 16 MFMA rows brings it to 89 KB of LDS, so a CU
+// holds one).
 template <int NREP, int BITS>
 constexpr int waves_for() { return BITS >= 7 && NREP <= 4 ? 8 : 4; }
 template <int NREP>

@@ -1,8 +1,8 @@
 // Quantize + bit-pack and dequantize kernels (gfx950, wave64).
 //
-// Quantize: 8 lanes per 64-value group, 8 consecutive values per lane, so a
-// wave quantizes 8 groups.  The group min/max is an in-lane reduction plus 3
-// DPP steps; the group's compander parameters are computed once per lane; every
+// Quantize: 2 lanes per 64-value group, 32 consecutive values per lane, so a
+// wave quantizes 32 groups.  The group min/max is an in-lane reduction plus
+// one DPP step; the group's compander parameters are computed once per lane; every
 // per-element op of the reference quantizer (muzero/quantizer.py:161-186) is
 // evaluated in its own dtype with IEEE rounding and no contraction, and the
 // one transcendental step (round(log1p(alpha*p)/lb*bins)) comes from a
