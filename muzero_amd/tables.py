@@ -34,8 +34,8 @@ the reference:
     ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
     as two fp16 packed in one uint32 (P in the low half), with
     ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; row zl, column q, zero
-    beyond qmax: 16 x 16 for 1-4 bits, (qmax+1) x 64 for 5 and 6 bits (the
-    layout the kernel keeps in LDS).  The decode kernel rewrites the
+    beyond qmax: 16 x 16 for 1-4 bits, (qmax+1) x 64 for 5 and 6 bits,
+    128 x 128 for 7 bits (the rows the kernel keeps in LDS).  The decode kernel rewrites the
     reference's dequantization as ``a + bp*P + bn*N`` per group and looks
     these pairs up per code.
 
