@@ -11,7 +11,9 @@
  * count and whether a kernel's dynamic-LDS limit has been raised on it (the
  * general decode kernels, the qk / av kernels with more than 64 KB of LDS),
  * filled on the first call on that device (idempotent, so concurrent first
- * calls are harmless).
+ * calls are harmless), and the static decode scratch array that
+ * muzero_decode_attention_noalloc uses instead of a workspace (each device
+ * holds its own copy while the library is loaded).
  *
  * Reference boundary being replaced: the pybind11 module returned by
  * load_mu_zero_cuda_extension() (muzero/kernels/loader.py:37-94, 1862-1880),
