@@ -81,6 +81,32 @@ def test_quantize_rows_random_vs_oracle(dname, bits):
         np.testing.assert_array_equal(bits_of(sc), bits_of(esc))
 
 
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 8])
+def test_quantize_rows_16bit_extreme_ranges_vs_oracle(dname, bits):
+    """16-bit rows at the ends of the dtype's range: subnormal-sized groups,
+    groups whose range overflows the dtype (scale inf), near-constant groups
+    (the fp16 epsilon rounds to 0), and large offsets (|mn| >> scale)."""
+    g = torch.Generator().manual_seed(700 + bits)
+    x = torch.randn(2048, 64, generator=g)
+    big = 6.0e4 if dname == "float16" else 1.0e30
+    x[0::9] *= 1e-6                       # subnormal fp16 values
+    x[1::9] *= 2e-5
+    x[2::9] = x[2::9] * 10.0 + 1000.0     # offset groups, all positive
+    x[3::9] = x[3::9] * 0.01 - 500.0      # narrow, all negative
+    x[4::9] = 7.0                         # constant
+    x[4::9, 5] = 7.0 + 1.0 / 64           # one value off a constant group
+    x[5::9] *= big / 4                    # range beyond the dtype's max
+    x[6::9, :32] = big; x[6::9, 32:] = -big
+    x = x.to(DT[dname])
+    for alpha in (2.0, 16.0):
+        pq, mn, sc = _quantize_gpu(x, bits, alpha)
+        epq, emn, esc = ref.quantize_rows(x, bits, alpha, 1e-8, torch.float16)
+        np.testing.assert_array_equal(pq.numpy(), epq.numpy())
+        np.testing.assert_array_equal(bits_of(mn), bits_of(emn))
+        np.testing.assert_array_equal(bits_of(sc), bits_of(esc))
+
+
 @pytest.mark.parametrize("bits", [2, 4])
 def test_quantize_rows_exhaustive_boundaries_fp32(bits):
     """Rows whose normalised distances sit exactly on and next to every code threshold."""
@@ -213,7 +239,7 @@ def test_quantize_rows_many_rows(dname, bits):
     np.testing.assert_array_equal(bits_of(sc), bits_of(esc))
 
 
-@pytest.mark.parametrize("dname", ["bfloat16", "float32"])
+@pytest.mark.parametrize("dname", ["bfloat16", "float32", "float16"])
 @pytest.mark.parametrize("bits", [2, 4])
 def test_quantize_blocks_aligned_vector_path(dname, bits):
     """Contiguous, 16-byte aligned blocks take the vector-load path of the value kernel."""
