@@ -6,7 +6,10 @@
  * enums and a hipStream_t (0 = the default stream), launches asynchronously
  * and returns an int status (0 = success, negative = argument error, or the
  * positive hipError_t of a failed launch).  Nothing here allocates device
- * memory; callers own every buffer.  Calls are thread-safe.  The library's
+ * memory; callers own every buffer.  Calls are thread-safe, except
+ * muzero_decode_attention_noalloc: its calls on one device share that
+ * device's static scratch array, so calls that overlap there (from two
+ * threads, or on two streams) race.  The library's
  * only mutable state is per device and process: each device's compute-unit
  * count and whether a kernel's dynamic-LDS limit has been raised on it (the
  * general decode kernels, the qk / av kernels with more than 64 KB of LDS),
@@ -249,6 +252,37 @@ int muzero_decode_partials(const mz_decode_args* args, mz_stream_t stream);
 int muzero_decode_combine(const mz_decode_args* args, mz_stream_t stream);
 
 /*
+ * Online-softmax state of a packed prefix: the fused prefix decode that
+ * returns (acc, m, l) instead of the normalized output, for the caller to
+ * merge with its own dense tail.
+ * Replaces: prefix_decode(query, K..., V..., output_accum, output_m,
+ *   output_l, alpha_key, alpha_value, num_key_value_groups, scaling) and
+ *   prefix_decode_chunked(..., partial_accum, partial_m, partial_l,
+ *   output_accum, output_m, output_l, ...) (muzero/kernels/loader.py:54-84,
+ *   host :1689-1858, kernels :1046-1285), whose caller merges the residual
+ *   window in torch (muzero/cache/attention.py:91-177).  The reference builds
+ *   them for 4 bits only; here every width 1-8 (the kernel muzero_decode_attention
+ *   would run for these arguments).
+ * args: a decode call over the packed prefix alone (n_residual = 0, aligned
+ * value prefix), with its workspace (muzero_decode_workspace_bytes of args
+ * with n_split set to n_chunks when n_chunks > 0).  Writes, per (b, h):
+ * m = the maximum of the scaled (and masked) logits, l = sum_t exp(s_t - m),
+ * acc[0..D) = sum_t exp(s_t - m) * v_t (fp32, v_t the dequantized value), to
+ * acc[b*acc_sb + h*acc_sh + c], m / l[b*ml_sb + h].  With n_chunks > 0 the
+ * prefix is cut into n_chunks runs of ceil(n_groups / n_chunks) groups (the
+ * reference's chunks) and each run's own (acc, m, l) also goes to part_acc
+ * [B*Hq][n_chunks][D], part_m / part_l [B*Hq][n_chunks] (contiguous); runs
+ * past the end of the prefix hold acc = 0, m = -inf, l = 0.
+ */
+typedef struct mz_prefix_state_args {
+  float* acc; int64_t acc_sb, acc_sh;
+  float* m; float* l; int64_t ml_sb;
+  float* part_acc; float* part_m; float* part_l;
+  int n_chunks;  /* 0: the library's split choice, no partials written */
+} mz_prefix_state_args;
+int muzero_decode_prefix_state(const mz_decode_args* args, const mz_prefix_state_args* state, mz_stream_t stream);
+
+/*
  * muzero_decode_attention without a caller workspace: a split call keeps its
  * partial records in a static device array of MZ_DECODE_SCRATCH_BYTES inside
  * the library (one per device, held until the process ends); args->workspace
@@ -260,6 +294,10 @@ int muzero_decode_combine(const mz_decode_args* args, mz_stream_t stream);
  * records stay in it; each call writes every record it reads), so calls that
  * overlap on one device, on different streams or threads, race.  Same
  * results as muzero_decode_attention with a workspace, bit for bit.
+ * The first call on a device does one-time runtime set-up there (the
+ * scratch array's address, a kernel's LDS limit): a caller that captures
+ * the call in a HIP graph makes one call on that device before the capture
+ * begins.
  * No counterpart in the reference; it is for callers that cannot allocate.
  */
 #define MZ_DECODE_SCRATCH_BYTES (8u << 20)

@@ -100,6 +100,17 @@ class PrologueArgs(ctypes.Structure):
     ]
 
 
+class PrefixStateArgs(ctypes.Structure):
+    """Mirror of ``mz_prefix_state_args`` (include/muzero_hip.h)."""
+
+    _fields_ = [
+        ("acc", c_vp), ("acc_sb", c_i64), ("acc_sh", c_i64),
+        ("m", c_vp), ("l", c_vp), ("ml_sb", c_i64),
+        ("part_acc", c_vp), ("part_m", c_vp), ("part_l", c_vp),
+        ("n_chunks", c_int),
+    ]
+
+
 MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2
 MZ_ESCRATCH = -4
 MZ_DECODE_SCRATCH_BYTES = 8 << 20  # the static scratch of muzero_decode_attention_noalloc
@@ -127,6 +138,7 @@ SIGNATURES = {
     "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_attention_noalloc": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    "muzero_decode_prefix_state": (c_int, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(PrefixStateArgs), c_vp]),
     "muzero_decode_prologue": (c_int, [ctypes.POINTER(PrologueArgs), c_vp]),
     "muzero_stream_read": (c_int, [c_vp, c_i64, c_vp, c_int, c_vp]),
 }

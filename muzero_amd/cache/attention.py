@@ -29,10 +29,20 @@ Shapes the fused kernels do not take (head_dim other than 64 / 128, fp32
 queries) run the reference's default path itself: the separate ``qk`` / ``av``
 launches (``muzero_qk`` / ``muzero_av``) around a torch softmax and the
 residual matmuls, counted as ``fused_qk_success`` / ``fused_av_success``.
+
+Kernel choice, in the reference's environment-switch style (``attention.py:92``,
+``:110``, ``:128``): ``MUZERO_DECODE_KERNEL=exact`` runs every fused call on the
+exact-dequantize kernel, whose dequantized values are rounded to the layer dtype
+like the reference's dequantize-then-attend path (``attention.py:213-226``,
+``:274-283``); ``fold`` requires the fold kernel (its full-precision values are
+those of the reference's fused CUDA kernels, ``loader.py:197-263``) and raises
+where it does not apply; unset or ``auto``, the fold kernel serves the calls it
+takes (1-7 bits) and the exact kernel the rest.
 """
 
 from __future__ import annotations
 
+import os
 from collections import defaultdict
 
 import torch
@@ -105,15 +115,16 @@ def mu_zero_decode_attention_forward(
     # residual lengths and the output: once the arguments have been built and
     # validated for a layer's storage, later steps only patch those fields.
     fast = getattr(layer, "_hip_decode", None)
+    kernel_path = _kernel_path()
     key = None
     if attention_mask is None and has_res and value_prefix_length == key_prefix_length:
         storage = _storage_key(layer)
         if storage is not None:
             key = (storage, query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key,
-                   alpha_value, float(scaling))
+                   alpha_value, float(scaling), kernel_path)
     try:
         out = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
-                      scaling, attention_mask, value_prefix_length)
+                      scaling, attention_mask, value_prefix_length, kernel_path)
     except Exception:
         _count(key_prefix_length, value_prefix_length, "fallback")
         raise
@@ -121,6 +132,17 @@ def mu_zero_decode_attention_forward(
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1
     return out, None
+
+
+_KERNEL_PATHS = ("auto", "exact", "fold")
+
+
+def _kernel_path() -> str:
+    """The decode kernel the environment asks for (``MUZERO_DECODE_KERNEL``)."""
+    path = os.environ.get("MUZERO_DECODE_KERNEL", "auto").strip().lower() or "auto"
+    if path not in _KERNEL_PATHS:
+        raise ValueError(f"MUZERO_DECODE_KERNEL must be one of {_KERNEL_PATHS}, got {path!r}")
+    return path
 
 
 def _count(key_prefix_length: int, value_prefix_length: int, outcome: str) -> None:
@@ -206,7 +228,7 @@ def _storage_key(layer):
 
 
 def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value, scaling,
-            attention_mask, value_prefix_length):
+            attention_mask, value_prefix_length, kernel_path="auto"):
     if fast is not None and key is not None and fast.key == key:
         out = fast.launch(query, n_groups, r)
     else:
@@ -221,6 +243,7 @@ def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_k
             scaling=float(scaling),
             attention_mask=attention_mask,
             value_prefix=value_prefix_length,
+            kernel_path=kernel_path,
         )
         out = plan.run()
         # cache the validated arguments only when every pointer they hold is

@@ -607,6 +607,51 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(const float* __restri
   store_val(out, b * out_sb + (int64_t)h * out_sh + c, o, out_dtype);
 }
 
+// The online-softmax state of a packed prefix, for one (batch, q-head): the
+// split records merged into (acc, m, l) with acc and l relative to the merged
+// maximum m (the state the reference's prefix_decode kernels return, and what
+// its reduce kernel forms from its chunk records, loader.py:1251-1285), and,
+// when requested, the records themselves as the reference's chunk partials
+// (chunks past the split count hold the empty state acc = 0, m = -inf, l = 0,
+// as an empty reference chunk does).
+template <int D>
+__global__ __launch_bounds__(D) void prefix_state_kernel(const float* __restrict__ ws, int n_split, int Hq,
+                                                         mz_prefix_state_args st) {
+  const int bh = blockIdx.x;
+  const int c = threadIdx.x;
+  const float* base = ws + (int64_t)bh * n_split * (D + 2);
+  float M_ = -INFINITY;
+  for (int s = 0; s < n_split; ++s)
+    if (base[s * (D + 2) + D + 1] > 0.f) M_ = fmaxf(M_, base[s * (D + 2) + D]);
+  float acc = 0.f, l = 0.f;
+  if (M_ != -INFINITY) {
+    for (int s = 0; s < n_split; ++s) {
+      const float ls = base[s * (D + 2) + D + 1];
+      if (!(ls > 0.f)) continue;  // an empty record (every logit masked) adds nothing
+      const float f = __expf(base[s * (D + 2) + D] - M_);
+      acc += f * base[s * (D + 2) + c];
+      l += f * ls;
+    }
+  }
+  const int b = bh / Hq, h = bh - b * Hq;
+  st.acc[b * st.acc_sb + (int64_t)h * st.acc_sh + c] = acc;
+  if (c == 0) {
+    st.m[b * st.ml_sb + h] = M_;
+    st.l[b * st.ml_sb + h] = l;
+  }
+  if (st.n_chunks > 0) {
+    for (int s = 0; s < st.n_chunks; ++s) {
+      const bool real = s < n_split;
+      const int64_t row = (int64_t)bh * st.n_chunks + s;
+      st.part_acc[row * D + c] = real ? base[s * (D + 2) + c] : 0.f;
+      if (c == 0) {
+        st.part_m[row] = real ? base[s * (D + 2) + D] : -INFINITY;
+        st.part_l[row] = real ? base[s * (D + 2) + D + 1] : 0.f;
+      }
+    }
+  }
+}
+
 bool fold_supported(const mz_decode_args* a);
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
@@ -619,7 +664,7 @@ static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
   if (ns <= 0) {
     // fill the resident workgroup slots (two per CU) once: each workgroup then
     // loads its tables and query once and runs all its tiles in one pass
-    const int64_t units = (int64_t)a->batch * a->kv_heads;
+    const int64_t units = std::max<int64_t>(1, (int64_t)a->batch * a->kv_heads);  // an empty batch splits nothing
     const int64_t slots = 2 * (int64_t)device_cu_count();
     ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
@@ -776,6 +821,40 @@ extern "C" int muzero_decode_combine(const mz_decode_args* a, mz_stream_t stream
   return a->io_dtype == MZ_BF16 ? launch_combine<64, MZ_BF16>(a, s) : launch_combine<64, MZ_F16>(a, s);
 }
 
+extern "C" int muzero_decode_prefix_state(const mz_decode_args* a, const mz_prefix_state_args* st,
+                                          mz_stream_t stream) {
+  if (!a || !st) return MZ_EINVAL;
+  // the packed prefix alone, keys and values aligned
+  if (a->n_residual != 0 || (a->v_prefix != 0 && a->v_prefix != a->n_groups * kTile)) return MZ_EINVAL;
+  if (st->n_chunks < 0) return MZ_EINVAL;
+  mz_decode_args b = *a;
+  b.v_prefix = 0;
+  if (st->n_chunks > 0) b.n_split = st->n_chunks;
+  int ns = 0;
+  const int64_t need = muzero_decode_workspace_bytes(&b, &ns);
+  if (need < 0) {
+    const int c = check_args(&b);
+    return c != MZ_OK ? c : MZ_EUNSUPPORTED;
+  }
+  if (b.batch == 0) return MZ_OK;
+  if (b.n_groups <= 0) return MZ_EINVAL;
+  if (!st->acc || !st->m || !st->l) return MZ_EINVAL;
+  if (st->n_chunks > 0 && (!st->part_acc || !st->part_m || !st->part_l)) return MZ_EINVAL;
+  if (!b.workspace || b.workspace_bytes < need) return MZ_EWORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  const int r = muzero_decode_partials(&b, stream);
+  if (r != MZ_OK) return r;
+  const int Hq = b.kv_heads * b.n_rep;
+  if (b.head_dim == 128)
+    hipLaunchKernelGGL((prefix_state_kernel<128>), dim3(b.batch * Hq), dim3(128), 0, s,
+                       (const float*)b.workspace, ns, Hq, *st);
+  else
+    hipLaunchKernelGGL((prefix_state_kernel<64>), dim3(b.batch * Hq), dim3(64), 0, s,
+                       (const float*)b.workspace, ns, Hq, *st);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MZ_OK : (int)e;
+}
+
 extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stream) {
   // one split: the split kernel writes the output (no workspace, no combine)
   if (decode_check_launchable(a) == MZ_OK && a->out && !(a->kernel_path == MZ_PATH_FOLD && !fold_supported(a))) {
@@ -817,7 +896,11 @@ extern "C" int muzero_decode_attention_noalloc(const mz_decode_args* a, mz_strea
   if (!a) return MZ_EINVAL;
   int ns = 0;
   const int64_t need = muzero_decode_workspace_bytes(a, &ns);
-  if (need < 0) return MZ_EINVAL;
+  if (need < 0) {
+    // the status muzero_decode_attention gives for the same arguments
+    const int c = check_args(a);
+    return c != MZ_OK ? c : MZ_EUNSUPPORTED;  // a forced fold path the fold kernel does not take
+  }
   // a single split writes the output directly and reads no workspace
   if (ns > 1 && need > (int64_t)MZ_DECODE_SCRATCH_BYTES) return MZ_ESCRATCH;
   mz_decode_args b = *a;

@@ -1236,7 +1236,7 @@ int fold_choose_split(const mz_decode_args* a, int* tiles_per_split) {
     // tiles in one pass with its tables loaded once.  Two workgroups fit a
     // CU up to 4 query heads per kv-head and 6 bits; the 8-head kernels and
     // the 7-bit workgroups take a CU alone.
-    const int64_t units = (int64_t)a->batch * a->kv_heads;
+    const int64_t units = std::max<int64_t>(1, (int64_t)a->batch * a->kv_heads);  // an empty batch splits nothing
     const int per_cu = (a->n_rep > 4 || a->bits >= 7) ? 1 : 2;
     const int64_t slots = per_cu * (int64_t)device_cu_count();
     ns = (int)((slots + units - 1) / units);

@@ -48,10 +48,54 @@ def _qbytes(bits: int) -> int:
     return (GROUP * bits + 7) // 8
 
 
+class MuZeroHipExtension:
+    """What :func:`load_mu_zero_cuda_extension` returns: the reference extension's six functions
+    (``quantize``, ``dequantize``, ``qk``, ``av``, ``prefix_decode``, ``prefix_decode_chunked``;
+    pybind module of ``loader.py:86-93``) with its argument order and meaning, each a call into
+    ``libmuzero_hip.so``.  Outputs are written in place into the caller's tensors, on torch's
+    current stream, as the reference's are.  The ctypes library itself is ``lib``; its
+    ``muzero_*`` entry points are also reachable as attributes of this object."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self.lib = lib
+
+    def __getattr__(self, name: str):
+        if name.startswith("muzero_"):
+            return getattr(self.lib, name)
+        raise AttributeError(name)
+
+    def quantize(self, grouped, packed_q, mn, scale, bits, alpha, eps):
+        mu_zero_quantize_cuda(grouped, packed_q, mn, scale, bits, alpha, eps)
+
+    def dequantize(self, packed_q, mn, scale, output, bits, alpha):
+        mu_zero_dequantize_cuda(packed_q, mn, scale, output, bits, alpha)
+
+    def qk(self, query, packed_q, mn, scale, output, bits, alpha, num_key_value_groups, scaling):
+        mu_zero_qk_cuda(query, packed_q, mn, scale, output, bits, alpha, num_key_value_groups, scaling)
+
+    def av(self, attn_weights, packed_q, mn, scale, output, bits, alpha, num_key_value_groups, group_size):
+        mu_zero_av_cuda(attn_weights, packed_q, mn, scale, output, bits, alpha, num_key_value_groups, group_size)
+
+    def prefix_decode(self, query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                      output_accum, output_m, output_l, alpha_key, alpha_value, num_key_value_groups, scaling):
+        mu_zero_prefix_decode_cuda(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                                   output_accum, output_m, output_l, alpha_key, alpha_value,
+                                   num_key_value_groups, scaling)
+
+    def prefix_decode_chunked(self, query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn,
+                              value_scale, partial_accum, partial_m, partial_l, output_accum, output_m, output_l,
+                              alpha_key, alpha_value, num_key_value_groups, scaling):
+        mu_zero_prefix_decode_chunked_cuda(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn,
+                                           value_scale, partial_accum, partial_m, partial_l, output_accum,
+                                           output_m, output_l, alpha_key, alpha_value, num_key_value_groups,
+                                           scaling)
+
+
 @lru_cache(maxsize=1)
-def load_mu_zero_cuda_extension():
-    """Load the HIP library (reference name kept: ``loader.py:1862``)."""
-    return load()
+def load_mu_zero_cuda_extension() -> MuZeroHipExtension:
+    """The HIP library as the reference's extension object (reference name and caching kept:
+    ``loader.py:1862-1880``)."""
+    return MuZeroHipExtension(load())
 
 
 # --------------------------------------------------------------------------- quantize
@@ -317,6 +361,32 @@ class DecodePlan:
         check(self._lib.muzero_decode_combine(self._argp, stream_ptr(self.device)), "muzero_decode_combine")
         return self.out
 
+    def prefix_state(self, acc: torch.Tensor, m: torch.Tensor, l: torch.Tensor,
+                     part_acc: torch.Tensor | None = None, part_m: torch.Tensor | None = None,
+                     part_l: torch.Tensor | None = None) -> None:
+        """The packed prefix's online-softmax state (``muzero_decode_prefix_state``): fp32
+        ``acc [B, Hq, D]``, ``m`` / ``l [B, Hq]``, and with ``part_*`` the per-chunk records
+        ``[B*Hq, n_chunks, D]`` / ``[B*Hq, n_chunks]`` of the plan's ``n_split`` chunks.  The plan
+        must cover the prefix alone (no residual)."""
+        b, _, hq, d = self.out.shape
+        for t, shape in ((acc, (b, hq, d)), (m, (b, hq)), (l, (b, hq))):
+            _require(t.dtype == torch.float32 and t.device == self.device and tuple(t.shape) == shape
+                     and t.stride(-1) == 1, f"prefix state outputs must be fp32 {shape} on the plan's device")
+        _require(m.stride() == l.stride(), "m and l must share a layout")
+        st = _lib.PrefixStateArgs()
+        st.acc, st.acc_sb, st.acc_sh = ptr(acc), acc.stride(0), acc.stride(1)
+        st.m, st.l, st.ml_sb = ptr(m), ptr(l), m.stride(0)
+        if part_acc is not None:
+            nch = int(part_m.shape[1])
+            _require(nch == self.args.n_split > 0, "chunk records need the plan built with n_split = chunks")
+            for t, shape in ((part_acc, (b * hq, nch, d)), (part_m, (b * hq, nch)), (part_l, (b * hq, nch))):
+                _require(t.dtype == torch.float32 and t.device == self.device and tuple(t.shape) == shape
+                         and t.is_contiguous(), f"chunk records must be contiguous fp32 {shape}")
+            st.part_acc, st.part_m, st.part_l, st.n_chunks = ptr(part_acc), ptr(part_m), ptr(part_l), nch
+        keep = (acc, m, l, part_acc, part_m, part_l)  # noqa: F841 (alive across the launch call)
+        check(self._lib.muzero_decode_prefix_state(self._argp, ctypes.byref(st), stream_ptr(self.device)),
+              "muzero_decode_prefix_state")
+
 
 class StepDecode:
     """A validated :class:`DecodePlan` re-launched for later decode steps of the same
@@ -420,6 +490,56 @@ def mu_zero_decode_attention_hip(query: torch.Tensor, **kwargs) -> torch.Tensor:
     :class:`DecodePlan`.
     """
     return DecodePlan(query, **kwargs).run()
+
+
+def _prefix_plan(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                 alpha_key, alpha_value, num_key_value_groups, scaling, n_split) -> DecodePlan:
+    """A decode plan over a packed prefix alone, from the reference prefix_decode arguments:
+    ``query [B, Hq, 1, D]``, ``key_packed_q [B, Hkv, G, D, 8*bits]``, ``key_mn / key_scale
+    [B, Hkv, G, D(, 1)]``, ``value_packed_q [B, Hkv, 64*G, ng, 8*bits]``, ``value_mn /
+    value_scale [B, Hkv, 64*G, ng(, 1)]``.  The width comes from the packed row length, as the
+    reference's own check does (``loader.py:1712-1716``); every width 1-8 is taken."""
+    _on_gpu(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale)
+    _require(query.dim() == 4 and query.shape[2] == 1, "query must be [B, Hq, 1, D]")
+    _require(key_packed_q.dim() == 5 and value_packed_q.dim() == 5, "packed K / V must be 5-d")
+    qb = int(key_packed_q.shape[4])
+    _require(qb % 8 == 0 and 1 <= qb // 8 <= 8 and int(value_packed_q.shape[4]) == qb,
+             "packed rows must hold 64 codes of 1-8 bits (8 * bits bytes)")
+    hkv, n_groups = int(key_packed_q.shape[1]), int(key_packed_q.shape[2])
+    _require(int(num_key_value_groups) >= 1 and query.shape[1] == hkv * int(num_key_value_groups),
+             "query heads must equal kv heads * num_key_value_groups")
+    _require(int(value_packed_q.shape[2]) == GROUP * n_groups,
+             "the value prefix must hold 64 tokens per key group")
+    return DecodePlan(query, bits=qb // 8, n_groups=n_groups, k_packed=key_packed_q, k_mn=key_mn,
+                      k_scale=key_scale, v_packed=value_packed_q, v_mn=value_mn, v_scale=value_scale,
+                      k_res=None, v_res=None, alpha_key=float(alpha_key), alpha_value=float(alpha_value),
+                      scaling=float(scaling), n_split=int(n_split))
+
+
+def mu_zero_prefix_decode_cuda(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                               output_accum, output_m, output_l, alpha_key, alpha_value, num_key_value_groups,
+                               scaling) -> None:
+    """Online-softmax state of a packed prefix, in place: ``output_m [B, Hq]`` = the largest
+    scaled logit, ``output_l [B, Hq]`` = sum of exp(logit - m), ``output_accum [B, Hq, D]`` = the
+    same weights times the dequantized values (all fp32).  Reference ``loader.py:1895`` (host
+    ``:1689-1770``, kernel ``:1046-1144``), whose caller merges the dense tail with this state
+    (``attention.py:104-169``)."""
+    plan = _prefix_plan(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                        alpha_key, alpha_value, num_key_value_groups, scaling, 0)
+    plan.prefix_state(output_accum, output_m, output_l)
+
+
+def mu_zero_prefix_decode_chunked_cuda(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn,
+                                       value_scale, partial_accum, partial_m, partial_l, output_accum, output_m,
+                                       output_l, alpha_key, alpha_value, num_key_value_groups, scaling) -> None:
+    """:func:`mu_zero_prefix_decode_cuda` with the prefix cut into ``partial_m.shape[1]`` chunks of
+    ``ceil(G / chunks)`` key groups, each chunk's own state written to ``partial_accum
+    [B*Hq, chunks, D]``, ``partial_m / partial_l [B*Hq, chunks]`` and the merged state to the
+    outputs.  Reference ``loader.py:1901`` (host ``:1772-1858``, kernels ``:1146-1285``)."""
+    _require(partial_m.dim() == 2 and partial_m.shape[1] >= 1, "partial_m must be [B*Hq, chunks]")
+    plan = _prefix_plan(query, key_packed_q, key_mn, key_scale, value_packed_q, value_mn, value_scale,
+                        alpha_key, alpha_value, num_key_value_groups, scaling, int(partial_m.shape[1]))
+    plan.prefix_state(output_accum, output_m, output_l, partial_accum, partial_m, partial_l)
 
 
 # --------------------------------------------------------------------------- separate qk / av

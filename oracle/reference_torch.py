@@ -353,6 +353,92 @@ def prefix_weighted_values(weights: torch.Tensor, pq: torch.Tensor, mn: torch.Te
     return torch.matmul(weights.double().unsqueeze(2), v)[:, :, 0, :]
 
 
+def prefix_decode_state(query: torch.Tensor, pk: torch.Tensor, kmn: torch.Tensor, ksc: torch.Tensor,
+                        pv: torch.Tensor, vmn: torch.Tensor, vsc: torch.Tensor, bits: int, alpha_k: float,
+                        alpha_v: float, n_rep: int, scaling: float, num_chunks: Optional[int] = None,
+                        group_size: int = 64, dequant_dtype: torch.dtype = torch.float32):
+    """The reference's fused prefix decode (loader.py:1046-1285): online-softmax state of the
+    packed prefix per (batch, q-head), in fp64 over the fp32-dequantized keys and values.
+
+    Chunk ``c`` of ``num_chunks`` covers key groups ``[c*cg, min(G, (c+1)*cg))`` with
+    ``cg = ceil(G / num_chunks)`` (:1826); its state is ``m = max s``, ``l = sum exp(s - m)``,
+    ``acc = sum exp(s - m) * v`` (:1191-1235), an empty chunk ``(0, -inf, 0)``.  The reduce
+    (:1251-1285) skips chunks with ``l <= 0`` and rescales the others to the largest ``m``.
+    ``num_chunks=None`` is the one-block kernel (:1046-1144), the same state over all groups.
+    ``dequant_dtype``: the precision of the dequantized keys and values (the reference kernels'
+    fp32; the layer dtype gives the state of the dequantize-then-attend semantics).
+    Returns ``(acc [B,Hq,hd], m [B,Hq], l [B,Hq], partials)`` with ``partials = (acc
+    [B*Hq,chunks,hd], m [B*Hq,chunks], l [B*Hq,chunks])`` or None.
+    """
+    b, hkv, ng_k, d, _ = pk.shape
+    hq = query.shape[1]
+    keys = dequantize_key_block(pk, kmn.reshape(pk.shape[:4]), ksc.reshape(pk.shape[:4]), bits, alpha_k,
+                                group_size, dequant_dtype)
+    s = torch.matmul(query.double(), repeat_kv(keys.double(), n_rep).transpose(2, 3))[:, :, 0, :] * scaling
+    t = pv.shape[2]
+    vals = dequantize_value_block(pv, vmn.reshape(pv.shape[:4]), vsc.reshape(pv.shape[:4]), bits, alpha_v,
+                                  group_size, d, dequant_dtype)
+    v = repeat_kv(vals.double(), n_rep)  # [B,Hq,T,hd]
+    assert t == s.shape[-1]
+
+    def state(lo: int, hi: int):
+        if hi <= lo:
+            return (torch.zeros(b, hq, d, dtype=torch.float64), torch.full((b, hq), -math.inf, dtype=torch.float64),
+                    torch.zeros(b, hq, dtype=torch.float64))
+        ss = s[..., lo:hi]
+        m = ss.amax(-1)
+        e = torch.exp(ss - m[..., None])
+        return torch.matmul(e.unsqueeze(2), v[:, :, lo:hi])[:, :, 0], m, e.sum(-1)
+
+    if num_chunks is None:
+        acc, m, l = state(0, t)
+        return acc, m, l, None
+    cg = -(-ng_k // num_chunks)
+    parts = [state(c * cg * group_size, min(ng_k, (c + 1) * cg) * group_size) for c in range(num_chunks)]
+    m_all = torch.stack([p[1] for p in parts], -1)  # [B,Hq,C]
+    l_all = torch.stack([p[2] for p in parts], -1)
+    a_all = torch.stack([p[0] for p in parts], -2)  # [B,Hq,C,hd]
+    live = l_all > 0
+    mm = torch.where(live, m_all, torch.full_like(m_all, -math.inf)).amax(-1)
+    f = torch.where(live, torch.exp(m_all - mm[..., None]), torch.zeros_like(m_all))
+    acc = (f[..., None] * a_all).sum(-2)
+    l = (f * l_all).sum(-1)
+    partials = (a_all.reshape(b * hq, num_chunks, d), m_all.reshape(b * hq, num_chunks),
+                l_all.reshape(b * hq, num_chunks))
+    return acc, mm, l, partials
+
+
+def default_path_decode(query: torch.Tensor, state: dict, bits: int, alpha_k: float, alpha_v: float, n_rep: int,
+                        scaling: float) -> torch.Tensor:
+    """The reference's default GPU decode (attention.py:179-295 with its qk / av launches), with
+    its roundings, on the state of :func:`reference_decode`: the prefix logits of the qk launch
+    (fp32-dequantized keys, :46-49 / :389-450) rounded to the query dtype; the residual's logits
+    a matmul in the query dtype, then times ``scaling`` rounded again (:228-230); an fp32 softmax
+    cast back to the query dtype (:235-237); the av launch's sum (fp32-dequantized values,
+    :50-53 / :677-751) rounded to the query dtype; the residual's weighted sum rounded; their sum
+    rounded (:287-290).  Returns ``[B,Hq,hd]`` float32 (values of the query dtype)."""
+    dt = query.dtype
+    parts = []
+    if state["lq"]:
+        parts.append(prefix_logits(query, state["packed_k"], state["k_mn"], state["k_scale"], bits, alpha_k,
+                                   n_rep, scaling).to(dt))
+    dk = repeat_kv(state["res_k"], n_rep)
+    if dk.shape[2]:
+        lg = torch.matmul(query.double(), dk.double().transpose(2, 3)).to(dt)
+        parts.append((lg.double() * scaling).to(dt)[:, :, 0])
+    w = torch.softmax(torch.cat(parts, -1), -1, dtype=torch.float32).to(dt)
+    lv = state["lv"]
+    out = None
+    if lv:
+        out = prefix_weighted_values(w[..., :lv], state["packed_v"], state["v_mn"], state["v_scale"], bits,
+                                     alpha_v, n_rep, query.shape[-1]).to(dt)
+    dv = repeat_kv(state["res_v"], n_rep)
+    if dv.shape[2]:
+        dense = torch.matmul(w[..., lv:].unsqueeze(2).double(), dv.double())[:, :, 0].to(dt)
+        out = dense if out is None else (out.double() + dense.double()).to(dt)
+    return out.float()
+
+
 # ---------------------------------------------------------------------------
 # Cache-level convenience used by the parity tests and the CPU baseline
 # ---------------------------------------------------------------------------

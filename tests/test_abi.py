@@ -51,7 +51,8 @@ def test_version_and_strerror():
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 @pytest.mark.parametrize("cls,cname", [(_lib.DecodeArgs, "mz_decode_args"), (_lib.PrologueArgs, "mz_prologue_args"),
-                                       (_lib.QkArgs, "mz_qk_args"), (_lib.AvArgs, "mz_av_args")])
+                                       (_lib.QkArgs, "mz_qk_args"), (_lib.AvArgs, "mz_av_args"),
+                                       (_lib.PrefixStateArgs, "mz_prefix_state_args")])
 def test_args_layout_matches_c(tmp_path, cls, cname):
     fields = [f for f, _ in cls._fields_]
     src = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{HEADER}"', "int main(void) {",
@@ -138,3 +139,50 @@ def test_stream_read_rejects_bad_args_without_a_device():
     assert lib.muzero_stream_read(src, 16, out, 0, None) == -1
     assert lib.muzero_stream_read(src, 16, out, 65536, None) == -1
     assert lib.muzero_stream_read(src, -16, out, 1, None) == -1
+
+
+def test_noalloc_status_codes_match_the_workspace_entry_point_without_a_device():
+    """muzero_decode_attention_noalloc returns the status muzero_decode_attention gives for the same
+    arguments when the arguments are rejected: MZ_EUNSUPPORTED for head_dim 96 and for n_rep 17,
+    MZ_EINVAL for bits 9 (all before any device work; the pointers are placeholders)."""
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = 1, 1, 4, 96, 4
+    a.n_groups, a.n_residual = 0, 16
+    a.meta_dtype, a.io_dtype, a.out_dtype = _lib.MZ_F16, _lib.MZ_BF16, _lib.MZ_BF16
+    for field, value, want in (("head_dim", 96, -2), ("n_rep", 17, -2), ("bits", 9, -1)):
+        b = _lib.DecodeArgs.from_buffer_copy(a)
+        b.head_dim = 128
+        setattr(b, field, value)
+        assert lib.muzero_decode_attention(ctypes.byref(b), None) == want, field
+        assert lib.muzero_decode_attention_noalloc(ctypes.byref(b), None) == want, field
+
+
+def test_prefix_state_rejects_bad_args_without_a_device():
+    """muzero_decode_prefix_state takes the packed prefix alone: a residual, a negative chunk count,
+    missing outputs or chunk records are rejected (MZ_EINVAL) before any device work; an empty batch
+    is a no-op."""
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    a.batch, a.kv_heads, a.n_rep, a.head_dim, a.bits = 1, 1, 4, 128, 4
+    a.n_groups, a.n_residual = 2, 0
+    a.meta_dtype, a.io_dtype, a.out_dtype = _lib.MZ_F16, _lib.MZ_BF16, _lib.MZ_BF16
+    fake = 1 << 20
+    a.query = a.k_packed = a.k_mn = a.k_scale = a.v_packed = a.v_mn = a.v_scale = a.e_key = a.e_value = fake
+    a.out = fake
+    st = _lib.PrefixStateArgs()
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -1  # no outputs
+    st.acc = st.m = st.l = fake
+    st.n_chunks = -1
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -1
+    st.n_chunks = 3  # chunk records missing
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -1
+    st.n_chunks = 0
+    a.n_residual = 16  # not a prefix-only call
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -1
+    a.n_residual = 0
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -3  # no workspace
+    a.head_dim = 96
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == -2
+    a.head_dim, a.batch = 128, 0
+    assert lib.muzero_decode_prefix_state(ctypes.byref(a), ctypes.byref(st), None) == 0

@@ -1,0 +1,189 @@
+"""The reference's extension object on the GPU: ``load_mu_zero_cuda_extension()`` and its six
+functions, called exactly as the reference's own callers call them.
+
+* ``quantize`` / ``dequantize`` as ``quantizer.py:140-145`` / ``:220-223`` call them: codes and
+  metadata bit-identical to the oracle (the reference torch quantizer restated), dequantized
+  values bit-identical to its dequantizer.
+* ``qk`` and ``av`` as ``attention.py:186-201`` / ``:248-263`` call them, on a cache layer's
+  packed prefix (``.contiguous()`` copies of its views included), against the oracle's
+  restatement of those launches (fp32 dequantized keys / values, one rounding to the query dtype).
+* ``prefix_decode`` and ``prefix_decode_chunked`` as ``attention.py:104-151`` call them, followed by
+  the reference's own log-sum-exp merge with the dense residual (``:153-169``, restated here as
+  the caller's code): the prefix state ``(acc, m, l)`` and the chunk records against the
+  oracle's restatement of the reference's prefix-decode kernels, and the merged output against
+  the fp64 attention oracle at the attention tolerance.
+"""
+
+import math
+
+import pytest
+import torch
+
+import muzero_amd as mz
+from muzero_amd.cache.layer import MuZeroCacheLayer
+from muzero_amd.kernels import load_mu_zero_cuda_extension
+from oracle import reference_torch as ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+MAX_ABS = 2e-3
+MEAN_ABS = 1e-3
+
+
+def _layer(bits, B=2, hkv=2, n_rep=4, d=128, prefill=1000, seed=21, dtype=torch.bfloat16):
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill, d, hkv * n_rep, seed=seed, dtype=dtype)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=bits, alpha_key=2.0, alpha_value=2.0))
+    layer.update(k.to(DEV), v.to(DEV), {"materialize_full_kv": False})
+    return layer, k, v, q
+
+
+def test_extension_object_quantize_dequantize():
+    ext = load_mu_zero_cuda_extension()
+    assert ext is load_mu_zero_cuda_extension()  # cached, as the reference's lru_cache
+    g = torch.Generator().manual_seed(3)
+    rows = (torch.randn(300, 64, generator=g) * 3 + 0.5).to(torch.bfloat16)
+    for bits in (1, 2, 3, 4, 5, 7, 8):
+        qb = 8 * bits
+        packed = torch.empty(300, qb, dtype=torch.uint8, device=DEV)
+        mn = torch.empty(300, 1, dtype=torch.float16, device=DEV)
+        sc = torch.empty_like(mn)
+        ext.quantize(rows.to(DEV), packed, mn, sc, bits, 2.0, 1e-8)
+        wp, wmn, wsc = ref.quantize_rows(rows, bits, 2.0)
+        torch.cuda.synchronize()
+        assert torch.equal(packed.cpu(), wp), bits
+        assert torch.equal(mn.cpu().view(torch.int16), wmn.view(torch.int16)), bits
+        assert torch.equal(sc.cpu().view(torch.int16), wsc.view(torch.int16)), bits
+        out = torch.empty(300, 64, dtype=torch.float32, device=DEV)
+        ext.dequantize(packed, mn, sc, out, bits, 2.0)
+        want = ref.dequantize_rows(wp, wmn, wsc, bits, 2.0, 64, torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want), bits
+
+
+@pytest.mark.parametrize("bits", [4, 2, 3, 8])
+def test_extension_qk_av_as_the_default_decode_calls_them(bits):
+    n_rep, d = 4, 128
+    layer, k, v, q = _layer(bits)
+    state = layer.get_attention_state()
+    lq = state["key_prefix_length"]
+    lv = state["value_prefix_length"]
+    assert lq == lv > 0
+    query = q.to(DEV)
+    scaling = d ** -0.5
+    ext = load_mu_zero_cuda_extension()
+    # attention.py:186-201
+    prefix_logits = torch.empty((query.shape[0], query.shape[1], lq), dtype=query.dtype, device=query.device)
+    ext.qk(query.contiguous(), layer._packed_key_q.contiguous(), layer._key_mn.contiguous(),
+           layer._key_scale.contiguous(), prefix_logits, layer.nbits, float(layer._selected_alpha_key), n_rep,
+           scaling)
+    _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    want = ref.prefix_logits(q, st["packed_k"], st["k_mn"], st["k_scale"], bits, 2.0, n_rep, scaling)
+    torch.cuda.synchronize()
+    got = prefix_logits.cpu().double()
+    # one rounding of the fp32 sum to bf16: within a bf16 ulp of the fp64 value (plus fp32 noise)
+    assert bool(((got - want).abs() <= want.abs() * 2.0 ** -8 + 1e-4).all())
+    # attention.py:248-263, with the weights of a softmax over the prefix logits and the residual's
+    dense = torch.matmul(query, ref.repeat_kv(layer.keys, n_rep).transpose(2, 3).contiguous()) * scaling
+    attn_weights = torch.softmax(torch.cat([prefix_logits.unsqueeze(2), dense], -1), -1,
+                                 dtype=torch.float32).to(query.dtype)
+    prefix_output = torch.empty((query.shape[0], query.shape[1], layer.v_head_dim), dtype=query.dtype,
+                                device=query.device)
+    ext.av(attn_weights[..., :lv].squeeze(2).contiguous(), layer._packed_value_q[:, :, :lv, ...].contiguous(),
+           layer._value_mn[:, :, :lv, ...].contiguous(), layer._value_scale[:, :, :lv, ...].contiguous(),
+           prefix_output, layer.nbits, float(layer._selected_alpha_value), n_rep, layer.q_group_size)
+    w = attn_weights[..., :lv].squeeze(2).cpu()
+    want_o = ref.prefix_weighted_values(w, st["packed_v"], st["v_mn"], st["v_scale"], bits, 2.0, n_rep, d)
+    torch.cuda.synchronize()
+    got_o = prefix_output.cpu().double()
+    assert bool(((got_o - want_o).abs() <= want_o.abs() * 2.0 ** -8 + 1e-4).all())
+
+
+def _merge_dense(query, layer, n_rep, scaling, prefix_accum, prefix_m, prefix_l):
+    """The reference's caller code after prefix_decode (attention.py:153-169)."""
+    dense_keys = ref.repeat_kv(layer.keys, n_rep)
+    dense_vals = ref.repeat_kv(layer.values, n_rep)
+    dense_logits = (torch.matmul(query, dense_keys.transpose(2, 3).contiguous()) * scaling).squeeze(2).float()
+    dense_m = dense_logits.amax(dim=-1)
+    dense_exp = torch.exp(dense_logits - dense_m.unsqueeze(-1))
+    dense_l = dense_exp.sum(dim=-1)
+    dense_accum = torch.matmul(dense_exp.unsqueeze(2), dense_vals.float()).squeeze(2)
+    merged_m = torch.maximum(prefix_m, dense_m)
+    prefix_factor = torch.exp(prefix_m - merged_m)
+    dense_factor = torch.exp(dense_m - merged_m)
+    merged_l = prefix_l * prefix_factor + dense_l * dense_factor
+    merged_accum = prefix_accum * prefix_factor.unsqueeze(-1) + dense_accum * dense_factor.unsqueeze(-1)
+    out = merged_accum / merged_l.clamp_min(1e-20).unsqueeze(-1)
+    return out.to(query.dtype).unsqueeze(1).contiguous()
+
+
+def _check_state(acc, m, l, want):
+    """Kernel state against the oracle's: the normalized prefix output acc / l at the attention
+    tolerance, m and the log-sum-exp m + log(l) to within the fold kernel's logit rounding."""
+    wacc, wm, wl = want[:3]
+    o, wo = acc.cpu().double() / l.cpu().double()[..., None], wacc / wl[..., None]
+    err = (o - wo).abs()
+    assert err.max().item() < MAX_ABS and err.mean().item() < MEAN_ABS, (err.max().item(), err.mean().item())
+    assert (m.cpu().double() - wm).abs().max().item() < 2e-2
+    lse, wlse = m.cpu().double() + torch.log(l.cpu().double()), wm + torch.log(wl)
+    assert (lse - wlse).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("bits", [4, 2, 3, 8])
+@pytest.mark.parametrize("chunk_groups", [None, 2, 5])
+def test_extension_prefix_decode_as_the_reference_calls_it(bits, chunk_groups):
+    """chunk_groups None: prefix_decode (MUZERO_FUSED_PREFIX_DECODE_LEGACY=1); otherwise
+    prefix_decode_chunked with num_chunks = ceil(G / chunk_groups) (MUZERO_PREFIX_CHUNK_GROUPS, the
+    reference default 2), and once with more chunks than groups (empty chunks)."""
+    n_rep, d = 4, 128
+    layer, k, v, q = _layer(bits, prefill=1100)
+    state = layer.get_attention_state()
+    lv = state["value_prefix_length"]
+    query = q.to(DEV)
+    scaling = d ** -0.5
+    ext = load_mu_zero_cuda_extension()
+    batch_size, num_heads, _, head_dim = query.shape
+    prefix_accum = torch.empty((batch_size, num_heads, head_dim), dtype=torch.float32, device=query.device)
+    prefix_m = torch.empty((batch_size, num_heads), dtype=torch.float32, device=query.device)
+    prefix_l = torch.empty((batch_size, num_heads), dtype=torch.float32, device=query.device)
+    args = (query.contiguous(), layer._packed_key_q.contiguous(), layer._key_mn.contiguous(),
+            layer._key_scale.contiguous(), layer._packed_value_q[:, :, :lv, ...].contiguous(),
+            layer._value_mn[:, :, :lv, ...].contiguous(), layer._value_scale[:, :, :lv, ...].contiguous())
+    tail = (float(layer._selected_alpha_key), float(layer._selected_alpha_value), n_rep, scaling)
+    n_groups = layer._packed_key_q.shape[2]
+    # fp32 dequantized values (the reference kernels' codebooks) for the fold widths; the exact
+    # kernel that serves 8 bits rounds them to the layer dtype
+    ddt = torch.float32 if bits <= 7 else torch.bfloat16
+    _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    sargs = (q, st["packed_k"], st["k_mn"], st["k_scale"], st["packed_v"], st["v_mn"], st["v_scale"], bits,
+             2.0, 2.0, n_rep, scaling)
+    if chunk_groups is None:
+        ext.prefix_decode(*args, prefix_accum, prefix_m, prefix_l, *tail)
+        want = ref.prefix_decode_state(*sargs, dequant_dtype=ddt)
+        torch.cuda.synchronize()
+    else:
+        for num_chunks in (max(1, (n_groups + chunk_groups - 1) // chunk_groups), n_groups + 3):
+            partial_accum = torch.empty((batch_size * num_heads, num_chunks, head_dim), dtype=torch.float32,
+                                        device=query.device)
+            partial_m = torch.empty((batch_size * num_heads, num_chunks), dtype=torch.float32, device=query.device)
+            partial_l = torch.empty((batch_size * num_heads, num_chunks), dtype=torch.float32, device=query.device)
+            ext.prefix_decode_chunked(*args, partial_accum, partial_m, partial_l, prefix_accum, prefix_m, prefix_l,
+                                      *tail)
+            want = ref.prefix_decode_state(*sargs, num_chunks=num_chunks, dequant_dtype=ddt)
+            torch.cuda.synchronize()
+            pa, pm, pl = want[3]
+            live = pl > 0
+            gm, gl = partial_m.cpu().double(), partial_l.cpu().double()
+            assert torch.equal(gl > 0, live), num_chunks
+            assert bool((gm[~live] == -math.inf).all()) and bool((gl[~live] == 0).all())
+            assert bool((partial_accum.cpu()[~live] == 0).all())
+            _check_state(partial_accum.cpu()[live], gm[live], gl[live], (pa[live], pm[live], pl[live]))
+            _check_state(prefix_accum, prefix_m, prefix_l, want)
+    _check_state(prefix_accum, prefix_m, prefix_l, want)
+    # the reference's caller then merges the dense residual (attention.py:153-169)
+    out = _merge_dense(query, layer, n_rep, scaling, prefix_accum, prefix_m, prefix_l)
+    exact, _ = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                    dequant_dtype=ddt)
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= MAX_ABS + half_ulp).all()), (err - MAX_ABS - half_ulp).max().item()
+    assert err.mean().item() < MEAN_ABS + (exact.to(torch.bfloat16).double() - exact).abs().mean().item()

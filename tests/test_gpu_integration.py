@@ -535,3 +535,144 @@ def test_generate_with_head_dim_96(monkeypatch):
         scale = b.abs().max().item()
         assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
     assert torch.equal(split.sequences[:, :301], dense.sequences[:, :301])
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_four_group_flush_stream(bits):
+    """decode_flush_by_group=False (layer.py:378-396): a decode step flushes the key excess over
+    residual_length four groups (256 tokens) at a time, the prefill flush one group at a time.
+    After every step of a 600-step stream the stored prefix is byte-equal to the oracle's cache
+    of that prefix, and after each flush (and at the end) the fused decode matches the oracle."""
+    B, hkv, n_rep, d, prefill, steps, R = 2, 2, 4, 128, 700, 600, 128
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + steps, d, hkv * n_rep, seed=23 + bits)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=bits, alpha_key=2.0, alpha_value=2.0, residual_length=R,
+                                             decode_flush_by_group=False))
+    layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
+    lq = (prefill - R) // 64 * 64  # the prefill flush: whole groups of the excess
+    flushes = 0
+    qd = q.to(DEV)
+    for t in range(prefill, prefill + steps):
+        layer.update(k[:, :, t:t + 1].to(DEV), v[:, :, t:t + 1].to(DEV), {"materialize_full_kv": False})
+        length = t + 1
+        new_lq = lq + (length - lq - R) // 256 * 256
+        state = layer.get_attention_state()
+        assert state["key_prefix_length"] == state["value_prefix_length"] == new_lq, t
+        if new_lq == lq and t != prefill + steps - 1:
+            continue
+        flushes += new_lq != lq
+        lq = new_lq
+        # the oracle's cache of the same prefix: its residual is everything after lq
+        exact, st = ref.reference_decode(q, k[:, :, :length], v[:, :, :length], bits=bits, alpha_k=2.0,
+                                         alpha_v=2.0, group_size=64, residual=length - lq,
+                                         dequant_dtype=torch.float32)
+        assert st["lq"] == lq
+        assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"]), t
+        assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"]), t
+        for got, want in ((layer._key_mn, st["k_mn"]), (layer._key_scale, st["k_scale"]),
+                          (layer._value_mn, st["v_mn"]), (layer._value_scale, st["v_scale"])):
+            assert torch.equal(got.cpu().contiguous().view(torch.int16), want.contiguous().view(torch.int16)), t
+        assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+        out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), qd, None, d ** -0.5, state)
+        torch.cuda.synchronize()
+        err = (out.cpu().double() - exact).abs()
+        half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+        assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (t, err.max().item())
+    assert flushes == 2  # residual 140 -> 396 at step 256, flush; again 256 steps later
+
+
+def test_offload_prefetch_round_trip_then_decode():
+    """offload() moves the residual and the packed prefix to host memory and prefetch() brings them
+    back (layer.py:525-541); every byte survives, and the next decode step (with its flush) matches
+    the oracle's cache and attention."""
+    B, hkv, n_rep, d, prefill = 2, 2, 4, 128, 760
+    k, v, q, _ = ref.synthetic_kv(B, hkv, prefill + 1, d, hkv * n_rep, seed=29)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4, alpha_key=2.0, alpha_value=2.0))
+    _feed(layer, k[:, :, :prefill], v[:, :, :prefill], prefill - 60)
+    before = {n: getattr(layer, n).clone() for n in ("keys", "values", "_packed_key_q", "_key_mn", "_key_scale",
+                                                      "_packed_value_q", "_value_mn", "_value_scale")}
+    layer.offload()
+    torch.cuda.synchronize()
+    for n, t in before.items():
+        got = getattr(layer, n)
+        assert got.device.type == "cpu", n
+        assert torch.equal(got.contiguous().view(torch.uint8), t.cpu().contiguous().view(torch.uint8)), n
+    layer.prefetch()
+    torch.cuda.synchronize()
+    for n, t in before.items():
+        got = getattr(layer, n)
+        assert got.device == t.device, n
+        assert torch.equal(got.contiguous().view(torch.uint8), t.contiguous().view(torch.uint8)), n
+    layer.update(k[:, :, prefill:].to(DEV), v[:, :, prefill:].to(DEV), {"materialize_full_kv": False})
+    exact, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     dequant_dtype=torch.float32)
+    state = layer.get_attention_state()
+    assert state["key_prefix_length"] == st["lq"]
+    assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
+    assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
+    assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
+    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3, (err.max().item(), err.mean().item())
+
+
+def test_decode_kernel_switch_exact_matches_layer_dtype_path(monkeypatch):
+    """MUZERO_DECODE_KERNEL=exact sends the decode hook to the exact-dequantize kernel (dequantized
+    values rounded to the layer dtype, the reference's dequantize-then-attend semantics,
+    attention.py:213-226): at config 1's row shape it meets the attention tolerance against the
+    layer-dtype oracle; an unknown value raises."""
+    B, hkv, n_rep, d, length = 1, 8, 4, 128, 4096
+    k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=1234)
+    layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4))
+    layer.update(k.to(DEV), v.to(DEV), {"materialize_full_kv": False})
+    exact, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    state = layer.get_attention_state()
+    assert state["key_prefix_length"] == st["lq"] == 3968
+    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "exact")
+    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    torch.cuda.synchronize()
+    from muzero_amd import _lib
+    assert layer._hip_decode is not None and layer._hip_decode.args.kernel_path == _lib.MZ_PATH_EXACT
+    err = (out.cpu().double() - exact).abs()
+    half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
+    rounding = (exact.to(torch.bfloat16).double() - exact).abs().mean().item()
+    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3 + rounding, err.max().item()
+    # the cached launch follows the switch: back to the fold kernel when it is unset
+    monkeypatch.delenv("MUZERO_DECODE_KERNEL")
+    mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+    assert layer._hip_decode.args.kernel_path == _lib.MZ_PATH_AUTO
+    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "fastest")
+    with pytest.raises(ValueError):
+        mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+
+
+def test_generate_with_exact_decode_kernel_matches_dequant_path(monkeypatch):
+    """generate() with MUZERO_DECODE_KERNEL=exact runs the fused exact kernel on every decode step;
+    its decode-step logits match the dequantize-then-attend run through the model's own attention
+    (MUZERO_DISABLE_FUSED_DECODE=1: the same layer-dtype values), and the prefill token agrees."""
+    mz.patch_transformers()
+    model = _tiny_model("qwen3")
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 512, (2, 300), generator=g).to(DEV)
+    kw = dict(max_new_tokens=3, do_sample=False, cache_implementation="mu_zero_4bit",
+              cache_config={"residual_length": 128}, output_scores=True, return_dict_in_generate=True,
+              pad_token_id=0)
+    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "exact")
+    mz.reset_mu_zero_decode_stats()
+    with torch.no_grad():
+        fused = model.generate(ids, **kw)
+    stats = mz.get_mu_zero_decode_stats()
+    assert stats.get("hip_fused_decode", 0) == 2 * 2
+    for layer in fused.past_key_values.layers:
+        from muzero_amd import _lib
+        assert layer._hip_decode.args.kernel_path == _lib.MZ_PATH_EXACT
+    monkeypatch.delenv("MUZERO_DECODE_KERNEL")
+    monkeypatch.setenv("MUZERO_DISABLE_FUSED_DECODE", "1")
+    with torch.no_grad():
+        dense = model.generate(ids, **kw)
+    for s in (1, 2):
+        a, b = fused.scores[s].float(), dense.scores[s].float()
+        scale = b.abs().max().item()
+        assert (a - b).abs().max().item() <= 2e-2 * max(scale, 1.0), (s, (a - b).abs().max().item(), scale)
+    assert torch.equal(fused.sequences[:, :301], dense.sequences[:, :301])

@@ -346,3 +346,16 @@ def test_decode_stats_counter_names():
     assert s["fused_prefix_decode_chunked_success"] == 1
     assert s["fused_qk_fallback"] == s["fused_av_fallback"] == s["fused_prefix_decode_fallback"] == 1
     A.reset_mu_zero_decode_stats()
+
+
+def test_decode_kernel_switch_parsing(monkeypatch):
+    """MUZERO_DECODE_KERNEL: unset / empty -> auto; exact, fold (any case, spaces); anything else raises."""
+    from muzero_amd.cache import attention as A
+    monkeypatch.delenv("MUZERO_DECODE_KERNEL", raising=False)
+    assert A._kernel_path() == "auto"
+    for raw, want in (("", "auto"), ("exact", "exact"), (" FOLD ", "fold"), ("Auto", "auto")):
+        monkeypatch.setenv("MUZERO_DECODE_KERNEL", raw)
+        assert A._kernel_path() == want
+    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "dense")
+    with pytest.raises(ValueError):
+        A._kernel_path()

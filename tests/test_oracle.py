@@ -367,3 +367,70 @@ def test_qk_softmax_av_composes_to_decode_attention():
     vq = ref.dequantize_value_block(pv, vmn, vsc, 3, 2.0, 64, hd, torch.float32)
     exact = ref.decode_attention_exact(q, kq, vq, None, hd ** -0.5)[:, 0]
     assert torch.allclose(out, exact, atol=1e-12, rtol=0)
+
+
+# ------------------------------------------------------- prefix decode state, default path
+
+@pytest.mark.parametrize("num_chunks", [None, 1, 3, 5, 9])
+def test_prefix_decode_state_brute_force(num_chunks):
+    """prefix_decode_state against an explicit per-(b, h) loop over the brute-force-pinned
+    prefix_logits / fp32 value rows: m is the largest logit of the chunk, l and acc the
+    exp(s - m) sums; chunk c covers groups [c*cg, (c+1)*cg), cg = ceil(G / chunks), chunks past
+    the prefix are (0, -inf, 0); the merged state is the same sums over every chunk."""
+    g = torch.Generator().manual_seed(31)
+    b, hkv, n_rep, nsg, hd = 1, 2, 2, 4, 8
+    keys = torch.randn(b, hkv, 64 * nsg, hd, generator=g) * 2
+    vals = torch.randn(b, hkv, 64 * nsg, hd, generator=g)
+    q = torch.randn(b, hkv * n_rep, 1, hd, generator=g)
+    pk, kmn, ksc = ref.quantize_key_block(keys, 3, 2.0)
+    pv, vmn, vsc = ref.quantize_value_block(vals, 3, 4.0)
+    acc, m, l, parts = ref.prefix_decode_state(q, pk, kmn, ksc, pv, vmn, vsc, 3, 2.0, 4.0, n_rep, 0.3,
+                                               num_chunks=num_chunks)
+    logits = ref.prefix_logits(q, pk, kmn, ksc, 3, 2.0, n_rep, 0.3)[0]  # [Hq, L]
+    vrows = _rows_fp32(pv, vmn, vsc, 3, 4.0)[0, :, :, 0, :hd]  # [hkv, L, hd]
+    chunks = 1 if num_chunks is None else num_chunks
+    cg = -(-nsg // chunks)
+    for h in range(hkv * n_rep):
+        s = [float(x) for x in logits[h]]
+        mx = max(s)
+        ll = sum(math.exp(x - mx) for x in s)
+        aa = [sum(math.exp(s[t] - mx) * float(vrows[h // n_rep, t, c]) for t in range(len(s))) for c in range(hd)]
+        assert abs(float(m[0, h]) - mx) < 1e-12 and abs(float(l[0, h]) - ll) < 1e-9 * ll
+        assert max(abs(float(acc[0, h, c]) - aa[c]) for c in range(hd)) < 1e-9 * (1 + max(map(abs, aa)))
+        if num_chunks is None:
+            assert parts is None
+            continue
+        for c in range(chunks):
+            lo, hi = 64 * min(nsg, c * cg), 64 * min(nsg, (c + 1) * cg)
+            row = h  # b = 0
+            if hi <= lo:
+                assert parts[1][row, c] == -math.inf and parts[2][row, c] == 0 and parts[0][row, c].abs().max() == 0
+                continue
+            cm = max(s[lo:hi])
+            assert abs(float(parts[1][row, c]) - cm) < 1e-12
+            assert abs(float(parts[2][row, c]) - sum(math.exp(x - cm) for x in s[lo:hi])) < 1e-9 * (hi - lo)
+
+
+def test_default_path_decode_in_fp32_is_the_fp32_dequant_attention():
+    """With fp32 queries every rounding of default_path_decode is an fp32 rounding, so it equals the
+    fp64 attention over the fp32-dequantized prefix plus the residual to ~1e-6 (a dropped term,
+    a wrong index or a swapped prefix / residual split would not)."""
+    k, v, q, _ = ref.synthetic_kv(2, 2, 700, 64, 8, seed=3, dtype=torch.float32)
+    exact, st = ref.reference_decode(q, k, v, bits=3, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     dequant_dtype=torch.float32)
+    got = ref.default_path_decode(q, st, 3, 2.0, 2.0, 4, 64 ** -0.5)
+    assert got.shape == (2, 8, 64)
+    assert (got.double() - exact[:, 0]).abs().max().item() < 5e-6
+
+
+def test_default_path_decode_rounds_like_the_reference_in_bf16():
+    """In bf16 the default path's roundings (logits and weights to bf16) move it away from the exact
+    fp32-dequant attention by more than fp32 noise but by less than a few 1e-2 on these inputs, and
+    its values are bf16 numbers."""
+    k, v, q, _ = ref.synthetic_kv(1, 2, 900, 128, 8, seed=4)
+    exact, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
+                                     dequant_dtype=torch.float32)
+    got = ref.default_path_decode(q, st, 4, 2.0, 2.0, 4, 128 ** -0.5)
+    assert torch.equal(got, got.to(torch.bfloat16).float())
+    d = (got.double() - exact[:, 0]).abs()
+    assert 1e-4 < d.max().item() < 5e-2

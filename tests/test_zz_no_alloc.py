@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def _plan(B, hkv, length, bits, seed, n_split=0):
+def _plan(B, hkv, length, bits, seed, n_split=0, kernel_path="auto"):
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(B, hkv, length, 128, hkv * 4, seed=seed)
     _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
@@ -29,7 +29,7 @@ def _plan(B, hkv, length, bits, seed, n_split=0):
     return L.DecodePlan(d(q), bits=bits, n_groups=st["lq"] // 64, k_packed=d(st["packed_k"]), k_mn=d(st["k_mn"]),
                         k_scale=d(st["k_scale"]), v_packed=d(st["packed_v"]), v_mn=d(st["v_mn"]),
                         v_scale=d(st["v_scale"]), k_res=d(st["res_k"]), v_res=d(st["res_v"]), alpha_key=2.0,
-                        alpha_value=2.0, scaling=128 ** -0.5, n_split=n_split)
+                        alpha_value=2.0, scaling=128 ** -0.5, n_split=n_split, kernel_path=kernel_path)
 
 
 def _noalloc(plan):
@@ -44,11 +44,13 @@ def _noalloc(plan):
     return st, out
 
 
-@pytest.mark.parametrize("bits", [4, 5])
-def test_noalloc_matches_workspace_entry_point(bits):
-    """bits 4: the fold kernel, bits 5: the general kernel; both calls split over tokens."""
+@pytest.mark.parametrize("bits,kernel_path,fold", [(4, "auto", True), (8, "auto", False), (4, "exact", False)])
+def test_noalloc_matches_workspace_entry_point(bits, kernel_path, fold):
+    """The fold kernel (4 bits) and the general kernel (8 bits, and 4 bits forced onto it), both
+    calls split over tokens."""
     for B, hkv, length, seed in ((2, 2, 4096, 1), (1, 1, 1024, 2)):
-        plan = _plan(B, hkv, length, bits, seed)
+        plan = _plan(B, hkv, length, bits, seed, kernel_path=kernel_path)
+        assert plan.uses_fold == fold  # the kernel this case is meant to send through the scratch
         assert plan.n_split > 1  # the call goes through the scratch
         want = plan.run().clone()
         st, got = _noalloc(plan)
