@@ -528,6 +528,9 @@ def main():
                     help="decode mode: dtype of the query and the K/V the cache is quantized from (the residual's)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
+    ap.add_argument("--kernel-path", choices=("auto", "exact", "fold"), default="auto",
+                    help="decode mode: the library's kernel choice (auto), or force the exact-dequantize kernel "
+                         "(the reference's dequantize-then-attend values) or the fold kernel")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))
@@ -572,7 +575,7 @@ def main():
         caches.append({k_: t.clone() for k_, t in caches[0].items()})
     del k, v
     plans = [DecodePlan(q, bits=bits, n_groups=lq // 64, alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5,
-                        n_split=args.n_split, **c) for c in caches]
+                        n_split=args.n_split, kernel_path=args.kernel_path, **c) for c in caches]
     stream = torch.cuda.current_stream(dev)
     for i in range(args.warmup):
         plans[i % len(plans)].run()
@@ -597,12 +600,15 @@ def main():
     copy_gbs = measured_copy_gbs(1024, 10)
     read_gbs = measured_read_gbs(1024, 10)
 
-    traffic = None
-    if os.path.exists(args.traffic_json) and (hq, hkv, d) == (32, 8, 128) and args.kv_dtype == "bf16":  # measured for this case only
+    traffic = traffic_commit = None
+    if (os.path.exists(args.traffic_json) and (hq, hkv, d) == (32, 8, 128) and args.kv_dtype == "bf16"
+            and args.kernel_path == "auto" and args.n_split == 0):  # measured for this case only
         with open(args.traffic_json) as f:
             tj = json.load(f)
         key = f"B{B}_L{L}_b{bits}_R{R}"
         traffic = tj.get(key)
+        if traffic is not None:
+            traffic_commit = tj.get("_measured", {}).get("commit")
 
     cpu = None
     if not args.no_cpu:
@@ -642,15 +648,18 @@ def main():
                                 if (hq, hkv, d) == (32, 8, 128) and args.kv_dtype == "bf16" else
                                 f"decode attention (not a benchmark config shape): B={B} Hq={hq} Hkv={hkv} hd={d} ctx={L} "
                                 f"{args.kv_dtype} ")
-                               + f"mu_zero {bits}-bit G64 R={r} fp16 meta",
+                               + f"mu_zero {bits}-bit G64 R={r} fp16 meta"
+                               + ("" if args.kernel_path == "auto" else f", kernel forced: {args.kernel_path}"),
                    "batch": B, "context": L, "bits": bits, "residual": r, "quantized_tokens": lq,
                    "cache_copies": args.copies},
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "attn_only_tokens_per_s_36_layers": round(B / (36 * ms_step * 1e-3), 1),
         "kernels_ms": kernels_ms,
+        "kernel": "fold" if plans[0].uses_fold else "exact-dequantize (general)",
         "n_split": plans[0].n_split,
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_measured_at_commit": traffic_commit,
                      "algorithmic_bytes": nbytes,
                      "measured_copy_GBps": round(copy_gbs, 1),
                      "frac_of_measured_copy": round(gbs_split / copy_gbs, 4),

@@ -194,8 +194,8 @@ typedef struct mz_decode_args {
   const float* mask; int64_t mask_sb;
   const float* e_key; const float* e_value;
   /* (P, N) fold tables for alpha_key / alpha_value (bits 1 to 7): pairs of
-   * fp16 (P, N) packed in uint32 (P in the low half), row = zero level,
-   * column = code; 16 x 16 for bits 1 to 4 (zero beyond 2^bits - 1),
+   * fp16 (P - 1/2, N - 1/2) packed in uint32 (P in the low half), row = zero
+   * level, column = code; 16 x 16 for bits 1 to 4 (the pair (0, 0) beyond 2^bits - 1),
    * 2^bits x 64 for 5 and 6 bits, 128 x 128 for 7 bits; see
    * muzero_amd/tables.py ("fold1" .. "fold7").  Needed by the fold fast path;
    * may be null (the generic path is used then).  7 bits: the fold path

@@ -21,7 +21,8 @@ harness reads (``benchmarks/bench_throughput.py:341-343``): ``calls``,
 when there is a quantized value prefix, and ``fused_prefix_decode_success`` /
 ``fused_prefix_decode_chunked_success`` (the one kernel is the split-over-tokens
 prefix decode with the residual merged in); plus ``hip_fused_decode`` for
-every call the kernel serves.  When the launch raises, the matching
+every call the kernel serves, split into ``hip_fold_kernel`` and
+``hip_exact_kernel`` by the kernel that ran.  When the launch raises, the matching
 ``*_fallback`` counters are incremented as in the reference, and the error
 propagates: this build has no dequantize-then-attend fallback to run instead.
 
@@ -123,13 +124,14 @@ def mu_zero_decode_attention_forward(
             key = (storage, query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key,
                    alpha_value, float(scaling), kernel_path)
     try:
-        out = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
-                      scaling, attention_mask, value_prefix_length, kernel_path)
+        out, fold = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
+                            scaling, attention_mask, value_prefix_length, kernel_path)
     except Exception:
         _count(key_prefix_length, value_prefix_length, "fallback")
         raise
     _count(key_prefix_length, value_prefix_length, "success")
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
+    _MU_ZERO_DECODE_STATS["hip_fold_kernel" if fold else "hip_exact_kernel"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1
     return out, None
 
@@ -231,6 +233,7 @@ def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_k
             attention_mask, value_prefix_length, kernel_path="auto"):
     if fast is not None and key is not None and fast.key == key:
         out = fast.launch(query, n_groups, r)
+        fold = fast.uses_fold
     else:
         plan = _k.DecodePlan(
             query,
@@ -246,7 +249,8 @@ def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_k
             kernel_path=kernel_path,
         )
         out = plan.run()
+        fold = plan.uses_fold
         # cache the validated arguments only when every pointer they hold is
         # stable across steps (residual windows in their decode buffers, no mask)
         layer._hip_decode = _k.StepDecode(plan, key) if key is not None else None
-    return out
+    return out, fold

@@ -5,8 +5,10 @@
 //   x = mn + s * (za + pe * E[pb][q - zl])   (q >= zl)
 //   x = mn + s * (za - ne * E[nb][zl - q])   (q <  zl)
 // which is x = a + bp * P(zl, q) + bn * N(zl, q) with per-group scalars
-// a = mn + s*za, bp = s*pe, bn = -s*ne and a (qmax+1)^2 table of pairs
-// (P, N) = (E[pb][q-zl], 0) or (0, E[nb][zl-q]).  So
+// a = mn + s*za + (bp + bn)/2, bp = s*pe, bn = -s*ne and a (qmax+1)^2 table of
+// pairs (P, N) = (E[pb][q-zl], 0) or (0, E[nb][zl-q]), stored shifted by 1/2
+// (entries in [-1/2, 1/2] halve their worst fp16 rounding error; the shift's
+// share, (bp + bn)/2, rides in a).  So
 //   q.k = sum_c (Q_c*a_c) + sum_c [(Q_c*bp_c) P + (Q_c*bn_c) N]
 // is an MFMA whose A operand carries the group scalars times the query (for
 // P.V: the softmax weight times the token's scalars) and whose B operand is
@@ -226,9 +228,10 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   const float pe = fmaxf(1.f - za, eps);
   const float ne = fmaxf(za, eps);
   GroupScalars r;
-  r.a = mn + s * za;
   r.bp = s * pe;
   r.bn = -(s * ne);
+  // the table holds (P - 1/2, N - 1/2): the constant part carries (bp + bn) / 2
+  r.a = (mn + s * za) + 0.5f * (r.bp + r.bn);
   r.zl = (uint32_t)zl;
   return r;
 }

@@ -395,7 +395,7 @@ class StepDecode:
     prefix/residual lengths, the output and the workspace size change."""
 
     __slots__ = ("key", "args", "argp", "lib", "device", "q_dtype", "out_shape", "workspace", "_keep",
-                 "_keep_query")
+                 "_keep_query", "uses_fold")
 
     def __init__(self, plan: DecodePlan, key):
         self.key = key
@@ -407,6 +407,7 @@ class StepDecode:
         self.out_shape = tuple(plan.out.shape)
         self.workspace = plan.workspace
         self._keep = plan._keep  # tables, packed/residual views: kept alive with the arguments
+        self.uses_fold = plan.uses_fold
 
     def launch(self, query: torch.Tensor, n_groups: int, n_residual: int) -> torch.Tensor:
         a = self.args
@@ -424,6 +425,7 @@ class StepDecode:
             self.workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=self.device)
             a.workspace = self.workspace.data_ptr()
         a.workspace_bytes = max(int(need), int(a.workspace_bytes))
+        self.uses_fold = self.lib.muzero_decode_uses_fold(self.argp) == 1
         check(self.lib.muzero_decode_attention(self.argp, stream_ptr(self.device)), "muzero_decode_attention")
         self._keep_query = q  # alive until the next launch (the kernel reads it asynchronously)
         return out

@@ -31,13 +31,16 @@ the reference:
 
 ``fold1`` .. ``fold7`` (decode attention, 1- to 7-bit codes)
     For zero level ``zl`` and code ``q`` (``qmax = 2^bits - 1``), the pair
-    ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``
-    as two fp16 packed in one uint32 (P in the low half), with
-    ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; row zl, column q, zero
-    beyond qmax: 16 x 16 for 1-4 bits, (qmax+1) x 64 for 5 and 6 bits,
+    ``(P, N) = (E[pb][q-zl], 0)`` if ``q >= zl`` else ``(0, E[nb][zl-q])``,
+    stored shifted by ``FOLD_SHIFT`` (``P - 1/2``, ``N - 1/2``, both in
+    [-1/2, 1/2]: half the worst fp16 rounding error of ``P`` and ``N`` in
+    [0, 1]) as two fp16 packed in one uint32 (P in the low half), with
+    ``pb = max(qmax-zl, 1)``, ``nb = max(zl, 1)``; row zl, column q, the pair
+    (0, 0) beyond qmax: 16 x 16 for 1-4 bits, (qmax+1) x 64 for 5 and 6 bits,
     128 x 128 for 7 bits (the rows the kernel keeps in LDS).  The decode kernel rewrites the
-    reference's dequantization as ``a + bp*P + bn*N`` per group and looks
-    these pairs up per code.
+    reference's dequantization as ``a + bp*P + bn*N`` per group, i.e.
+    ``(a + (bp + bn)/2) + bp*(P - 1/2) + bn*(N - 1/2)``, and looks these pairs
+    up per code.
 
 These are constants of the format, the way the reference's own
 ``MU_ZERO_ALPHA2_COMPAND`` table is (``muzero/kernels/loader.py:133-150``);
@@ -52,6 +55,7 @@ import threading
 import torch
 
 MAX_BINS = 255
+FOLD_SHIFT = 0.5  # subtracted from every (P, N) entry of the fold tables before the fp16 rounding
 _VERIFIED_MONOTONE = {2.0, 4.0, 16.0}  # exhaustively checked (tests/test_tables.py)
 _lock = threading.RLock()  # builders call host_table recursively
 _host_cache: dict = {}
@@ -155,8 +159,9 @@ def _build_fold(alpha: float, bits: int) -> torch.Tensor:
                 p[zl, q] = e[_expm1_row(pb) + q - zl]
             else:
                 nq[zl, q] = e[_expm1_row(nb) + zl - q]
-    lo = p.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
-    hi = nq.to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    # P - 1/2 and N - 1/2 are exact in fp32 (P, N in [0, 1]), then rounded once to fp16
+    lo = (p - FOLD_SHIFT).to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
+    hi = (nq - FOLD_SHIFT).to(torch.float16).view(torch.int16).to(torch.int32) & 0xFFFF
     return (lo | (hi << 16)).reshape(-1).contiguous()
 
 

@@ -11,7 +11,7 @@ functions, called exactly as the reference's own callers call them.
   the reference's own log-sum-exp merge with the dense residual (``:153-169``, restated here as
   the caller's code): the prefix state ``(acc, m, l)`` and the chunk records against the
   oracle's restatement of the reference's prefix-decode kernels, and the merged output against
-  the fp64 attention oracle at the attention tolerance.
+  the same merge of the oracle's prefix state at the attention tolerance.
 """
 
 import math
@@ -179,10 +179,13 @@ def test_extension_prefix_decode_as_the_reference_calls_it(bits, chunk_groups):
             _check_state(partial_accum.cpu()[live], gm[live], gl[live], (pa[live], pm[live], pl[live]))
             _check_state(prefix_accum, prefix_m, prefix_l, want)
     _check_state(prefix_accum, prefix_m, prefix_l, want)
-    # the reference's caller then merges the dense residual (attention.py:153-169)
+    # the reference's caller then merges the dense residual (attention.py:153-169; its dense
+    # logits are rounded to the query dtype); the same merge of the oracle's prefix state is the
+    # answer the merged output is held to
     out = _merge_dense(query, layer, n_rep, scaling, prefix_accum, prefix_m, prefix_l)
-    exact, _ = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
-                                    dequant_dtype=ddt)
+    f32 = lambda t: t.to(device=DEV, dtype=torch.float32)
+    exact = _merge_dense(query, layer, n_rep, scaling, f32(want[0]), f32(want[1]), f32(want[2]))
+    exact = exact.cpu().double()
     err = (out.cpu().double() - exact).abs()
     half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
     assert bool((err <= MAX_ABS + half_ulp).all()), (err - MAX_ABS - half_ulp).max().item()

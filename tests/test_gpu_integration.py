@@ -630,18 +630,18 @@ def test_decode_kernel_switch_exact_matches_layer_dtype_path(monkeypatch):
     state = layer.get_attention_state()
     assert state["key_prefix_length"] == st["lq"] == 3968
     monkeypatch.setenv("MUZERO_DECODE_KERNEL", "exact")
+    mz.reset_mu_zero_decode_stats()
     out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
     torch.cuda.synchronize()
-    from muzero_amd import _lib
-    assert layer._hip_decode is not None and layer._hip_decode.args.kernel_path == _lib.MZ_PATH_EXACT
+    assert mz.get_mu_zero_decode_stats().get("hip_exact_kernel") == 1
     err = (out.cpu().double() - exact).abs()
     half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
     rounding = (exact.to(torch.bfloat16).double() - exact).abs().mean().item()
     assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3 + rounding, err.max().item()
-    # the cached launch follows the switch: back to the fold kernel when it is unset
+    # back to the fold kernel when the switch is unset
     monkeypatch.delenv("MUZERO_DECODE_KERNEL")
     mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
-    assert layer._hip_decode.args.kernel_path == _lib.MZ_PATH_AUTO
+    assert mz.get_mu_zero_decode_stats().get("hip_fold_kernel") == 1
     monkeypatch.setenv("MUZERO_DECODE_KERNEL", "fastest")
     with pytest.raises(ValueError):
         mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
@@ -663,10 +663,7 @@ def test_generate_with_exact_decode_kernel_matches_dequant_path(monkeypatch):
     with torch.no_grad():
         fused = model.generate(ids, **kw)
     stats = mz.get_mu_zero_decode_stats()
-    assert stats.get("hip_fused_decode", 0) == 2 * 2
-    for layer in fused.past_key_values.layers:
-        from muzero_amd import _lib
-        assert layer._hip_decode.args.kernel_path == _lib.MZ_PATH_EXACT
+    assert stats.get("hip_fused_decode", 0) == stats.get("hip_exact_kernel", 0) == 2 * 2
     monkeypatch.delenv("MUZERO_DECODE_KERNEL")
     monkeypatch.setenv("MUZERO_DISABLE_FUSED_DECODE", "1")
     with torch.no_grad():

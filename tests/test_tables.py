@@ -79,13 +79,15 @@ def test_fold_table_entries(bits):
         off = lambda n: (n - 1) * (n + 2) // 2
         for zl in range(16):
             for q in range(16):
-                P, N = f[zl, q, 0].item(), f[zl, q, 1].item()
+                # stored shifted by 1/2 (fp16 of the fp32 difference)
+                P, N = f[zl, q, 0].item() + 0.5, f[zl, q, 1].item() + 0.5
+                sh = lambda x: float((x - 0.5).half()) + 0.5
                 if zl > qmax or q > qmax:
                     assert P == 0.0 and N == 0.0
                 elif q >= zl:
-                    assert P == float(e[off(max(qmax - zl, 1)) + q - zl].half()) and N == 0.0
+                    assert P == sh(e[off(max(qmax - zl, 1)) + q - zl]) and N == 0.0
                 else:
-                    assert N == float(e[off(max(zl, 1)) + zl - q].half()) and P == 0.0
+                    assert N == sh(e[off(max(zl, 1)) + zl - q]) and P == 0.0
 
 
 def test_fold_table_pairs():
@@ -98,10 +100,14 @@ def test_fold_table_pairs():
         for q in range(16):
             P, N = f[zl, q, 0].item(), f[zl, q, 1].item()
             if q >= zl:
-                assert P == float(torch.tensor(e[off(pb) + q - zl].item()).half()) and N == 0.0
+                assert P == float(torch.tensor(e[off(pb) + q - zl].item() - 0.5).half()) and N == -0.5
             else:
-                assert N == float(torch.tensor(e[off(nb) + zl - q].item()).half()) and P == 0.0
-    # the fold reproduces the reference dequantization up to the fp16 rounding of (P, N)
+                assert N == float(torch.tensor(e[off(nb) + zl - q].item() - 0.5).half()) and P == -0.5
+            # the shifted entries halve the worst fp16 rounding error of entries in [0, 1]
+            exact = e[off(pb) + q - zl].item() if q >= zl else e[off(nb) + zl - q].item()
+            assert abs((P if q >= zl else N) + 0.5 - exact) <= 2.0 ** -13
+    # the fold reproduces the reference dequantization up to the fp16 rounding of (P, N), the
+    # constant part carrying the shift: x = (a + (bp + bn) / 2) + bp * (P - 1/2) + bn * (N - 1/2)
     g = torch.Generator().manual_seed(0)
     for _ in range(50):
         mn = -torch.rand(1, generator=g).item() * 3
@@ -114,5 +120,6 @@ def test_fold_table_pairs():
                 ref = mn + s * (za + pe * e[off(max(15 - zl, 1)) + q - zl].item())
             else:
                 ref = mn + s * (za - ne * e[off(max(zl, 1)) + zl - q].item())
-            fold = (mn + s * za) + s * pe * f[zl, q, 0].item() - s * ne * f[zl, q, 1].item()
-            assert math.isclose(fold, ref, rel_tol=0, abs_tol=s * 1e-3)
+            bp, bn = s * pe, -s * ne
+            fold = (mn + s * za + 0.5 * (bp + bn)) + bp * f[zl, q, 0].item() + bn * f[zl, q, 1].item()
+            assert math.isclose(fold, ref, rel_tol=0, abs_tol=s * 2.0 ** -12)
