@@ -183,6 +183,46 @@ def dequantize_rows(packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor,
     return (unit * span + lo).to(out_dtype)
 
 
+FOLD = "fold"  # dequantization semantics of the fused decode kernel (dequantize_rows_fold)
+
+
+def dequantize_rows_fold(packed: torch.Tensor, mn: torch.Tensor, scale: torch.Tensor, bits: int,
+                         alpha: float, group_size: int, eps: float = AMAX_EPS) -> torch.Tensor:
+    """The dequantized values the library's fused decode kernel computes with (float64).
+
+    Same group quantities as :func:`dequantize_rows` (fp32, from the stored metadata, the
+    scale guarded as the reference CUDA kernel does, ``loader.py:201``), but the value is formed
+    as ``a + bp*P + bn*N`` with ``bp = s*pe``, ``bn = -s*ne``, ``a = (mn + s*za) + (bp + bn)/2``
+    (fp32 ops) and ``(P, N)`` the code's expm1 entry on its side of the zero level, stored as
+    fp16 after subtracting 1/2.  That fp16 rounding (at most 2^-13 per entry) is the only place
+    it departs from the reference's fp32 value (``quantizer.py:241-255``); the sum is taken in
+    float64.  Test infrastructure: the kernel's own arithmetic is checked against this at the
+    attention tolerance, and this against :func:`dequantize_rows` by the rounding bound.
+    """
+    top = float((1 << bits) - 1)
+    q = unpack_q(packed, bits, group_size).to(torch.float32)
+    lo = mn.to(torch.float32)
+    span = scale.to(torch.float32).clamp_min(eps)
+    anchor = ((0.0 - lo) / span).clamp(0.0, 1.0)
+    anchor_level = torch.round(anchor * top)
+    up_bins = (top - anchor_level).clamp_min(1.0)
+    down_bins = anchor_level.clamp_min(1.0)
+    up_extent = (1.0 - anchor).clamp_min(eps)
+    down_extent = anchor.clamp_min(eps)
+    log_base = torch.log1p(torch.tensor(alpha, device=packed.device, dtype=torch.float32))
+    up_frac = ((q - anchor_level) / up_bins).clamp(0.0, 1.0)
+    down_frac = ((anchor_level - q) / down_bins).clamp(0.0, 1.0)
+    pos = q >= anchor_level
+    p_val = torch.where(pos, torch.expm1(up_frac * log_base) / alpha, torch.zeros_like(q))
+    n_val = torch.where(pos, torch.zeros_like(q), torch.expm1(down_frac * log_base) / alpha)
+    bp = span * up_extent
+    bn = -(span * down_extent)
+    a = (lo + span * anchor) + 0.5 * (bp + bn)
+    p16 = (p_val - 0.5).to(torch.float16).double()
+    n16 = (n_val - 0.5).to(torch.float16).double()
+    return a.double() + bp.double() * p16 + bn.double() * n16
+
+
 # ---------------------------------------------------------------------------
 # K/V grouping — muzero/cache/layer.py:271-345
 # ---------------------------------------------------------------------------
@@ -226,20 +266,30 @@ def quantize_value_block(values: torch.Tensor, bits: int, alpha: float, group_si
 
 def dequantize_key_block(pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor, bits: int,
                          alpha: float, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:
-    """Packed keys ``[B,H,nsg,hd,qb]`` -> ``[B,H,nsg*G,hd]`` (layer.py:324-334)."""
+    """Packed keys ``[B,H,nsg,hd,qb]`` -> ``[B,H,nsg*G,hd]`` (layer.py:324-334); ``out_dtype``
+    :data:`FOLD` gives the fused decode kernel's values (:func:`dequantize_rows_fold`)."""
     b, h, nsg, d, qb = pq.shape
-    rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
-                          group_size, out_dtype)
+    if out_dtype == FOLD:
+        rec = dequantize_rows_fold(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                                   group_size)
+    else:
+        rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                              group_size, out_dtype)
     return rec.reshape(b, h, nsg, d, group_size).permute(0, 1, 2, 4, 3).reshape(b, h, nsg * group_size, d)
 
 
 def dequantize_value_block(pq: torch.Tensor, mn: torch.Tensor, sc: torch.Tensor, bits: int,
                            alpha: float, group_size: int, head_dim: int,
                            out_dtype: torch.dtype) -> torch.Tensor:
-    """Packed values ``[B,H,T,ng,qb]`` -> ``[B,H,T,hd]`` (layer.py:336-345)."""
+    """Packed values ``[B,H,T,ng,qb]`` -> ``[B,H,T,hd]`` (layer.py:336-345); ``out_dtype``
+    :data:`FOLD` gives the fused decode kernel's values (:func:`dequantize_rows_fold`)."""
     b, h, t, ng, qb = pq.shape
-    rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
-                          group_size, out_dtype)
+    if out_dtype == FOLD:
+        rec = dequantize_rows_fold(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                                   group_size)
+    else:
+        rec = dequantize_rows(pq.reshape(-1, qb), mn.reshape(-1, 1), sc.reshape(-1, 1), bits, alpha,
+                              group_size, out_dtype)
     return rec.reshape(b, h, t, ng * group_size)[..., :head_dim]
 
 
@@ -467,7 +517,8 @@ def reference_decode(query: torch.Tensor, keys: torch.Tensor, values: torch.Tens
     dequantized prefix in the layer dtype (``layer.py:263``, ``attention.py:213-226``),
     while its fused CUDA kernels keep the dequantized values in fp32 registers
     (``dequantize_mu_zero_q``/``fill_mu_zero_codebook``, ``loader.py:197-263``).
-    Default: the layer dtype (``keys.dtype``).
+    Default: the layer dtype (``keys.dtype``).  :data:`FOLD`: the fused decode kernel's own
+    values (:func:`dequantize_rows_fold`).
 
     ``value_prefix``: quantized value tokens when the layout flushes values per
     token (``logq_compatible_layout``, ``layer.py:389-396``): ``lq <= value_prefix

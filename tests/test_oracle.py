@@ -434,3 +434,30 @@ def test_default_path_decode_rounds_like_the_reference_in_bf16():
     assert torch.equal(got, got.to(torch.bfloat16).float())
     d = (got.double() - exact[:, 0]).abs()
     assert 1e-4 < d.max().item() < 5e-2
+
+
+# ------------------------------------------------------- the fused decode kernel's dequantization
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7])
+def test_fold_dequantization_within_its_table_rounding(bits):
+    """dequantize_rows_fold departs from the fixture-pinned fp32 dequantizer only by the fp16
+    rounding of its shifted (P, N) entries: |x_fold - x| <= (|bp| + |bn|) * 2^-13 per value (plus
+    the float64-vs-fp32 evaluation-order noise), and at 1 bit, where P, N are 0 or 1 and the
+    shifted entries are exact, the two agree to that noise alone.  A dropped shift, a swapped side
+    or a wrong zero level would break the bound by orders of magnitude."""
+    g = torch.Generator().manual_seed(40 + bits)
+    rows = torch.randn(4000, 64, generator=g) * (torch.rand(4000, 1, generator=g) * 8 + 0.1)
+    rows[::5] += 20.0  # one-signed groups (large a)
+    rows[1::7] -= 7.0
+    for alpha in (2.0, 4.0):
+        pq, mn, sc = ref.quantize_rows(rows.to(torch.bfloat16), bits, alpha)
+        x = ref.dequantize_rows(pq, mn, sc, bits, alpha, 64, torch.float32).double()
+        xf = ref.dequantize_rows_fold(pq, mn, sc, bits, alpha, 64)
+        s = sc.float().clamp_min(1e-8).double()
+        noise = 4 * 2.0 ** -24 * (x.abs() + s * 2)
+        d = (xf - x).abs()
+        if bits == 1:
+            assert bool((d <= noise).all()), (d - noise).max().item()
+        else:
+            assert bool((d <= s * 2.0 ** -13 + noise).all()), (d - s * 2.0 ** -13 - noise).max().item()
+            assert d.max().item() > 0  # the fp16 rounding is there (the check can fail)
