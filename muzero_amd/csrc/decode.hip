@@ -60,10 +60,17 @@ struct Lds {
   static constexpr int RED_FLOATS = 32 + 16 * D;  // per wave at the end (aliases the wave areas)
   static constexpr int WAVES_BYTES =
       kWaves * WAVE_HALVES * 2 > kWaves * RED_FLOATS * 4 ? kWaves * WAVE_HALVES * 2 : kWaves * RED_FLOATS * 4;
+  // per-wave codebooks (codes of up to 4 bits): the lane's two groups' 2^bits
+  // staged values, [group r][code q][64 lane slots] halves, the slots of
+  // lanes L and L + 32 side by side in one dword (a half-wave's 32 lanes then
+  // read 32 different banks)
+  static constexpr int cb_halves(int bits) { return bits <= 4 ? 2 * (1 << bits) * 64 : 0; }
+  static constexpr int CB_BYTES4 = kWaves * 2 * 16 * 64 * 2;  // the largest (4 bits), for offsets
   // expm1 rows for bins 1..qmax (codes of up to 6 bits), forward and
   // reversed, one pair of tables per alpha
   static constexpr int e_floats(int bits) { return bits <= 6 ? ((1 << bits) - 1) * ((1 << bits) + 2) / 2 : 0; }
-  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + 4 * (size_t)e_floats(bits) * 4; }
+  static constexpr size_t cb_bytes(int bits) { return (size_t)kWaves * cb_halves(bits) * 2; }
+  static constexpr size_t bytes(int bits) { return (size_t)WAVES_BYTES + cb_bytes(bits) + 4 * (size_t)e_floats(bits) * 4; }
 };
 
 // One group's dequantization parameters (muzero/quantizer.py:241-255, from the
@@ -204,8 +211,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   uint16_t* kv = lds + wave * L::WAVE_HALVES;
   uint16_t* pb = kv + L::STAGE;
-  constexpr int EK_BASE = L::WAVES_BYTES;                              // key table
-  constexpr int EV_BASE = L::WAVES_BYTES + 8 * EF;  // value table
+  // codes of up to 4 bits are staged through per-group codebooks: the 2^bits
+  // exact values of each of the lane's two groups, built once per tile (keys)
+  // or value chunk, then one LDS read per code instead of its dequantization
+  constexpr bool kCB = BITS <= 4;
+  constexpr int NQ = 1 << BITS;
+  constexpr int CB_BASE = L::WAVES_BYTES;
+  constexpr int EK_BASE = L::WAVES_BYTES + (int)L::cb_bytes(BITS);  // key table
+  constexpr int EV_BASE = EK_BASE + 8 * EF;                          // value table
+  // this lane's codebook slots (group 0, code 0) and (group 1, code 0); code q is 64 halves further
+  uint16_t* cb0 = (uint16_t*)((uint8_t*)lds + CB_BASE) + wave * L::cb_halves(BITS) + 2 * (lane & 31) + (lane >> 5);
+  uint16_t* cb1 = cb0 + NQ * 64;
   if constexpr (kTab) {
     // the expm1 tables exist only when there is a quantized prefix
     if (a.n_groups > 0 || a.v_prefix > 0) {
@@ -293,6 +309,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         vmeta[vg][r][1] = meta_load(a.v_scale, mi, a.meta_dtype);
       }
   };
+  // The 2^bits staged values of the lane's two groups: each the reference's
+  // exact dequantized value (deq_code), rounded as `pack` stages it, into the
+  // lane's own codebook slots (only this lane reads them back, so program
+  // order is the only ordering needed).
+  auto build_codebooks = [&](const DeqG (&gg)[2], auto pack) __attribute__((always_inline)) {
+    if constexpr (kCB) {
+      float z0[NQ], z1[NQ];
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        z0[q] = deq_fetch<BITS>(gg[0], q);
+        z1[q] = deq_fetch<BITS>(gg[1], q);
+      }
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const uint32_t h = pack(deq_apply<BITS>(gg[0], q, z0[q]), deq_apply<BITS>(gg[1], q, z1[q]));
+        cb0[q * 64] = (uint16_t)h;
+        cb1[q * 64] = (uint16_t)(h >> 16);
+      }
+    }
+  };
   {
     const int t0 = t_begin + wave;
     if (t0 < t_end && t0 < a.n_groups) {
@@ -317,10 +353,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (quant) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) gk[r] = deq_group<BITS>(kmeta[r][0], kmeta[r][1], EK_BASE, a.e_key);
+      if constexpr (kCB) build_codebooks(gk, [](float x0, float x1) { return pack_io<IO>(x0, x1); });
     }
 #pragma unroll
     for (int kc = 0; kc < KCH; ++kc) {
-      if (quant) {
+      if (quant && kCB) {
+        // the staged pair of each token: one codebook read per code
+#pragma unroll
+        for (int u = 0; u < 32; ++u) {
+          const int wi = (KCH == 2 ? 32 * kc : 0) + u;  // code index in the lane's words
+          const int row = (KCH == 2 ? 0 : 32 * ts) + u;  // token row of the chunk
+          const uint32_t h0 = cb0[code_at<BITS>(kw[0], wi) * 64];
+          const uint32_t h1 = cb1[code_at<BITS>(kw[1], wi) * 64];
+          *(uint32_t*)(kv + row * L::K_LD + 2 * cp) = h0 | (h1 << 16);
+        }
+      } else if (quant) {
         // blocks of 8 tokens: all 16 table reads issued, then used
 #pragma unroll
         for (int i0 = 0; i0 < 32; i0 += 8) {
@@ -423,7 +470,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int vc = 0; vc < NG; ++vc) {
       // V^T chunk -> kv[c * V_LD + t]: lane = tokens 2tp, 2tp+1, channels 32cs..32cs+31
-      if (quant) {
+      if (quant && kCB) {
+        DeqG gv[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], EV_BASE, a.e_value);
+        build_codebooks(gv, [](float x0, float x1) { return pack_io_f16<IO>(x0, x1); });
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const uint32_t h0 = cb0[code_at<BITS>(vw[vc][0], i) * 64];
+          const uint32_t h1 = cb1[code_at<BITS>(vw[vc][1], i) * 64];
+          *(uint32_t*)(kv + (32 * cs + i) * L::V_LD + cs * L::V_HI + 2 * tp) = h0 | (h1 << 16);
+        }
+      } else if (quant) {
         DeqG gv[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) gv[r] = deq_group<BITS>(vmeta[vc][r][0], vmeta[vc][r][1], EV_BASE, a.e_value);
