@@ -528,9 +528,9 @@ def main():
                     help="decode mode: dtype of the query and the K/V the cache is quantized from (the residual's)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
-    ap.add_argument("--kernel-path", choices=("auto", "exact", "fold"), default="auto",
+    ap.add_argument("--kernel-path", choices=("auto", "exact", "fold", "codebook"), default="auto",
                     help="decode mode: the library's kernel choice (auto), or force the exact-dequantize kernel "
-                         "(the reference's dequantize-then-attend values) or the fold kernel")
+                         "(the reference's dequantize-then-attend values), the fold kernel or the codebook kernel")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))
@@ -586,7 +586,7 @@ def main():
     ms_step = time_region(lambda i: plans[i % len(plans)].run(), args.steps, stream)
     single = plans[0].n_split == 1
     if single:
-        kernels_ms = {("decode_fold_direct" if plans[0].uses_fold else "decode_general_direct"): round(ms_step, 5)}
+        kernels_ms = {f"decode_{plans[0].kernel}_direct": round(ms_step, 5)}
         ms_kernel = ms_step
     else:
         ms_split = time_region(lambda i: plans[i % len(plans)].partials(), args.steps, stream)
@@ -655,7 +655,8 @@ def main():
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "attn_only_tokens_per_s_36_layers": round(B / (36 * ms_step * 1e-3), 1),
         "kernels_ms": kernels_ms,
-        "kernel": "fold" if plans[0].uses_fold else "exact-dequantize (general)",
+        "kernel": {"fold": "fold", "codebook": "codebook (exact values)",
+                   "general": "exact-dequantize (general)"}[plans[0].kernel],
         "n_split": plans[0].n_split,
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs_split / PEAK_HBM_GBS, 4), "traffic": traffic,

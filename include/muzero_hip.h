@@ -224,7 +224,7 @@ typedef struct mz_decode_args {
  * (other counts than 1, 2, 4, 8 run the kernel built for the next larger
  * one), fold tables given, at 7 bits one table for keys and values) and the
  * exact-dequantize kernel otherwise. */
-enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2 };
+enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments
  * (and the split count it will use, written to *n_split_out if non-null). */
@@ -236,6 +236,11 @@ int64_t muzero_decode_workspace_bytes(const mz_decode_args* args, int* n_split_o
  * loader.py:1360-1687, picks kernels internally); used by tests and the
  * benchmark to report which kernel they measured. */
 int muzero_decode_uses_fold(const mz_decode_args* args);
+/* The kernel muzero_decode_attention runs for these arguments: 0 the general
+ * exact-dequantize kernel, 1 the fold kernel, 2 the codebook kernel; -1 if the
+ * arguments are rejected (or a forced kernel does not take them).  An
+ * introspection helper like muzero_decode_uses_fold. */
+int muzero_decode_kernel(const mz_decode_args* args);
 int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
 
 /* The two launches of muzero_decode_attention, for callers that time or merge

@@ -111,7 +111,7 @@ class PrefixStateArgs(ctypes.Structure):
     ]
 
 
-MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD = 0, 1, 2
+MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD, MZ_PATH_CODEBOOK = 0, 1, 2, 3
 MZ_ESCRATCH = -4
 MZ_DECODE_SCRATCH_BYTES = 8 << 20  # the static scratch of muzero_decode_attention_noalloc
 
@@ -135,6 +135,7 @@ SIGNATURES = {
     "muzero_decode_workspace_bytes": (c_i64, [ctypes.POINTER(DecodeArgs), ctypes.POINTER(c_int)]),
     "muzero_decode_attention": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_uses_fold": (c_int, [ctypes.POINTER(DecodeArgs)]),
+    "muzero_decode_kernel": (c_int, [ctypes.POINTER(DecodeArgs)]),
     "muzero_decode_partials": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_combine": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     "muzero_decode_attention_noalloc": (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),

@@ -713,6 +713,9 @@ __global__ __launch_bounds__(D) void prefix_state_kernel(const float* __restrict
 bool fold_supported(const mz_decode_args* a);
 int fold_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
+bool cb_supported(const mz_decode_args* a);
+int cb_choose_split(const mz_decode_args* a, int* tiles_per_split);
+int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
@@ -740,7 +743,7 @@ static int check_args(const mz_decode_args* a) {
   if (a->io_dtype != MZ_BF16 && a->io_dtype != MZ_F16) return MZ_EINVAL;
   if (a->meta_dtype != MZ_F16 && a->meta_dtype != MZ_BF16 && a->meta_dtype != MZ_F32) return MZ_EINVAL;
   if (a->out_dtype != a->io_dtype && a->out_dtype != MZ_F32) return MZ_EINVAL;
-  if (a->kernel_path < MZ_PATH_AUTO || a->kernel_path > MZ_PATH_FOLD) return MZ_EINVAL;
+  if (a->kernel_path < MZ_PATH_AUTO || a->kernel_path > MZ_PATH_CODEBOOK) return MZ_EINVAL;
   if (a->head_dim != 64 && a->head_dim != 128) return MZ_EUNSUPPORTED;
   if (a->n_rep > 16) return MZ_EUNSUPPORTED;
   if (a->batch == 0) return MZ_OK;
@@ -769,15 +772,32 @@ static int check_args(const mz_decode_args* a) {
   return MZ_OK;
 }
 
-// Which kernel runs and with how many splits (both kernels share the
+// Which kernel runs and with how many splits (the kernels share the
 // workspace layout and the combine kernel).
-static bool use_fold(const mz_decode_args* a) {
-  if (a->kernel_path == MZ_PATH_EXACT) return false;
-  return fold_supported(a);
+enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2 };
+
+static Kernel which_kernel(const mz_decode_args* a) {
+  if (a->kernel_path == MZ_PATH_EXACT) return K_GENERAL;
+  if (a->kernel_path == MZ_PATH_CODEBOOK) return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
+  return fold_supported(a) ? K_FOLD : K_GENERAL;
+}
+
+// A forced kernel that does not take these arguments.
+static bool forced_unsupported(const mz_decode_args* a) {
+  return (a->kernel_path == MZ_PATH_FOLD && !fold_supported(a)) ||
+         (a->kernel_path == MZ_PATH_CODEBOOK && !cb_supported(a));
 }
 
 static int plan_split(const mz_decode_args* a, int* tps) {
-  return use_fold(a) ? fold_choose_split(a, tps) : choose_split(a, tps);
+  switch (which_kernel(a)) {
+    case K_FOLD: return fold_choose_split(a, tps);
+    case K_CODEBOOK: return cb_choose_split(a, tps);
+    default: return choose_split(a, tps);
+  }
+}
+
+static int launch_fast(const mz_decode_args* a, hipStream_t s, bool direct) {
+  return which_kernel(a) == K_FOLD ? fold_launch_partials(a, s, direct) : cb_launch_partials(a, s, direct);
 }
 
 }  // namespace mz
@@ -786,7 +806,7 @@ using namespace mz;
 
 extern "C" int64_t muzero_decode_workspace_bytes(const mz_decode_args* a, int* n_split_out) {
   if (check_args(a) != MZ_OK) return -1;
-  if (a->kernel_path == MZ_PATH_FOLD && !fold_supported(a)) return -1;
+  if (forced_unsupported(a)) return -1;
   int tps;
   const int ns = plan_split(a, &tps);
   if (n_split_out) *n_split_out = ns;
@@ -795,7 +815,12 @@ extern "C" int64_t muzero_decode_workspace_bytes(const mz_decode_args* a, int* n
 
 extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
   if (check_args(a) != MZ_OK) return -1;
-  return use_fold(a) ? 1 : 0;
+  return which_kernel(a) == K_FOLD ? 1 : 0;
+}
+
+extern "C" int muzero_decode_kernel(const mz_decode_args* a) {
+  if (check_args(a) != MZ_OK || forced_unsupported(a)) return -1;
+  return (int)which_kernel(a);
 }
 
 template <int D, int IO>
@@ -858,13 +883,13 @@ extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t strea
   const int st = decode_check_launchable(a);
   if (st) return st == 1 ? MZ_OK : st;
   hipStream_t s = (hipStream_t)stream;
-  if (a->kernel_path == MZ_PATH_FOLD && !fold_supported(a)) return MZ_EUNSUPPORTED;
-  if (use_fold(a)) {
+  if (forced_unsupported(a)) return MZ_EUNSUPPORTED;
+  if (which_kernel(a) != K_GENERAL) {
     int tps;
-    const int ns = fold_choose_split(a, &tps);
+    const int ns = plan_split(a, &tps);
     const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
     if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
-    return fold_launch_partials(a, s, false);
+    return launch_fast(a, s, false);
   }
   return launch_general(a, s, false);
 }
@@ -915,11 +940,11 @@ extern "C" int muzero_decode_prefix_state(const mz_decode_args* a, const mz_pref
 
 extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stream) {
   // one split: the split kernel writes the output (no workspace, no combine)
-  if (decode_check_launchable(a) == MZ_OK && a->out && !(a->kernel_path == MZ_PATH_FOLD && !fold_supported(a))) {
+  if (decode_check_launchable(a) == MZ_OK && a->out && !forced_unsupported(a)) {
     int tps;
     if (plan_split(a, &tps) == 1)
-      return use_fold(a) ? fold_launch_partials(a, (hipStream_t)stream, true)
-                         : launch_general(a, (hipStream_t)stream, true);
+      return which_kernel(a) != K_GENERAL ? launch_fast(a, (hipStream_t)stream, true)
+                                          : launch_general(a, (hipStream_t)stream, true);
   }
   const int st = muzero_decode_partials(a, stream);
   if (st != MZ_OK) return st;

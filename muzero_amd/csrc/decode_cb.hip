@@ -1,0 +1,678 @@
+// Packed-KV decode attention over per-tile codebooks, 4-bit codes (gfx950,
+// wave64, MFMA 16x16x32 in the layer dtype).
+//
+// Every value this kernel attends with is the reference's dequantize-then-
+// attend value bit for bit: a quantized group (one key channel or one value
+// token-group of 64 elements) has only 2^bits distinct values, so each wave
+// forms, for each group of its tile, those values with the reference's own
+// fp32 operation order (muzero/quantizer.py:241-255: t = pe*E or -ne*E,
+// unit = za + t, x = unit*s + mn) rounded to the layer dtype
+// (muzero/cache/layer.py:263) -- the group's codebook, in LDS -- and then
+// reads each code's value straight into an MFMA operand register.  Q.K is
+// then an MFMA of the query (in its own dtype) against the keys' values,
+// P.V one of the softmax weights against the values' values, both
+// accumulated in fp32: no operand products, no constant-part MFMAs, 32 MFMAs
+// per tile.
+//
+// Work of one wave: a 64-token tile = one key group per channel and one
+// value group per (token, 64 channels).
+//   QK: MFMA rows = query heads (row RS*h, RS = 16 / NREP; the other rows
+//   zero); columns = tokens 4n+jt of N-tiles jt = 0..3; lane (n, g) of
+//   k-step kt holds channels 32kt+8g+{0..7} and needs, for each, the 4 codes
+//   of its tokens 4n..4n+3 (16 bits of the channel's 32-byte row).
+//   PV: rows RS*h / RS*h+1 = the high / low parts of the head's weights in
+//   the layer dtype (their sum carries each weight to ~2^-17); columns =
+//   channels 64vg+4n+jt; lane (n, g) of step (kt, vg) holds tokens
+//   32kt+8g+{0..7} and needs, for each, the codes of its channels 4n..4n+3.
+//   Lanes 2m, 2m+1 load a word of two different rows and swap halves with
+//   one DPP move, so each lane then holds its 16 bits of both rows.
+// Codebook layout (per wave, keys and values alike): group r's 16 entries
+// (2 bytes each) at byte 288*(r/8) + 32*(r%8) + 2q.  One lookup instruction
+// reads one group per lane group (16 lanes, 32 bytes = 8 banks), and the 32
+// bytes of padding per 8 groups put the 4 lane groups of every instruction
+// in disjoint bank octets: the lookups are free of bank conflicts.  The
+// address is one v_perm per code: byte 0 = 2q (+32g), bytes 1-3 = the lane
+// group's block base; the row and step offsets ride in the instruction.
+// The (E+, E-) pairs the codebooks are formed from (E+ = E[pb][q-zl] above
+// the zero level, E- = E[nb][zl-q] below it, the other 0) are a 16 x 16
+// table per alpha in LDS, built at setup from the expm1 rows; a pair turns
+// the side's product into t = fma(pe, E+, -ne*E-) with no per-code select.
+//
+// Launch, splits, wave priorities and the final merge are those of the fold
+// kernel (decode_fold.hip): one workgroup of 4 waves per (batch, kv-head,
+// split), residual tiles first, waves take every 4th tile; one split writes
+// the output itself, more go through the workspace and the combine kernel.
+#include <type_traits>
+
+#include "decode_tile.hpp"
+
+namespace mz {
+
+namespace cb {
+
+constexpr int D = 128;
+constexpr int TILE = 64;
+constexpr int WAVES = 4;
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kLn2 = 0.693147180559945309f;
+
+constexpr int BITS = 4;
+constexpr int QMAX = (1 << BITS) - 1;
+constexpr int QB = 8 * BITS;          // bytes per packed 64-code row
+
+// codebooks: 128 groups, 16 entries of 2 bytes, 32 bytes of padding per 8 groups
+constexpr int CB_GROUP = 32;
+constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
+constexpr int CB_BYTES = 16 * CB_BLOCK;  // 4608 = 18 * 256
+// (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
+// bytes so that lanes reading different zero levels at one code use
+// different banks
+constexpr int ET_ROW = 16 * 8 + 8;
+constexpr int ET_BYTES = 16 * ET_ROW;
+constexpr int QROW = D * 2 + 16;       // bytes per head row of the query copy
+constexpr int PROW = TILE * 2 + 16;    // bytes per head row of the weight staging
+
+template <int NREP>
+struct Smem {
+  static constexpr int ETK = 0;
+  static constexpr int ETV = ET_BYTES;
+  static constexpr int QIO = 2 * ET_BYTES;            // query, io dtype [NREP][QROW]
+  static constexpr int ZERO = QIO + NREP * QROW;      // 256 zero bytes: A rows that must be 0
+  static constexpr int WAVE0 = (ZERO + 256 + 255) / 256 * 256;
+  // per wave (256-aligned: a lane group's codebook base has byte 0 = 32g)
+  static constexpr int KCB = 0;
+  static constexpr int VCB = CB_BYTES;
+  static constexpr int PST = 2 * CB_BYTES;            // io dtype [2 parts][NREP][PROW]: weights hi / lo
+  static constexpr int PER_WAVE = (PST + 2 * NREP * PROW + 255) / 256 * 256;
+  static constexpr int MERGE = (2 * NREP + NREP * D) * 4;  // per wave at the end (aliases the wave area)
+  static constexpr int TOTAL = WAVE0 + WAVES * (PER_WAVE > MERGE ? PER_WAVE : MERGE);
+};
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t lds_u16(const uint8_t* smem, uint32_t addr) {
+  return *(const uint16_t*)(smem + addr);
+}
+
+// Two fp32 values rounded to the io dtype (round to nearest even), packed
+// low / high.
+template <int IO>
+__device__ __forceinline__ uint32_t pack_io2(float x0, float x1) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  if constexpr (IO == MZ_BF16) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x0, x1}), b2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{x0, x1}), h2));
+  }
+}
+
+template <int IO>
+__device__ __forceinline__ float io_to_f32(uint16_t h) {
+  return IO == MZ_BF16 ? bf2f(h) : h2f(h);
+}
+
+// Dequantization quantities of one stored group (mn, s), as the reference
+// forms them from the stored metadata (quantizer.py:241-249), the scale
+// guarded like the reference CUDA extension (loader.py:201) so that an
+// all-zero group (stored scale 0) gives x = mn.
+struct Group {
+  float mn, s, za, pe, mne;  // mne = -ne
+  uint32_t row;              // byte offset of the zero level's (E+, E-) row
+};
+
+__device__ __forceinline__ Group group_of(float mn, float s) {
+  const float eps = 1e-8f;
+  Group r;
+  r.mn = mn;
+  r.s = s >= eps ? s : eps;                        // NaN -> eps, as deq_row
+  r.za = clamp01((0.f - mn) / r.s);                // IEEE division: the zero level must match
+  const float zl = rintf(r.za * (float)QMAX);
+  r.pe = clamp_min(1.f - r.za, eps);
+  r.mne = -clamp_min(r.za, eps);
+  // a NaN zero level (NaN metadata) reads row 0: the values are NaN anyway
+  r.row = (uint32_t)__builtin_amdgcn_fmed3f(zl == zl ? zl : 0.f, 0.f, (float)QMAX) * ET_ROW;
+  return r;
+}
+
+// The group's 16 values in the io dtype, written as its codebook (32 bytes
+// at `dst`).  unit = za + t needs no clamp: for finite metadata it lies in
+// [0, 1] already (t = pe*E with pe = fl(1 - za) gives za + t <= 1 after
+// rounding; t = -za*E gives za + t >= 0), and NaN metadata propagates.
+template <int IO>
+__device__ __forceinline__ void build_codebook(const uint8_t* smem, int et, const Group& gr, uint8_t* dst) {
+  uint32_t w[8];
+#pragma unroll
+  for (int q2 = 0; q2 < 8; ++q2) {
+    float x[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int q = 2 * q2 + e;
+      const float2 pn = *(const float2*)(smem + et + gr.row + 8 * q);
+      const float t = __builtin_fmaf(gr.pe, pn.x, gr.mne * pn.y);
+      const float unit = gr.za + t;
+      const float u = unit * gr.s;
+      x[e] = u + gr.mn;
+    }
+    w[q2] = pack_io2<IO>(x[0], x[1]);
+  }
+  *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
+  *(u32x4*)(dst + 16) = u32x4{w[4], w[5], w[6], w[7]};
+}
+
+__device__ __forceinline__ uint32_t cb_offset(int r) { return (uint32_t)((r >> 3) * CB_BLOCK + (r & 7) * CB_GROUP); }
+
+// The B operands (columns jt = 0..3) of one step from its 4 code words:
+// w[p] = this lane's word of the step's row 2p + (n & 1).  `lb`: the lane
+// group's codebook base (byte 0 = 32g); IMM: the step's block offset.
+template <int IMM>
+__device__ __forceinline__ void lookup_step(const uint8_t* smem, const uint32_t* w, uint32_t lb, uint32_t gb,
+                                            bool odd, u32x4 (&B)[4]) {
+  // after the swap: low half = the lane's 4 codes of row 2p, high half =
+  // those of row 2p + 1 (code jt at bits 4jt)
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+  uint32_t ev[4], od[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t r = __builtin_amdgcn_perm(dpp_swap_pairs(w[p]), w[p], sel);
+    ev[p] = ((r << 1) & 0x1E1E1E1Eu) | gb;  // 2q of codes 0, 2 of each row, one per byte
+    od[p] = ((r >> 3) & 0x1E1E1E1Eu) | gb;  // codes 1, 3
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t e = (jt & 1) ? od[i] : ev[i];
+      const uint32_t a0 = __builtin_amdgcn_perm(lb, e, 0x07060500u | (uint32_t)(jt >> 1));
+      const uint32_t a1 = __builtin_amdgcn_perm(lb, e, 0x07060500u | (uint32_t)(2 + (jt >> 1)));
+      const uint16_t lo = lds_u16(smem, a0 + (IMM + 2 * i * CB_GROUP));
+      const uint16_t hi = lds_u16(smem, a1 + (IMM + (2 * i + 1) * CB_GROUP));
+      B[jt][i] = __builtin_bit_cast(uint32_t, u16x2{lo, hi});
+    }
+}
+
+template <int IO, int NREP, int MW>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void cb_kernel(
+    const mz_decode_args a, int tiles_per_split, int n_split, int direct, int cus) {
+  constexpr int NT = 64 * WAVES;
+  using M = Mfma<IO>;
+  using S = Smem<NREP>;
+  static_assert(S::TOTAL <= 80 * 1024, "two workgroups per CU");
+  constexpr int RS = 16 / NREP;               // MFMA row stride between query heads
+  static_assert(RS >= 2, "P.V needs a second row per head for the weights' low part");
+  constexpr int HS = NREP > 4 ? NREP / 4 : 1;  // head slots per lane of the MFMA output
+  constexpr int NGH = 2;                        // value groups per token
+  __shared__ __align__(256) uint8_t smem[S::TOTAL];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const bool odd = (n & 1) != 0;
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+
+  const int n_tiles_d = (a.n_residual + TILE - 1) / TILE;
+  const int n_tiles = a.n_groups + n_tiles_d;
+  const int t_begin = split * tiles_per_split;
+  const int t_end = min(n_tiles, t_begin + tiles_per_split);
+  constexpr int meta_es = 2 * MW;
+  Bufs bf;
+  {
+    const int64_t ng = a.n_groups;
+    bf.kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * QB);
+    bf.vp = make_buf(a.v_packed + b * a.vp_sb + kvh * a.vp_sh, ng * TILE * NGH * QB);
+    const int64_t km = b * a.km_sb + kvh * a.km_sh, vm = b * a.vm_sb + kvh * a.vm_sh;
+    bf.kmn = make_buf((const uint8_t*)a.k_mn + km * meta_es, ng * D * meta_es);
+    bf.ksc = make_buf((const uint8_t*)a.k_scale + km * meta_es, ng * D * meta_es);
+    bf.vmn = make_buf((const uint8_t*)a.v_mn + vm * meta_es, ng * TILE * NGH * meta_es);
+    bf.vsc = make_buf((const uint8_t*)a.v_scale + vm * meta_es, ng * TILE * NGH * meta_es);
+    bf.kr = (const uint16_t*)a.k_res + b * a.kr_sb + kvh * a.kr_sh;
+    bf.vr = (const uint16_t*)a.v_res + b * a.vr_sb + kvh * a.vr_sh;
+  }
+
+  // the split's tiles in virtual order: residual tiles first, quantized
+  // after; wave w takes virtual tiles w, w + WAVES, ...
+  const int n_quant = max(0, min(t_end, a.n_groups) - t_begin);
+  const int n_res = (t_end - t_begin) - n_quant;
+  const int n_virt = t_end - t_begin;
+  auto tile_of = [&](int v) { return v < n_res ? max(t_begin, a.n_groups) + v : t_begin + (v - n_res); };
+  // loads are issued unconditionally; an index that is not a quantized tile
+  // is replaced by one this split reads anyway
+  const int q_last = max(0, min(t_end, a.n_groups) - 1);
+  const int v0 = wave;
+
+  // ---------------- workgroup setup: (E+, E-) tables and the query in LDS
+  constexpr int EW = (2 * 256 + NT - 1) / NT;  // table entries per thread
+  constexpr int QW = (NREP * D + NT - 1) / NT;  // query elements per thread
+  float2 et[EW];
+  uint16_t qraw[QW];
+#pragma unroll
+  for (int j = 0; j < EW; ++j) {
+    const int i = threadIdx.x + j * NT;
+    const int t = i >> 8, zl = (i >> 4) & 15, q = i & 15;
+    const float* E = t ? a.e_value : a.e_key;
+    float ep = 0.f, en = 0.f;
+    if (q >= zl) {
+      const int pb = max(QMAX - zl, 1);
+      ep = E[expm1_row(pb) + q - zl];
+    } else {
+      const int nb = max(zl, 1);
+      en = E[expm1_row(nb) + zl - q];
+    }
+    et[j] = float2{ep, en};
+  }
+#pragma unroll
+  for (int j = 0; j < QW; ++j) {
+    const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
+    qraw[j] = h < a.n_rep ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * a.n_rep + h) * a.q_sh + c] : 0;
+  }
+  MetaWords<MW> MT;  // metadata of the current tile
+  uint32_t KW[16], VW[16];
+  // key words: KW[4kt + p] = this lane's word of channel row 32kt + 8g + 2p + (n & 1)
+  const int kvoff = (8 * g + (n & 1)) * QB + 4 * (n >> 1);
+  auto load_kw = [&](int tile) __attribute__((always_inline)) {
+    const int soff = tile * D * QB;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        KW[4 * kt + p] = __builtin_amdgcn_raw_buffer_load_b32(bf.kp, kvoff, soff + (32 * kt + 2 * p) * QB, 0);
+  };
+  // value words: VW[4(2kt + vg) + p] = this lane's word of token row 32kt + 8g + 2p + (n & 1), group vg
+  const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + 4 * (n >> 1);
+  auto load_vw = [&](int tile) __attribute__((always_inline)) {
+    const int soff = tile * TILE * NGH * QB;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int vg = 0; vg < NGH; ++vg)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          VW[4 * (2 * kt + vg) + p] = __builtin_amdgcn_raw_buffer_load_b32(
+              bf.vp, vvoff, soff + (32 * kt + 2 * p) * (NGH * QB) + QB * vg, 0);
+  };
+  load_meta_tile<MW, D>(MT, bf, min(tile_of(v0), q_last), lane);
+  load_kw(min(tile_of(v0), q_last));
+#pragma unroll
+  for (int j = 0; j < EW; ++j) {
+    const int i = threadIdx.x + j * NT;
+    const int t = i >> 8, zl = (i >> 4) & 15, q = i & 15;
+    *(float2*)(smem + (t ? S::ETV : S::ETK) + zl * ET_ROW + 8 * q) = et[j];
+  }
+  for (int i = threadIdx.x; i < 64; i += NT) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
+#pragma unroll
+  for (int j = 0; j < QW; ++j) {
+    const int i = threadIdx.x + j * NT, h = i / D, c = i - h * D;
+    if (i < NREP * D) *(uint16_t*)(smem + S::QIO + h * QROW + 2 * c) = qraw[j];
+  }
+  __syncthreads();
+
+  uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
+  const uint32_t wbase = (uint32_t)(S::WAVE0 + wave * S::PER_WAVE);  // LDS byte address of W (smem is at 0)
+  const uint32_t lbk = wbase + S::KCB + CB_BLOCK * g;  // this lane group's key codebook block (byte 0 = 32g)
+  const uint32_t lbv = wbase + S::VCB + CB_BLOCK * g;
+  const uint32_t gb = 0x20202020u * (uint32_t)g;
+
+  // MFMA A rows: row n of this lane belongs to head hA = n / RS; for Q.K row
+  // 0 of a head's rows is its query, the others zero; for P.V row 0 is the
+  // weights' high part, row 1 their low part, the others zero
+  const int hA = n / RS;
+  const int rA = n % RS;
+  u32x4 qa[4];
+#pragma unroll
+  for (int kq = 0; kq < 4; ++kq)
+    qa[kq] = rA == 0 ? *(const u32x4*)(smem + S::QIO + hA * QROW + (32 * kq + 8 * g) * 2) : u32x4{0u, 0u, 0u, 0u};
+  const uint8_t* pv_row = rA < 2 ? W + S::PST + (rA * NREP + hA) * PROW : smem + S::ZERO;
+  // MFMA output element (g, i) = row 4g + i: head slot s is element i = s*RS
+  // when 4g % RS == 0 (the lane group holds query heads), head 4g/RS + s
+  const bool owner = ((4 * g) % RS) == 0;
+  const int h0 = (4 * g) / RS;
+
+  float m_run[HS], l_run[HS];
+#pragma unroll
+  for (int s = 0; s < HS; ++s) m_run[s] = -INFINITY, l_run[s] = 0.f;
+  f32x4 acc[NGH][4];
+#pragma unroll
+  for (int vg = 0; vg < NGH; ++vg)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[vg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // logits in base-2 units (times log2(e)): the exponentials are single v_exp_f32 ops
+  const float scaling2 = a.scaling * kLog2e;
+
+  // the codebooks of a quantized tile from its metadata: key groups =
+  // channels 2*lane, 2*lane + 1; value groups = token lane, both groups
+  auto build_codebooks = [&](const MetaWords<MW>& Mw) __attribute__((always_inline)) {
+    const float2 kmn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), ksc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
+    const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
+    build_codebook<IO>(smem, S::ETK, group_of(kmn.x, ksc.x), W + S::KCB + cb_offset(2 * lane));
+    build_codebook<IO>(smem, S::ETK, group_of(kmn.y, ksc.y), W + S::KCB + cb_offset(2 * lane + 1));
+    build_codebook<IO>(smem, S::ETV, group_of(vmn.x, vsc.x), W + S::VCB + cb_offset(lane));
+    build_codebook<IO>(smem, S::ETV, group_of(vmn.y, vsc.y), W + S::VCB + cb_offset(TILE + lane));
+  };
+
+  // one tile.  Loads in flight: this tile's value words and the next tile's
+  // metadata (issued here), the next tile's key words (after this tile's Q.K)
+  auto process = [&](auto quant_tag, const int tile, const int tn) {
+    constexpr bool quant = decltype(quant_tag)::value;
+    const int tl = min(tn, q_last);
+    load_vw(min(tile, q_last));
+    MetaWords<MW> MN;
+    load_meta_tile<MW, D>(MN, bf, tl, lane);
+    int n_valid, pos0, r0 = 0;
+    if constexpr (quant) {
+      n_valid = TILE;
+      pos0 = TILE * tile;
+    } else {
+      r0 = (tile - a.n_groups) * TILE;
+      n_valid = min(TILE, a.n_residual - r0);
+      pos0 = TILE * a.n_groups + r0;
+    }
+
+    f32x4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (quant) {
+      build_codebooks(MT);
+      wave_lds_sync();  // the codebooks were written by other lanes
+      // ---------- S = Q K^T over the keys' values
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        u32x4 B[4];
+        switch (kt) {
+          case 0: lookup_step<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B); break;
+          case 1: lookup_step<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B); break;
+          case 2: lookup_step<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B); break;
+          default: lookup_step<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B); break;
+        }
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], B[jt], s[jt]);
+      }
+    } else {
+      // ---------- residual tile: dense keys; rows past the filled ones read 0
+      // (their logits are masked below)
+      const int kst = a.kr_st * 2;
+      const __amdgpu_buffer_rsrc_t krb = make_buf(bf.kr + (int64_t)r0 * a.kr_st, (n_valid - 1) * kst + D * 2);
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        u32x4 kb[2][4];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt)
+            kb[k2][jt] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(krb, (4 * n + jt) * kst + 16 * g, 64 * (2 * kh + k2), 0));
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[2 * kh + k2], kb[k2][jt], s[jt]);
+      }
+    }
+    load_kw(tl);
+
+    // ---------- online softmax in registers: head slot sl of this lane group
+    // owns tokens 4n + jt (jt = 0..3) of the 16 lanes of its row
+    float corr[HS];
+#pragma unroll
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS;  // MFMA output element of this head slot
+      float x[4];
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) {
+        const int tt = 4 * n + jt;
+        float v = s[jt][i] * scaling2;
+        if (tt >= n_valid) v = -INFINITY;
+        else if (a.mask) v = __builtin_fmaf(a.mask[b * a.mask_sb + pos0 + tt], kLog2e, v);
+        x[jt] = v;
+        tmax = fmaxf(tmax, v);
+      }
+      tmax = group_reduce<16>(tmax, OpMax());
+      const float m_new = fmaxf(m_run[sl], tmax);
+      // while a row is fully masked its maximum stays -inf; 0 stands in for
+      // it, so exp2(-inf - 0) gives zero weights and a zero correction
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      corr[sl] = __builtin_amdgcn_exp2f(m_run[sl] - m_use);
+      m_run[sl] = m_new;
+      float p[4];
+#pragma unroll
+      for (int jt = 0; jt < 4; ++jt) p[jt] = __builtin_amdgcn_exp2f(x[jt] - m_use);
+      // l_run is a per-lane partial sum (this lane's 4 tokens of every tile;
+      // the correction is the same in the 16 lanes of the row): summed over
+      // the row once, at the end
+      l_run[sl] = l_run[sl] * corr[sl] + ((p[0] + p[1]) + (p[2] + p[3]));
+      if (owner) {
+        // the weights as high + low parts in the io dtype
+        const uint32_t h01 = pack_io2<IO>(p[0], p[1]), h23 = pack_io2<IO>(p[2], p[3]);
+        const uint32_t l01 = pack_io2<IO>(p[0] - io_to_f32<IO>((uint16_t)h01), p[1] - io_to_f32<IO>((uint16_t)(h01 >> 16)));
+        const uint32_t l23 = pack_io2<IO>(p[2] - io_to_f32<IO>((uint16_t)h23), p[3] - io_to_f32<IO>((uint16_t)(h23 >> 16)));
+        const int h = h0 + sl;
+        *(uint2*)(W + S::PST + h * PROW + 8 * n) = uint2{h01, h23};
+        *(uint2*)(W + S::PST + (NREP + h) * PROW + 8 * n) = uint2{l01, l23};
+      }
+    }
+    // ---------- rescale the accumulators (rows i, i + 1 of each head slot)
+#pragma unroll
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS;
+#pragma unroll
+      for (int vg = 0; vg < NGH; ++vg)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[vg][j][i] *= corr[sl], acc[vg][j][i + 1] *= corr[sl];
+    }
+    wave_lds_sync();  // the weights were written by other lanes
+
+    // ---------- acc += P V
+    if constexpr (quant) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kt = st >> 1, vg = st & 1;
+        const u32x4 A = *(const u32x4*)(pv_row + (32 * kt + 8 * g) * 2);
+        u32x4 B[4];
+        switch (st) {
+          case 0: lookup_step<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B); break;
+          case 1: lookup_step<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B); break;
+          case 2: lookup_step<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B); break;
+          default: lookup_step<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B); break;
+        }
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(A, B[jt], acc[vg][jt]);
+      }
+    } else {
+      // residual values: lane (n, g) of step (kt, vg) needs tokens
+      // 32kt + 8g + j (j = 0..7) of channels 64vg + 4n + jt: one 8-byte load
+      // per token (its 4 channels), then the halves paired per token pair.
+      // The buffer starts at the step's first row and ends after its last
+      // filled row (padding rows read 0; their weights are 0)
+      const int vst = a.vr_st * 2;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const u32x4 A = *(const u32x4*)(pv_row + (32 * kt + 8 * g) * 2);
+        const int rows = n_valid - 32 * kt;
+        const __amdgpu_buffer_rsrc_t vrb =
+            make_buf(bf.vr + (int64_t)(r0 + 32 * kt) * a.vr_st, rows > 0 ? (rows - 1) * vst + D * 2 : 0);
+#pragma unroll
+        for (int vg = 0; vg < NGH; ++vg) {
+          uint32_t vv[8][2];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const auto raw = __builtin_amdgcn_raw_buffer_load_b64(vrb, (8 * g + j) * vst + 8 * n, 128 * vg, 0);
+            vv[j][0] = raw[0];
+            vv[j][1] = raw[1];
+          }
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) {
+            u32x4 B;
+            const uint32_t sel = (jt & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) B[i] = __builtin_amdgcn_perm(vv[2 * i + 1][jt >> 1], vv[2 * i][jt >> 1], sel);
+            acc[vg][jt] = M::run(A, B, acc[vg][jt]);
+          }
+        }
+      }
+    }
+    MT = MN;
+    wave_lds_sync();  // this tile's codebooks and weights are read before the next tile overwrites them
+  };
+
+  // tiles of this wave; the wave priority falls with its progress (as in the
+  // fold kernel: the SIMD then favours the wave that is behind)
+  const int n_mine = (n_virt - v0 + WAVES - 1) / WAVES;
+  const int wg_lin = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const int older = wg_lin < cus ? 1 : 0;
+  int done = 0;
+  if (older) __builtin_amdgcn_s_setprio(2);
+  else __builtin_amdgcn_s_setprio(3);
+  auto step = [&](auto quant_tag, const int v) {
+    process(quant_tag, tile_of(v), v + WAVES < n_virt ? tile_of(v + WAVES) : q_last);
+    ++done;
+    switch ((4 * done) / max(n_mine, 1) + older) {
+      case 0: break;
+      case 1: __builtin_amdgcn_s_setprio(2); break;
+      case 2: __builtin_amdgcn_s_setprio(1); break;
+      default: __builtin_amdgcn_s_setprio(0); break;
+    }
+  };
+  int v = v0;
+  for (; v < n_res; v += WAVES) step(std::false_type{}, v);
+  for (; v < n_virt; v += WAVES) step(std::true_type{}, v);
+  __builtin_amdgcn_s_setprio(0);
+
+  // ---------------- merge the waves and write this split's partial records
+  __syncthreads();
+  float* red = (float*)(smem + S::WAVE0);
+  constexpr int RED = 2 * NREP + NREP * D;  // per wave: m[NREP], l[NREP], acc[NREP][D]
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int tid_e = wave * 64 + lane_e;
+  const int n_e = lane_e & 15, g_e = lane_e >> 4;
+  if (((4 * g_e) % RS) == 0) {
+    const int h0e = (4 * g_e) / RS;
+    float* w = red + wave * RED;
+#pragma unroll
+    for (int sl = 0; sl < HS; ++sl) {
+      const int i = sl * RS, h = h0e + sl;
+      const float l_row = group_reduce<16>(l_run[sl], OpAdd());
+      if (n_e == 0) {
+        w[h] = m_run[sl];
+        w[NREP + h] = l_row;
+      }
+#pragma unroll
+      for (int vg = 0; vg < NGH; ++vg)
+        *(f32x4*)(w + 2 * NREP + h * D + 64 * vg + 4 * n_e) =
+            f32x4{acc[vg][0][i] + acc[vg][0][i + 1], acc[vg][1][i] + acc[vg][1][i + 1],
+                  acc[vg][2][i] + acc[vg][2][i + 1], acc[vg][3][i] + acc[vg][3][i + 1]};
+    }
+  }
+  __syncthreads();
+  if (direct) {
+    for (int e = tid_e; e < a.n_rep * D; e += NT) {
+      const int h = e / D;
+      const int c = e - h * D;
+      float M_ = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
+      float num = 0.f, den = 0.f;
+      if (M_ != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+          const float f = __builtin_amdgcn_exp2f(red[w * RED + h] - M_);
+          num += f * red[w * RED + 2 * NREP + h * D + c];
+          den += f * red[w * RED + NREP + h];
+        }
+      }
+      store_val(a.out, b * a.out_sb + (int64_t)(kvh * a.n_rep + h) * a.out_sh + c, den > 0.f ? num / den : 0.f,
+                a.out_dtype);
+    }
+    return;
+  }
+  for (int e = tid_e; e < a.n_rep * (D + 2); e += NT) {
+    const int h = e / (D + 2);
+    const int c = e - h * (D + 2);
+    float M_ = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) M_ = fmaxf(M_, red[w * RED + h]);
+    float val = 0.f;
+    if (c == D) {
+      val = M_ * kLn2;  // the record's maximum in natural-log units
+    } else if (M_ != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        const float f = __builtin_amdgcn_exp2f(red[w * RED + h] - M_);
+        val += f * (c == D + 1 ? red[w * RED + NREP + h] : red[w * RED + 2 * NREP + h * D + c]);
+      }
+    }
+    ws_record<D>(a, b, kvh * a.n_rep + h, split, n_split)[c] = val;
+  }
+}
+
+}  // namespace cb
+
+// ------------------------------------------------------------------ host side
+
+static bool cb_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
+  const int pair = dt == MZ_F32 ? 8 : 4;  // two adjacent entries are read at once
+  return ((uintptr_t)p % pair) == 0 && sb % 2 == 0 && sh % 2 == 0;
+}
+
+bool cb_supported(const mz_decode_args* a) {
+  const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
+  const int64_t qb = 8 * (int64_t)a->bits;
+  // buffer-resource ranges are 32-bit
+  const bool fits = (int64_t)a->n_groups * cb::TILE * 2 * qb < ((int64_t)1 << 31) &&
+                    (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
+  const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * cb::TILE;
+  return a->bits == cb::BITS && a->head_dim == cb::D && a->n_groups > 0 && fits && aligned && a->n_rep >= 1 &&
+         a->n_rep <= 8 && a->e_key && a->e_value && ((uintptr_t)a->k_packed % 4) == 0 &&
+         ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 && a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 &&
+         a->vp_sh % 4 == 0 && cb_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
+         cb_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
+         cb_meta_aligned(a->v_mn, a->vm_sb, a->vm_sh, a->meta_dtype) &&
+         cb_meta_aligned(a->v_scale, a->vm_sb, a->vm_sh, a->meta_dtype);
+}
+
+int cb_choose_split(const mz_decode_args* a, int* tiles_per_split) {
+  const int n_tiles = a->n_groups + (a->n_residual + cb::TILE - 1) / cb::TILE;
+  int ns = a->n_split;
+  if (ns <= 0) {
+    // fill the resident workgroup slots (two per CU) once
+    const int64_t units = std::max<int64_t>(1, (int64_t)a->batch * a->kv_heads);
+    const int64_t slots = 2 * (int64_t)device_cu_count();
+    ns = (int)((slots + units - 1) / units);
+    ns = max(1, min(ns, (n_tiles + 7) / 8));  // at least 2 tiles per wave
+  }
+  ns = min(ns, n_tiles);
+  const int tps = (n_tiles + ns - 1) / ns;
+  *tiles_per_split = tps;
+  return (n_tiles + tps - 1) / tps;
+}
+
+int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
+  int tps;
+  const int ns = cb_choose_split(a, &tps);
+  const dim3 grid(ns, a->kv_heads, a->batch);
+  const int dir = direct ? 1 : 0;
+  const int cus = device_cu_count();
+  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
+  const int nrep_pad = a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0;
+#define MZ_CB(IOV, NR)                                                                                       \
+  if (a->meta_dtype == MZ_F32)                                                                               \
+    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 2>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus); \
+  else                                                                                                       \
+    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 1>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus)
+#define MZ_CB_NREP(IOV)                \
+  switch (nrep_pad) {                  \
+    case 1: MZ_CB(IOV, 1); break;      \
+    case 2: MZ_CB(IOV, 2); break;      \
+    case 4: MZ_CB(IOV, 4); break;      \
+    case 8: MZ_CB(IOV, 8); break;      \
+    default: return MZ_EUNSUPPORTED;   \
+  }
+  if (a->io_dtype == MZ_BF16) { MZ_CB_NREP(MZ_BF16) } else { MZ_CB_NREP(MZ_F16) }
+#undef MZ_CB_NREP
+#undef MZ_CB
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MZ_OK : (int)e;
+}
+
+}  // namespace mz

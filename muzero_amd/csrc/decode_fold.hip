@@ -58,7 +58,7 @@
 // writes the output itself.
 #include <type_traits>
 
-#include "decode_common.hpp"
+#include "decode_tile.hpp"
 
 namespace mz {
 
@@ -172,8 +172,6 @@ struct Smem {
   static constexpr int TOTAL = WAVE0 + WAVE_AREA;
 };
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
 }
@@ -236,50 +234,13 @@ __device__ __forceinline__ GroupScalars group_scalars(float mn, float s) {
   return r;
 }
 
-// Buffer resources of one (batch, kv-head): the packed prefix and metadata
-// (bounded by their filled length, so a load past it reads 0, never faults).
-struct Bufs {
-  __amdgpu_buffer_rsrc_t kp, vp, kmn, ksc, vmn, vsc;
-  // first residual row of this (batch, kv-head); each residual tile bounds its
-  // own buffer by its filled rows (padding tokens read 0)
-  const uint16_t* kr;
-  const uint16_t* vr;
-};
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_buf(const void* p, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
-}
-
-// Global data of one quantized tile.  Code words: lanes 2m and 2m+1 of a
+// Code words of a quantized tile: lanes 2m and 2m+1 of a
 // lane group read the same 2*LB bytes of two rows of a pair (key: channels,
 // value: tokens); addr_ktile() later swaps halves between them so each lane
 // ends with the bytes of both rows that hold ITS codes.
 //   4-bit: kw[kt*2+p] = 32 bits of row 16kt+4g+2p+(n&1)
 //   2-bit: kw[kt*2+h] = 16 bits of row 16kt+4g+2h+(n&1)
 // (values: vw[(kt*NG+vg)*2 + p|h], rows = tokens, bytes of value group vg).
-// Metadata words: MW = 1 (fp16 / bf16: one word holds both entries) or 2 (fp32).
-template <int MW>
-struct MetaWords {
-  uint32_t kmn[MW], ksc[MW];  // key groups of channels 2*lane, 2*lane+1 (raw bits)
-  uint32_t vmn[MW], vsc[MW];  // value groups 0, 1 of token lane (raw bits)
-};
-
-template <int MW>
-__device__ __forceinline__ float2 meta_cvt(const uint32_t (&w)[MW], int dt) {
-  if constexpr (MW == 2) {
-    return float2{__builtin_bit_cast(float, w[0]), __builtin_bit_cast(float, w[1])};
-  } else {
-    if (dt == MZ_F16) return float2{h2f((uint16_t)w[0]), h2f((uint16_t)(w[0] >> 16))};
-    return float2{bf2f((uint16_t)w[0]), bf2f((uint16_t)(w[0] >> 16))};
-  }
-}
-
-template <int MW>
-__device__ __forceinline__ void load_meta(uint32_t (&w)[MW], const __amdgpu_buffer_rsrc_t& r, int voff, int soff) {
-  w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-  if constexpr (MW == 2) w[1] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4, soff, 0);
-}
-
 // `imm` (a compile-time offset within the tile) rides in the scalar offset
 // with the tile's own; the tile index is always a quantized tile, so the
 // address stays inside the buffer whatever the range check counts.
@@ -288,28 +249,6 @@ __device__ __forceinline__ uint32_t load_code_word(const __amdgpu_buffer_rsrc_t&
   if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff + imm, 0);
   else if constexpr (BITS == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff + imm, 0);
   else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff + imm, 0);
-}
-
-// All metadata of a tile (loaded one tile ahead of its use).  HD = head_dim
-// (64 or 128): HD / 64 value groups per token; with HD = 64 the key entries
-// of lanes 32..63 lie past the tile's own (they are not used).
-template <int MW, int HD>
-__device__ __forceinline__ void load_meta_tile(MetaWords<MW>& t, const Bufs& bf, int tile, int lane) {
-  constexpr int ES = 2 * MW;  // bytes per metadata entry
-  constexpr int NGH = HD / 64;
-  const int kmo = 2 * lane * ES, kms = tile * HD * ES;
-  load_meta<MW>(t.kmn, bf.kmn, kmo, kms);
-  load_meta<MW>(t.ksc, bf.ksc, kmo, kms);
-  const int vmo = NGH * lane * ES, vms = tile * TILE * NGH * ES;
-  if constexpr (NGH == 1 && MW == 1) {
-    // one 16-bit entry per token: a 32-bit read would reach past the buffer's
-    // end at the last token of the last tile (and then read 0 as a whole)
-    t.vmn[0] = __builtin_amdgcn_raw_buffer_load_b16(bf.vmn, vmo, vms, 0);
-    t.vsc[0] = __builtin_amdgcn_raw_buffer_load_b16(bf.vsc, vmo, vms, 0);
-  } else {
-    load_meta<MW>(t.vmn, bf.vmn, vmo, vms);
-    load_meta<MW>(t.vsc, bf.vsc, vmo, vms);
-  }
 }
 
 // Key code words of a tile (issued once the previous tile's key words are
@@ -366,10 +305,6 @@ __device__ __forceinline__ void load_vw(uint32_t (&vw)[8 * Fmt<BITS>::WPK], cons
       for (int p = 0; p < 2; ++p)
         vw[(kt * NGH + vg) * 2 + p] =
             load_code_word<BITS>(bf.vp, voff, soff, (16 * kt + 2 * p) * (NGH * F::QB) + F::QB * vg);
-}
-
-__device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_XOR1, 0xF, 0xF, true);
 }
 
 // The table addresses of one k-tile's B operands (4 rows ii of this lane's

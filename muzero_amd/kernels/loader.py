@@ -219,6 +219,10 @@ def prepare_mask(attention_mask: torch.Tensor | None, batch: int, length: int) -
     return m
 
 
+# muzero_decode_kernel() -> name
+DECODE_KERNELS = ("general", "fold", "codebook")
+
+
 class DecodePlan:
     """Validated, ready-to-launch arguments of one fused decode-attention call.
 
@@ -301,7 +305,8 @@ class DecodePlan:
             fv = tables.device_table(f"fold{int(bits)}", alpha_value, dev)
             a.fold_k, a.fold_v = ptr(fk), ptr(fv)
             keep += [fk, fv]
-        paths = {"auto": _lib.MZ_PATH_AUTO, "exact": _lib.MZ_PATH_EXACT, "fold": _lib.MZ_PATH_FOLD}
+        paths = {"auto": _lib.MZ_PATH_AUTO, "exact": _lib.MZ_PATH_EXACT, "fold": _lib.MZ_PATH_FOLD,
+                 "codebook": _lib.MZ_PATH_CODEBOOK}
         _require(kernel_path in paths, f"kernel_path must be one of {sorted(paths)}")
         a.kernel_path = paths[kernel_path]
 
@@ -342,8 +347,9 @@ class DecodePlan:
         a.workspace, a.workspace_bytes = ptr(ws), int(need)
         self.args = a
         self.n_split = ns.value
-        # whether the library runs the fold kernel for these arguments (bits 4/2, hd 128, ...)
-        self.uses_fold = bool(lib.muzero_decode_uses_fold(ctypes.byref(a)))
+        # the kernel the library runs for these arguments: "general" (exact-dequantize), "fold", "codebook"
+        self.kernel = DECODE_KERNELS[lib.muzero_decode_kernel(ctypes.byref(a))]
+        self.uses_fold = self.kernel == "fold"
         self.out = out
         self.workspace = ws
         self._keep = keep

@@ -60,7 +60,7 @@ def _offset_inputs(k, v, q, *, k_offset=0.0, v_offset=0.0, q_scale=1.0, seed=0):
 
 def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n_split=0,
               dtype=torch.bfloat16, meta=torch.float16, alpha_k=2.0, alpha_v=2.0, outliers=4,
-              kernel_path="auto", k_offset=0.0, v_offset=0.0, q_scale=1.0):
+              kernel_path="auto", k_offset=0.0, v_offset=0.0, q_scale=1.0, expect_kernel=None):
     """Returns (fp32-output max err, mean err, io-dtype output, fp64 oracle).
 
     ``mask``: False, True / "float" (additive, the HF form) or "bool" (keep-mask, converted by
@@ -92,7 +92,10 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
               k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=alpha_k, alpha_value=alpha_v,
               scaling=d ** -0.5, attention_mask=dev(am_kernel), n_split=n_split, kernel_path=kernel_path)
     qd = dev(q)
-    out32 = L.DecodePlan(qd, out_dtype=torch.float32, **kw).run()
+    plan32 = L.DecodePlan(qd, out_dtype=torch.float32, **kw)
+    if expect_kernel is not None:
+        assert plan32.kernel == expect_kernel, plan32.kernel
+    out32 = plan32.run()
     out = L.DecodePlan(qd, **kw).run()
     torch.cuda.synchronize()
     out32, out = out32.cpu(), out.cpu()
@@ -523,3 +526,88 @@ def test_three_paths_against_the_layer_dtype_path(bits, case):
     if case != "peaked":
         assert f.max().item() <= dflt.max().item(), (f.max().item(), dflt.max().item())
     assert f.mean().item() <= dflt.mean().item(), (f.mean().item(), dflt.mean().item())
+
+
+# ---------------------------------------------------------------- codebook kernel
+# The codebook kernel attends with the layer-dtype dequantized values themselves (each group's
+# values formed with the reference's fp32 operation order and rounded to the layer dtype), so
+# against the fp64 oracle over those same values only its fp32 accumulation, the v_exp_f32
+# exponentials and the weights' high + low split (~2^-17) remain: its fp32 output is held to
+# CB_MAX_ABS, a tenth of the attention tolerance (the fold kernel's fp32 values alone are up to
+# ~1e-2 from this oracle).
+
+CB_MAX_ABS = 2e-4
+CB_MEAN_ABS = 2e-5
+
+CB_CASES = [
+    # B, hkv, n_rep, d, length, bits, residual
+    (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
+    (2, 2, 4, 128, 1088, 4, 128),   # 15 groups: odd tile count per wave
+    (1, 2, 1, 128, 700, 4, 128),
+    (1, 2, 2, 128, 700, 4, 128),
+    (1, 2, 3, 128, 700, 4, 128),    # the 4-head kernel, one head idle
+    (1, 1, 8, 128, 700, 4, 128),
+    (2, 2, 7, 128, 1024, 4, 128),
+    (1, 2, 4, 128, 4096, 4, 128),   # many tiles per wave
+    (2, 1, 4, 128, 300, 4, 0),      # no residual
+    (1, 2, 4, 128, 900, 4, 191),    # residual spans two tiles, partial
+    (3, 2, 2, 128, 330, 4, 10),     # short partial residual tile
+]
+
+
+@pytest.mark.parametrize("case", CB_CASES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_b{}_R{}".format(*c))
+def test_codebook_kernel(case):
+    mx, mean, _, _ = _run_case(*case, kernel_path="codebook", expect_kernel="codebook")
+    print(f"{case}: max {mx:.2e} mean {mean:.2e}", flush=True)
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("dtype,meta", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                        (torch.bfloat16, torch.float32), (torch.float16, torch.float32)])
+def test_codebook_kernel_dtypes(dtype, meta):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 4, 128, dtype=dtype, meta=meta, kernel_path="codebook",
+                               expect_kernel="codebook")
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("mask", ["float", "bool"])
+@pytest.mark.parametrize("n_split", [0, 1, 3, 64])
+def test_codebook_kernel_split_and_mask(n_split, mask):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, 4, 128, mask=mask, n_split=n_split, kernel_path="codebook",
+                               alpha_k=16.0, alpha_v=4.0, expect_kernel="codebook")
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("q_scale", [1.0, 4.0])
+def test_codebook_kernel_offset_and_peaked(q_scale):
+    """One-signed key and value groups (|mn| >> scale) and, with the query x4, peaked rows."""
+    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, 4, 128, seed=11, k_offset=20.0, v_offset=5.0,
+                                   q_scale=q_scale, kernel_path="codebook", expect_kernel="codebook")
+    scale = max(1.0, exact.abs().max().item())
+    print(f"q_scale={q_scale}: max {mx:.2e} mean {mean:.2e} (outputs up to {scale:.1f})", flush=True)
+    assert mx < CB_MAX_ABS * scale and mean < CB_MEAN_ABS * scale, (mx, mean)
+
+
+@pytest.mark.parametrize("length", [8192, 32768])
+def test_codebook_kernel_long_context(length):
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, 4, 128, seed=length, kernel_path="codebook",
+                               expect_kernel="codebook")
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path():
+    from muzero_amd.kernels import loader as L
+    k, v, q, _ = ref.synthetic_kv(2, 2, 900, 128, 8, seed=3)
+    _, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    kw = dict(bits=4, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=2.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1, kernel_path="codebook")
+    plan = L.DecodePlan(q.to(DEV), **kw)
+    assert plan.n_split == 1 and plan.kernel == "codebook"
+    direct = plan.run().clone()
+    plan.out.zero_()
+    plan.partials()
+    two = plan.combine().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
