@@ -204,7 +204,7 @@ typedef struct mz_decode_args {
   void* out; int64_t out_sb, out_sh;
   void* workspace; int64_t workspace_bytes;
   int n_split;      /* 0 = let the library choose */
-  int kernel_path;  /* MZ_PATH_AUTO, or force MZ_PATH_EXACT / MZ_PATH_FOLD */
+  int kernel_path;  /* MZ_PATH_AUTO, or MZ_PATH_EXACT / _FOLD / _CODEBOOK / _GENERAL (below) */
   /* The compander alphas the expm1 and fold tables were built for.  Recorded
    * for the caller; the kernels read every table value from e_key / e_value /
    * fold_k / fold_v and do not read these. */
@@ -219,12 +219,21 @@ typedef struct mz_decode_args {
   int v_prefix;
 } mz_decode_args;
 
-/* kernel paths of muzero_decode_attention: AUTO uses the fold kernel when it
- * applies (bits 1 to 7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8
- * (other counts than 1, 2, 4, 8 run the kernel built for the next larger
- * one), fold tables given, at 7 bits one table for keys and values) and the
- * exact-dequantize kernel otherwise. */
-enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3 };
+/* Kernel paths of muzero_decode_attention.  Three kernels:
+ *  - codebook: attends with the reference's dequantize-then-attend values
+ *    (every dequantized value rounded to the layer dtype, bit for bit);
+ *    4-bit codes, head_dim 128, aligned prefixes, n_rep 1 to 8 (other counts
+ *    than 1, 2, 4, 8 run the kernel built for the next larger one);
+ *  - fold: the reference's fused-kernel values (fp32 dequantized values,
+ *    up to the fp16 rounding of its shifted (P, N) table entries); bits 1 to
+ *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
+ *    given, at 7 bits one table for keys and values;
+ *  - general: the dequantize-then-attend values, every width and layout.
+ * AUTO runs the codebook kernel where it applies, else the fold kernel, else
+ * the general one; EXACT the codebook kernel where it applies, else the
+ * general one; FOLD, CODEBOOK and GENERAL force that kernel (a forced fold or
+ * codebook kernel that does not take the arguments is MZ_EUNSUPPORTED). */
+enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3, MZ_PATH_GENERAL = 4 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments
  * (and the split count it will use, written to *n_split_out if non-null). */

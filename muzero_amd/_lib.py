@@ -111,7 +111,7 @@ class PrefixStateArgs(ctypes.Structure):
     ]
 
 
-MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD, MZ_PATH_CODEBOOK = 0, 1, 2, 3
+MZ_PATH_AUTO, MZ_PATH_EXACT, MZ_PATH_FOLD, MZ_PATH_CODEBOOK, MZ_PATH_GENERAL = 0, 1, 2, 3, 4
 MZ_ESCRATCH = -4
 MZ_DECODE_SCRATCH_BYTES = 8 << 20  # the static scratch of muzero_decode_attention_noalloc
 

@@ -21,8 +21,10 @@ harness reads (``benchmarks/bench_throughput.py:341-343``): ``calls``,
 when there is a quantized value prefix, and ``fused_prefix_decode_success`` /
 ``fused_prefix_decode_chunked_success`` (the one kernel is the split-over-tokens
 prefix decode with the residual merged in); plus ``hip_fused_decode`` for
-every call the kernel serves, split into ``hip_fold_kernel`` and
-``hip_exact_kernel`` by the kernel that ran.  When the launch raises, the matching
+every call the kernel serves, split into ``hip_fold_kernel`` (the fold
+kernel's fp32 values) and ``hip_exact_kernel`` (the layer-dtype values: the
+codebook or the general kernel), and ``hip_{codebook,fold,general}_kernel_calls``
+by the kernel that ran.  When the launch raises, the matching
 ``*_fallback`` counters are incremented as in the reference, and the error
 propagates: this build has no dequantize-then-attend fallback to run instead.
 
@@ -32,13 +34,19 @@ launches (``muzero_qk`` / ``muzero_av``) around a torch softmax and the
 residual matmuls, counted as ``fused_qk_success`` / ``fused_av_success``.
 
 Kernel choice, in the reference's environment-switch style (``attention.py:92``,
-``:110``, ``:128``): ``MUZERO_DECODE_KERNEL=exact`` runs every fused call on the
-exact-dequantize kernel, whose dequantized values are rounded to the layer dtype
-like the reference's dequantize-then-attend path (``attention.py:213-226``,
-``:274-283``); ``fold`` requires the fold kernel (its full-precision values are
-those of the reference's fused CUDA kernels, ``loader.py:197-263``) and raises
-where it does not apply; unset or ``auto``, the fold kernel serves the calls it
-takes (1-7 bits) and the exact kernel the rest.
+``:110``, ``:128``), ``MUZERO_DECODE_KERNEL``:
+
+* unset or ``auto``: the codebook kernel where it applies (4-bit codes,
+  head_dim 128), else the fold kernel (1-7 bits), else the general kernel;
+* ``exact``: dequantized values rounded to the layer dtype like the
+  reference's dequantize-then-attend path (``attention.py:213-226``,
+  ``:274-283``, ``layer.py:263``) on every call: the codebook kernel where it
+  applies, the general kernel elsewhere;
+* ``fold``: the fold kernel, whose full-precision values are those of the
+  reference's fused CUDA kernels (``loader.py:197-263``); raises where it
+  does not apply;
+* ``codebook`` / ``general``: that kernel (``codebook`` raises where it does
+  not apply).
 """
 
 from __future__ import annotations
@@ -124,19 +132,21 @@ def mu_zero_decode_attention_forward(
             key = (storage, query.dtype, tuple(query.shape), query.stride(), layer.nbits, alpha_key,
                    alpha_value, float(scaling), kernel_path)
     try:
-        out, fold = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
-                            scaling, attention_mask, value_prefix_length, kernel_path)
+        out, kernel = _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_key, alpha_value,
+                              scaling, attention_mask, value_prefix_length, kernel_path)
     except Exception:
         _count(key_prefix_length, value_prefix_length, "fallback")
         raise
     _count(key_prefix_length, value_prefix_length, "success")
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
-    _MU_ZERO_DECODE_STATS["hip_fold_kernel" if fold else "hip_exact_kernel"] += 1
+    # hip_exact_kernel: calls whose values are the layer-dtype dequantized values (codebook or general kernel)
+    _MU_ZERO_DECODE_STATS["hip_fold_kernel" if kernel == "fold" else "hip_exact_kernel"] += 1
+    _MU_ZERO_DECODE_STATS[f"hip_{kernel}_kernel_calls"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1
     return out, None
 
 
-_KERNEL_PATHS = ("auto", "exact", "fold")
+_KERNEL_PATHS = ("auto", "exact", "fold", "codebook", "general")
 
 
 def _kernel_path() -> str:
@@ -233,7 +243,7 @@ def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_k
             attention_mask, value_prefix_length, kernel_path="auto"):
     if fast is not None and key is not None and fast.key == key:
         out = fast.launch(query, n_groups, r)
-        fold = fast.uses_fold
+        kernel = fast.kernel
     else:
         plan = _k.DecodePlan(
             query,
@@ -249,8 +259,8 @@ def _launch(layer, fast, key, query, n_groups, r, has_res, keys, values, alpha_k
             kernel_path=kernel_path,
         )
         out = plan.run()
-        fold = plan.uses_fold
+        kernel = plan.kernel
         # cache the validated arguments only when every pointer they hold is
         # stable across steps (residual windows in their decode buffers, no mask)
         layer._hip_decode = _k.StepDecode(plan, key) if key is not None else None
-    return out, fold
+    return out, kernel

@@ -743,7 +743,7 @@ static int check_args(const mz_decode_args* a) {
   if (a->io_dtype != MZ_BF16 && a->io_dtype != MZ_F16) return MZ_EINVAL;
   if (a->meta_dtype != MZ_F16 && a->meta_dtype != MZ_BF16 && a->meta_dtype != MZ_F32) return MZ_EINVAL;
   if (a->out_dtype != a->io_dtype && a->out_dtype != MZ_F32) return MZ_EINVAL;
-  if (a->kernel_path < MZ_PATH_AUTO || a->kernel_path > MZ_PATH_CODEBOOK) return MZ_EINVAL;
+  if (a->kernel_path < MZ_PATH_AUTO || a->kernel_path > MZ_PATH_GENERAL) return MZ_EINVAL;
   if (a->head_dim != 64 && a->head_dim != 128) return MZ_EUNSUPPORTED;
   if (a->n_rep > 16) return MZ_EUNSUPPORTED;
   if (a->batch == 0) return MZ_OK;
@@ -776,10 +776,18 @@ static int check_args(const mz_decode_args* a) {
 // workspace layout and the combine kernel).
 enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2 };
 
+// AUTO: the codebook kernel where it applies (the layer-dtype values, at the
+// fold kernel's speed), else the fold kernel, else the general one.  EXACT:
+// the layer-dtype values, the codebook kernel where it applies, else the
+// general kernel.
 static Kernel which_kernel(const mz_decode_args* a) {
-  if (a->kernel_path == MZ_PATH_EXACT) return K_GENERAL;
-  if (a->kernel_path == MZ_PATH_CODEBOOK) return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
-  return fold_supported(a) ? K_FOLD : K_GENERAL;
+  switch (a->kernel_path) {
+    case MZ_PATH_GENERAL: return K_GENERAL;
+    case MZ_PATH_FOLD: return fold_supported(a) ? K_FOLD : K_GENERAL;
+    case MZ_PATH_CODEBOOK: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
+    case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
+    default: return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : K_GENERAL;
+  }
 }
 
 // A forced kernel that does not take these arguments.

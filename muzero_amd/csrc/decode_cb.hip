@@ -135,29 +135,31 @@ __device__ __forceinline__ Group group_of(float mn, float s) {
   return r;
 }
 
-// The group's 16 values in the io dtype, written as its codebook (32 bytes
-// at `dst`).  unit = za + t needs no clamp: for finite metadata it lies in
-// [0, 1] already (t = pe*E with pe = fl(1 - za) gives za + t <= 1 after
-// rounding; t = -za*E gives za + t >= 0), and NaN metadata propagates.
-template <int IO>
-__device__ __forceinline__ void build_codebook(const uint8_t* smem, int et, const Group& gr, uint8_t* dst) {
-  uint32_t w[8];
+// Values 8*HALF .. 8*HALF + 7 of the group's codebook in the io dtype,
+// written to its 16 bytes at `cbg` + 16*HALF (cbg: the group's 32 bytes).
+// unit = za + t needs no clamp: for finite metadata it lies in [0, 1]
+// already (t = pe*E with pe = fl(1 - za) gives za + t <= 1 after rounding;
+// t = -za*E gives za + t >= 0), and NaN metadata propagates.
+template <int IO, int HALF>
+__device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Group& gr, uint8_t* cbg) {
+  float2 pn[8];
 #pragma unroll
-  for (int q2 = 0; q2 < 8; ++q2) {
+  for (int e = 0; e < 8; ++e) pn[e] = *(const float2*)(smem + et + gr.row + 8 * (8 * HALF + e));
+  uint32_t w[4];
+#pragma unroll
+  for (int q2 = 0; q2 < 4; ++q2) {
     float x[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const int q = 2 * q2 + e;
-      const float2 pn = *(const float2*)(smem + et + gr.row + 8 * q);
-      const float t = __builtin_fmaf(gr.pe, pn.x, gr.mne * pn.y);
+      const float2 v = pn[2 * q2 + e];
+      const float t = __builtin_fmaf(gr.pe, v.x, gr.mne * v.y);
       const float unit = gr.za + t;
       const float u = unit * gr.s;
       x[e] = u + gr.mn;
     }
     w[q2] = pack_io2<IO>(x[0], x[1]);
   }
-  *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
-  *(u32x4*)(dst + 16) = u32x4{w[4], w[5], w[6], w[7]};
+  *(u32x4*)(cbg + 16 * HALF) = u32x4{w[0], w[1], w[2], w[3]};
 }
 
 __device__ __forceinline__ uint32_t cb_offset(int r) { return (uint32_t)((r >> 3) * CB_BLOCK + (r & 7) * CB_GROUP); }
@@ -341,16 +343,45 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // logits in base-2 units (times log2(e)): the exponentials are single v_exp_f32 ops
   const float scaling2 = a.scaling * kLog2e;
 
-  // the codebooks of a quantized tile from its metadata: key groups =
-  // channels 2*lane, 2*lane + 1; value groups = token lane, both groups
-  auto build_codebooks = [&](const MetaWords<MW>& Mw) __attribute__((always_inline)) {
-    const float2 kmn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), ksc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
-    const float2 vmn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), vsc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
-    build_codebook<IO>(smem, S::ETK, group_of(kmn.x, ksc.x), W + S::KCB + cb_offset(2 * lane));
-    build_codebook<IO>(smem, S::ETK, group_of(kmn.y, ksc.y), W + S::KCB + cb_offset(2 * lane + 1));
-    build_codebook<IO>(smem, S::ETV, group_of(vmn.x, vsc.x), W + S::VCB + cb_offset(lane));
-    build_codebook<IO>(smem, S::ETV, group_of(vmn.y, vsc.y), W + S::VCB + cb_offset(TILE + lane));
+  // Codebooks, a quarter at a time (half a group of this lane): the key
+  // groups of a tile are channels 2*lane, 2*lane + 1 (quarter c: group c/2,
+  // half c%2), its value groups token lane's two (quarter c likewise).  The
+  // value codebooks of a tile are built during its Q.K, the key codebooks of
+  // the next tile during its P.V: each is written after the last read of
+  // the one it replaces and read after the wave fence that follows.
+  uint8_t* const kcb0 = W + S::KCB + cb_offset(2 * lane);
+  uint8_t* const kcb1 = W + S::KCB + cb_offset(2 * lane + 1);
+  uint8_t* const vcb0 = W + S::VCB + cb_offset(lane);
+  uint8_t* const vcb1 = W + S::VCB + cb_offset(TILE + lane);
+  auto key_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
+    const float2 mn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
+    g0 = group_of(mn.x, sc.x);
+    g1 = group_of(mn.y, sc.y);
   };
+  auto value_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
+    const float2 mn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
+    g0 = group_of(mn.x, sc.x);
+    g1 = group_of(mn.y, sc.y);
+  };
+  auto build_quarter = [&](int et, const Group& g0, const Group& g1, uint8_t* c0, uint8_t* c1,
+                           auto quarter) __attribute__((always_inline)) {
+    constexpr int c = decltype(quarter)::value;
+    build_half<IO, c & 1>(smem, et, c < 2 ? g0 : g1, c < 2 ? c0 : c1);
+  };
+  using Q0 = std::integral_constant<int, 0>;
+  using Q1 = std::integral_constant<int, 1>;
+  using Q2 = std::integral_constant<int, 2>;
+  using Q3 = std::integral_constant<int, 3>;
+  // the first tile's key codebooks
+  {
+    Group g0, g1;
+    key_groups(MT, g0, g1);
+    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q0{});
+    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q1{});
+    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q2{});
+    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q3{});
+  }
+  wave_lds_sync();
 
   // one tile.  Loads in flight: this tile's value words and the next tile's
   // metadata (issued here), the next tile's key words (after this tile's Q.K)
@@ -374,17 +405,30 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (quant) {
-      build_codebooks(MT);
-      wave_lds_sync();  // the codebooks were written by other lanes
-      // ---------- S = Q K^T over the keys' values
+      // ---------- S = Q K^T over the keys' values; this tile's value
+      // codebooks are built alongside
+      Group gv0, gv1;
+      value_groups(MT, gv0, gv1);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         u32x4 B[4];
         switch (kt) {
-          case 0: lookup_step<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B); break;
-          case 1: lookup_step<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B); break;
-          case 2: lookup_step<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B); break;
-          default: lookup_step<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B); break;
+          case 0:
+            lookup_step<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
+            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q0{});
+            break;
+          case 1:
+            lookup_step<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
+            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q1{});
+            break;
+          case 2:
+            lookup_step<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
+            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q2{});
+            break;
+          default:
+            lookup_step<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
+            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q3{});
+            break;
         }
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], B[jt], s[jt]);
@@ -461,9 +505,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[vg][j][i] *= corr[sl], acc[vg][j][i + 1] *= corr[sl];
     }
-    wave_lds_sync();  // the weights were written by other lanes
+    wave_lds_sync();  // the weights and value codebooks were written by other lanes
 
-    // ---------- acc += P V
+    // ---------- acc += P V; the next tile's key codebooks are built alongside
+    Group gk0, gk1;
+    key_groups(MN, gk0, gk1);
     if constexpr (quant) {
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
@@ -471,10 +517,22 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         const u32x4 A = *(const u32x4*)(pv_row + (32 * kt + 8 * g) * 2);
         u32x4 B[4];
         switch (st) {
-          case 0: lookup_step<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B); break;
-          case 1: lookup_step<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B); break;
-          case 2: lookup_step<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B); break;
-          default: lookup_step<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B); break;
+          case 0:
+            lookup_step<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
+            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q0{});
+            break;
+          case 1:
+            lookup_step<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
+            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q1{});
+            break;
+          case 2:
+            lookup_step<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
+            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q2{});
+            break;
+          default:
+            lookup_step<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
+            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q3{});
+            break;
         }
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(A, B[jt], acc[vg][jt]);
@@ -511,9 +569,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
           }
         }
       }
+      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q0{});
+      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q1{});
+      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q2{});
+      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q3{});
     }
     MT = MN;
-    wave_lds_sync();  // this tile's codebooks and weights are read before the next tile overwrites them
+    wave_lds_sync();  // the next tile's key codebooks were written by other lanes; this tile's weights
+                      // and value codebooks are read before the next tile overwrites them
   };
 
   // tiles of this wave; the wave priority falls with its progress (as in the

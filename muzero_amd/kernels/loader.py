@@ -306,7 +306,7 @@ class DecodePlan:
             a.fold_k, a.fold_v = ptr(fk), ptr(fv)
             keep += [fk, fv]
         paths = {"auto": _lib.MZ_PATH_AUTO, "exact": _lib.MZ_PATH_EXACT, "fold": _lib.MZ_PATH_FOLD,
-                 "codebook": _lib.MZ_PATH_CODEBOOK}
+                 "codebook": _lib.MZ_PATH_CODEBOOK, "general": _lib.MZ_PATH_GENERAL}
         _require(kernel_path in paths, f"kernel_path must be one of {sorted(paths)}")
         a.kernel_path = paths[kernel_path]
 
@@ -401,7 +401,7 @@ class StepDecode:
     prefix/residual lengths, the output and the workspace size change."""
 
     __slots__ = ("key", "args", "argp", "lib", "device", "q_dtype", "out_shape", "workspace", "_keep",
-                 "_keep_query", "uses_fold")
+                 "_keep_query", "uses_fold", "kernel")
 
     def __init__(self, plan: DecodePlan, key):
         self.key = key
@@ -414,6 +414,7 @@ class StepDecode:
         self.workspace = plan.workspace
         self._keep = plan._keep  # tables, packed/residual views: kept alive with the arguments
         self.uses_fold = plan.uses_fold
+        self.kernel = plan.kernel
 
     def launch(self, query: torch.Tensor, n_groups: int, n_residual: int) -> torch.Tensor:
         a = self.args
@@ -431,7 +432,8 @@ class StepDecode:
             self.workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=self.device)
             a.workspace = self.workspace.data_ptr()
         a.workspace_bytes = max(int(need), int(a.workspace_bytes))
-        self.uses_fold = self.lib.muzero_decode_uses_fold(self.argp) == 1
+        self.kernel = DECODE_KERNELS[self.lib.muzero_decode_kernel(self.argp)]
+        self.uses_fold = self.kernel == "fold"
         check(self.lib.muzero_decode_attention(self.argp, stream_ptr(self.device)), "muzero_decode_attention")
         self._keep_query = q  # alive until the next launch (the kernel reads it asynchronously)
         return out

@@ -58,6 +58,18 @@ def _offset_inputs(k, v, q, *, k_offset=0.0, v_offset=0.0, q_scale=1.0, seed=0):
     return k.to(dtype), v.to(dtype), q.to(dtype)
 
 
+def expected_kernel(kernel_path, bits, d, n_rep, lq0, alpha_k=2.0, alpha_v=2.0):
+    """The kernel the library runs for a call (muzero_decode_kernel's choice, restated)."""
+    if kernel_path in ("fold", "codebook", "general"):
+        return kernel_path
+    cb = bits == 4 and d == 128 and 1 <= n_rep <= 8 and lq0 > 0
+    if kernel_path == "exact":
+        return "codebook" if cb else "general"
+    fold = (d in (64, 128) and lq0 > 0 and 1 <= n_rep <= 8
+            and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v)))
+    return "codebook" if cb else "fold" if fold else "general"
+
+
 def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n_split=0,
               dtype=torch.bfloat16, meta=torch.float16, alpha_k=2.0, alpha_v=2.0, outliers=4,
               kernel_path="auto", k_offset=0.0, v_offset=0.0, q_scale=1.0, expect_kernel=None):
@@ -77,10 +89,9 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
         am = torch.zeros(B, 1, 1, length, dtype=dtype).masked_fill_(~keep, torch.finfo(dtype).min)
         am_kernel = keep if mask == "bool" else am
     lq0 = ref.split_prefix(length, residual, 64)
-    fold = (kernel_path == "fold" or (kernel_path == "auto" and d in (64, 128) and lq0 > 0
-                                      and ((1 <= bits <= 4 and 1 <= n_rep <= 8)
-                                           or (bits in (5, 6) and 1 <= n_rep <= 8)
-                                           or (bits == 7 and 1 <= n_rep <= 8 and alpha_k == alpha_v))))
+    kernel = expected_kernel(kernel_path, bits, d, n_rep, lq0, alpha_k, alpha_v)
+    assert expect_kernel is None or expect_kernel == kernel
+    fold = kernel == "fold"
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=alpha_k, alpha_v=alpha_v, group_size=64,
                                      residual=residual, amax_dtype=meta, attention_mask=am,
                                      dequant_dtype=ref.FOLD if fold else None)
@@ -93,8 +104,7 @@ def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n
               scaling=d ** -0.5, attention_mask=dev(am_kernel), n_split=n_split, kernel_path=kernel_path)
     qd = dev(q)
     plan32 = L.DecodePlan(qd, out_dtype=torch.float32, **kw)
-    if expect_kernel is not None:
-        assert plan32.kernel == expect_kernel, plan32.kernel
+    assert plan32.kernel == kernel, (plan32.kernel, kernel)
     out32 = plan32.run()
     out = L.DecodePlan(qd, **kw).run()
     torch.cuda.synchronize()
@@ -247,7 +257,7 @@ FOLD_CASES = [
 ]
 
 
-@pytest.mark.parametrize("path", ["fold", "exact"])
+@pytest.mark.parametrize("path", ["fold", "exact", "general"])
 @pytest.mark.parametrize("case", FOLD_CASES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_b{}_R{}".format(*c))
 def test_decode_fold_and_exact_paths(case, path):
     mx, mean, _, _ = _run_case(*case, kernel_path=path)
@@ -314,9 +324,9 @@ def test_single_split_direct_output_matches_two_kernel_path(bits):
     kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
               k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
               v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
-              alpha_key=2.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1)
+              alpha_key=2.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1, kernel_path="fold")
     plan = L.DecodePlan(q.to(DEV), **kw)
-    assert plan.n_split == 1 and plan.uses_fold
+    assert plan.n_split == 1 and plan.kernel == "fold"
     direct = plan.run().clone()
     plan.out.zero_()
     plan.partials()
@@ -335,9 +345,9 @@ def test_general_single_split_direct_output_matches_two_kernel_path(bits, d):
     kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
               k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
               v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
-              alpha_key=2.0, alpha_value=3.0, scaling=d ** -0.5, n_split=1, kernel_path="exact")
+              alpha_key=2.0, alpha_value=3.0, scaling=d ** -0.5, n_split=1, kernel_path="general")
     plan = L.DecodePlan(q.to(DEV), **kw)
-    assert plan.n_split == 1 and not plan.uses_fold
+    assert plan.n_split == 1 and plan.kernel == "general"
     direct = plan.run().clone()
     plan.out.zero_()
     plan.partials()
@@ -390,10 +400,10 @@ def test_long_context_matches_oracle(length, bits):
     kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
               k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
               v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
-              alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5, out_dtype=torch.float32)
+              alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5, out_dtype=torch.float32, kernel_path="fold")
     for n_split in (0, 1):
         plan = L.DecodePlan(q.to(DEV), n_split=n_split, **kw)
-        assert plan.uses_fold and (n_split == 0 or plan.n_split == 1)
+        assert plan.kernel == "fold" and (n_split == 0 or plan.n_split == 1)
         out = plan.run()
         torch.cuda.synchronize()
         err = (out.cpu().double() - exact).abs()
@@ -470,12 +480,12 @@ def test_peaked_offset_groups_fold_kernel(bits, split_mask):
 
 def _three_paths(bits, *, seed=1234, **offsets):
     """Config 1's row shape (8 kv heads x 4 query heads, 4096 tokens, 3968 quantized, outlier key
-    channels, seed 1234): the bf16 outputs of (i) the fold kernel (the library's choice for 1-7
-    bits), (ii) the reference's default GPU decode restated with its roundings
-    (oracle.default_path_decode: fp32-codebook qk logits rounded to bf16, fp32 softmax, bf16
-    weights, av, the residual's bf16 matmuls), (iii) the exact kernel (kernel_path="exact"), and
-    the fp64 layer-dtype dequantize-then-attend oracle (attention.py:213-226, :274-283), the path
-    the attention tolerance is stated against."""
+    channels, seed 1234): the bf16 outputs of (i) the fold kernel, (ii) the reference's default
+    GPU decode restated with its roundings (oracle.default_path_decode: fp32-codebook qk logits
+    rounded to bf16, fp32 softmax, bf16 weights, av, the residual's bf16 matmuls), (iii) the
+    general exact-dequantize kernel, (iv) the codebook kernel where it applies (the library's
+    choice there), and the fp64 layer-dtype dequantize-then-attend oracle (attention.py:213-226,
+    :274-283), the path the attention tolerance is stated against."""
     from muzero_amd.kernels import loader as L
     hkv, n_rep, d, length = 8, 4, 128, 4096
     k, v, q, _ = ref.synthetic_kv(1, hkv, length, d, hkv * n_rep, seed=seed)
@@ -486,23 +496,24 @@ def _three_paths(bits, *, seed=1234, **offsets):
               k_scale=dev(st["k_scale"]), v_packed=dev(st["packed_v"]), v_mn=dev(st["v_mn"]),
               v_scale=dev(st["v_scale"]), k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=2.0,
               alpha_value=2.0, scaling=d ** -0.5)
-    plan = L.DecodePlan(dev(q), **kw)
-    assert plan.uses_fold
-    fold = plan.run()
-    exact_k = L.DecodePlan(dev(q), kernel_path="exact", **kw).run()
+    fold = L.DecodePlan(dev(q), kernel_path="fold", **kw).run()
+    exact_k = L.DecodePlan(dev(q), kernel_path="general", **kw).run()
+    outs = [("fold", fold), ("exact", exact_k)]
+    if expected_kernel("auto", bits, d, n_rep, st["lq"]) == "codebook":
+        outs.append(("codebook", L.DecodePlan(dev(q), kernel_path="codebook", **kw).run()))
     torch.cuda.synchronize()
     default = ref.default_path_decode(q, st, bits, 2.0, 2.0, n_rep, d ** -0.5)
     layer = layer[:, 0]
-    dist = {name: (o.double() - layer).abs() for name, o in
-            (("fold", fold.cpu()[:, 0]), ("default", default), ("exact", exact_k.cpu()[:, 0]))}
+    dist = {"default": (default.double() - layer).abs()}
+    dist.update({name: (o.cpu()[:, 0].double() - layer).abs() for name, o in outs})
     return dist, layer
 
 
 @pytest.mark.parametrize("bits", [4, 2, 3, 1, 5, 6, 7])
 @pytest.mark.parametrize("case", ["cfg1", "offset", "peaked"])
 def test_three_paths_against_the_layer_dtype_path(bits, case):
-    """Against the layer-dtype dequantize-then-attend path: the exact kernel meets the attention
-    tolerance (2e-3 max-abs plus half a bf16 ulp of the answer, 1e-3 mean-abs plus the answer's own
+    """Against the layer-dtype dequantize-then-attend path: the general and codebook kernels meet
+    the attention tolerance (2e-3 max-abs plus half a bf16 ulp of the answer, 1e-3 mean-abs plus the answer's own
     bf16 rounding), and the fold kernel, which keeps the dequantized values at full precision as
     the reference's CUDA kernels do, is no further from that path than the reference's own default
     GPU decode is: in max and in mean on config 1's inputs and on key channels offset by +-20 with
@@ -519,9 +530,11 @@ def test_three_paths_against_the_layer_dtype_path(bits, case):
     print(f"bits={bits} {case}: distance to the layer-dtype path: {line}", flush=True)
     half_ulp = _half_ulp_bf16(layer)
     rounding = (layer.to(torch.bfloat16).double() - layer).abs().mean().item()
-    ex = dist["exact"]
-    assert bool((ex <= MAX_ABS + half_ulp).all()), (ex - MAX_ABS - half_ulp).max().item()
-    assert ex.mean().item() < MEAN_ABS + rounding, (ex.mean().item(), rounding)
+    for name in ("exact", "codebook"):
+        if name in dist:
+            ex = dist[name]
+            assert bool((ex <= MAX_ABS + half_ulp).all()), (name, (ex - MAX_ABS - half_ulp).max().item())
+            assert ex.mean().item() < MEAN_ABS + rounding, (name, ex.mean().item(), rounding)
     f, dflt = dist["fold"], dist["default"]
     if case != "peaked":
         assert f.max().item() <= dflt.max().item(), (f.max().item(), dflt.max().item())

@@ -57,7 +57,7 @@ def test_captured_decode_replays_match_eager(bits, n_split, b, hkv, noalloc):
     assert plan.args.query == q.data_ptr()  # the graph reads the query buffer itself
     check = L.DecodePlan(q, **kw)  # eager reference: its own output and workspace
     assert plan.n_split == check.n_split and (n_split == 0 or plan.n_split == n_split)
-    print(f"bits={bits} n_split={plan.n_split} fold={plan.uses_fold} noalloc={noalloc}", flush=True)
+    print(f"bits={bits} n_split={plan.n_split} kernel={plan.kernel} noalloc={noalloc}", flush=True)
     _launch(plan, noalloc)  # first call on the device outside the capture
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()

@@ -28,6 +28,13 @@ class _Module:
         self.training = False
 
 
+def _hook_dequant_dtype(bits, d=128):
+    """The oracle's dequantization precision for the decode hook's kernel: the codebook kernel
+    (4 bits, head_dim 128) and the general kernel (8 bits) attend with the values rounded to the
+    layer dtype (None), the fold kernel (the other widths up to 7) with fp32 ones."""
+    return None if (bits == 4 and d == 128) or bits > 7 else torch.float32
+
+
 def _feed(layer, k, v, prefill):
     layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
     for t in range(prefill, k.shape[2]):
@@ -42,10 +49,8 @@ def test_cache_layer_matches_oracle_cache(bits, dtype, meta):
     cfg = mz.MuZeroConfig(bits=bits, amax_dtype=meta, alpha_key=2.0, alpha_value=2.0)
     layer = MuZeroCacheLayer(cfg)
     _feed(layer, k, v, prefill)
-    fold = 1 <= bits <= 7  # the fold kernel (fp32 dequantized values) serves 1- to 7-bit (n_rep 4)
     exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
-                                     amax_dtype=getattr(torch, meta),
-                                     dequant_dtype=torch.float32 if fold else None)
+                                     amax_dtype=getattr(torch, meta), dequant_dtype=_hook_dequant_dtype(bits))
     state = layer.get_attention_state()
     assert state["key_prefix_length"] == st["lq"] == state["value_prefix_length"]
     assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
@@ -138,7 +143,7 @@ def test_crop_then_decode(keep):
     seq_k = torch.cat([dense_k, k[:, :, prefill:]], dim=2)
     seq_v = torch.cat([dense_v, v[:, :, prefill:]], dim=2)
     exact, st2 = ref.reference_decode(q, seq_k, seq_v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64,
-                                      residual=128, dequant_dtype=torch.float32)
+                                      residual=128, dequant_dtype=_hook_dequant_dtype(4))
     state = layer.get_attention_state()
     assert state["key_prefix_length"] == st2["lq"] == layer.get_seq_length() - layer.keys.shape[2]
     if st2["lq"]:
@@ -306,7 +311,6 @@ def test_decode_stream_with_flushes_matches_oracle(bits):
     cfg.bits = bits
     layer = MuZeroCacheLayer(cfg)
     layer.update(k[:, :, :prefill].to(DEV), v[:, :, :prefill].to(DEV), {"materialize_full_kv": False})
-    fold = bits <= 7
     qd = q.to(DEV)
     checked = flushes = 0
     for t in range(prefill, prefill + steps):
@@ -321,8 +325,7 @@ def test_decode_stream_with_flushes_matches_oracle(bits):
         torch.cuda.synchronize()
         n = t + 1
         exact, st = ref.reference_decode(q, k[:, :, :n], v[:, :, :n], bits=bits, alpha_k=2.0, alpha_v=2.0,
-                                         group_size=64, residual=128,
-                                         dequant_dtype=torch.float32 if fold else None)
+                                         group_size=64, residual=128, dequant_dtype=_hook_dequant_dtype(bits))
         assert state["key_prefix_length"] == st["lq"], t
         err = (out.cpu().double() - exact).abs()
         half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
@@ -564,7 +567,7 @@ def test_four_group_flush_stream(bits):
         # the oracle's cache of the same prefix: its residual is everything after lq
         exact, st = ref.reference_decode(q, k[:, :, :length], v[:, :, :length], bits=bits, alpha_k=2.0,
                                          alpha_v=2.0, group_size=64, residual=length - lq,
-                                         dequant_dtype=torch.float32)
+                                         dequant_dtype=_hook_dequant_dtype(bits))
         assert st["lq"] == lq
         assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"]), t
         assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"]), t
@@ -604,7 +607,7 @@ def test_offload_prefetch_round_trip_then_decode():
         assert torch.equal(got.contiguous().view(torch.uint8), t.contiguous().view(torch.uint8)), n
     layer.update(k[:, :, prefill:].to(DEV), v[:, :, prefill:].to(DEV), {"materialize_full_kv": False})
     exact, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128,
-                                     dequant_dtype=torch.float32)
+                                     dequant_dtype=_hook_dequant_dtype(4))
     state = layer.get_attention_state()
     assert state["key_prefix_length"] == st["lq"]
     assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
@@ -618,10 +621,11 @@ def test_offload_prefetch_round_trip_then_decode():
 
 
 def test_decode_kernel_switch_exact_matches_layer_dtype_path(monkeypatch):
-    """MUZERO_DECODE_KERNEL=exact sends the decode hook to the exact-dequantize kernel (dequantized
-    values rounded to the layer dtype, the reference's dequantize-then-attend semantics,
-    attention.py:213-226): at config 1's row shape it meets the attention tolerance against the
-    layer-dtype oracle; an unknown value raises."""
+    """MUZERO_DECODE_KERNEL picks the decode hook's kernel.  Unset (auto) and ``exact`` run the
+    codebook kernel at 4 bits, ``general`` the general kernel: dequantized values rounded to the
+    layer dtype, the reference's dequantize-then-attend semantics (attention.py:213-226), so at
+    config 1's row shape each meets the attention tolerance against the layer-dtype oracle;
+    ``fold`` runs the fold kernel; an unknown value raises."""
     B, hkv, n_rep, d, length = 1, 8, 4, 128, 4096
     k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=1234)
     layer = MuZeroCacheLayer(mz.MuZeroConfig(bits=4))
@@ -629,17 +633,21 @@ def test_decode_kernel_switch_exact_matches_layer_dtype_path(monkeypatch):
     exact, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
     state = layer.get_attention_state()
     assert state["key_prefix_length"] == st["lq"] == 3968
-    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "exact")
-    mz.reset_mu_zero_decode_stats()
-    out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
-    torch.cuda.synchronize()
-    assert mz.get_mu_zero_decode_stats().get("hip_exact_kernel") == 1
-    err = (out.cpu().double() - exact).abs()
     half_ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp_min(2.0 ** -126))) - 8)
     rounding = (exact.to(torch.bfloat16).double() - exact).abs().mean().item()
-    assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3 + rounding, err.max().item()
-    # back to the fold kernel when the switch is unset
-    monkeypatch.delenv("MUZERO_DECODE_KERNEL")
+    for env, kernel in ((None, "codebook"), ("exact", "codebook"), ("general", "general")):
+        if env is None:
+            monkeypatch.delenv("MUZERO_DECODE_KERNEL", raising=False)
+        else:
+            monkeypatch.setenv("MUZERO_DECODE_KERNEL", env)
+        mz.reset_mu_zero_decode_stats()
+        out, _ = mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
+        torch.cuda.synchronize()
+        stats = mz.get_mu_zero_decode_stats()
+        assert stats.get("hip_exact_kernel") == 1 and stats.get(f"hip_{kernel}_kernel_calls") == 1, (env, stats)
+        err = (out.cpu().double() - exact).abs()
+        assert bool((err <= 2e-3 + half_ulp).all()) and err.mean().item() < 1e-3 + rounding, (env, err.max().item())
+    monkeypatch.setenv("MUZERO_DECODE_KERNEL", "fold")
     mz.mu_zero_decode_attention_forward(_Module(n_rep), q.to(DEV), None, d ** -0.5, state)
     assert mz.get_mu_zero_decode_stats().get("hip_fold_kernel") == 1
     monkeypatch.setenv("MUZERO_DECODE_KERNEL", "fastest")

@@ -349,11 +349,13 @@ def test_decode_stats_counter_names():
 
 
 def test_decode_kernel_switch_parsing(monkeypatch):
-    """MUZERO_DECODE_KERNEL: unset / empty -> auto; exact, fold (any case, spaces); anything else raises."""
+    """MUZERO_DECODE_KERNEL: unset / empty -> auto; exact, fold, codebook, general (any case, spaces);
+    anything else raises."""
     from muzero_amd.cache import attention as A
     monkeypatch.delenv("MUZERO_DECODE_KERNEL", raising=False)
     assert A._kernel_path() == "auto"
-    for raw, want in (("", "auto"), ("exact", "exact"), (" FOLD ", "fold"), ("Auto", "auto")):
+    for raw, want in (("", "auto"), ("exact", "exact"), (" FOLD ", "fold"), ("Auto", "auto"),
+                      ("codebook", "codebook"), ("General", "general")):
         monkeypatch.setenv("MUZERO_DECODE_KERNEL", raw)
         assert A._kernel_path() == want
     monkeypatch.setenv("MUZERO_DECODE_KERNEL", "dense")

@@ -3,8 +3,8 @@
 ``muzero_decode_attention_noalloc`` keeps a split call's partial records in the
 library's static per-device scratch instead of a caller workspace.  Through the
 C ABI it must give the workspace entry point's output bit for bit, on calls
-that use the scratch (split over tokens) for the fold kernel and the general
-kernel, two calls in a row (the second one smaller, so it reads only what it
+that use the scratch (split over tokens) for the codebook, fold and general
+kernels, two calls in a row (the second one smaller, so it reads only what it
 wrote over the first call's records), and for a single-split call, which
 needs no scratch.  The rejection of a call whose partials exceed the scratch
 is host logic, checked on the CPU in test_abi.py.
@@ -44,13 +44,14 @@ def _noalloc(plan):
     return st, out
 
 
-@pytest.mark.parametrize("bits,kernel_path,fold", [(4, "auto", True), (8, "auto", False), (4, "exact", False)])
-def test_noalloc_matches_workspace_entry_point(bits, kernel_path, fold):
-    """The fold kernel (4 bits) and the general kernel (8 bits, and 4 bits forced onto it), both
-    calls split over tokens."""
+@pytest.mark.parametrize("bits,kernel_path,kernel", [(4, "auto", "codebook"), (4, "fold", "fold"), (2, "auto", "fold"),
+                                                     (8, "auto", "general"), (4, "general", "general")])
+def test_noalloc_matches_workspace_entry_point(bits, kernel_path, kernel):
+    """The codebook kernel (4 bits), the fold kernel (2 bits, and 4 bits forced onto it) and the
+    general kernel (8 bits, and 4 bits forced onto it), both calls split over tokens."""
     for B, hkv, length, seed in ((2, 2, 4096, 1), (1, 1, 1024, 2)):
         plan = _plan(B, hkv, length, bits, seed, kernel_path=kernel_path)
-        assert plan.uses_fold == fold  # the kernel this case is meant to send through the scratch
+        assert plan.kernel == kernel  # the kernel this case is meant to send through the scratch
         assert plan.n_split > 1  # the call goes through the scratch
         want = plan.run().clone()
         st, got = _noalloc(plan)
