@@ -1,5 +1,5 @@
-// Packed-KV decode attention over per-tile codebooks, 4-bit codes (gfx950,
-// wave64, MFMA 16x16x32 in the layer dtype).
+// Packed-KV decode attention over per-tile codebooks, 4- and 2-bit codes
+// (gfx950, wave64, MFMA 16x16x32 in the layer dtype).
 //
 // Every value this kernel attends with is the reference's dequantize-then-
 // attend value bit for bit: a quantized group (one key channel or one value
@@ -26,13 +26,21 @@
 //   32kt+8g+{0..7} and needs, for each, the codes of its channels 4n..4n+3.
 //   Lanes 2m, 2m+1 load a word of two different rows and swap halves with
 //   one DPP move, so each lane then holds its 16 bits of both rows.
-// Codebook layout (per wave, keys and values alike): group r's 16 entries
-// (2 bytes each) at byte 288*(r/8) + 32*(r%8) + 2q.  One lookup instruction
-// reads one group per lane group (16 lanes, 32 bytes = 8 banks), and the 32
-// bytes of padding per 8 groups put the 4 lane groups of every instruction
-// in disjoint bank octets: the lookups are free of bank conflicts.  The
-// address is one v_perm per code: byte 0 = 2q (+32g), bytes 1-3 = the lane
-// group's block base; the row and step offsets ride in the instruction.
+// 4-bit codebook layout (per wave, keys and values alike): group r's 16
+// entries (2 bytes each) at byte 288*(r/8) + 32*(r%8) + 2q.  One lookup
+// instruction reads one group per lane group (16 lanes, 32 bytes = 8 banks),
+// and the 32 bytes of padding per 8 groups put the 4 lane groups of every
+// instruction in disjoint bank octets: the lookups are free of bank
+// conflicts.  The address is one v_perm per code: byte 0 = 2q (+32g), bytes
+// 1-3 = the lane group's block base; the row and step offsets ride in the
+// instruction.  Two lookups fill one B register (rows 2i, 2i+1).
+// 2-bit codes: the two rows of a B register (channels or tokens 2i, 2i+1)
+// share a joint codebook of their 4 x 4 code pairs, each entry the two
+// values as one dword: one 32-bit read per code pair fills a B register,
+// its address one v_dot4_u32_u8 of the two codes (masked in place) plus the
+// lane group's base.  A pair's 16 entries take 64 bytes = 16 banks; the
+// pairs of lane groups g and g ^ 1 (one half-wave) lie in opposite bank
+// halves.
 // The (E+, E-) pairs the codebooks are formed from (E+ = E[pb][q-zl] above
 // the zero level, E- = E[nb][zl-q] below it, the other 0) are a 16 x 16
 // table per alpha in LDS, built at setup from the expm1 rows; a pair turns
@@ -56,14 +64,20 @@ constexpr int WAVES = 4;
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr float kLn2 = 0.693147180559945309f;
 
-constexpr int BITS = 4;
-constexpr int QMAX = (1 << BITS) - 1;
-constexpr int QB = 8 * BITS;          // bytes per packed 64-code row
-
-// codebooks: 128 groups, 16 entries of 2 bytes, 32 bytes of padding per 8 groups
+// 4 bits: per group 16 entries of 2 bytes, 32 bytes of padding per 8 groups
 constexpr int CB_GROUP = 32;
 constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
-constexpr int CB_BYTES = 16 * CB_BLOCK;  // 4608 = 18 * 256
+// 2 bits: per row pair 16 entries of 4 bytes
+constexpr int CB_PAIR = 64;
+
+template <int BITS>
+struct Fmt {
+  static constexpr int QMAX = (1 << BITS) - 1;
+  static constexpr int QB = 8 * BITS;       // bytes per packed 64-code row
+  static constexpr bool PAIR = BITS == 2;   // joint codebooks of row pairs
+  // codebook bytes per side and wave (128 groups; 2 bits: 64 row pairs), a multiple of 256
+  static constexpr int CB_BYTES = PAIR ? 64 * CB_PAIR : 16 * CB_BLOCK;
+};
 // (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
 // bytes so that lanes reading different zero levels at one code use
 // different banks
@@ -72,8 +86,9 @@ constexpr int ET_BYTES = 16 * ET_ROW;
 constexpr int QROW = D * 2 + 16;       // bytes per head row of the query copy
 constexpr int PROW = TILE * 2 + 16;    // bytes per head row of the weight staging
 
-template <int NREP>
+template <int NREP, int BITS>
 struct Smem {
+  static constexpr int CB_BYTES = Fmt<BITS>::CB_BYTES;
   static constexpr int ETK = 0;
   static constexpr int ETV = ET_BYTES;
   static constexpr int QIO = 2 * ET_BYTES;            // query, io dtype [NREP][QROW]
@@ -121,6 +136,7 @@ struct Group {
   uint32_t row;              // byte offset of the zero level's (E+, E-) row
 };
 
+template <int QMAX>
 __device__ __forceinline__ Group group_of(float mn, float s) {
   const float eps = 1e-8f;
   Group r;
@@ -135,11 +151,46 @@ __device__ __forceinline__ Group group_of(float mn, float s) {
   return r;
 }
 
+// The value of the code whose (E+, E-) pair is `v`: the reference's fp32
+// operation order (quantizer.py:250-255).  unit = za + t needs no clamp: for
+// finite metadata it lies in [0, 1] already (t = pe*E with pe = fl(1 - za)
+// gives za + t <= 1 after rounding; t = -za*E gives za + t >= 0), and NaN
+// metadata propagates.
+__device__ __forceinline__ float code_value(const Group& gr, float2 v) {
+  const float t = __builtin_fmaf(gr.pe, v.x, gr.mne * v.y);
+  const float unit = gr.za + t;
+  const float u = unit * gr.s;
+  return u + gr.mn;
+}
+
+// A group's 4 values (2-bit codes) in the io dtype: (x0, x1), (x2, x3).
+template <int IO>
+__device__ __forceinline__ uint2 values4(const uint8_t* smem, int et, const Group& gr) {
+  float2 pn[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pn[q] = *(const float2*)(smem + et + gr.row + 8 * q);
+  return uint2{pack_io2<IO>(code_value(gr, pn[0]), code_value(gr, pn[1])),
+               pack_io2<IO>(code_value(gr, pn[2]), code_value(gr, pn[3]))};
+}
+
+// The joint codebook of a row pair from the rows' values lo (first row) and
+// hi (second): entry q0 + 4*q1 = (lo[q0], hi[q1]) as one dword, 64 bytes at `dst`.
+__device__ __forceinline__ void build_pair(const uint2 lo, const uint2 hi, uint8_t* dst) {
+  uint32_t w[16];
+#pragma unroll
+  for (int q1 = 0; q1 < 4; ++q1)
+#pragma unroll
+    for (int q0 = 0; q0 < 4; ++q0) {
+      const uint32_t l = q0 < 2 ? lo.x : lo.y, h = q1 < 2 ? hi.x : hi.y;
+      const uint32_t sel = (q0 & 1 ? 0x0302u : 0x0100u) | (q1 & 1 ? 0x07060000u : 0x05040000u);
+      w[q0 + 4 * q1] = __builtin_amdgcn_perm(h, l, sel);
+    }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) *(u32x4*)(dst + 16 * k) = u32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
+}
+
 // Values 8*HALF .. 8*HALF + 7 of the group's codebook in the io dtype,
 // written to its 16 bytes at `cbg` + 16*HALF (cbg: the group's 32 bytes).
-// unit = za + t needs no clamp: for finite metadata it lies in [0, 1]
-// already (t = pe*E with pe = fl(1 - za) gives za + t <= 1 after rounding;
-// t = -za*E gives za + t >= 0), and NaN metadata propagates.
 template <int IO, int HALF>
 __device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Group& gr, uint8_t* cbg) {
   float2 pn[8];
@@ -150,13 +201,7 @@ __device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Gr
   for (int q2 = 0; q2 < 4; ++q2) {
     float x[2];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const float2 v = pn[2 * q2 + e];
-      const float t = __builtin_fmaf(gr.pe, v.x, gr.mne * v.y);
-      const float unit = gr.za + t;
-      const float u = unit * gr.s;
-      x[e] = u + gr.mn;
-    }
+    for (int e = 0; e < 2; ++e) x[e] = code_value(gr, pn[2 * q2 + e]);
     w[q2] = pack_io2<IO>(x[0], x[1]);
   }
   *(u32x4*)(cbg + 16 * HALF) = u32x4{w[0], w[1], w[2], w[3]};
@@ -164,11 +209,11 @@ __device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Gr
 
 __device__ __forceinline__ uint32_t cb_offset(int r) { return (uint32_t)((r >> 3) * CB_BLOCK + (r & 7) * CB_GROUP); }
 
-// The B operands (columns jt = 0..3) of one step from its 4 code words:
-// w[p] = this lane's word of the step's row 2p + (n & 1).  `lb`: the lane
-// group's codebook base (byte 0 = 32g); IMM: the step's block offset.
+// 4-bit codes: the B operands (columns jt = 0..3) of one step from its 4
+// code words: w[p] = this lane's word of the step's row 2p + (n & 1).  `lb`:
+// the lane group's codebook base (byte 0 = 32g); IMM: the step's block offset.
 template <int IMM>
-__device__ __forceinline__ void lookup_step(const uint8_t* smem, const uint32_t* w, uint32_t lb, uint32_t gb,
+__device__ __forceinline__ void lookup4(const uint8_t* smem, const uint32_t* w, uint32_t lb, uint32_t gb,
                                             bool odd, u32x4 (&B)[4]) {
   // after the swap: low half = the lane's 4 codes of row 2p, high half =
   // those of row 2p + 1 (code jt at bits 4jt)
@@ -193,12 +238,49 @@ __device__ __forceinline__ void lookup_step(const uint8_t* smem, const uint32_t*
     }
 }
 
-template <int IO, int NREP, int MW>
+// 2-bit codes: the B operands of one step from its 4 code words: w[p] = 16
+// bits of the step's row 2p + (n & 1) (the codes of tokens / channels 8m ..
+// 8m + 7, m = n / 2).  After the swap, byte r of W[h] = this lane's 4 codes
+// of row 4h + r (code jt at bits 2jt).  `lb`: the lane group's base (pair
+// g of the step); IMM: the step's first pair; pair i lies 4*CB_PAIR further.
+template <int IMM>
+__device__ __forceinline__ void lookup2(const uint8_t* smem, const uint32_t* w, uint32_t lb, bool odd,
+                                        u32x4 (&B)[4]) {
+  const uint32_t sel = odd ? 0x03070105u : 0x06020400u;
+  uint32_t W[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t own = w[2 * h] | (w[2 * h + 1] << 16);
+    W[h] = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, sel);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t W2 = W[h] >> 4;  // codes 2, 3 at bits 0 and 2 of each byte
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      // the two rows' codes of column jt in place (times 1 or 4), then the
+      // entry offset 4*q0 + 16*q1 of each of the word's two pairs
+      const uint32_t t = (jt < 2 ? W[h] : W2) & ((jt & 1) ? 0x0C0C0C0Cu : 0x03030303u);
+      const uint32_t w0 = (jt & 1) ? 0x00000401u : 0x00001004u;
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const int i = 2 * h + pp;
+        const uint32_t ad = __builtin_amdgcn_udot4(t, w0 << (16 * pp), lb, false);
+        B[jt][i] = *(const uint32_t*)(smem + ad + (IMM + 4 * CB_PAIR * i));
+      }
+    }
+  }
+}
+
+template <int IO, int NREP, int MW, int BITS>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void cb_kernel(
     const mz_decode_args a, int tiles_per_split, int n_split, int direct, int cus) {
   constexpr int NT = 64 * WAVES;
   using M = Mfma<IO>;
-  using S = Smem<NREP>;
+  using F = Fmt<BITS>;
+  using S = Smem<NREP, BITS>;
+  constexpr int QMAX = F::QMAX;
+  constexpr int QB = F::QB;
   static_assert(S::TOTAL <= 80 * 1024, "two workgroups per CU");
   constexpr int RS = 16 / NREP;               // MFMA row stride between query heads
   static_assert(RS >= 2, "P.V needs a second row per head for the weights' low part");
@@ -256,7 +338,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const int t = i >> 8, zl = (i >> 4) & 15, q = i & 15;
     const float* E = t ? a.e_value : a.e_key;
     float ep = 0.f, en = 0.f;
-    if (q >= zl) {
+    if (zl > QMAX || q > QMAX) {
+      // not a code of this width: never read
+    } else if (q >= zl) {
       const int pb = max(QMAX - zl, 1);
       ep = E[expm1_row(pb) + q - zl];
     } else {
@@ -272,18 +356,24 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   }
   MetaWords<MW> MT;  // metadata of the current tile
   uint32_t KW[16], VW[16];
+  // the lane pair's word of a row: the codes of tokens (keys) / channels
+  // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2 bits
+  constexpr int WB = BITS;  // bytes of the word
+  auto load_word = [&](const __amdgpu_buffer_rsrc_t& r, int voff, int soff) __attribute__((always_inline)) {
+    if constexpr (WB == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  };
   // key words: KW[4kt + p] = this lane's word of channel row 32kt + 8g + 2p + (n & 1)
-  const int kvoff = (8 * g + (n & 1)) * QB + 4 * (n >> 1);
+  const int kvoff = (8 * g + (n & 1)) * QB + WB * (n >> 1);
   auto load_kw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * D * QB;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-        KW[4 * kt + p] = __builtin_amdgcn_raw_buffer_load_b32(bf.kp, kvoff, soff + (32 * kt + 2 * p) * QB, 0);
+      for (int p = 0; p < 4; ++p) KW[4 * kt + p] = load_word(bf.kp, kvoff, soff + (32 * kt + 2 * p) * QB);
   };
   // value words: VW[4(2kt + vg) + p] = this lane's word of token row 32kt + 8g + 2p + (n & 1), group vg
-  const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + 4 * (n >> 1);
+  const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + WB * (n >> 1);
   auto load_vw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * TILE * NGH * QB;
 #pragma unroll
@@ -292,8 +382,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
       for (int vg = 0; vg < NGH; ++vg)
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          VW[4 * (2 * kt + vg) + p] = __builtin_amdgcn_raw_buffer_load_b32(
-              bf.vp, vvoff, soff + (32 * kt + 2 * p) * (NGH * QB) + QB * vg, 0);
+          VW[4 * (2 * kt + vg) + p] = load_word(bf.vp, vvoff, soff + (32 * kt + 2 * p) * (NGH * QB) + QB * vg);
   };
   load_meta_tile<MW, D>(MT, bf, min(tile_of(v0), q_last), lane);
   load_kw(min(tile_of(v0), q_last));
@@ -313,8 +402,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
   const uint32_t wbase = (uint32_t)(S::WAVE0 + wave * S::PER_WAVE);  // LDS byte address of W (smem is at 0)
-  const uint32_t lbk = wbase + S::KCB + CB_BLOCK * g;  // this lane group's key codebook block (byte 0 = 32g)
-  const uint32_t lbv = wbase + S::VCB + CB_BLOCK * g;
+  // this lane group's codebook bases: 4 bits, its block (byte 0 = 32g); 2 bits, its pair of each step
+  const uint32_t lbk = wbase + S::KCB + (F::PAIR ? CB_PAIR : CB_BLOCK) * g;
+  const uint32_t lbv = wbase + S::VCB + (F::PAIR ? CB_PAIR : CB_BLOCK) * g;
   const uint32_t gb = 0x20202020u * (uint32_t)g;
 
   // MFMA A rows: row n of this lane belongs to head hA = n / RS; for Q.K row
@@ -343,31 +433,55 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // logits in base-2 units (times log2(e)): the exponentials are single v_exp_f32 ops
   const float scaling2 = a.scaling * kLog2e;
 
-  // Codebooks, a quarter at a time (half a group of this lane): the key
-  // groups of a tile are channels 2*lane, 2*lane + 1 (quarter c: group c/2,
-  // half c%2), its value groups token lane's two (quarter c likewise).  The
-  // value codebooks of a tile are built during its Q.K, the key codebooks of
-  // the next tile during its P.V: each is written after the last read of
-  // the one it replaces and read after the wave fence that follows.
-  uint8_t* const kcb0 = W + S::KCB + cb_offset(2 * lane);
-  uint8_t* const kcb1 = W + S::KCB + cb_offset(2 * lane + 1);
-  uint8_t* const vcb0 = W + S::VCB + cb_offset(lane);
-  uint8_t* const vcb1 = W + S::VCB + cb_offset(TILE + lane);
+  // Codebooks.  The key groups of a tile are channels 2*lane, 2*lane + 1,
+  // its value groups token lane's two.  The value codebooks of a tile are
+  // built during its Q.K, the key codebooks of the next tile during its P.V:
+  // each is written after the last read of the one it replaces and read
+  // after the wave fence that follows.  4 bits: a quarter per step (quarter
+  // c: group c/2, half c%2).  2 bits: all in the first step; the lane's two
+  // channels are one key row pair (pair lane of the tile: step lane/16, lane
+  // group lane/4 % 4, pair lane % 4); the value row pair of tokens 2m, 2m+1
+  // of group vg is built by lane 2m + vg from its own and its partner's values.
+  uint8_t* const kcb0 = W + S::KCB + (F::PAIR ? 0 : cb_offset(2 * lane));
+  uint8_t* const kcb1 = W + S::KCB + (F::PAIR ? 0 : cb_offset(2 * lane + 1));
+  uint8_t* const vcb0 = W + S::VCB + (F::PAIR ? 0 : cb_offset(lane));
+  uint8_t* const vcb1 = W + S::VCB + (F::PAIR ? 0 : cb_offset(TILE + lane));
+  const int kpair = ((lane >> 4) * 16 + (lane & 3) * 4 + ((lane >> 2) & 3)) * CB_PAIR;
+  const int vm = lane >> 1;
+  const int vpair = (((vm >> 4) * 2 + (lane & 1)) * 16 + (vm & 3) * 4 + ((vm >> 2) & 3)) * CB_PAIR;
   auto key_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
     const float2 mn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
-    g0 = group_of(mn.x, sc.x);
-    g1 = group_of(mn.y, sc.y);
+    g0 = group_of<QMAX>(mn.x, sc.x);
+    g1 = group_of<QMAX>(mn.y, sc.y);
   };
   auto value_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
     const float2 mn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
-    g0 = group_of(mn.x, sc.x);
-    g1 = group_of(mn.y, sc.y);
+    g0 = group_of<QMAX>(mn.x, sc.x);
+    g1 = group_of<QMAX>(mn.y, sc.y);
   };
-  auto build_quarter = [&](int et, const Group& g0, const Group& g1, uint8_t* c0, uint8_t* c1,
-                           auto quarter) __attribute__((always_inline)) {
-    constexpr int c = decltype(quarter)::value;
-    build_half<IO, c & 1>(smem, et, c < 2 ? g0 : g1, c < 2 ? c0 : c1);
+  // part c (0..3) of the key (VALUES false) or value codebooks of groups g0, g1
+  auto build_part = [&](auto values_tag, const Group& g0, const Group& g1, auto part) __attribute__((always_inline)) {
+    constexpr bool values = decltype(values_tag)::value;
+    constexpr int c = decltype(part)::value;
+    constexpr int et = values ? S::ETV : S::ETK;
+    if constexpr (F::PAIR) {
+      if constexpr (c == 0) {
+        const uint2 x0 = values4<IO>(smem, et, g0), x1 = values4<IO>(smem, et, g1);
+        if constexpr (values) {
+          // lane 2m builds group 0's pair of tokens 2m, 2m+1, lane 2m+1 group 1's
+          const uint2 give = odd ? x0 : x1;
+          const uint2 got = uint2{dpp_swap_pairs(give.x), dpp_swap_pairs(give.y)};
+          build_pair(odd ? got : x0, odd ? x1 : got, W + S::VCB + vpair);
+        } else {
+          build_pair(x0, x1, W + S::KCB + kpair);
+        }
+      }
+    } else {
+      build_half<IO, c & 1>(smem, et, c < 2 ? g0 : g1, values ? (c < 2 ? vcb0 : vcb1) : (c < 2 ? kcb0 : kcb1));
+    }
   };
+  using KEYS = std::false_type;
+  using VALUES = std::true_type;
   using Q0 = std::integral_constant<int, 0>;
   using Q1 = std::integral_constant<int, 1>;
   using Q2 = std::integral_constant<int, 2>;
@@ -376,10 +490,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   {
     Group g0, g1;
     key_groups(MT, g0, g1);
-    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q0{});
-    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q1{});
-    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q2{});
-    build_quarter(S::ETK, g0, g1, kcb0, kcb1, Q3{});
+    build_part(KEYS{}, g0, g1, Q0{});
+    build_part(KEYS{}, g0, g1, Q1{});
+    build_part(KEYS{}, g0, g1, Q2{});
+    build_part(KEYS{}, g0, g1, Q3{});
   }
   wave_lds_sync();
 
@@ -414,20 +528,24 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (kt) {
           case 0:
-            lookup_step<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
-            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q0{});
+            if constexpr (F::PAIR) lookup2<0 * 16 * CB_PAIR>(smem, KW + 0, lbk, odd, B);
+            else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
+            build_part(VALUES{}, gv0, gv1, Q0{});
             break;
           case 1:
-            lookup_step<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
-            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q1{});
+            if constexpr (F::PAIR) lookup2<1 * 16 * CB_PAIR>(smem, KW + 4, lbk, odd, B);
+            else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
+            build_part(VALUES{}, gv0, gv1, Q1{});
             break;
           case 2:
-            lookup_step<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
-            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q2{});
+            if constexpr (F::PAIR) lookup2<2 * 16 * CB_PAIR>(smem, KW + 8, lbk, odd, B);
+            else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
+            build_part(VALUES{}, gv0, gv1, Q2{});
             break;
           default:
-            lookup_step<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
-            build_quarter(S::ETV, gv0, gv1, vcb0, vcb1, Q3{});
+            if constexpr (F::PAIR) lookup2<3 * 16 * CB_PAIR>(smem, KW + 12, lbk, odd, B);
+            else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
+            build_part(VALUES{}, gv0, gv1, Q3{});
             break;
         }
 #pragma unroll
@@ -518,20 +636,24 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (st) {
           case 0:
-            lookup_step<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
-            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q0{});
+            if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 16 * CB_PAIR>(smem, VW + 0, lbv, odd, B);
+            else lookup4<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
+            build_part(KEYS{}, gk0, gk1, Q0{});
             break;
           case 1:
-            lookup_step<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
-            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q1{});
+            if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 16 * CB_PAIR>(smem, VW + 4, lbv, odd, B);
+            else lookup4<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
+            build_part(KEYS{}, gk0, gk1, Q1{});
             break;
           case 2:
-            lookup_step<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
-            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q2{});
+            if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 16 * CB_PAIR>(smem, VW + 8, lbv, odd, B);
+            else lookup4<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
+            build_part(KEYS{}, gk0, gk1, Q2{});
             break;
           default:
-            lookup_step<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
-            build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q3{});
+            if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 16 * CB_PAIR>(smem, VW + 12, lbv, odd, B);
+            else lookup4<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
+            build_part(KEYS{}, gk0, gk1, Q3{});
             break;
         }
 #pragma unroll
@@ -569,10 +691,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
           }
         }
       }
-      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q0{});
-      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q1{});
-      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q2{});
-      build_quarter(S::ETK, gk0, gk1, kcb0, kcb1, Q3{});
+      build_part(KEYS{}, gk0, gk1, Q0{});
+      build_part(KEYS{}, gk0, gk1, Q1{});
+      build_part(KEYS{}, gk0, gk1, Q2{});
+      build_part(KEYS{}, gk0, gk1, Q3{});
     }
     MT = MN;
     wave_lds_sync();  // the next tile's key codebooks were written by other lanes; this tile's weights
@@ -681,11 +803,12 @@ static bool cb_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
 bool cb_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   const int64_t qb = 8 * (int64_t)a->bits;
+  const bool bits_ok = a->bits == 4 || a->bits == 2;
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * cb::TILE * 2 * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * cb::TILE;
-  return a->bits == cb::BITS && a->head_dim == cb::D && a->n_groups > 0 && fits && aligned && a->n_rep >= 1 &&
+  return bits_ok && a->head_dim == cb::D && a->n_groups > 0 && fits && aligned && a->n_rep >= 1 &&
          a->n_rep <= 8 && a->e_key && a->e_value && ((uintptr_t)a->k_packed % 4) == 0 &&
          ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 && a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 &&
          a->vp_sh % 4 == 0 && cb_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
@@ -718,11 +841,14 @@ int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   const int cus = device_cu_count();
   // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
   const int nrep_pad = a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0;
-#define MZ_CB(IOV, NR)                                                                                       \
-  if (a->meta_dtype == MZ_F32)                                                                               \
-    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 2>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus); \
-  else                                                                                                       \
-    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 1>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus)
+#define MZ_CB_B(IOV, NR, BB)                                                                                      \
+  if (a->meta_dtype == MZ_F32)                                                                                    \
+    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 2, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus); \
+  else                                                                                                            \
+    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 1, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus)
+#define MZ_CB(IOV, NR)                    \
+  if (a->bits == 4) { MZ_CB_B(IOV, NR, 4); } \
+  else { MZ_CB_B(IOV, NR, 2); }
 #define MZ_CB_NREP(IOV)                \
   switch (nrep_pad) {                  \
     case 1: MZ_CB(IOV, 1); break;      \
@@ -734,6 +860,7 @@ int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   if (a->io_dtype == MZ_BF16) { MZ_CB_NREP(MZ_BF16) } else { MZ_CB_NREP(MZ_F16) }
 #undef MZ_CB_NREP
 #undef MZ_CB
+#undef MZ_CB_B
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MZ_OK : (int)e;
 }

@@ -46,3 +46,19 @@ def bits_of(t) -> np.ndarray:
     if t.dtype == torch.float32:
         return t.numpy().view(np.uint32)
     return t.numpy()
+
+
+# Bit widths the codebook decode kernel takes (head_dim 128, n_rep 1..8, a quantized prefix).
+CODEBOOK_BITS = (2, 4)
+
+
+def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
+    """The decode kernel the library runs for a call (muzero_decode_kernel's choice, restated):
+    "codebook" and "general" attend with the values rounded to the layer dtype, "fold" with fp32 ones."""
+    if kernel_path in ("fold", "codebook", "general"):
+        return kernel_path
+    cb = bits in CODEBOOK_BITS and d == 128 and 1 <= n_rep <= 8 and lq > 0
+    if kernel_path == "exact":
+        return "codebook" if cb else "general"
+    fold = d in (64, 128) and lq > 0 and 1 <= n_rep <= 8 and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v))
+    return "codebook" if cb else "fold" if fold else "general"

@@ -26,6 +26,7 @@ average, so no bf16 result can meet the bare bounds there).
 import pytest
 import torch
 
+from conftest import expected_kernel
 from oracle import reference_torch as ref
 
 pytestmark = pytest.mark.gpu
@@ -56,18 +57,6 @@ def _offset_inputs(k, v, q, *, k_offset=0.0, v_offset=0.0, q_scale=1.0, seed=0):
     if q_scale != 1.0:
         q = q.float() * q_scale
     return k.to(dtype), v.to(dtype), q.to(dtype)
-
-
-def expected_kernel(kernel_path, bits, d, n_rep, lq0, alpha_k=2.0, alpha_v=2.0):
-    """The kernel the library runs for a call (muzero_decode_kernel's choice, restated)."""
-    if kernel_path in ("fold", "codebook", "general"):
-        return kernel_path
-    cb = bits == 4 and d == 128 and 1 <= n_rep <= 8 and lq0 > 0
-    if kernel_path == "exact":
-        return "codebook" if cb else "general"
-    fold = (d in (64, 128) and lq0 > 0 and 1 <= n_rep <= 8
-            and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v)))
-    return "codebook" if cb else "fold" if fold else "general"
 
 
 def _run_case(B, hkv, n_rep, d, length, bits, residual, *, seed=0, mask=False, n_split=0,
@@ -552,67 +541,76 @@ def test_three_paths_against_the_layer_dtype_path(bits, case):
 CB_MAX_ABS = 2e-4
 CB_MEAN_ABS = 2e-5
 
-CB_CASES = [
-    # B, hkv, n_rep, d, length, bits, residual
-    (2, 2, 4, 128, 1024, 4, 128),   # 14 groups + 2 residual tiles
-    (2, 2, 4, 128, 1088, 4, 128),   # 15 groups: odd tile count per wave
-    (1, 2, 1, 128, 700, 4, 128),
-    (1, 2, 2, 128, 700, 4, 128),
-    (1, 2, 3, 128, 700, 4, 128),    # the 4-head kernel, one head idle
-    (1, 1, 8, 128, 700, 4, 128),
-    (2, 2, 7, 128, 1024, 4, 128),
-    (1, 2, 4, 128, 4096, 4, 128),   # many tiles per wave
-    (2, 1, 4, 128, 300, 4, 0),      # no residual
-    (1, 2, 4, 128, 900, 4, 191),    # residual spans two tiles, partial
-    (3, 2, 2, 128, 330, 4, 10),     # short partial residual tile
+CB_SHAPES = [
+    # B, hkv, n_rep, d, length, residual
+    (2, 2, 4, 128, 1024, 128),   # 14 groups + 2 residual tiles
+    (2, 2, 4, 128, 1088, 128),   # 15 groups: odd tile count per wave
+    (1, 2, 1, 128, 700, 128),
+    (1, 2, 2, 128, 700, 128),
+    (1, 2, 3, 128, 700, 128),    # the 4-head kernel, one head idle
+    (1, 1, 8, 128, 700, 128),
+    (2, 2, 7, 128, 1024, 128),
+    (1, 2, 4, 128, 4096, 128),   # many tiles per wave
+    (2, 1, 4, 128, 300, 0),      # no residual
+    (1, 2, 4, 128, 900, 191),    # residual spans two tiles, partial
+    (3, 2, 2, 128, 330, 10),     # short partial residual tile
 ]
+CB_BITS = [4, 2]
 
 
-@pytest.mark.parametrize("case", CB_CASES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_b{}_R{}".format(*c))
-def test_codebook_kernel(case):
-    mx, mean, _, _ = _run_case(*case, kernel_path="codebook", expect_kernel="codebook")
-    print(f"{case}: max {mx:.2e} mean {mean:.2e}", flush=True)
+@pytest.mark.parametrize("bits", CB_BITS)
+@pytest.mark.parametrize("shape", CB_SHAPES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_R{}".format(*c))
+def test_codebook_kernel(shape, bits):
+    B, hkv, n_rep, d, length, residual = shape
+    mx, mean, _, _ = _run_case(B, hkv, n_rep, d, length, bits, residual, kernel_path="codebook",
+                               expect_kernel="codebook")
+    print(f"{shape} bits={bits}: max {mx:.2e} mean {mean:.2e}", flush=True)
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", CB_BITS)
 @pytest.mark.parametrize("dtype,meta", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
                                         (torch.bfloat16, torch.float32), (torch.float16, torch.float32)])
-def test_codebook_kernel_dtypes(dtype, meta):
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 4, 128, dtype=dtype, meta=meta, kernel_path="codebook",
+def test_codebook_kernel_dtypes(dtype, meta, bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, bits, 128, dtype=dtype, meta=meta, kernel_path="codebook",
                                expect_kernel="codebook")
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", CB_BITS)
 @pytest.mark.parametrize("mask", ["float", "bool"])
 @pytest.mark.parametrize("n_split", [0, 1, 3, 64])
-def test_codebook_kernel_split_and_mask(n_split, mask):
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, 4, 128, mask=mask, n_split=n_split, kernel_path="codebook",
+def test_codebook_kernel_split_and_mask(n_split, mask, bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, mask=mask, n_split=n_split, kernel_path="codebook",
                                alpha_k=16.0, alpha_v=4.0, expect_kernel="codebook")
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", CB_BITS)
 @pytest.mark.parametrize("q_scale", [1.0, 4.0])
-def test_codebook_kernel_offset_and_peaked(q_scale):
+def test_codebook_kernel_offset_and_peaked(q_scale, bits):
     """One-signed key and value groups (|mn| >> scale) and, with the query x4, peaked rows."""
-    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, 4, 128, seed=11, k_offset=20.0, v_offset=5.0,
+    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, bits, 128, seed=11, k_offset=20.0, v_offset=5.0,
                                    q_scale=q_scale, kernel_path="codebook", expect_kernel="codebook")
     scale = max(1.0, exact.abs().max().item())
-    print(f"q_scale={q_scale}: max {mx:.2e} mean {mean:.2e} (outputs up to {scale:.1f})", flush=True)
+    print(f"bits={bits} q_scale={q_scale}: max {mx:.2e} mean {mean:.2e} (outputs up to {scale:.1f})", flush=True)
     assert mx < CB_MAX_ABS * scale and mean < CB_MEAN_ABS * scale, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", CB_BITS)
 @pytest.mark.parametrize("length", [8192, 32768])
-def test_codebook_kernel_long_context(length):
-    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, 4, 128, seed=length, kernel_path="codebook",
+def test_codebook_kernel_long_context(length, bits):
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, bits, 128, seed=length, kernel_path="codebook",
                                expect_kernel="codebook")
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
-def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path():
+@pytest.mark.parametrize("bits", CB_BITS)
+def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path(bits):
     from muzero_amd.kernels import loader as L
     k, v, q, _ = ref.synthetic_kv(2, 2, 900, 128, 8, seed=3)
-    _, st = ref.reference_decode(q, k, v, bits=4, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
-    kw = dict(bits=4, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+    _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
+    kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
               k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
               v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
               alpha_key=2.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1, kernel_path="codebook")

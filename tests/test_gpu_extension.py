@@ -22,6 +22,7 @@ import torch
 import muzero_amd as mz
 from muzero_amd.cache.layer import MuZeroCacheLayer
 from muzero_amd.kernels import load_mu_zero_cuda_extension
+from conftest import expected_kernel
 from oracle import reference_torch as ref
 
 pytestmark = pytest.mark.gpu
@@ -150,10 +151,10 @@ def test_extension_prefix_decode_as_the_reference_calls_it(bits, chunk_groups):
             layer._value_mn[:, :, :lv, ...].contiguous(), layer._value_scale[:, :, :lv, ...].contiguous())
     tail = (float(layer._selected_alpha_key), float(layer._selected_alpha_value), n_rep, scaling)
     n_groups = layer._packed_key_q.shape[2]
-    # the kernel the library runs: the codebook kernel (4 bits) and the general kernel (8 bits)
-    # attend with the values rounded to the layer dtype, the fold kernel (2, 3 bits) with the fp32
+    # the kernel the library runs: the codebook kernel (2, 4 bits) and the general kernel (8 bits)
+    # attend with the values rounded to the layer dtype, the fold kernel (3 bits) with the fp32
     # values of the reference kernels' codebooks
-    ddt = torch.bfloat16 if bits in (4, 8) else torch.float32
+    ddt = torch.float32 if expected_kernel("auto", bits, d, n_rep, 64) == "fold" else torch.bfloat16
     _, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64, residual=128)
     sargs = (q, st["packed_k"], st["k_mn"], st["k_scale"], st["packed_v"], st["v_mn"], st["v_scale"], bits,
              2.0, 2.0, n_rep, scaling)

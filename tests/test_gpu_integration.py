@@ -16,6 +16,7 @@ import torch
 
 import muzero_amd as mz
 from muzero_amd.cache.layer import MuZeroCacheLayer
+from conftest import expected_kernel
 from oracle import reference_torch as ref
 
 pytestmark = pytest.mark.gpu
@@ -29,10 +30,10 @@ class _Module:
 
 
 def _hook_dequant_dtype(bits, d=128):
-    """The oracle's dequantization precision for the decode hook's kernel: the codebook kernel
-    (4 bits, head_dim 128) and the general kernel (8 bits) attend with the values rounded to the
-    layer dtype (None), the fold kernel (the other widths up to 7) with fp32 ones."""
-    return None if (bits == 4 and d == 128) or bits > 7 else torch.float32
+    """The oracle's dequantization precision for the decode hook's kernel (n_rep 4): the codebook
+    and general kernels attend with the values rounded to the layer dtype (None), the fold kernel
+    with fp32 ones."""
+    return torch.float32 if expected_kernel("auto", bits, d, 4, 64) == "fold" else None
 
 
 def _feed(layer, k, v, prefill):
@@ -170,7 +171,7 @@ def test_batch_select_then_decode():
     layer.reorder_cache(idx.to(DEV))
     layer.update(k[idx, :, prefill:].to(DEV), v[idx, :, prefill:].to(DEV), {"materialize_full_kv": False})
     exact, st = ref.reference_decode(q[idx], k[idx], v[idx], bits=2, alpha_k=2.0, alpha_v=2.0, group_size=64,
-                                     residual=128, dequant_dtype=torch.float32)
+                                     residual=128, dequant_dtype=_hook_dequant_dtype(2))
     assert torch.equal(layer._packed_key_q.cpu(), st["packed_k"])
     assert torch.equal(layer._packed_value_q.cpu(), st["packed_v"])
     assert torch.equal(layer.keys.cpu(), st["res_k"]) and torch.equal(layer.values.cpu(), st["res_v"])
