@@ -38,9 +38,12 @@
 // share a joint codebook of their 4 x 4 code pairs, each entry the two
 // values as one dword: one 32-bit read per code pair fills a B register,
 // its address one v_dot4_u32_u8 of the two codes (masked in place) plus the
-// lane group's base.  A pair's 16 entries take 64 bytes = 16 banks; the
-// pairs of lane groups g and g ^ 1 (one half-wave) lie in opposite bank
-// halves.
+// lane group's base.  A pair's 16 entries take 64 bytes = 16 banks; pair
+// (step s, i, lane group g) lies at byte 272*(4s + i) + 64g: the pairs of
+// lane groups g and g ^ 1 (one half-wave) lie in opposite bank halves, and
+// the 16 bytes of padding per 4 pairs put the pairs that 8 consecutive lanes
+// write (i = 0..3, two lane groups) in 8 different 16-byte bank slots, so the
+// 128-bit codebook stores are free of conflicts too.
 // The (E+, E-) pairs the codebooks are formed from (E+ = E[pb][q-zl] above
 // the zero level, E- = E[nb][zl-q] below it, the other 0) are a 16 x 16
 // table per alpha in LDS, built at setup from the expm1 rows; a pair turns
@@ -67,8 +70,10 @@ constexpr float kLn2 = 0.693147180559945309f;
 // 4 bits: per group 16 entries of 2 bytes, 32 bytes of padding per 8 groups
 constexpr int CB_GROUP = 32;
 constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
-// 2 bits: per row pair 16 entries of 4 bytes
+// 2 bits: per row pair 16 entries of 4 bytes; the 4 lane groups' pairs of one
+// (step, i) in a block of 4 pairs + 16 bytes
 constexpr int CB_PAIR = 64;
+constexpr int CB_PAIRS = 4 * CB_PAIR + 16;
 
 template <int BITS>
 struct Fmt {
@@ -76,7 +81,7 @@ struct Fmt {
   static constexpr int QB = 8 * BITS;       // bytes per packed 64-code row
   static constexpr bool PAIR = BITS == 2;   // joint codebooks of row pairs
   // codebook bytes per side and wave (128 groups; 2 bits: 64 row pairs), a multiple of 256
-  static constexpr int CB_BYTES = PAIR ? 64 * CB_PAIR : 16 * CB_BLOCK;
+  static constexpr int CB_BYTES = PAIR ? 16 * CB_PAIRS : 16 * CB_BLOCK;
 };
 // (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
 // bytes so that lanes reading different zero levels at one code use
@@ -242,7 +247,7 @@ __device__ __forceinline__ void lookup4(const uint8_t* smem, const uint32_t* w, 
 // bits of the step's row 2p + (n & 1) (the codes of tokens / channels 8m ..
 // 8m + 7, m = n / 2).  After the swap, byte r of W[h] = this lane's 4 codes
 // of row 4h + r (code jt at bits 2jt).  `lb`: the lane group's base (pair
-// g of the step); IMM: the step's first pair; pair i lies 4*CB_PAIR further.
+// g of the step); IMM: the step's first pair block; pair i's lies CB_PAIRS further.
 template <int IMM>
 __device__ __forceinline__ void lookup2(const uint8_t* smem, const uint32_t* w, uint32_t lb, bool odd,
                                         u32x4 (&B)[4]) {
@@ -266,7 +271,7 @@ __device__ __forceinline__ void lookup2(const uint8_t* smem, const uint32_t* w, 
       for (int pp = 0; pp < 2; ++pp) {
         const int i = 2 * h + pp;
         const uint32_t ad = __builtin_amdgcn_udot4(t, w0 << (16 * pp), lb, false);
-        B[jt][i] = *(const uint32_t*)(smem + ad + (IMM + 4 * CB_PAIR * i));
+        B[jt][i] = *(const uint32_t*)(smem + ad + (IMM + CB_PAIRS * i));
       }
     }
   }
@@ -446,9 +451,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   uint8_t* const kcb1 = W + S::KCB + (F::PAIR ? 0 : cb_offset(2 * lane + 1));
   uint8_t* const vcb0 = W + S::VCB + (F::PAIR ? 0 : cb_offset(lane));
   uint8_t* const vcb1 = W + S::VCB + (F::PAIR ? 0 : cb_offset(TILE + lane));
-  const int kpair = ((lane >> 4) * 16 + (lane & 3) * 4 + ((lane >> 2) & 3)) * CB_PAIR;
+  const int kpair = ((lane >> 4) * 4 + (lane & 3)) * CB_PAIRS + ((lane >> 2) & 3) * CB_PAIR;
   const int vm = lane >> 1;
-  const int vpair = (((vm >> 4) * 2 + (lane & 1)) * 16 + (vm & 3) * 4 + ((vm >> 2) & 3)) * CB_PAIR;
+  const int vpair = (((vm >> 4) * 2 + (lane & 1)) * 4 + (vm & 3)) * CB_PAIRS + ((vm >> 2) & 3) * CB_PAIR;
   auto key_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
     const float2 mn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
     g0 = group_of<QMAX>(mn.x, sc.x);
@@ -528,22 +533,22 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (kt) {
           case 0:
-            if constexpr (F::PAIR) lookup2<0 * 16 * CB_PAIR>(smem, KW + 0, lbk, odd, B);
+            if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
             else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q0{});
             break;
           case 1:
-            if constexpr (F::PAIR) lookup2<1 * 16 * CB_PAIR>(smem, KW + 4, lbk, odd, B);
+            if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
             else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q1{});
             break;
           case 2:
-            if constexpr (F::PAIR) lookup2<2 * 16 * CB_PAIR>(smem, KW + 8, lbk, odd, B);
+            if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
             else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q2{});
             break;
           default:
-            if constexpr (F::PAIR) lookup2<3 * 16 * CB_PAIR>(smem, KW + 12, lbk, odd, B);
+            if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
             else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q3{});
             break;
@@ -636,22 +641,22 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (st) {
           case 0:
-            if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 16 * CB_PAIR>(smem, VW + 0, lbv, odd, B);
+            if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
             else lookup4<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q0{});
             break;
           case 1:
-            if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 16 * CB_PAIR>(smem, VW + 4, lbv, odd, B);
+            if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
             else lookup4<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q1{});
             break;
           case 2:
-            if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 16 * CB_PAIR>(smem, VW + 8, lbv, odd, B);
+            if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
             else lookup4<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q2{});
             break;
           default:
-            if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 16 * CB_PAIR>(smem, VW + 12, lbv, odd, B);
+            if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
             else lookup4<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q3{});
             break;
