@@ -628,8 +628,11 @@ def main():
                "gpu_vs_cpu_path": {"max_abs": round(diff.max().item(), 6), "mean_abs": round(diff.mean().item(), 7),
                                    "note": f"{args.kv_dtype} outputs of the sampled rows; the CPU path rounds dequantized "
                                            f"values, logits and weights to {args.kv_dtype} (the reference's dequantize-then-"
-                                           "attend), the fold kernel keeps fp32 codebook values (its fused "
-                                           "kernels' semantics)"}}
+                                           "attend with its matmuls in the layer dtype); the "
+                                           + ("fold kernel keeps fp32 dequantized values (its fused kernels' semantics)"
+                                              if plans[0].kernel == "fold" else
+                                              f"{plans[0].kernel} kernel attends with the same dequantized values")
+                                           + " and keeps logits and weights in fp32"}}
 
     line = {
         "metric": "packed-KV decode attn HBM GB/s (% of peak); decode tokens/sec at B=64 ctx 4096",

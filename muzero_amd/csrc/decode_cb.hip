@@ -194,13 +194,14 @@ __device__ __forceinline__ void build_pair(const uint2 lo, const uint2 hi, uint8
   for (int k = 0; k < 4; ++k) *(u32x4*)(dst + 16 * k) = u32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
 }
 
-// Values 8*HALF .. 8*HALF + 7 of the group's codebook in the io dtype,
-// written to its 16 bytes at `cbg` + 16*HALF (cbg: the group's 32 bytes).
-template <int IO, int HALF>
-__device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Group& gr, uint8_t* cbg) {
+// Values 8*half .. 8*half + 7 of the group's codebook in the io dtype,
+// written to its 16 bytes at `cbg` + 16*half (cbg: the group's 32 bytes).
+template <int IO>
+__device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Group& gr, uint8_t* cbg, int half) {
   float2 pn[8];
+  const uint8_t* src = smem + et + gr.row + 64 * half;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pn[e] = *(const float2*)(smem + et + gr.row + 8 * (8 * HALF + e));
+  for (int e = 0; e < 8; ++e) pn[e] = *(const float2*)(src + 8 * e);
   uint32_t w[4];
 #pragma unroll
   for (int q2 = 0; q2 < 4; ++q2) {
@@ -209,7 +210,7 @@ __device__ __forceinline__ void build_half(const uint8_t* smem, int et, const Gr
     for (int e = 0; e < 2; ++e) x[e] = code_value(gr, pn[2 * q2 + e]);
     w[q2] = pack_io2<IO>(x[0], x[1]);
   }
-  *(u32x4*)(cbg + 16 * HALF) = u32x4{w[0], w[1], w[2], w[3]};
+  *(u32x4*)(cbg + 16 * half) = u32x4{w[0], w[1], w[2], w[3]};
 }
 
 __device__ __forceinline__ uint32_t cb_offset(int r) { return (uint32_t)((r >> 3) * CB_BLOCK + (r & 7) * CB_GROUP); }
@@ -443,7 +444,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   // built during its Q.K, the key codebooks of the next tile during its P.V:
   // each is written after the last read of the one it replaces and read
   // after the wave fence that follows.  4 bits: a quarter per step (quarter
-  // c: group c/2, half c%2).  2 bits: all in the first step; the lane's two
+  // c: group c/2, half c%2 xor a lane bit: 8 consecutive lanes then store to
+  // 8 different 16-byte bank slots).  2 bits: all in the first step; the lane's two
   // channels are one key row pair (pair lane of the tile: step lane/16, lane
   // group lane/4 % 4, pair lane % 4); the value row pair of tokens 2m, 2m+1
   // of group vg is built by lane 2m + vg from its own and its partner's values.
@@ -464,6 +466,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     g0 = group_of<QMAX>(mn.x, sc.x);
     g1 = group_of<QMAX>(mn.y, sc.y);
   };
+  // 4 bits: the half a lane builds in parts 0 and 2 (see above)
+  const int krot = (lane >> 1) & 1, vrot = (lane >> 2) & 1;
   // part c (0..3) of the key (VALUES false) or value codebooks of groups g0, g1
   auto build_part = [&](auto values_tag, const Group& g0, const Group& g1, auto part) __attribute__((always_inline)) {
     constexpr bool values = decltype(values_tag)::value;
@@ -482,7 +486,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         }
       }
     } else {
-      build_half<IO, c & 1>(smem, et, c < 2 ? g0 : g1, values ? (c < 2 ? vcb0 : vcb1) : (c < 2 ? kcb0 : kcb1));
+      build_half<IO>(smem, et, c < 2 ? g0 : g1, values ? (c < 2 ? vcb0 : vcb1) : (c < 2 ? kcb0 : kcb1),
+                     (c & 1) ^ (values ? vrot : krot));
     }
   };
   using KEYS = std::false_type;
