@@ -1,4 +1,4 @@
-// Packed-KV decode attention over per-tile codebooks, 4- and 2-bit codes
+// Packed-KV decode attention over per-tile codebooks, 2- to 4-bit codes
 // (gfx950, wave64, MFMA 16x16x32 in the layer dtype).
 //
 // Every value this kernel attends with is the reference's dequantize-then-
@@ -34,6 +34,11 @@
 // conflicts.  The address is one v_perm per code: byte 0 = 2q (+32g), bytes
 // 1-3 = the lane group's block base; the row and step offsets ride in the
 // instruction.  Two lookups fill one B register (rows 2i, 2i+1).
+// 3-bit codes: group r's 8 entries at byte 144*(r/8) + 16*(r%8) + 2q; the 16
+// bytes of padding per 8 groups put the 4 lane groups of a lookup in 4
+// different 16-byte bank slots and 8 consecutive lanes' codebook stores (16
+// bytes each) in 8.  The address is a bit-field extract of the code and one
+// shift-or onto the lane group's base per code (3-bit codes straddle bytes).
 // 2-bit codes: the two rows of a B register (channels or tokens 2i, 2i+1)
 // share a joint codebook of their 4 x 4 code pairs, each entry the two
 // values as one dword: one 32-bit read per code pair fills a B register,
@@ -70,6 +75,8 @@ constexpr float kLn2 = 0.693147180559945309f;
 // 4 bits: per group 16 entries of 2 bytes, 32 bytes of padding per 8 groups
 constexpr int CB_GROUP = 32;
 constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
+// 3 bits: per group 8 entries of 2 bytes, 16 bytes of padding per 8 groups
+constexpr int CB_BLOCK3 = 8 * 16 + 16;
 // 2 bits: per row pair 16 entries of 4 bytes; the 4 lane groups' pairs of one
 // (step, i) in a block of 4 pairs + 16 bytes
 constexpr int CB_PAIR = 64;
@@ -81,7 +88,7 @@ struct Fmt {
   static constexpr int QB = 8 * BITS;       // bytes per packed 64-code row
   static constexpr bool PAIR = BITS == 2;   // joint codebooks of row pairs
   // codebook bytes per side and wave (128 groups; 2 bits: 64 row pairs), a multiple of 256
-  static constexpr int CB_BYTES = PAIR ? 16 * CB_PAIRS : 16 * CB_BLOCK;
+  static constexpr int CB_BYTES = PAIR ? 16 * CB_PAIRS : BITS == 3 ? 16 * CB_BLOCK3 : 16 * CB_BLOCK;
 };
 // (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
 // bytes so that lanes reading different zero levels at one code use
@@ -178,6 +185,20 @@ __device__ __forceinline__ uint2 values4(const uint8_t* smem, int et, const Grou
                pack_io2<IO>(code_value(gr, pn[2]), code_value(gr, pn[3]))};
 }
 
+// A group's 8 values (3-bit codes) in the io dtype, written as its codebook (16 bytes at `dst`).
+template <int IO>
+__device__ __forceinline__ void build_group8(const uint8_t* smem, int et, const Group& gr, uint8_t* dst) {
+  float2 pn[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) pn[q] = *(const float2*)(smem + et + gr.row + 8 * q);
+  uint32_t w[4];
+#pragma unroll
+  for (int q2 = 0; q2 < 4; ++q2) w[q2] = pack_io2<IO>(code_value(gr, pn[2 * q2]), code_value(gr, pn[2 * q2 + 1]));
+  *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+__device__ __forceinline__ uint32_t cb3_offset(int r) { return (uint32_t)((r >> 3) * CB_BLOCK3 + (r & 7) * 16); }
+
 // The joint codebook of a row pair from the rows' values lo (first row) and
 // hi (second): entry q0 + 4*q1 = (lo[q0], hi[q1]) as one dword, 64 bytes at `dst`.
 __device__ __forceinline__ void build_pair(const uint2 lo, const uint2 hi, uint8_t* dst) {
@@ -240,6 +261,33 @@ __device__ __forceinline__ void lookup4(const uint8_t* smem, const uint32_t* w, 
       const uint32_t a1 = __builtin_amdgcn_perm(lb, e, 0x07060500u | (uint32_t)(2 + (jt >> 1)));
       const uint16_t lo = lds_u16(smem, a0 + (IMM + 2 * i * CB_GROUP));
       const uint16_t hi = lds_u16(smem, a1 + (IMM + (2 * i + 1) * CB_GROUP));
+      B[jt][i] = __builtin_bit_cast(uint32_t, u16x2{lo, hi});
+    }
+}
+
+// 3-bit codes: the B operands of one step from its 4 code words: w[p] = the
+// dword of the step's row 2p + (n & 1) holding the codes of the lane pair
+// (read at byte min(3m, 20) of the 24-byte row, m = n / 2); this lane's code
+// jt of a row is at bit sh + 3jt of it.  `lb`: the lane group's block base
+// (its low 4 bits 0); IMM: the step's first block.
+template <int IMM>
+__device__ __forceinline__ void lookup3(const uint8_t* smem, const uint32_t* w, uint32_t lb, bool odd, uint32_t sh,
+                                        u32x4 (&B)[4]) {
+  uint32_t R[8];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t o = dpp_swap_pairs(w[p]);
+    R[2 * p] = odd ? o : w[p];
+    R[2 * p + 1] = odd ? w[p] : o;
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a0 = (__builtin_amdgcn_ubfe(R[2 * i], sh + 3 * jt, 3) << 1) | lb;
+      const uint32_t a1 = (__builtin_amdgcn_ubfe(R[2 * i + 1], sh + 3 * jt, 3) << 1) | lb;
+      const uint16_t lo = lds_u16(smem, a0 + (IMM + 2 * i * 16));
+      const uint16_t hi = lds_u16(smem, a1 + (IMM + (2 * i + 1) * 16));
       B[jt][i] = __builtin_bit_cast(uint32_t, u16x2{lo, hi});
     }
 }
@@ -363,14 +411,17 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   MetaWords<MW> MT;  // metadata of the current tile
   uint32_t KW[16], VW[16];
   // the lane pair's word of a row: the codes of tokens (keys) / channels
-  // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2 bits
-  constexpr int WB = BITS;  // bytes of the word
+  // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2 bits; at 3
+  // bits the dword at byte min(3m, 20) (read unaligned; the last pair's moved
+  // back inside the row), this lane's codes from bit sh3
+  const int pbyte = BITS == 3 ? min(3 * (n >> 1), QB - 4) : BITS * (n >> 1);
+  const uint32_t sh3 = (uint32_t)(8 * (3 * (n >> 1) - pbyte) + 12 * (n & 1));
   auto load_word = [&](const __amdgpu_buffer_rsrc_t& r, int voff, int soff) __attribute__((always_inline)) {
-    if constexpr (WB == 4) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
     else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
   };
   // key words: KW[4kt + p] = this lane's word of channel row 32kt + 8g + 2p + (n & 1)
-  const int kvoff = (8 * g + (n & 1)) * QB + WB * (n >> 1);
+  const int kvoff = (8 * g + (n & 1)) * QB + pbyte;
   auto load_kw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * D * QB;
 #pragma unroll
@@ -379,7 +430,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
       for (int p = 0; p < 4; ++p) KW[4 * kt + p] = load_word(bf.kp, kvoff, soff + (32 * kt + 2 * p) * QB);
   };
   // value words: VW[4(2kt + vg) + p] = this lane's word of token row 32kt + 8g + 2p + (n & 1), group vg
-  const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + WB * (n >> 1);
+  const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + pbyte;
   auto load_vw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * TILE * NGH * QB;
 #pragma unroll
@@ -409,8 +460,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
   const uint32_t wbase = (uint32_t)(S::WAVE0 + wave * S::PER_WAVE);  // LDS byte address of W (smem is at 0)
   // this lane group's codebook bases: 4 bits, its block (byte 0 = 32g); 2 bits, its pair of each step
-  const uint32_t lbk = wbase + S::KCB + (F::PAIR ? CB_PAIR : CB_BLOCK) * g;
-  const uint32_t lbv = wbase + S::VCB + (F::PAIR ? CB_PAIR : CB_BLOCK) * g;
+  constexpr int LGSTRIDE = F::PAIR ? CB_PAIR : BITS == 3 ? CB_BLOCK3 : CB_BLOCK;
+  const uint32_t lbk = wbase + S::KCB + LGSTRIDE * g;
+  const uint32_t lbv = wbase + S::VCB + LGSTRIDE * g;
   const uint32_t gb = 0x20202020u * (uint32_t)g;
 
   // MFMA A rows: row n of this lane belongs to head hA = n / RS; for Q.K row
@@ -473,7 +525,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     constexpr bool values = decltype(values_tag)::value;
     constexpr int c = decltype(part)::value;
     constexpr int et = values ? S::ETV : S::ETK;
-    if constexpr (F::PAIR) {
+    if constexpr (BITS == 3) {
+      // group c of the two (keys: channels 2*lane + c; values: token lane, group c)
+      if constexpr (c < 2)
+        build_group8<IO>(smem, et, c == 0 ? g0 : g1,
+                         W + (values ? S::VCB + cb3_offset(TILE * c + lane) : S::KCB + cb3_offset(2 * lane + c)));
+    } else if constexpr (F::PAIR) {
       if constexpr (c == 0) {
         const uint2 x0 = values4<IO>(smem, et, g0), x1 = values4<IO>(smem, et, g1);
         if constexpr (values) {
@@ -539,21 +596,25 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         switch (kt) {
           case 0:
             if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
+            else if constexpr (BITS == 3) lookup3<0 * 4 * CB_BLOCK3>(smem, KW + 0, lbk, odd, sh3, B);
             else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q0{});
             break;
           case 1:
             if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
+            else if constexpr (BITS == 3) lookup3<1 * 4 * CB_BLOCK3>(smem, KW + 4, lbk, odd, sh3, B);
             else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q1{});
             break;
           case 2:
             if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
+            else if constexpr (BITS == 3) lookup3<2 * 4 * CB_BLOCK3>(smem, KW + 8, lbk, odd, sh3, B);
             else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q2{});
             break;
           default:
             if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
+            else if constexpr (BITS == 3) lookup3<3 * 4 * CB_BLOCK3>(smem, KW + 12, lbk, odd, sh3, B);
             else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q3{});
             break;
@@ -647,21 +708,29 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         switch (st) {
           case 0:
             if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
+            else if constexpr (BITS == 3)
+              lookup3<0 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 0, lbv, odd, sh3, B);
             else lookup4<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q0{});
             break;
           case 1:
             if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
+            else if constexpr (BITS == 3)
+              lookup3<1 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 4, lbv, odd, sh3, B);
             else lookup4<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q1{});
             break;
           case 2:
             if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
+            else if constexpr (BITS == 3)
+              lookup3<0 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 8, lbv, odd, sh3, B);
             else lookup4<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q2{});
             break;
           default:
             if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
+            else if constexpr (BITS == 3)
+              lookup3<1 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 12, lbv, odd, sh3, B);
             else lookup4<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q3{});
             break;
@@ -813,7 +882,7 @@ static bool cb_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
 bool cb_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   const int64_t qb = 8 * (int64_t)a->bits;
-  const bool bits_ok = a->bits == 4 || a->bits == 2;
+  const bool bits_ok = a->bits >= 2 && a->bits <= 4;
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * cb::TILE * 2 * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
@@ -856,8 +925,9 @@ int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
     hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 2, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus); \
   else                                                                                                            \
     hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 1, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus)
-#define MZ_CB(IOV, NR)                    \
-  if (a->bits == 4) { MZ_CB_B(IOV, NR, 4); } \
+#define MZ_CB(IOV, NR)                          \
+  if (a->bits == 4) { MZ_CB_B(IOV, NR, 4); }       \
+  else if (a->bits == 3) { MZ_CB_B(IOV, NR, 3); }  \
   else { MZ_CB_B(IOV, NR, 2); }
 #define MZ_CB_NREP(IOV)                \
   switch (nrep_pad) {                  \
