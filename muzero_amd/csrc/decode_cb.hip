@@ -1,4 +1,4 @@
-// Packed-KV decode attention over per-tile codebooks, 2- to 4-bit codes
+// Packed-KV decode attention over per-tile codebooks, 1- to 4-bit codes
 // (gfx950, wave64, MFMA 16x16x32 in the layer dtype).
 //
 // Every value this kernel attends with is the reference's dequantize-then-
@@ -49,6 +49,13 @@
 // the 16 bytes of padding per 4 pairs put the pairs that 8 consecutive lanes
 // write (i = 0..3, two lane groups) in 8 different 16-byte bank slots, so the
 // 128-bit codebook stores are free of conflicts too.
+// 1-bit codes: the four rows of two B registers (4h .. 4h + 3) share a quad
+// codebook of their 16 code combinations, each entry the four values as two
+// dwords: one 64-bit read per four codes, its address one v_dot4_u32_u8 of
+// the four code bits.  A quad's 128 bytes lie in a 256-byte slot, offset
+// within it so that the 8 lanes of one 128-bit store (4 quads, two halves
+// each) hit 8 different 16-byte bank slots; a 64-bit read serves one lane
+// group (one quad) per cycle, free of conflicts.
 // The (E+, E-) pairs the codebooks are formed from (E+ = E[pb][q-zl] above
 // the zero level, E- = E[nb][zl-q] below it, the other 0) are a 16 x 16
 // table per alpha in LDS, built at setup from the expm1 rows; a pair turns
@@ -75,6 +82,8 @@ constexpr float kLn2 = 0.693147180559945309f;
 // 4 bits: per group 16 entries of 2 bytes, 32 bytes of padding per 8 groups
 constexpr int CB_GROUP = 32;
 constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
+// 1 bit: per row quad 16 entries of 8 bytes, in a 256-byte slot
+constexpr int CB_QUAD = 256;
 // 3 bits: per group 8 entries of 2 bytes, 16 bytes of padding per 8 groups
 constexpr int CB_BLOCK3 = 8 * 16 + 16;
 // 2 bits: per row pair 16 entries of 4 bytes; the 4 lane groups' pairs of one
@@ -87,8 +96,9 @@ struct Fmt {
   static constexpr int QMAX = (1 << BITS) - 1;
   static constexpr int QB = 8 * BITS;       // bytes per packed 64-code row
   static constexpr bool PAIR = BITS == 2;   // joint codebooks of row pairs
+  static constexpr bool QUAD = BITS == 1;   // joint codebooks of row quads
   // codebook bytes per side and wave (128 groups; 2 bits: 64 row pairs), a multiple of 256
-  static constexpr int CB_BYTES = PAIR ? 16 * CB_PAIRS : BITS == 3 ? 16 * CB_BLOCK3 : 16 * CB_BLOCK;
+  static constexpr int CB_BYTES = QUAD ? 32 * CB_QUAD : PAIR ? 16 * CB_PAIRS : BITS == 3 ? 16 * CB_BLOCK3 : 16 * CB_BLOCK;
 };
 // (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
 // bytes so that lanes reading different zero levels at one code use
@@ -183,6 +193,55 @@ __device__ __forceinline__ uint2 values4(const uint8_t* smem, int et, const Grou
   for (int q = 0; q < 4; ++q) pn[q] = *(const float2*)(smem + et + gr.row + 8 * q);
   return uint2{pack_io2<IO>(code_value(gr, pn[0]), code_value(gr, pn[1])),
                pack_io2<IO>(code_value(gr, pn[2]), code_value(gr, pn[3]))};
+}
+
+// A group's 2 values (1-bit codes) in the io dtype, packed (x0, x1).
+template <int IO>
+__device__ __forceinline__ uint32_t values2(const uint8_t* smem, int et, const Group& gr) {
+  const float2 p0 = *(const float2*)(smem + et + gr.row), p1 = *(const float2*)(smem + et + gr.row + 8);
+  return pack_io2<IO>(code_value(gr, p0), code_value(gr, p1));
+}
+
+// Half B3 of a quad codebook (entries 8*B3 .. 8*B3 + 7, 64 bytes at `dst`)
+// from the four rows' packed values R[r] = (x_r(0), x_r(1)): entry e =
+// (x_0(b0), x_1(b1)), (x_2(b2), x_3(b3)) for the bits b of e.  `hsel` = the
+// selector half taking x_3(B3): 0x07060000 for B3 = 1, else 0x05040000.
+__device__ __forceinline__ void build_quad_half(const uint32_t (&R)[4], uint32_t hsel, uint8_t* dst) {
+  uint32_t d0[4], d1[2];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    d0[b] = __builtin_amdgcn_perm(R[1], R[0], (b & 1 ? 0x0302u : 0x0100u) | (b & 2 ? 0x07060000u : 0x05040000u));
+#pragma unroll
+  for (int b2 = 0; b2 < 2; ++b2) d1[b2] = __builtin_amdgcn_perm(R[3], R[2], (b2 ? 0x0302u : 0x0100u) | hsel);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    *(u32x4*)(dst + 16 * k) = u32x4{d0[2 * (k & 1)], d1[k >> 1], d0[2 * (k & 1) + 1], d1[k >> 1]};
+}
+
+// 1-bit codes: the B operands of one step from its 4 code words: w[p] = the
+// byte of the step's row 2p + (n & 1) holding the codes of the lane pair
+// (tokens / channels 8m .. 8m + 7, m = n / 2); this lane's codes from bit
+// sh1 = 4 (n & 1).  lb[h]: the lane group's base of its quad h codebook;
+// IMM[h]: the step's offset of quad h.
+template <int IMM0, int IMM1>
+__device__ __forceinline__ void lookup1(const uint8_t* smem, const uint32_t* w, const uint32_t (&lb)[2], bool odd,
+                                        uint32_t sh1, u32x4 (&B)[4]) {
+  const uint32_t sel = odd ? 0x02060004u : 0x06020400u;
+  uint32_t W[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t own = w[2 * h] | (w[2 * h + 1] << 16);
+    W[h] = __builtin_amdgcn_perm(dpp_swap_pairs(own), own, sel) >> sh1;  // byte r: codes of row 4h + r, bit jt
+  }
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t ad = __builtin_amdgcn_udot4(W[h] & (0x01010101u << jt), 0x40201008u >> jt, lb[h], false);
+      const uint2 v = *(const uint2*)(smem + ad + (h ? IMM1 : IMM0));
+      B[jt][2 * h] = v.x;
+      B[jt][2 * h + 1] = v.y;
+    }
 }
 
 // A group's 8 values (3-bit codes) in the io dtype, written as its codebook (16 bytes at `dst`).
@@ -411,14 +470,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   MetaWords<MW> MT;  // metadata of the current tile
   uint32_t KW[16], VW[16];
   // the lane pair's word of a row: the codes of tokens (keys) / channels
-  // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2 bits; at 3
+  // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2, 8 at 1; at 3
   // bits the dword at byte min(3m, 20) (read unaligned; the last pair's moved
   // back inside the row), this lane's codes from bit sh3
   const int pbyte = BITS == 3 ? min(3 * (n >> 1), QB - 4) : BITS * (n >> 1);
   const uint32_t sh3 = (uint32_t)(8 * (3 * (n >> 1) - pbyte) + 12 * (n & 1));
   auto load_word = [&](const __amdgpu_buffer_rsrc_t& r, int voff, int soff) __attribute__((always_inline)) {
     if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-    else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    else if constexpr (BITS == 2) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+    else return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
   };
   // key words: KW[4kt + p] = this lane's word of channel row 32kt + 8g + 2p + (n & 1)
   const int kvoff = (8 * g + (n & 1)) * QB + pbyte;
@@ -460,9 +520,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
   const uint32_t wbase = (uint32_t)(S::WAVE0 + wave * S::PER_WAVE);  // LDS byte address of W (smem is at 0)
   // this lane group's codebook bases: 4 bits, its block (byte 0 = 32g); 2 bits, its pair of each step
-  constexpr int LGSTRIDE = F::PAIR ? CB_PAIR : BITS == 3 ? CB_BLOCK3 : CB_BLOCK;
+  constexpr int LGSTRIDE = F::QUAD ? CB_QUAD : F::PAIR ? CB_PAIR : BITS == 3 ? CB_BLOCK3 : CB_BLOCK;
   const uint32_t lbk = wbase + S::KCB + LGSTRIDE * g;
   const uint32_t lbv = wbase + S::VCB + LGSTRIDE * g;
+  // 1 bit: quad (step, h, lane group g) at slot (4*(2*step + h) + g) * 256,
+  // offset 16 * ((h + 2 z) % 4) within it (z = g for keys, the value group
+  // for values): the lane bases of a step's quads h = 0, 1
+  const uint32_t lbk1[2] = {lbk + 16u * (uint32_t)((2 * g) & 3), lbk + 16u * (uint32_t)((1 + 2 * g) & 3)};
+  const uint32_t lbv1[2] = {lbv, lbv};
+  const uint32_t sh1 = 4u * (uint32_t)(n & 1);
   const uint32_t gb = 0x20202020u * (uint32_t)g;
 
   // MFMA A rows: row n of this lane belongs to head hA = n / RS; for Q.K row
@@ -506,6 +572,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   uint8_t* const vcb0 = W + S::VCB + (F::PAIR ? 0 : cb_offset(lane));
   uint8_t* const vcb1 = W + S::VCB + (F::PAIR ? 0 : cb_offset(TILE + lane));
   const int kpair = ((lane >> 4) * 4 + (lane & 3)) * CB_PAIRS + ((lane >> 2) & 3) * CB_PAIR;
+  // 1 bit: the key quad of this lane's channels (Q = lane / 2: step Q / 8, lane group Q / 2 % 4,
+  // h = Q % 2) and the value quad this lane builds (tokens of Q' = lane / 4, value group
+  // (lane >> 1) & 1), each at its half (lane & 1)
+  const int kq = lane >> 1, kqg = (kq >> 1) & 3, kqh = kq & 1;
+  const int kquad = ((2 * (kq >> 3) + kqh) * 4 + kqg) * CB_QUAD + 16 * ((kqh + 2 * kqg) & 3) + 64 * (lane & 1);
+  const int vq = lane >> 2, vqg = (vq >> 1) & 3, vqh = vq & 1, vqv = (lane >> 1) & 1;
+  const int vquad = ((2 * (2 * (vq >> 3) + vqv) + vqh) * 4 + vqg) * CB_QUAD + 16 * ((vqh + 2 * vqv) & 3) + 64 * (lane & 1);
   const int vm = lane >> 1;
   const int vpair = (((vm >> 4) * 2 + (lane & 1)) * 4 + (vm & 3)) * CB_PAIRS + ((vm >> 2) & 3) * CB_PAIR;
   auto key_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
@@ -525,7 +598,34 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     constexpr bool values = decltype(values_tag)::value;
     constexpr int c = decltype(part)::value;
     constexpr int et = values ? S::ETV : S::ETK;
-    if constexpr (BITS == 3) {
+    if constexpr (F::QUAD) {
+      if constexpr (c == 0) {
+        const uint32_t x0 = values2<IO>(smem, et, g0), x1 = values2<IO>(smem, et, g1);
+        // this lane builds half b3 = lane & 1 of one quad
+        const uint32_t hsel = (lane & 1) ? 0x07060000u : 0x05040000u;
+        uint32_t R[4];
+        if constexpr (values) {
+          // the quad of tokens 4Q'..4Q'+3 (lanes 4Q'+r) and value group (lane >> 1) & 1: every
+          // lane of the lane quad reads both groups' values of the four, then keeps its group's
+          const bool vg1 = (lane & 2) != 0;
+          const uint32_t a0 = dpp_sel_u<0x00>(x0), a1 = dpp_sel_u<0x55>(x0), a2 = dpp_sel_u<0xAA>(x0), a3 = dpp_sel_u<0xFF>(x0);
+          const uint32_t b0 = dpp_sel_u<0x00>(x1), b1 = dpp_sel_u<0x55>(x1), b2 = dpp_sel_u<0xAA>(x1), b3 = dpp_sel_u<0xFF>(x1);
+          R[0] = vg1 ? b0 : a0;
+          R[1] = vg1 ? b1 : a1;
+          R[2] = vg1 ? b2 : a2;
+          R[3] = vg1 ? b3 : a3;
+          build_quad_half(R, hsel, W + S::VCB + vquad);
+        } else {
+          // the quad of channels 4Q..4Q+3 (lanes 2Q, 2Q+1: two channels each)
+          const uint32_t o0 = dpp_swap_pairs(x0), o1 = dpp_swap_pairs(x1);
+          R[0] = odd ? o0 : x0;
+          R[1] = odd ? o1 : x1;
+          R[2] = odd ? x0 : o0;
+          R[3] = odd ? x1 : o1;
+          build_quad_half(R, hsel, W + S::KCB + kquad);
+        }
+      }
+    } else if constexpr (BITS == 3) {
       // group c of the two (keys: channels 2*lane + c; values: token lane, group c)
       if constexpr (c < 2)
         build_group8<IO>(smem, et, c == 0 ? g0 : g1,
@@ -595,25 +695,29 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (kt) {
           case 0:
-            if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
+            if constexpr (F::QUAD) lookup1<(2 * 0) * 4 * CB_QUAD, (2 * 0 + 1) * 4 * CB_QUAD>(smem, KW + 0, lbk1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<0 * 4 * CB_BLOCK3>(smem, KW + 0, lbk, odd, sh3, B);
             else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q0{});
             break;
           case 1:
-            if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
+            if constexpr (F::QUAD) lookup1<(2 * 1) * 4 * CB_QUAD, (2 * 1 + 1) * 4 * CB_QUAD>(smem, KW + 4, lbk1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<1 * 4 * CB_BLOCK3>(smem, KW + 4, lbk, odd, sh3, B);
             else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q1{});
             break;
           case 2:
-            if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
+            if constexpr (F::QUAD) lookup1<(2 * 2) * 4 * CB_QUAD, (2 * 2 + 1) * 4 * CB_QUAD>(smem, KW + 8, lbk1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<2 * 4 * CB_BLOCK3>(smem, KW + 8, lbk, odd, sh3, B);
             else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q2{});
             break;
           default:
-            if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
+            if constexpr (F::QUAD) lookup1<(2 * 3) * 4 * CB_QUAD, (2 * 3 + 1) * 4 * CB_QUAD>(smem, KW + 12, lbk1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<3 * 4 * CB_BLOCK3>(smem, KW + 12, lbk, odd, sh3, B);
             else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q3{});
@@ -707,28 +811,40 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (st) {
           case 0:
-            if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
+            if constexpr (F::QUAD)
+              lookup1<(2 * 0) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 0 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
+                  smem, VW + 0, lbv1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
             else if constexpr (BITS == 3)
               lookup3<0 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 0, lbv, odd, sh3, B);
             else lookup4<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q0{});
             break;
           case 1:
-            if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
+            if constexpr (F::QUAD)
+              lookup1<(2 * 1) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 1 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
+                  smem, VW + 4, lbv1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
             else if constexpr (BITS == 3)
               lookup3<1 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 4, lbv, odd, sh3, B);
             else lookup4<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q1{});
             break;
           case 2:
-            if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
+            if constexpr (F::QUAD)
+              lookup1<(2 * 2) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 2 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
+                  smem, VW + 8, lbv1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
             else if constexpr (BITS == 3)
               lookup3<0 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 8, lbv, odd, sh3, B);
             else lookup4<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
             build_part(KEYS{}, gk0, gk1, Q2{});
             break;
           default:
-            if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
+            if constexpr (F::QUAD)
+              lookup1<(2 * 3) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 3 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
+                  smem, VW + 12, lbv1, odd, sh1, B);
+            else if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
             else if constexpr (BITS == 3)
               lookup3<1 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 12, lbv, odd, sh3, B);
             else lookup4<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
@@ -882,7 +998,7 @@ static bool cb_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
 bool cb_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   const int64_t qb = 8 * (int64_t)a->bits;
-  const bool bits_ok = a->bits >= 2 && a->bits <= 4;
+  const bool bits_ok = a->bits >= 1 && a->bits <= 4;
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * cb::TILE * 2 * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
@@ -928,7 +1044,8 @@ int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
 #define MZ_CB(IOV, NR)                          \
   if (a->bits == 4) { MZ_CB_B(IOV, NR, 4); }       \
   else if (a->bits == 3) { MZ_CB_B(IOV, NR, 3); }  \
-  else { MZ_CB_B(IOV, NR, 2); }
+  else if (a->bits == 2) { MZ_CB_B(IOV, NR, 2); }  \
+  else { MZ_CB_B(IOV, NR, 1); }
 #define MZ_CB_NREP(IOV)                \
   switch (nrep_pad) {                  \
     case 1: MZ_CB(IOV, 1); break;      \

@@ -49,7 +49,7 @@ def bits_of(t) -> np.ndarray:
 
 
 # Bit widths the codebook decode kernel takes (head_dim 128, n_rep 1..8, a quantized prefix).
-CODEBOOK_BITS = (2, 3, 4)
+CODEBOOK_BITS = (1, 2, 3, 4)
 
 
 def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):

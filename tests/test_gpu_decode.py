@@ -555,7 +555,7 @@ CB_SHAPES = [
     (1, 2, 4, 128, 900, 191),    # residual spans two tiles, partial
     (3, 2, 2, 128, 330, 10),     # short partial residual tile
 ]
-CB_BITS = [4, 2, 3]
+CB_BITS = [4, 2, 3, 1]
 
 
 @pytest.mark.parametrize("bits", CB_BITS)
