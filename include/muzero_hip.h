@@ -222,8 +222,8 @@ typedef struct mz_decode_args {
 /* Kernel paths of muzero_decode_attention.  Three kernels:
  *  - codebook: attends with the reference's dequantize-then-attend values
  *    (every dequantized value rounded to the layer dtype, bit for bit);
- *    4-bit codes, head_dim 128, aligned prefixes, n_rep 1 to 8 (other counts
- *    than 1, 2, 4, 8 run the kernel built for the next larger one);
+ *    1- to 4-bit codes, head_dim 128, aligned prefixes, n_rep 1 to 8 (other
+ *    counts than 1, 2, 4, 8 run the kernel built for the next larger one);
  *  - fold: the reference's fused-kernel values (fp32 dequantized values,
  *    up to the fp16 rounding of its shifted (P, N) table entries); bits 1 to
  *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
