@@ -528,9 +528,10 @@ def main():
                     help="decode mode: dtype of the query and the K/V the cache is quantized from (the residual's)")
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--n-split", type=int, default=0, help="splits per (batch, kv-head); 0 = the library's choice")
-    ap.add_argument("--kernel-path", choices=("auto", "exact", "fold", "codebook"), default="auto",
-                    help="decode mode: the library's kernel choice (auto), or force the exact-dequantize kernel "
-                         "(the reference's dequantize-then-attend values), the fold kernel or the codebook kernel")
+    ap.add_argument("--kernel-path", choices=("auto", "exact", "fold", "codebook", "general"), default="auto",
+                    help="decode mode: the library's kernel choice (auto), the reference's dequantize-then-attend "
+                         "values on the fastest kernel that gives them (exact), or force the fold, codebook or "
+                         "general kernel")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-sample-batch", type=int, default=1)
     ap.add_argument("--traffic-json", default=os.path.join(ROOT, "profiles", "traffic.json"))

@@ -223,15 +223,17 @@ typedef struct mz_decode_args {
  *  - codebook: attends with the reference's dequantize-then-attend values
  *    (every dequantized value rounded to the layer dtype, bit for bit);
  *    1- to 4-bit codes, head_dim 128, aligned prefixes, n_rep 1 to 8 (other
- *    counts than 1, 2, 4, 8 run the kernel built for the next larger one);
+ *    counts than 1, 2, 4, 8 run the kernel built for the next larger one),
+ *    and 5-bit codes with one expm1 table for keys and values (e_key ==
+ *    e_value) and n_rep 1 to 4;
  *  - fold: the reference's fused-kernel values (fp32 dequantized values,
  *    up to the fp16 rounding of its shifted (P, N) table entries); bits 1 to
  *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
  *    given, at 7 bits one table for keys and values;
  *  - general: the dequantize-then-attend values, every width and layout.
- * AUTO runs the codebook kernel where it applies, else the fold kernel, else
- * the general one; EXACT the codebook kernel where it applies, else the
- * general one; FOLD, CODEBOOK and GENERAL force that kernel (a forced fold or
+ * AUTO runs the codebook kernel at 1 to 4 bits where it applies, else the
+ * fold kernel, else the codebook kernel (5 bits), else the general one;
+ * EXACT the codebook kernel where it applies, else the general one; FOLD, CODEBOOK and GENERAL force that kernel (a forced fold or
  * codebook kernel that does not take the arguments is MZ_EUNSUPPORTED). */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3, MZ_PATH_GENERAL = 4 };
 

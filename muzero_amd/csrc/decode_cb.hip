@@ -1,4 +1,4 @@
-// Packed-KV decode attention over per-tile codebooks, 1- to 4-bit codes
+// Packed-KV decode attention over per-tile codebooks, 1- to 5-bit codes
 // (gfx950, wave64, MFMA 16x16x32 in the layer dtype).
 //
 // Every value this kernel attends with is the reference's dequantize-then-
@@ -39,6 +39,14 @@
 // different 16-byte bank slots and 8 consecutive lanes' codebook stores (16
 // bytes each) in 8.  The address is a bit-field extract of the code and one
 // shift-or onto the lane group's base per code (3-bit codes straddle bytes).
+// 5-bit codes: group r's 32 entries (64 bytes) at byte 512*(r/8) +
+// 64*((r%8) ^ (r/8 % 2)): the groups of lane groups g and g ^ 1 in one lookup
+// lie in opposite bank halves (two lane bases per lane, for even and odd
+// rows), and each lane stores its 16-byte codebook chunks in a rotated order
+// so that 8 lanes' stores hit 8 bank slots.  Each lane reads its own dword
+// of every row (4 codes of 5 bits); the address is a bit-field extract and a
+// shift-or per code.  The (E+, E-) table is 32 x 32 pairs; one table serves
+// keys and values (5-bit calls with two alphas run the fold kernel).
 // 2-bit codes: the two rows of a B register (channels or tokens 2i, 2i+1)
 // share a joint codebook of their 4 x 4 code pairs, each entry the two
 // values as one dword: one 32-bit read per code pair fills a B register,
@@ -84,6 +92,8 @@ constexpr int CB_GROUP = 32;
 constexpr int CB_BLOCK = 8 * CB_GROUP + 32;
 // 1 bit: per row quad 16 entries of 8 bytes, in a 256-byte slot
 constexpr int CB_QUAD = 256;
+// 5 bits: per group 32 entries of 2 bytes, 8 groups per 512-byte block
+constexpr int CB_BLOCK5 = 8 * 64;
 // 3 bits: per group 8 entries of 2 bytes, 16 bytes of padding per 8 groups
 constexpr int CB_BLOCK3 = 8 * 16 + 16;
 // 2 bits: per row pair 16 entries of 4 bytes; the 4 lane groups' pairs of one
@@ -97,23 +107,28 @@ struct Fmt {
   static constexpr int QB = 8 * BITS;       // bytes per packed 64-code row
   static constexpr bool PAIR = BITS == 2;   // joint codebooks of row pairs
   static constexpr bool QUAD = BITS == 1;   // joint codebooks of row quads
+  static constexpr bool WIDE = BITS == 5;   // one dword per lane and row
+  // (E+, E-) table: rows of zero levels, 8 bytes per code, 8 bytes of padding;
+  // 5 bits: one table for keys and values
+  static constexpr int ET_ROW = (QMAX + 1 > 16 ? QMAX + 1 : 16) * 8 + 8;
+  static constexpr int ET_BYTES = (QMAX + 1 > 16 ? QMAX + 1 : 16) * ET_ROW;
+  static constexpr int ET_TABLES = WIDE ? 1 : 2;
+  static constexpr int CODE_WORDS = WIDE ? 32 : 16;  // code words per lane and tile, each of keys and values
   // codebook bytes per side and wave (128 groups; 2 bits: 64 row pairs), a multiple of 256
-  static constexpr int CB_BYTES = QUAD ? 32 * CB_QUAD : PAIR ? 16 * CB_PAIRS : BITS == 3 ? 16 * CB_BLOCK3 : 16 * CB_BLOCK;
+  static constexpr int CB_BYTES =
+      WIDE ? 16 * CB_BLOCK5 : QUAD ? 32 * CB_QUAD : PAIR ? 16 * CB_PAIRS : BITS == 3 ? 16 * CB_BLOCK3 : 16 * CB_BLOCK;
 };
-// (E+, E-) table: 16 zero levels x 16 codes x 8 bytes, rows padded by 8
-// bytes so that lanes reading different zero levels at one code use
-// different banks
-constexpr int ET_ROW = 16 * 8 + 8;
-constexpr int ET_BYTES = 16 * ET_ROW;
 constexpr int QROW = D * 2 + 16;       // bytes per head row of the query copy
 constexpr int PROW = TILE * 2 + 16;    // bytes per head row of the weight staging
 
 template <int NREP, int BITS>
 struct Smem {
   static constexpr int CB_BYTES = Fmt<BITS>::CB_BYTES;
+  // (E+, E-) tables: rows padded by 8 bytes so that lanes reading different
+  // zero levels at one code use different banks
   static constexpr int ETK = 0;
-  static constexpr int ETV = ET_BYTES;
-  static constexpr int QIO = 2 * ET_BYTES;            // query, io dtype [NREP][QROW]
+  static constexpr int ETV = Fmt<BITS>::ET_TABLES == 2 ? Fmt<BITS>::ET_BYTES : 0;
+  static constexpr int QIO = Fmt<BITS>::ET_TABLES * Fmt<BITS>::ET_BYTES;  // query, io dtype [NREP][QROW]
   static constexpr int ZERO = QIO + NREP * QROW;      // 256 zero bytes: A rows that must be 0
   static constexpr int WAVE0 = (ZERO + 256 + 255) / 256 * 256;
   // per wave (256-aligned: a lane group's codebook base has byte 0 = 32g)
@@ -158,7 +173,7 @@ struct Group {
   uint32_t row;              // byte offset of the zero level's (E+, E-) row
 };
 
-template <int QMAX>
+template <int QMAX, int ET_ROW>
 __device__ __forceinline__ Group group_of(float mn, float s) {
   const float eps = 1e-8f;
   Group r;
@@ -241,6 +256,43 @@ __device__ __forceinline__ void lookup1(const uint8_t* smem, const uint32_t* w, 
       const uint2 v = *(const uint2*)(smem + ad + (h ? IMM1 : IMM0));
       B[jt][2 * h] = v.x;
       B[jt][2 * h + 1] = v.y;
+    }
+}
+
+// Values 8c .. 8c + 7 of a 5-bit group's codebook, written to its 16 bytes at
+// `cbg` + 16c (cbg: the group's 64 bytes).
+template <int IO>
+__device__ __forceinline__ void build_chunk5(const uint8_t* smem, int et, const Group& gr, uint8_t* cbg, int c) {
+  float2 pn[8];
+  const uint8_t* src = smem + et + gr.row + 64 * c;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pn[e] = *(const float2*)(src + 8 * e);
+  uint32_t w[4];
+#pragma unroll
+  for (int q2 = 0; q2 < 4; ++q2) w[q2] = pack_io2<IO>(code_value(gr, pn[2 * q2]), code_value(gr, pn[2 * q2 + 1]));
+  *(u32x4*)(cbg + 16 * c) = u32x4{w[0], w[1], w[2], w[3]};
+}
+
+__device__ __forceinline__ uint32_t cb5_offset(int r) {
+  return (uint32_t)((r >> 3) * CB_BLOCK5 + 64 * ((r & 7) ^ ((r >> 3) & 1)));
+}
+
+// 5-bit codes: the B operands of one step from its 8 code words: w[j] = this
+// lane's dword of the step's row j, its code jt at bit sh + 5jt.  lb[j % 2]:
+// the lane group's base for even / odd rows (bits 0-5 zero); IMM: the step's
+// first block.
+template <int IMM>
+__device__ __forceinline__ void lookup5(const uint8_t* smem, const uint32_t* w, const uint32_t (&lb)[2], uint32_t sh,
+                                        u32x4 (&B)[4]) {
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a0 = (__builtin_amdgcn_ubfe(w[2 * i], sh + 5 * jt, 5) << 1) | lb[0];
+      const uint32_t a1 = (__builtin_amdgcn_ubfe(w[2 * i + 1], sh + 5 * jt, 5) << 1) | lb[1];
+      const uint16_t lo = lds_u16(smem, a0 + (IMM + 2 * i * 64));
+      const uint16_t hi = lds_u16(smem, a1 + (IMM + (2 * i + 1) * 64));
+      B[jt][i] = __builtin_bit_cast(uint32_t, u16x2{lo, hi});
     }
 }
 
@@ -441,14 +493,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int v0 = wave;
 
   // ---------------- workgroup setup: (E+, E-) tables and the query in LDS
-  constexpr int EW = (2 * 256 + NT - 1) / NT;  // table entries per thread
+  constexpr int EZ = F::ET_BYTES / F::ET_ROW;   // zero-level rows per table (16, or 32 at 5 bits)
+  constexpr int EN = F::ET_TABLES * EZ * EZ;    // table entries
+  constexpr int EW = (EN + NT - 1) / NT;        // table entries per thread
   constexpr int QW = (NREP * D + NT - 1) / NT;  // query elements per thread
   float2 et[EW];
   uint16_t qraw[QW];
 #pragma unroll
   for (int j = 0; j < EW; ++j) {
-    const int i = threadIdx.x + j * NT;
-    const int t = i >> 8, zl = (i >> 4) & 15, q = i & 15;
+    const int i = min(threadIdx.x + j * NT, EN - 1);
+    const int t = i / (EZ * EZ), zl = (i / EZ) % EZ, q = i % EZ;
     const float* E = t ? a.e_value : a.e_key;
     float ep = 0.f, en = 0.f;
     if (zl > QMAX || q > QMAX) {
@@ -468,12 +522,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     qraw[j] = h < a.n_rep ? ((const uint16_t*)a.query)[b * a.q_sb + (int64_t)(kvh * a.n_rep + h) * a.q_sh + c] : 0;
   }
   MetaWords<MW> MT;  // metadata of the current tile
-  uint32_t KW[16], VW[16];
+  uint32_t KW[F::CODE_WORDS], VW[F::CODE_WORDS];
   // the lane pair's word of a row: the codes of tokens (keys) / channels
   // (values) 8m .. 8m + 7, m = n / 2: 32 bits at 4 bits, 16 at 2, 8 at 1; at 3
   // bits the dword at byte min(3m, 20) (read unaligned; the last pair's moved
   // back inside the row), this lane's codes from bit sh3
   const int pbyte = BITS == 3 ? min(3 * (n >> 1), QB - 4) : BITS * (n >> 1);
+  // 5 bits: this lane's own dword of each row (its 4 codes at bit 20n; the
+  // last lane's dword moved back inside the 40-byte row)
+  const int wbyte = min((20 * n) >> 3, QB - 4);
+  const uint32_t sh5 = (uint32_t)(20 * n - 8 * wbyte);
   const uint32_t sh3 = (uint32_t)(8 * (3 * (n >> 1) - pbyte) + 12 * (n & 1));
   auto load_word = [&](const __amdgpu_buffer_rsrc_t& r, int voff, int soff) __attribute__((always_inline)) {
     if constexpr (BITS >= 3) return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
@@ -484,6 +542,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int kvoff = (8 * g + (n & 1)) * QB + pbyte;
   auto load_kw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * D * QB;
+    if constexpr (F::WIDE) {
+      // KW[8kt + j] = this lane's dword of channel row 32kt + 8g + j
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          KW[8 * kt + j] = __builtin_amdgcn_raw_buffer_load_b32(bf.kp, 8 * g * QB + wbyte, soff + (32 * kt + j) * QB, 0);
+      return;
+    }
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -493,6 +560,18 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int vvoff = (8 * g + (n & 1)) * (NGH * QB) + pbyte;
   auto load_vw = [&](int tile) __attribute__((always_inline)) {
     const int soff = tile * TILE * NGH * QB;
+    if constexpr (F::WIDE) {
+      // VW[8(2kt + vg) + j] = this lane's dword of token row 32kt + 8g + j, group vg
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int vg = 0; vg < NGH; ++vg)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            VW[8 * (2 * kt + vg) + j] = __builtin_amdgcn_raw_buffer_load_b32(
+                bf.vp, 8 * g * (NGH * QB) + wbyte, soff + (32 * kt + j) * (NGH * QB) + QB * vg, 0);
+      return;
+    }
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -506,8 +585,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
   for (int j = 0; j < EW; ++j) {
     const int i = threadIdx.x + j * NT;
-    const int t = i >> 8, zl = (i >> 4) & 15, q = i & 15;
-    *(float2*)(smem + (t ? S::ETV : S::ETK) + zl * ET_ROW + 8 * q) = et[j];
+    const int t = i / (EZ * EZ), zl = (i / EZ) % EZ, q = i % EZ;
+    if (i < EN) *(float2*)(smem + (t ? S::ETV : S::ETK) + zl * F::ET_ROW + 8 * q) = et[j];
   }
   for (int i = threadIdx.x; i < 64; i += NT) ((uint32_t*)(smem + S::ZERO))[i] = 0u;
 #pragma unroll
@@ -520,7 +599,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   uint8_t* W = smem + S::WAVE0 + wave * S::PER_WAVE;
   const uint32_t wbase = (uint32_t)(S::WAVE0 + wave * S::PER_WAVE);  // LDS byte address of W (smem is at 0)
   // this lane group's codebook bases: 4 bits, its block (byte 0 = 32g); 2 bits, its pair of each step
-  constexpr int LGSTRIDE = F::QUAD ? CB_QUAD : F::PAIR ? CB_PAIR : BITS == 3 ? CB_BLOCK3 : CB_BLOCK;
+  constexpr int LGSTRIDE = F::WIDE ? CB_BLOCK5 : F::QUAD ? CB_QUAD : F::PAIR ? CB_PAIR : BITS == 3 ? CB_BLOCK3 : CB_BLOCK;
   const uint32_t lbk = wbase + S::KCB + LGSTRIDE * g;
   const uint32_t lbv = wbase + S::VCB + LGSTRIDE * g;
   // 1 bit: quad (step, h, lane group g) at slot (4*(2*step + h) + g) * 256,
@@ -529,6 +608,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const uint32_t lbk1[2] = {lbk + 16u * (uint32_t)((2 * g) & 3), lbk + 16u * (uint32_t)((1 + 2 * g) & 3)};
   const uint32_t lbv1[2] = {lbv, lbv};
   const uint32_t sh1 = 4u * (uint32_t)(n & 1);
+  // 5 bits: the lane group's bases of even and odd rows (group j of its block at 64 * (j ^ (g & 1)))
+  const uint32_t lbk5[2] = {lbk + 64u * (uint32_t)(g & 1), lbk - 64u * (uint32_t)(g & 1)};
+  const uint32_t lbv5[2] = {lbv + 64u * (uint32_t)(g & 1), lbv - 64u * (uint32_t)(g & 1)};
   const uint32_t gb = 0x20202020u * (uint32_t)g;
 
   // MFMA A rows: row n of this lane belongs to head hA = n / RS; for Q.K row
@@ -583,13 +665,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   const int vpair = (((vm >> 4) * 2 + (lane & 1)) * 4 + (vm & 3)) * CB_PAIRS + ((vm >> 2) & 3) * CB_PAIR;
   auto key_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
     const float2 mn = meta_cvt<MW>(Mw.kmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.ksc, a.meta_dtype);
-    g0 = group_of<QMAX>(mn.x, sc.x);
-    g1 = group_of<QMAX>(mn.y, sc.y);
+    g0 = group_of<QMAX, F::ET_ROW>(mn.x, sc.x);
+    g1 = group_of<QMAX, F::ET_ROW>(mn.y, sc.y);
   };
   auto value_groups = [&](const MetaWords<MW>& Mw, Group& g0, Group& g1) __attribute__((always_inline)) {
     const float2 mn = meta_cvt<MW>(Mw.vmn, a.meta_dtype), sc = meta_cvt<MW>(Mw.vsc, a.meta_dtype);
-    g0 = group_of<QMAX>(mn.x, sc.x);
-    g1 = group_of<QMAX>(mn.y, sc.y);
+    g0 = group_of<QMAX, F::ET_ROW>(mn.x, sc.x);
+    g1 = group_of<QMAX, F::ET_ROW>(mn.y, sc.y);
   };
   // 4 bits: the half a lane builds in parts 0 and 2 (see above)
   const int krot = (lane >> 1) & 1, vrot = (lane >> 2) & 1;
@@ -598,7 +680,14 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     constexpr bool values = decltype(values_tag)::value;
     constexpr int c = decltype(part)::value;
     constexpr int et = values ? S::ETV : S::ETK;
-    if constexpr (F::QUAD) {
+    if constexpr (F::WIDE) {
+      // part c: group c / 2 of the two, its chunks 2(c % 2) and 2(c % 2) + 1 in the lane's
+      // rotated order (keys: channels 2*lane + c/2; values: token lane, group c/2)
+      const int rot = values ? (lane >> 1) & 3 : lane & 3;
+      uint8_t* cbg = W + (values ? S::VCB + cb5_offset(TILE * (c >> 1) + lane) : S::KCB + cb5_offset(2 * lane + (c >> 1)));
+      build_chunk5<IO>(smem, et, c < 2 ? g0 : g1, cbg, (2 * (c & 1) + rot) & 3);
+      build_chunk5<IO>(smem, et, c < 2 ? g0 : g1, cbg, (2 * (c & 1) + 1 + rot) & 3);
+    } else if constexpr (F::QUAD) {
       if constexpr (c == 0) {
         const uint32_t x0 = values2<IO>(smem, et, g0), x1 = values2<IO>(smem, et, g1);
         // this lane builds half b3 = lane & 1 of one quad
@@ -695,28 +784,32 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (kt) {
           case 0:
-            if constexpr (F::QUAD) lookup1<(2 * 0) * 4 * CB_QUAD, (2 * 0 + 1) * 4 * CB_QUAD>(smem, KW + 0, lbk1, odd, sh1, B);
+            if constexpr (F::WIDE) lookup5<0 * 4 * CB_BLOCK5>(smem, KW + 0, lbk5, sh5, B);
+            else if constexpr (F::QUAD) lookup1<(2 * 0) * 4 * CB_QUAD, (2 * 0 + 1) * 4 * CB_QUAD>(smem, KW + 0, lbk1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<0 * 4 * CB_BLOCK3>(smem, KW + 0, lbk, odd, sh3, B);
             else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q0{});
             break;
           case 1:
-            if constexpr (F::QUAD) lookup1<(2 * 1) * 4 * CB_QUAD, (2 * 1 + 1) * 4 * CB_QUAD>(smem, KW + 4, lbk1, odd, sh1, B);
+            if constexpr (F::WIDE) lookup5<1 * 4 * CB_BLOCK5>(smem, KW + 8, lbk5, sh5, B);
+            else if constexpr (F::QUAD) lookup1<(2 * 1) * 4 * CB_QUAD, (2 * 1 + 1) * 4 * CB_QUAD>(smem, KW + 4, lbk1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<1 * 4 * CB_BLOCK3>(smem, KW + 4, lbk, odd, sh3, B);
             else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q1{});
             break;
           case 2:
-            if constexpr (F::QUAD) lookup1<(2 * 2) * 4 * CB_QUAD, (2 * 2 + 1) * 4 * CB_QUAD>(smem, KW + 8, lbk1, odd, sh1, B);
+            if constexpr (F::WIDE) lookup5<2 * 4 * CB_BLOCK5>(smem, KW + 16, lbk5, sh5, B);
+            else if constexpr (F::QUAD) lookup1<(2 * 2) * 4 * CB_QUAD, (2 * 2 + 1) * 4 * CB_QUAD>(smem, KW + 8, lbk1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<2 * 4 * CB_BLOCK3>(smem, KW + 8, lbk, odd, sh3, B);
             else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
             build_part(VALUES{}, gv0, gv1, Q2{});
             break;
           default:
-            if constexpr (F::QUAD) lookup1<(2 * 3) * 4 * CB_QUAD, (2 * 3 + 1) * 4 * CB_QUAD>(smem, KW + 12, lbk1, odd, sh1, B);
+            if constexpr (F::WIDE) lookup5<3 * 4 * CB_BLOCK5>(smem, KW + 24, lbk5, sh5, B);
+            else if constexpr (F::QUAD) lookup1<(2 * 3) * 4 * CB_QUAD, (2 * 3 + 1) * 4 * CB_QUAD>(smem, KW + 12, lbk1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
             else if constexpr (BITS == 3) lookup3<3 * 4 * CB_BLOCK3>(smem, KW + 12, lbk, odd, sh3, B);
             else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
@@ -811,7 +904,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         u32x4 B[4];
         switch (st) {
           case 0:
-            if constexpr (F::QUAD)
+            if constexpr (F::WIDE)
+              lookup5<0 * 8 * CB_BLOCK5 + 0 * 4 * CB_BLOCK5>(smem, VW + 0, lbv5, sh5, B);
+            else if constexpr (F::QUAD)
               lookup1<(2 * 0) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 0 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
                   smem, VW + 0, lbv1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
@@ -821,7 +916,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
             build_part(KEYS{}, gk0, gk1, Q0{});
             break;
           case 1:
-            if constexpr (F::QUAD)
+            if constexpr (F::WIDE)
+              lookup5<1 * 8 * CB_BLOCK5 + 0 * 4 * CB_BLOCK5>(smem, VW + 8, lbv5, sh5, B);
+            else if constexpr (F::QUAD)
               lookup1<(2 * 1) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 1 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
                   smem, VW + 4, lbv1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
@@ -831,7 +928,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
             build_part(KEYS{}, gk0, gk1, Q1{});
             break;
           case 2:
-            if constexpr (F::QUAD)
+            if constexpr (F::WIDE)
+              lookup5<0 * 8 * CB_BLOCK5 + 1 * 4 * CB_BLOCK5>(smem, VW + 16, lbv5, sh5, B);
+            else if constexpr (F::QUAD)
               lookup1<(2 * 2) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 2 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
                   smem, VW + 8, lbv1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
@@ -841,7 +940,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
             build_part(KEYS{}, gk0, gk1, Q2{});
             break;
           default:
-            if constexpr (F::QUAD)
+            if constexpr (F::WIDE)
+              lookup5<1 * 8 * CB_BLOCK5 + 1 * 4 * CB_BLOCK5>(smem, VW + 24, lbv5, sh5, B);
+            else if constexpr (F::QUAD)
               lookup1<(2 * 3) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 3 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
                   smem, VW + 12, lbv1, odd, sh1, B);
             else if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
@@ -998,7 +1099,8 @@ static bool cb_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
 bool cb_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   const int64_t qb = 8 * (int64_t)a->bits;
-  const bool bits_ok = a->bits >= 1 && a->bits <= 4;
+  // 5 bits: one (E+, E-) table for keys and values, up to 4 query heads (LDS)
+  const bool bits_ok = (a->bits >= 1 && a->bits <= 4) || (a->bits == 5 && a->e_key == a->e_value && a->n_rep <= 4);
   // buffer-resource ranges are 32-bit
   const bool fits = (int64_t)a->n_groups * cb::TILE * 2 * qb < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * a->head_dim * es < ((int64_t)1 << 31);
@@ -1028,36 +1130,54 @@ int cb_choose_split(const mz_decode_args* a, int* tiles_per_split) {
   return (n_tiles + tps - 1) / tps;
 }
 
+// One width's kernel (meta dtype picked at run time).
+template <int IO, int NR, int BB>
+static void cb_launch_one(const mz_decode_args* a, hipStream_t s, dim3 grid, int tps, int ns, int dir, int cus) {
+  if (a->meta_dtype == MZ_F32)
+    hipLaunchKernelGGL((cb::cb_kernel<IO, NR, 2, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus);
+  else
+    hipLaunchKernelGGL((cb::cb_kernel<IO, NR, 1, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus);
+}
+
+template <int IO, int NR>
+static int cb_launch_nr(const mz_decode_args* a, hipStream_t s, dim3 grid, int tps, int ns, int dir, int cus) {
+  switch (a->bits) {
+    case 1: cb_launch_one<IO, NR, 1>(a, s, grid, tps, ns, dir, cus); break;
+    case 2: cb_launch_one<IO, NR, 2>(a, s, grid, tps, ns, dir, cus); break;
+    case 3: cb_launch_one<IO, NR, 3>(a, s, grid, tps, ns, dir, cus); break;
+    case 4: cb_launch_one<IO, NR, 4>(a, s, grid, tps, ns, dir, cus); break;
+    case 5:
+      // the 5-bit workgroup's LDS holds up to 4 query heads' staging
+      if constexpr (NR <= 4) {
+        cb_launch_one<IO, NR, 5>(a, s, grid, tps, ns, dir, cus);
+        break;
+      } else {
+        return MZ_EUNSUPPORTED;
+      }
+    default: return MZ_EUNSUPPORTED;
+  }
+  return MZ_OK;
+}
+
+template <int IO>
+static int cb_launch_io(const mz_decode_args* a, hipStream_t s, dim3 grid, int tps, int ns, int dir, int cus) {
+  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
+  switch (a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0) {
+    case 1: return cb_launch_nr<IO, 1>(a, s, grid, tps, ns, dir, cus);
+    case 2: return cb_launch_nr<IO, 2>(a, s, grid, tps, ns, dir, cus);
+    case 4: return cb_launch_nr<IO, 4>(a, s, grid, tps, ns, dir, cus);
+    case 8: return cb_launch_nr<IO, 8>(a, s, grid, tps, ns, dir, cus);
+    default: return MZ_EUNSUPPORTED;
+  }
+}
+
 int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct) {
   int tps;
   const int ns = cb_choose_split(a, &tps);
   const dim3 grid(ns, a->kv_heads, a->batch);
-  const int dir = direct ? 1 : 0;
-  const int cus = device_cu_count();
-  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
-  const int nrep_pad = a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0;
-#define MZ_CB_B(IOV, NR, BB)                                                                                      \
-  if (a->meta_dtype == MZ_F32)                                                                                    \
-    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 2, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus); \
-  else                                                                                                            \
-    hipLaunchKernelGGL((cb::cb_kernel<IOV, NR, 1, BB>), grid, dim3(64 * cb::WAVES), 0, s, *a, tps, ns, dir, cus)
-#define MZ_CB(IOV, NR)                          \
-  if (a->bits == 4) { MZ_CB_B(IOV, NR, 4); }       \
-  else if (a->bits == 3) { MZ_CB_B(IOV, NR, 3); }  \
-  else if (a->bits == 2) { MZ_CB_B(IOV, NR, 2); }  \
-  else { MZ_CB_B(IOV, NR, 1); }
-#define MZ_CB_NREP(IOV)                \
-  switch (nrep_pad) {                  \
-    case 1: MZ_CB(IOV, 1); break;      \
-    case 2: MZ_CB(IOV, 2); break;      \
-    case 4: MZ_CB(IOV, 4); break;      \
-    case 8: MZ_CB(IOV, 8); break;      \
-    default: return MZ_EUNSUPPORTED;   \
-  }
-  if (a->io_dtype == MZ_BF16) { MZ_CB_NREP(MZ_BF16) } else { MZ_CB_NREP(MZ_F16) }
-#undef MZ_CB_NREP
-#undef MZ_CB
-#undef MZ_CB_B
+  const int st = a->io_dtype == MZ_BF16 ? cb_launch_io<MZ_BF16>(a, s, grid, tps, ns, direct ? 1 : 0, device_cu_count())
+                                        : cb_launch_io<MZ_F16>(a, s, grid, tps, ns, direct ? 1 : 0, device_cu_count());
+  if (st != MZ_OK) return st;
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MZ_OK : (int)e;
 }

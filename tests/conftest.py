@@ -48,8 +48,15 @@ def bits_of(t) -> np.ndarray:
     return t.numpy()
 
 
-# Bit widths the codebook decode kernel takes (head_dim 128, n_rep 1..8, a quantized prefix).
-CODEBOOK_BITS = (1, 2, 3, 4)
+# Bit widths the codebook decode kernel takes (head_dim 128, n_rep 1..8, a quantized prefix; 5 bits
+# with one alpha for keys and values and n_rep up to 4).
+CODEBOOK_BITS = (1, 2, 3, 4, 5)
+
+
+def codebook_takes(bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
+    if bits == 5 and (alpha_k != alpha_v or n_rep > 4):
+        return False
+    return bits in CODEBOOK_BITS and d == 128 and 1 <= n_rep <= 8 and lq > 0
 
 
 def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
@@ -57,8 +64,9 @@ def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
     "codebook" and "general" attend with the values rounded to the layer dtype, "fold" with fp32 ones."""
     if kernel_path in ("fold", "codebook", "general"):
         return kernel_path
-    cb = bits in CODEBOOK_BITS and d == 128 and 1 <= n_rep <= 8 and lq > 0
+    cb = codebook_takes(bits, d, n_rep, lq, alpha_k, alpha_v)
     if kernel_path == "exact":
         return "codebook" if cb else "general"
     fold = d in (64, 128) and lq > 0 and 1 <= n_rep <= 8 and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v))
-    return "codebook" if cb else "fold" if fold else "general"
+    # auto: the codebook kernel at 1-4 bits, the fold kernel at 5-7 (faster there than the codebook's)
+    return "codebook" if cb and bits <= 4 else "fold" if fold else "codebook" if cb else "general"

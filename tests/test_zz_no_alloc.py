@@ -48,7 +48,7 @@ def _noalloc(plan):
                                                      (1, "auto", "codebook"), (4, "fold", "fold"), (5, "auto", "fold"),
                                                      (8, "auto", "general"), (4, "general", "general")])
 def test_noalloc_matches_workspace_entry_point(bits, kernel_path, kernel):
-    """The codebook kernel (1-4 bits), the fold kernel (5 bits, and 4 bits forced onto it) and the
+    """The codebook kernel (1, 2, 4 bits), the fold kernel (5 bits, and 4 bits forced onto it) and the
     general kernel (8 bits, and 4 bits forced onto it), both calls split over tokens."""
     for B, hkv, length, seed in ((2, 2, 4096, 1), (1, 1, 1024, 2)):
         plan = _plan(B, hkv, length, bits, seed, kernel_path=kernel_path)
