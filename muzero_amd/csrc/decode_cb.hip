@@ -854,7 +854,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         const int tt = 4 * n + jt;
         float v = s[jt][i] * scaling2;
         if (tt >= n_valid) v = -INFINITY;
-        else if (a.mask) v = __builtin_fmaf(a.mask[b * a.mask_sb + pos0 + tt], kLog2e, v);
+        else if (a.mask) v = add_mask_log2(v, a.mask[b * a.mask_sb + pos0 + tt]);
         x[jt] = v;
         tmax = fmaxf(tmax, v);
       }

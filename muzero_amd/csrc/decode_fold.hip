@@ -871,7 +871,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_simd<NREP>(), waves_per_simd<NREP>(
         const int tt = 4 * n + jt;
         float v = (s[jt][i] + s[jt][i + 1]) * unscale;
         if (tt >= n_valid) v = -INFINITY;
-        else if (a.mask) v = __builtin_fmaf(a.mask[b * a.mask_sb + pos0 + tt], kLog2e, v);
+        else if (a.mask) v = add_mask_log2(v, a.mask[b * a.mask_sb + pos0 + tt]);
         x[jt] = v;
         tmax = fmaxf(tmax, v);
       }

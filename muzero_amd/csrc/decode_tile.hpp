@@ -67,6 +67,17 @@ __device__ __forceinline__ void load_meta_tile(MetaWords<MW>& t, const Bufs& bf,
   }
 }
 
+// Logit v (base-2 units) plus the additive mask entry m, times log2(e).
+// Finite entries below -2^127 (the finfo.min masks of the 16-bit and fp32
+// dtypes) are raised to -2^127 first so the product stays finite: a row that
+// such entries mask everywhere then has equal logits and averages its values,
+// as the reference's softmax does over its equal shifted logits; -inf (the
+// boolean mask's excluded tokens) and NaN pass unchanged.
+__device__ __forceinline__ float add_mask_log2(float v, float m) {
+  const float mc = (m > -INFINITY && m < -0x1p127f) ? -0x1p127f : m;
+  return __builtin_fmaf(mc, 1.44269504088896341f, v);
+}
+
 // The word of the other lane of this lane's pair (lanes 2m, 2m+1).
 __device__ __forceinline__ uint32_t dpp_swap_pairs(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_XOR1, 0xF, 0xF, true);

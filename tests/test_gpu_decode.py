@@ -630,3 +630,41 @@ def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path(bits
     two = plan.combine().clone()
     torch.cuda.synchronize()
     assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
+
+
+@pytest.mark.parametrize("n_split", [1, 4])
+@pytest.mark.parametrize("path,bits", [("codebook", 4), ("codebook", 2), ("fold", 4), ("fold", 6),
+                                       ("general", 4), ("general", 8)])
+def test_fully_masked_row(path, bits, n_split):
+    """A batch row whose mask excludes every token.  With the additive finfo.min mask (the HF
+    form) every kernel averages the row's values, as the reference's softmax over its equal
+    shifted logits does, and so does the fp64 oracle: all rows match it.  With a boolean keep-mask
+    (-inf) the row gets zeros, not NaN (torch's softmax over an all -inf row gives NaN; generate
+    never asks for such a row, since the current token is always visible), and the other rows
+    still match the oracle."""
+    from muzero_amd.kernels import loader as L
+    B, hkv, n_rep, d, length, residual = 3, 2, 4, 128, 900, 128
+    k, v, q, _ = ref.synthetic_kv(B, hkv, length, d, hkv * n_rep, seed=5)
+    keep = torch.ones(B, 1, 1, length, dtype=torch.bool)
+    keep[1] = False                 # row 1: nothing visible
+    keep[2, ..., : length // 2] = False
+    am = torch.zeros(B, 1, 1, length, dtype=torch.bfloat16).masked_fill_(~keep, torch.finfo(torch.bfloat16).min)
+    exact, st = ref.reference_decode(q, k, v, bits=bits, alpha_k=2.0, alpha_v=2.0, group_size=64,
+                                     residual=residual, attention_mask=am,
+                                     dequant_dtype=ref.FOLD if path == "fold" else None)
+    kw = dict(bits=bits, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5, n_split=n_split, kernel_path=path)
+    for mask in (am, keep):
+        plan = L.DecodePlan(q.to(DEV), out_dtype=torch.float32, attention_mask=mask.to(DEV), **kw)
+        assert plan.kernel == path, (plan.kernel, path)
+        out = plan.run().cpu()
+        torch.cuda.synchronize()
+        rows = [0, 1, 2]
+        if mask.dtype == torch.bool:
+            assert torch.equal(out[1], torch.zeros_like(out[1])), out[1].abs().max()
+            rows = [0, 2]
+        err = (out[rows].double() - exact[rows]).abs()
+        assert err.max().item() < MAX_ABS and err.mean().item() < MEAN_ABS, \
+            (mask.dtype, err.max().item(), err.mean().item())
