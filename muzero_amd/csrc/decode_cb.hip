@@ -742,6 +742,32 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
   using Q1 = std::integral_constant<int, 1>;
   using Q2 = std::integral_constant<int, 2>;
   using Q3 = std::integral_constant<int, 3>;
+  // The B operands of key step kt (Q.K, channels 32kt ..) and of value step
+  // st = 2kt + vg (P.V, tokens 32kt .., channels 64vg ..) from their code words.
+  // PIPE (1 and 2 bits, where the kernel waits on LDS more than it computes):
+  // a step's lookups are issued one step ahead, before the previous step's
+  // MFMAs; at 3-5 bits, which are bound by their VALU work, that measured
+  // slower and the lookups stay in step order.
+  constexpr bool PIPE = BITS <= 2;
+  auto k_lookup = [&](auto kt_tag, u32x4(&B)[4]) __attribute__((always_inline)) {
+    constexpr int kt = decltype(kt_tag)::value;
+    if constexpr (F::WIDE) lookup5<kt * 4 * CB_BLOCK5>(smem, KW + 8 * kt, lbk5, sh5, B);
+    else if constexpr (F::QUAD)
+      lookup1<(2 * kt) * 4 * CB_QUAD, (2 * kt + 1) * 4 * CB_QUAD>(smem, KW + 4 * kt, lbk1, odd, sh1, B);
+    else if constexpr (F::PAIR) lookup2<kt * 4 * CB_PAIRS>(smem, KW + 4 * kt, lbk, odd, B);
+    else if constexpr (BITS == 3) lookup3<kt * 4 * CB_BLOCK3>(smem, KW + 4 * kt, lbk, odd, sh3, B);
+    else lookup4<kt * 4 * CB_BLOCK>(smem, KW + 4 * kt, lbk, gb, odd, B);
+  };
+  auto v_lookup = [&](auto st_tag, u32x4(&B)[4]) __attribute__((always_inline)) {
+    constexpr int st = decltype(st_tag)::value, kt = st >> 1, vg = st & 1;
+    if constexpr (F::WIDE) lookup5<vg * 8 * CB_BLOCK5 + kt * 4 * CB_BLOCK5>(smem, VW + 8 * st, lbv5, sh5, B);
+    else if constexpr (F::QUAD)
+      lookup1<(2 * st) * 4 * CB_QUAD + 16 * ((2 * vg) & 3), (2 * st + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * vg) & 3)>(
+          smem, VW + 4 * st, lbv1, odd, sh1, B);
+    else if constexpr (F::PAIR) lookup2<st * 4 * CB_PAIRS>(smem, VW + 4 * st, lbv, odd, B);
+    else if constexpr (BITS == 3) lookup3<vg * 8 * CB_BLOCK3 + kt * 4 * CB_BLOCK3>(smem, VW + 4 * st, lbv, odd, sh3, B);
+    else lookup4<vg * 8 * CB_BLOCK + kt * 4 * CB_BLOCK>(smem, VW + 4 * st, lbv, gb, odd, B);
+  };
   // the first tile's key codebooks
   {
     Group g0, g1;
@@ -779,45 +805,26 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
       // codebooks are built alongside
       Group gv0, gv1;
       value_groups(MT, gv0, gv1);
+      // PIPE: the next step's lookups are issued before this step's MFMAs
+      u32x4 Bc[4], Bn[4];
+      if constexpr (PIPE) k_lookup(Q0{}, Bc);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        u32x4 B[4];
         switch (kt) {
-          case 0:
-            if constexpr (F::WIDE) lookup5<0 * 4 * CB_BLOCK5>(smem, KW + 0, lbk5, sh5, B);
-            else if constexpr (F::QUAD) lookup1<(2 * 0) * 4 * CB_QUAD, (2 * 0 + 1) * 4 * CB_QUAD>(smem, KW + 0, lbk1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<0 * 4 * CB_PAIRS>(smem, KW + 0, lbk, odd, B);
-            else if constexpr (BITS == 3) lookup3<0 * 4 * CB_BLOCK3>(smem, KW + 0, lbk, odd, sh3, B);
-            else lookup4<0 * 4 * CB_BLOCK>(smem, KW + 0, lbk, gb, odd, B);
-            build_part(VALUES{}, gv0, gv1, Q0{});
-            break;
-          case 1:
-            if constexpr (F::WIDE) lookup5<1 * 4 * CB_BLOCK5>(smem, KW + 8, lbk5, sh5, B);
-            else if constexpr (F::QUAD) lookup1<(2 * 1) * 4 * CB_QUAD, (2 * 1 + 1) * 4 * CB_QUAD>(smem, KW + 4, lbk1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<1 * 4 * CB_PAIRS>(smem, KW + 4, lbk, odd, B);
-            else if constexpr (BITS == 3) lookup3<1 * 4 * CB_BLOCK3>(smem, KW + 4, lbk, odd, sh3, B);
-            else lookup4<1 * 4 * CB_BLOCK>(smem, KW + 4, lbk, gb, odd, B);
-            build_part(VALUES{}, gv0, gv1, Q1{});
-            break;
-          case 2:
-            if constexpr (F::WIDE) lookup5<2 * 4 * CB_BLOCK5>(smem, KW + 16, lbk5, sh5, B);
-            else if constexpr (F::QUAD) lookup1<(2 * 2) * 4 * CB_QUAD, (2 * 2 + 1) * 4 * CB_QUAD>(smem, KW + 8, lbk1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<2 * 4 * CB_PAIRS>(smem, KW + 8, lbk, odd, B);
-            else if constexpr (BITS == 3) lookup3<2 * 4 * CB_BLOCK3>(smem, KW + 8, lbk, odd, sh3, B);
-            else lookup4<2 * 4 * CB_BLOCK>(smem, KW + 8, lbk, gb, odd, B);
-            build_part(VALUES{}, gv0, gv1, Q2{});
-            break;
+          case 0: PIPE ? k_lookup(Q1{}, Bn) : k_lookup(Q0{}, Bc); build_part(VALUES{}, gv0, gv1, Q0{}); break;
+          case 1: PIPE ? k_lookup(Q2{}, Bn) : k_lookup(Q1{}, Bc); build_part(VALUES{}, gv0, gv1, Q1{}); break;
+          case 2: PIPE ? k_lookup(Q3{}, Bn) : k_lookup(Q2{}, Bc); build_part(VALUES{}, gv0, gv1, Q2{}); break;
           default:
-            if constexpr (F::WIDE) lookup5<3 * 4 * CB_BLOCK5>(smem, KW + 24, lbk5, sh5, B);
-            else if constexpr (F::QUAD) lookup1<(2 * 3) * 4 * CB_QUAD, (2 * 3 + 1) * 4 * CB_QUAD>(smem, KW + 12, lbk1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<3 * 4 * CB_PAIRS>(smem, KW + 12, lbk, odd, B);
-            else if constexpr (BITS == 3) lookup3<3 * 4 * CB_BLOCK3>(smem, KW + 12, lbk, odd, sh3, B);
-            else lookup4<3 * 4 * CB_BLOCK>(smem, KW + 12, lbk, gb, odd, B);
+            if constexpr (!PIPE) k_lookup(Q3{}, Bc);
             build_part(VALUES{}, gv0, gv1, Q3{});
             break;
         }
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], B[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], Bc[jt], s[jt]);
+        if constexpr (PIPE) {
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
+        }
       }
     } else {
       // ---------- residual tile: dense keys; rows past the filled ones read 0
@@ -897,63 +904,27 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     Group gk0, gk1;
     key_groups(MN, gk0, gk1);
     if constexpr (quant) {
+      u32x4 Bc[4], Bn[4];
+      if constexpr (PIPE) v_lookup(Q0{}, Bc);
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int kt = st >> 1, vg = st & 1;
         const u32x4 A = *(const u32x4*)(pv_row + (32 * kt + 8 * g) * 2);
-        u32x4 B[4];
         switch (st) {
-          case 0:
-            if constexpr (F::WIDE)
-              lookup5<0 * 8 * CB_BLOCK5 + 0 * 4 * CB_BLOCK5>(smem, VW + 0, lbv5, sh5, B);
-            else if constexpr (F::QUAD)
-              lookup1<(2 * 0) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 0 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
-                  smem, VW + 0, lbv1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<(0 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 0, lbv, odd, B);
-            else if constexpr (BITS == 3)
-              lookup3<0 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 0, lbv, odd, sh3, B);
-            else lookup4<0 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 0, lbv, gb, odd, B);
-            build_part(KEYS{}, gk0, gk1, Q0{});
-            break;
-          case 1:
-            if constexpr (F::WIDE)
-              lookup5<1 * 8 * CB_BLOCK5 + 0 * 4 * CB_BLOCK5>(smem, VW + 8, lbv5, sh5, B);
-            else if constexpr (F::QUAD)
-              lookup1<(2 * 1) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 1 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
-                  smem, VW + 4, lbv1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<(0 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 4, lbv, odd, B);
-            else if constexpr (BITS == 3)
-              lookup3<1 * 8 * CB_BLOCK3 + 0 * 4 * CB_BLOCK3>(smem, VW + 4, lbv, odd, sh3, B);
-            else lookup4<1 * 8 * CB_BLOCK + 0 * 4 * CB_BLOCK>(smem, VW + 4, lbv, gb, odd, B);
-            build_part(KEYS{}, gk0, gk1, Q1{});
-            break;
-          case 2:
-            if constexpr (F::WIDE)
-              lookup5<0 * 8 * CB_BLOCK5 + 1 * 4 * CB_BLOCK5>(smem, VW + 16, lbv5, sh5, B);
-            else if constexpr (F::QUAD)
-              lookup1<(2 * 2) * 4 * CB_QUAD + 16 * ((2 * 0) & 3), (2 * 2 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 0) & 3)>(
-                  smem, VW + 8, lbv1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<(1 * 2 + 0) * 4 * CB_PAIRS>(smem, VW + 8, lbv, odd, B);
-            else if constexpr (BITS == 3)
-              lookup3<0 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 8, lbv, odd, sh3, B);
-            else lookup4<0 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 8, lbv, gb, odd, B);
-            build_part(KEYS{}, gk0, gk1, Q2{});
-            break;
+          case 0: PIPE ? v_lookup(Q1{}, Bn) : v_lookup(Q0{}, Bc); build_part(KEYS{}, gk0, gk1, Q0{}); break;
+          case 1: PIPE ? v_lookup(Q2{}, Bn) : v_lookup(Q1{}, Bc); build_part(KEYS{}, gk0, gk1, Q1{}); break;
+          case 2: PIPE ? v_lookup(Q3{}, Bn) : v_lookup(Q2{}, Bc); build_part(KEYS{}, gk0, gk1, Q2{}); break;
           default:
-            if constexpr (F::WIDE)
-              lookup5<1 * 8 * CB_BLOCK5 + 1 * 4 * CB_BLOCK5>(smem, VW + 24, lbv5, sh5, B);
-            else if constexpr (F::QUAD)
-              lookup1<(2 * 3) * 4 * CB_QUAD + 16 * ((2 * 1) & 3), (2 * 3 + 1) * 4 * CB_QUAD + 16 * ((1 + 2 * 1) & 3)>(
-                  smem, VW + 12, lbv1, odd, sh1, B);
-            else if constexpr (F::PAIR) lookup2<(1 * 2 + 1) * 4 * CB_PAIRS>(smem, VW + 12, lbv, odd, B);
-            else if constexpr (BITS == 3)
-              lookup3<1 * 8 * CB_BLOCK3 + 1 * 4 * CB_BLOCK3>(smem, VW + 12, lbv, odd, sh3, B);
-            else lookup4<1 * 8 * CB_BLOCK + 1 * 4 * CB_BLOCK>(smem, VW + 12, lbv, gb, odd, B);
+            if constexpr (!PIPE) v_lookup(Q3{}, Bc);
             build_part(KEYS{}, gk0, gk1, Q3{});
             break;
         }
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(A, B[jt], acc[vg][jt]);
+        for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(A, Bc[jt], acc[vg][jt]);
+        if constexpr (PIPE) {
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) Bc[jt] = Bn[jt];
+        }
       }
     } else {
       // residual values: lane (n, g) of step (kt, vg) needs tokens
