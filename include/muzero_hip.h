@@ -233,8 +233,9 @@ typedef struct mz_decode_args {
  *  - general: the dequantize-then-attend values, every width and layout.
  * AUTO runs the codebook kernel at 1 to 4 bits where it applies, else the
  * fold kernel, else the codebook kernel (5 bits), else the general one;
- * EXACT the codebook kernel where it applies, else the general one; FOLD, CODEBOOK and GENERAL force that kernel (a forced fold or
- * codebook kernel that does not take the arguments is MZ_EUNSUPPORTED). */
+ * EXACT the codebook kernel where it applies, else the general one; FOLD,
+ * CODEBOOK and GENERAL force that kernel (a forced fold or codebook kernel
+ * that does not take the arguments is MZ_EUNSUPPORTED). */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3, MZ_PATH_GENERAL = 4 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments

@@ -342,7 +342,9 @@ class DecodePlan:
         lib = load()
         ns = ctypes.c_int(0)
         need = lib.muzero_decode_workspace_bytes(ctypes.byref(a), ctypes.byref(ns))
-        _require(need >= 0, "decode arguments rejected (head_dim must be 64 or 128, n_rep <= 16)")
+        _require(need >= 0, "decode arguments rejected (head_dim must be 64 or 128, n_rep <= 16"
+                 + ("" if kernel_path in ("auto", "exact", "general")
+                    else f"; or the forced {kernel_path} kernel does not take this call") + ")")
         ws = torch.empty((max(int(need), 4) + 3) // 4, dtype=torch.float32, device=dev)
         a.workspace, a.workspace_bytes = ptr(ws), int(need)
         self.args = a
