@@ -480,7 +480,11 @@ __global__ __launch_bounds__(QWG) void quantize_values_kernel(const void* __rest
 // registers before the current tile is quantized.  The grid holds as many
 // workgroups per CU as the table and the tile leave room for in LDS (at most
 // 4).
-constexpr int KEY_MAX_VEC = 8;  // 16-byte vectors per thread per tile: 64 * 256 / 8 / QWG
+// 16-byte vectors per thread per tile on the vector path: 64 tokens x D
+// channels / (16 / element bytes) / QWG, so at most D = 256 for 16-bit
+// inputs and D = 128 for fp32 (the host sends wider fp32 tiles to the scalar
+// path)
+constexpr int KEY_MAX_VEC = 8;
 
 template <int DT>
 struct Vec16 {
@@ -773,8 +777,9 @@ extern "C" int muzero_quantize_keys(const void* keys, int x_dtype, int B, int H,
   const int64_t ntiles = (int64_t)B * H * (T / 64);
   if (ntiles >= (int64_t)1 << 31) return MZ_EINVAL;
   const size_t es = x_dtype == MZ_F32 ? 4 : 2;
-  const bool vec = aligned16(keys) && D % 8 == 0 && D <= 256 && (x_sb * es) % 16 == 0 && (x_sh * es) % 16 == 0 &&
-                   (x_st * es) % 16 == 0;
+  // the vector path stages a whole tile in KEY_MAX_VEC 16-byte loads per thread
+  const bool vec = aligned16(keys) && D % 8 == 0 && (int64_t)64 * D * (int64_t)es <= (int64_t)KEY_MAX_VEC * QWG * 16 &&
+                   (x_sb * es) % 16 == 0 && (x_sh * es) % 16 == 0 && (x_st * es) % 16 == 0;
   hipStream_t s = (hipStream_t)stream;
   MZ_DT_SWITCH(x_dtype, MZ_BITS_SWITCH(bits,
       const size_t lds = (size_t)QTable<D_, B_>::LDS_BYTES +

@@ -132,9 +132,11 @@ def test_quantize_rows_exhaustive_boundaries_fp32(bits):
 
 @pytest.mark.parametrize("dname", ["bfloat16", "float32", "float16"])
 @pytest.mark.parametrize("bits", [1, 2, 3, 4, 8])
-@pytest.mark.parametrize("d", [64, 128, 80])
+@pytest.mark.parametrize("d", [64, 128, 80, 256])
 def test_quantize_key_value_blocks(dname, bits, d):
-    """Fused-transpose key kernel and value kernel vs the oracle's cache layouts (layer.py:271-301)."""
+    """Fused-transpose key kernel and value kernel vs the oracle's cache layouts (layer.py:271-301).
+    d = 256 with fp32 keys: a tile of 64 KB, wider than the key kernel's vector staging (it takes
+    the scalar path)."""
     from muzero_amd.kernels import loader as L
     g = torch.Generator().manual_seed(d + bits)
     B, H, T = 2, 3, 192
