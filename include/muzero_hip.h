@@ -231,9 +231,8 @@ typedef struct mz_decode_args {
  *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
  *    given, at 7 bits one table for keys and values;
  *  - general: the dequantize-then-attend values, every width and layout.
- * AUTO runs the codebook kernel at 1 to 4 bits where it applies, else the
- * fold kernel, else the codebook kernel (5 bits), else the general one;
- * EXACT the codebook kernel where it applies, else the general one; FOLD,
+ * AUTO and EXACT run the codebook kernel where it applies; else AUTO runs
+ * the fold kernel where it applies and EXACT the general one; FOLD,
  * CODEBOOK and GENERAL force that kernel (a forced fold or codebook kernel
  * that does not take the arguments is MZ_EUNSUPPORTED). */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3, MZ_PATH_GENERAL = 4 };

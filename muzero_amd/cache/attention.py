@@ -36,8 +36,8 @@ residual matmuls, counted as ``fused_qk_success`` / ``fused_av_success``.
 Kernel choice, in the reference's environment-switch style (``attention.py:92``,
 ``:110``, ``:128``), ``MUZERO_DECODE_KERNEL``:
 
-* unset or ``auto``: the codebook kernel where it applies at 1-4 bits
-  (head_dim 128), else the fold kernel (1-7 bits), else the general kernel;
+* unset or ``auto``: the codebook kernel where it applies (1-5 bits,
+  head_dim 128), else the fold kernel (1-7 bits), else the general kernel;
 * ``exact``: dequantized values rounded to the layer dtype like the
   reference's dequantize-then-attend path (``attention.py:213-226``,
   ``:274-283``, ``layer.py:263``) on every call: the codebook kernel where it

@@ -776,21 +776,18 @@ static int check_args(const mz_decode_args* a) {
 // workspace layout and the combine kernel).
 enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2 };
 
-// AUTO: the codebook kernel for 1-4 bits where it applies (the layer-dtype
-// values, at the fold kernel's speed or better), else the fold kernel (5-7
-// bits: faster than the 5-bit codebook kernel), else the general one.
-// EXACT: the layer-dtype values, the codebook kernel where it applies (1-5
-// bits), else the general kernel.
+// AUTO: the codebook kernel where it applies (1-5 bits, the layer-dtype
+// values: at 1-4 bits at the fold kernel's speed or better, at 5 bits ~13 %
+// slower, kept for the values), else the fold kernel (6-7 bits, head_dim
+// 64, 5 bits with two alphas or more query heads), else the general one.
+// EXACT: the codebook kernel where it applies, else the general kernel.
 static Kernel which_kernel(const mz_decode_args* a) {
   switch (a->kernel_path) {
     case MZ_PATH_GENERAL: return K_GENERAL;
     case MZ_PATH_FOLD: return fold_supported(a) ? K_FOLD : K_GENERAL;
     case MZ_PATH_CODEBOOK: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
     case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
-    default:
-      if (a->bits <= 4 && cb_supported(a)) return K_CODEBOOK;
-      if (fold_supported(a)) return K_FOLD;
-      return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
+    default: return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : K_GENERAL;
   }
 }
 

@@ -68,5 +68,4 @@ def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
     if kernel_path == "exact":
         return "codebook" if cb else "general"
     fold = d in (64, 128) and lq > 0 and 1 <= n_rep <= 8 and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v))
-    # auto: the codebook kernel at 1-4 bits, the fold kernel at 5-7 (faster there than the codebook's)
-    return "codebook" if cb and bits <= 4 else "fold" if fold else "codebook" if cb else "general"
+    return "codebook" if cb else "fold" if fold else "general"
