@@ -659,7 +659,7 @@ def main():
         "pct_of_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 2),
         "attn_only_tokens_per_s_36_layers": round(B / (36 * ms_step * 1e-3), 1),
         "kernels_ms": kernels_ms,
-        "kernel": {"fold": "fold", "codebook": "codebook (exact values)",
+        "kernel": {"fold": "fold", "codebook": "codebook (exact values)", "twopass": "two-pass (exact values)",
                    "general": "exact-dequantize (general)"}[plans[0].kernel],
         "n_split": plans[0].n_split,
         "roofline": {"bound": "hbm", "achieved": round(gbs_split, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",

@@ -230,11 +230,17 @@ typedef struct mz_decode_args {
  *    up to the fp16 rounding of its shifted (P, N) table entries); bits 1 to
  *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
  *    given, at 7 bits one table for keys and values;
+ *  - two-pass: the dequantize-then-attend values for 8-bit codes (keys'
+ *    logits with the key table in LDS, then softmax and values with the
+ *    value table); head_dim 128, aligned prefixes, n_rep 1 to 8; its
+ *    logits (4 bytes per query head and token) live in the workspace after
+ *    the split records, so it always runs split kernels + combine;
  *  - general: the dequantize-then-attend values, every width and layout.
  * AUTO and EXACT run the codebook kernel where it applies; else AUTO runs
- * the fold kernel where it applies and EXACT the general one; FOLD,
- * CODEBOOK and GENERAL force that kernel (a forced fold or codebook kernel
- * that does not take the arguments is MZ_EUNSUPPORTED). */
+ * the fold kernel where it applies; else both run the two-pass kernel where
+ * it applies, else the general one; FOLD, CODEBOOK and GENERAL force that
+ * kernel (a forced fold or codebook kernel that does not take the
+ * arguments is MZ_EUNSUPPORTED). */
 enum { MZ_PATH_AUTO = 0, MZ_PATH_EXACT = 1, MZ_PATH_FOLD = 2, MZ_PATH_CODEBOOK = 3, MZ_PATH_GENERAL = 4 };
 
 /* Bytes of workspace muzero_decode_attention needs for these arguments
@@ -248,9 +254,9 @@ int64_t muzero_decode_workspace_bytes(const mz_decode_args* args, int* n_split_o
  * benchmark to report which kernel they measured. */
 int muzero_decode_uses_fold(const mz_decode_args* args);
 /* The kernel muzero_decode_attention runs for these arguments: 0 the general
- * exact-dequantize kernel, 1 the fold kernel, 2 the codebook kernel; -1 if the
- * arguments are rejected (or a forced kernel does not take them).  An
- * introspection helper like muzero_decode_uses_fold. */
+ * exact-dequantize kernel, 1 the fold kernel, 2 the codebook kernel, 3 the
+ * two-pass kernel; -1 if the arguments are rejected (or a forced kernel does
+ * not take them).  An introspection helper like muzero_decode_uses_fold. */
 int muzero_decode_kernel(const mz_decode_args* args);
 int muzero_decode_attention(const mz_decode_args* args, mz_stream_t stream);
 
@@ -306,10 +312,14 @@ int muzero_decode_prefix_state(const mz_decode_args* args, const mz_prefix_state
  * callers that cannot call hipMalloc (code under HIP graph capture, tight
  * serving loops, harnesses that forbid allocation).  Returns MZ_ESCRATCH,
  * launching nothing, when a split call's muzero_decode_workspace_bytes(args)
- * exceeds the array (a single-split call uses no workspace).  Every call on a device shares that device's array (the last call's
+ * exceeds the array (a single-split call of the other kernels uses no
+ * workspace); a two-pass call whose logits and records exceed it runs the
+ * general kernel instead (the same dequantize-then-attend values, summed in
+ * another order).  Every call on a device shares that device's array (the last call's
  * records stay in it; each call writes every record it reads), so calls that
  * overlap on one device, on different streams or threads, race.  Same
- * results as muzero_decode_attention with a workspace, bit for bit.
+ * results as muzero_decode_attention with a workspace, bit for bit (except
+ * for the two-pass calls above that fall back to the general kernel).
  * The first call on a device does one-time runtime set-up there (the
  * scratch array's address, a kernel's LDS limit): a caller that captures
  * the call in a HIP graph makes one call on that device before the capture

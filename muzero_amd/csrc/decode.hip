@@ -716,6 +716,10 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 bool cb_supported(const mz_decode_args* a);
 int cb_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
+bool w8_supported(const mz_decode_args* a);
+int w8_choose_split(const mz_decode_args* a, int* tiles_per_split);
+int64_t w8_workspace_bytes(const mz_decode_args* a, int ns);
+int w8_launch_partials(const mz_decode_args* a, hipStream_t s);
 
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
@@ -774,20 +778,23 @@ static int check_args(const mz_decode_args* a) {
 
 // Which kernel runs and with how many splits (the kernels share the
 // workspace layout and the combine kernel).
-enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2 };
+enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2, K_TWOPASS = 3 };
 
 // AUTO: the codebook kernel where it applies (1-5 bits, the layer-dtype
 // values: at 1-4 bits at the fold kernel's speed or better, at 5 bits ~13 %
 // slower, kept for the values), else the fold kernel (6-7 bits, head_dim
-// 64, 5 bits with two alphas or more query heads), else the general one.
-// EXACT: the codebook kernel where it applies, else the general kernel.
+// 64, 5 bits with two alphas or more query heads), else the two-pass kernel
+// (8 bits, the layer-dtype values), else the general one.
+// EXACT: the codebook kernel where it applies, else the two-pass kernel,
+// else the general kernel.
 static Kernel which_kernel(const mz_decode_args* a) {
   switch (a->kernel_path) {
     case MZ_PATH_GENERAL: return K_GENERAL;
     case MZ_PATH_FOLD: return fold_supported(a) ? K_FOLD : K_GENERAL;
     case MZ_PATH_CODEBOOK: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
-    case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
-    default: return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : K_GENERAL;
+    case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : w8_supported(a) ? K_TWOPASS : K_GENERAL;
+    default:
+      return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : w8_supported(a) ? K_TWOPASS : K_GENERAL;
   }
 }
 
@@ -801,12 +808,26 @@ static int plan_split(const mz_decode_args* a, int* tps) {
   switch (which_kernel(a)) {
     case K_FOLD: return fold_choose_split(a, tps);
     case K_CODEBOOK: return cb_choose_split(a, tps);
+    case K_TWOPASS: return w8_choose_split(a, tps);
     default: return choose_split(a, tps);
   }
 }
 
+// Workspace bytes of a planned call: the split records, and for the
+// two-pass kernel its logits after them.
+static int64_t plan_workspace(const mz_decode_args* a, int ns) {
+  if (which_kernel(a) == K_TWOPASS) return w8_workspace_bytes(a, ns);
+  return (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
+}
+
+// The codebook, fold and two-pass kernels (the two-pass kernel always
+// writes records: `direct` is for the other two).
 static int launch_fast(const mz_decode_args* a, hipStream_t s, bool direct) {
-  return which_kernel(a) == K_FOLD ? fold_launch_partials(a, s, direct) : cb_launch_partials(a, s, direct);
+  switch (which_kernel(a)) {
+    case K_FOLD: return fold_launch_partials(a, s, direct);
+    case K_TWOPASS: return w8_launch_partials(a, s);
+    default: return cb_launch_partials(a, s, direct);
+  }
 }
 
 }  // namespace mz
@@ -819,7 +840,7 @@ extern "C" int64_t muzero_decode_workspace_bytes(const mz_decode_args* a, int* n
   int tps;
   const int ns = plan_split(a, &tps);
   if (n_split_out) *n_split_out = ns;
-  return (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
+  return plan_workspace(a, ns);
 }
 
 extern "C" int muzero_decode_uses_fold(const mz_decode_args* a) {
@@ -896,7 +917,7 @@ extern "C" int muzero_decode_partials(const mz_decode_args* a, mz_stream_t strea
   if (which_kernel(a) != K_GENERAL) {
     int tps;
     const int ns = plan_split(a, &tps);
-    const int64_t need = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
+    const int64_t need = plan_workspace(a, ns);
     if (!a->workspace || a->workspace_bytes < need) return MZ_EWORKSPACE;
     return launch_fast(a, s, false);
   }
@@ -948,8 +969,9 @@ extern "C" int muzero_decode_prefix_state(const mz_decode_args* a, const mz_pref
 }
 
 extern "C" int muzero_decode_attention(const mz_decode_args* a, mz_stream_t stream) {
-  // one split: the split kernel writes the output (no workspace, no combine)
-  if (decode_check_launchable(a) == MZ_OK && a->out && !forced_unsupported(a)) {
+  // one split: the split kernel writes the output (no workspace, no combine);
+  // the two-pass kernel always goes through the workspace
+  if (decode_check_launchable(a) == MZ_OK && a->out && !forced_unsupported(a) && which_kernel(a) != K_TWOPASS) {
     int tps;
     if (plan_split(a, &tps) == 1)
       return which_kernel(a) != K_GENERAL ? launch_fast(a, (hipStream_t)stream, true)
@@ -986,16 +1008,23 @@ static hipError_t scratch_address(void** out) {
 
 extern "C" int muzero_decode_attention_noalloc(const mz_decode_args* a, mz_stream_t stream) {
   if (!a) return MZ_EINVAL;
+  mz_decode_args b = *a;
   int ns = 0;
-  const int64_t need = muzero_decode_workspace_bytes(a, &ns);
+  int64_t need = muzero_decode_workspace_bytes(&b, &ns);
   if (need < 0) {
     // the status muzero_decode_attention gives for the same arguments
     const int c = check_args(a);
     return c != MZ_OK ? c : MZ_EUNSUPPORTED;  // a forced fold path the fold kernel does not take
   }
-  // a single split writes the output directly and reads no workspace
-  if (ns > 1 && need > (int64_t)MZ_DECODE_SCRATCH_BYTES) return MZ_ESCRATCH;
-  mz_decode_args b = *a;
+  // the two-pass kernel keeps its logits in the workspace as well: a call
+  // whose logits do not fit the scratch runs the general kernel instead
+  if (need > (int64_t)MZ_DECODE_SCRATCH_BYTES && b.batch > 0 && which_kernel(&b) == K_TWOPASS) {
+    b.kernel_path = MZ_PATH_GENERAL;
+    need = muzero_decode_workspace_bytes(&b, &ns);
+  }
+  // a single split of the other kernels writes the output directly and reads no workspace
+  const bool reads_ws = ns > 1 || (b.batch > 0 && which_kernel(&b) == K_TWOPASS);
+  if (reads_ws && need > (int64_t)MZ_DECODE_SCRATCH_BYTES) return MZ_ESCRATCH;
   const hipError_t e = scratch_address(&b.workspace);
   if (e != hipSuccess) return (int)e;
   b.workspace_bytes = (int64_t)MZ_DECODE_SCRATCH_BYTES;

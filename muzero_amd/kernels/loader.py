@@ -220,7 +220,7 @@ def prepare_mask(attention_mask: torch.Tensor | None, batch: int, length: int) -
 
 
 # muzero_decode_kernel() -> name
-DECODE_KERNELS = ("general", "fold", "codebook")
+DECODE_KERNELS = ("general", "fold", "codebook", "twopass")
 
 
 class DecodePlan:
@@ -349,7 +349,8 @@ class DecodePlan:
         a.workspace, a.workspace_bytes = ptr(ws), int(need)
         self.args = a
         self.n_split = ns.value
-        # the kernel the library runs for these arguments: "general" (exact-dequantize), "fold", "codebook"
+        # the kernel the library runs for these arguments: "general" (exact-dequantize), "fold", "codebook",
+        # "twopass" (8-bit codes)
         self.kernel = DECODE_KERNELS[lib.muzero_decode_kernel(ctypes.byref(a))]
         self.uses_fold = self.kernel == "fold"
         self.out = out

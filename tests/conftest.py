@@ -61,11 +61,13 @@ def codebook_takes(bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
 
 def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
     """The decode kernel the library runs for a call (muzero_decode_kernel's choice, restated):
-    "codebook" and "general" attend with the values rounded to the layer dtype, "fold" with fp32 ones."""
+    "codebook", "twopass" and "general" attend with the values rounded to the layer dtype, "fold" with fp32
+    ones."""
     if kernel_path in ("fold", "codebook", "general"):
         return kernel_path
     cb = codebook_takes(bits, d, n_rep, lq, alpha_k, alpha_v)
+    twopass = bits == 8 and d == 128 and lq > 0 and 1 <= n_rep <= 8
     if kernel_path == "exact":
-        return "codebook" if cb else "general"
+        return "codebook" if cb else "twopass" if twopass else "general"
     fold = d in (64, 128) and lq > 0 and 1 <= n_rep <= 8 and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v))
-    return "codebook" if cb else "fold" if fold else "general"
+    return "codebook" if cb else "fold" if fold else "twopass" if twopass else "general"

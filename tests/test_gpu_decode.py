@@ -632,10 +632,72 @@ def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path(bits
     assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
 
 
+# 8 bits: the two-pass kernel (AUTO and EXACT run it), the layer-dtype values like the codebook
+# kernel, so held to the same bounds against the fp64 oracle over those values.
+@pytest.mark.parametrize("shape", CB_SHAPES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_R{}".format(*c))
+def test_twopass_kernel(shape):
+    B, hkv, n_rep, d, length, residual = shape
+    mx, mean, _, _ = _run_case(B, hkv, n_rep, d, length, 8, residual, kernel_path="exact", expect_kernel="twopass")
+    print(f"{shape}: max {mx:.2e} mean {mean:.2e}", flush=True)
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("dtype,meta", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                        (torch.bfloat16, torch.float32), (torch.float16, torch.float32)])
+def test_twopass_kernel_dtypes(dtype, meta):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 8, 128, dtype=dtype, meta=meta, expect_kernel="twopass")
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("alphas", [(4.0, 2.0), (16.0, 16.0)])
+@pytest.mark.parametrize("mask", ["float", "bool"])
+@pytest.mark.parametrize("n_split", [0, 1, 3, 64])
+def test_twopass_kernel_split_and_mask(n_split, mask, alphas):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, 8, 128, mask=mask, n_split=n_split, expect_kernel="twopass",
+                               alpha_k=alphas[0], alpha_v=alphas[1])
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+@pytest.mark.parametrize("q_scale", [1.0, 4.0])
+def test_twopass_kernel_offset_and_peaked(q_scale):
+    """One-signed key and value groups (|mn| >> scale) and, with the query x4, peaked rows."""
+    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, 8, 128, seed=11, k_offset=20.0, v_offset=5.0,
+                                   q_scale=q_scale, expect_kernel="twopass")
+    scale = max(1.0, exact.abs().max().item())
+    assert mx < CB_MAX_ABS * scale and mean < CB_MEAN_ABS * scale, (mx, mean)
+
+
+@pytest.mark.parametrize("length", [8192, 32768])
+def test_twopass_kernel_long_context(length):
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, 8, 128, seed=length, expect_kernel="twopass")
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+def test_twopass_kernel_partials_and_combine():
+    """The two-pass kernel always writes split records; decode_partials + decode_combine give the
+    output of the one-call entry point bit for bit."""
+    from muzero_amd.kernels import loader as L
+    k, v, q, _ = ref.synthetic_kv(2, 2, 900, 128, 8, seed=3)
+    _, st = ref.reference_decode(q, k, v, bits=8, alpha_k=4.0, alpha_v=2.0, group_size=64, residual=128)
+    kw = dict(bits=8, n_groups=st["lq"] // 64, k_packed=st["packed_k"].to(DEV), k_mn=st["k_mn"].to(DEV),
+              k_scale=st["k_scale"].to(DEV), v_packed=st["packed_v"].to(DEV), v_mn=st["v_mn"].to(DEV),
+              v_scale=st["v_scale"].to(DEV), k_res=st["res_k"].to(DEV), v_res=st["res_v"].to(DEV),
+              alpha_key=4.0, alpha_value=2.0, scaling=128 ** -0.5, n_split=1)
+    plan = L.DecodePlan(q.to(DEV), **kw)
+    assert plan.n_split == 1 and plan.kernel == "twopass"
+    one = plan.run().clone()
+    plan.out.zero_()
+    plan.partials()
+    two = plan.combine().clone()
+    torch.cuda.synchronize()
+    assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+
+
 @pytest.mark.parametrize("n_split", [1, 4])
-@pytest.mark.parametrize("path,bits", [("codebook", 4), ("codebook", 2), ("fold", 4), ("fold", 6),
-                                       ("general", 4), ("general", 8)])
-def test_fully_masked_row(path, bits, n_split):
+@pytest.mark.parametrize("path,bits,kernel", [("codebook", 4, "codebook"), ("codebook", 2, "codebook"),
+                                              ("fold", 4, "fold"), ("fold", 6, "fold"), ("general", 4, "general"),
+                                              ("general", 8, "general"), ("exact", 8, "twopass")])
+def test_fully_masked_row(path, bits, kernel, n_split):
     """A batch row whose mask excludes every token.  With the additive finfo.min mask (the HF
     form) every kernel averages the row's values, as the reference's softmax over its equal
     shifted logits does, and so does the fp64 oracle: all rows match it.  With a boolean keep-mask
@@ -658,7 +720,7 @@ def test_fully_masked_row(path, bits, n_split):
               alpha_key=2.0, alpha_value=2.0, scaling=d ** -0.5, n_split=n_split, kernel_path=path)
     for mask in (am, keep):
         plan = L.DecodePlan(q.to(DEV), out_dtype=torch.float32, attention_mask=mask.to(DEV), **kw)
-        assert plan.kernel == path, (plan.kernel, path)
+        assert plan.kernel == kernel, (plan.kernel, kernel)
         out = plan.run().cpu()
         torch.cuda.synchronize()
         rows = [0, 1, 2]

@@ -46,10 +46,12 @@ def _noalloc(plan):
 
 @pytest.mark.parametrize("bits,kernel_path,kernel", [(4, "auto", "codebook"), (2, "auto", "codebook"),
                                                      (1, "auto", "codebook"), (4, "fold", "fold"), (6, "auto", "fold"),
-                                                     (8, "auto", "general"), (4, "general", "general")])
+                                                     (8, "auto", "twopass"), (8, "general", "general"),
+                                                     (4, "general", "general")])
 def test_noalloc_matches_workspace_entry_point(bits, kernel_path, kernel):
-    """The codebook kernel (1, 2, 4 bits), the fold kernel (6 bits, and 4 bits forced onto it) and the
-    general kernel (8 bits, and 4 bits forced onto it), both calls split over tokens."""
+    """The codebook kernel (1, 2, 4 bits), the fold kernel (6 bits, and 4 bits forced onto it), the
+    two-pass kernel (8 bits: its split records and logits in the scratch) and the general kernel (8 bits
+    and 4 bits forced onto it), both calls split over tokens."""
     for B, hkv, length, seed in ((2, 2, 4096, 1), (1, 1, 1024, 2)):
         plan = _plan(B, hkv, length, bits, seed, kernel_path=kernel_path)
         assert plan.kernel == kernel  # the kernel this case is meant to send through the scratch
