@@ -84,9 +84,9 @@ __device__ __forceinline__ float io_to_f32(uint16_t h) {
 // The dequantization quantities of one stored group (mn, s), formed as the
 // reference forms them from the stored metadata (quantizer.py:241-249), the
 // scale guarded like the reference CUDA extension (loader.py:201) so that an
-// all-zero group (stored scale 0) gives x = mn.  Up / down: the byte address
-// of expm1 entry 0 of the row for codes above / below the zero level, minus /
-// plus 4 zl, so that code q's entry lies at up + 4q (q >= zl) or dn - 4q.
+// all-zero group (stored scale 0) gives x = mn.  zl4 = 4 zl; up / down: the
+// byte address of expm1 entry 0 of the row for codes above / below the zero
+// level, so that code q's entry lies at 4|q - zl| past the side's row start.
 __device__ __forceinline__ void group_words(float mn, float s, uint32_t (&w)[PW]) {
   const float sg = s >= kEps ? s : kEps;  // NaN -> eps, as deq_row
   const float za = clamp01((0.f - mn) / sg);  // IEEE division: the zero level must match
@@ -94,44 +94,38 @@ __device__ __forceinline__ void group_words(float mn, float s, uint32_t (&w)[PW]
   // a NaN zero level (NaN metadata) reads row 0: the values are NaN anyway
   const int zl = (int)__builtin_amdgcn_fmed3f(zlf == zlf ? zlf : 0.f, 0.f, (float)QMAX);
   const int pb = max(QMAX - zl, 1), nb = max(zl, 1);
-  w[P_ZL] = (uint32_t)zl;
-  w[P_UP] = (uint32_t)(4 * (expm1_row(pb) - zl));
-  w[P_DN] = (uint32_t)(4 * (expm1_row(nb) + zl));
+  w[P_ZL] = (uint32_t)(4 * zl);
+  w[P_UP] = (uint32_t)(4 * expm1_row(pb));
+  w[P_DN] = (uint32_t)(4 * expm1_row(nb));
   w[P_PE] = __float_as_uint(clamp_min(1.f - za, kEps));
   w[P_ZA] = __float_as_uint(za);
   w[P_S] = __float_as_uint(sg);
   w[P_MN] = __float_as_uint(mn);
 }
 
-// The 8 groups of a step: word k of group j = G[k][j].  mne = -ne.
-struct Groups8 {
-  uint32_t zl[8], up[8], dn[8];
-  float pe[8], mne[8], za[8], s[8], mn[8];
+// Four groups of a step (rows 4h .. 4h + 3): word k of group j (zl: 4 zl).  mne = -ne.
+struct Groups4 {
+  uint32_t zl[4], up[4], dn[4];
+  float pe[4], mne[4], za[4], s[4], mn[4];
 };
 
-__device__ __forceinline__ void read_groups(const uint8_t* ps, int first, Groups8& G) {
-  auto rd = [&](int k, uint32_t (&o)[8]) __attribute__((always_inline)) {
-    const u32x4 lo = *(const u32x4*)(ps + k * PS_ROW + 4 * first);
-    const u32x4 hi = *(const u32x4*)(ps + k * PS_ROW + 4 * first + 16);
+// Groups first .. first + 3 of the wave's word arrays (one 16-byte read per
+// word; the lanes of a lane group read the same groups: a broadcast).
+__device__ __forceinline__ void read_groups(const uint8_t* ps, int first, Groups4& G) {
+  auto rd = [&](int k) __attribute__((always_inline)) { return *(const u32x4*)(ps + k * PS_ROW + 4 * first); };
+  const u32x4 zl = rd(P_ZL), up = rd(P_UP), dn = rd(P_DN), pe = rd(P_PE), za = rd(P_ZA), sc = rd(P_S),
+              mn = rd(P_MN);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = lo[j], o[4 + j] = hi[j];
-  };
-  uint32_t t[8];
-  rd(P_ZL, G.zl);
-  rd(P_UP, G.up);
-  rd(P_DN, G.dn);
-  rd(P_PE, t);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) G.pe[j] = __uint_as_float(t[j]);
-  rd(P_ZA, t);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) G.za[j] = __uint_as_float(t[j]), G.mne[j] = -clamp_min(G.za[j], kEps);
-  rd(P_S, t);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) G.s[j] = __uint_as_float(t[j]);
-  rd(P_MN, t);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) G.mn[j] = __uint_as_float(t[j]);
+  for (int j = 0; j < 4; ++j) {
+    G.zl[j] = zl[j];
+    G.up[j] = up[j];
+    G.dn[j] = dn[j];
+    G.pe[j] = __uint_as_float(pe[j]);
+    G.za[j] = __uint_as_float(za[j]);
+    G.mne[j] = -clamp_min(G.za[j], kEps);
+    G.s[j] = __uint_as_float(sc[j]);
+    G.mn[j] = __uint_as_float(mn[j]);
+  }
 }
 
 // The reference's fp32 value of code q of group j (quantizer.py:250-255).
@@ -139,9 +133,11 @@ __device__ __forceinline__ void read_groups(const uint8_t* ps, int first, Groups
 // finite metadata za + pe*E <= 1 and za - ne*E >= 0 after rounding, and NaN
 // metadata propagates.  Every address lies inside the table: q - zl <= pb
 // above the zero level, zl - q <= nb below it.
-__device__ __forceinline__ float code_value(const uint8_t* smem, uint32_t q, const Groups8& G, int j) {
-  const bool up = q >= G.zl[j];
-  const uint32_t addr = up ? G.up[j] + 4u * q : G.dn[j] - 4u * q;
+__device__ __forceinline__ float code_value(const uint8_t* smem, uint32_t q, const Groups4& G, int j) {
+  const uint32_t q4 = 4u * q;
+  const bool up = q4 >= G.zl[j];
+  // row start + 4|q - zl| (one v_sad_u16: both below 2^16)
+  const uint32_t addr = __builtin_amdgcn_sad_u16(q4, G.zl[j], up ? G.up[j] : G.dn[j]);
   const float e = *(const float*)(smem + addr);
   const float t = (up ? G.pe[j] : G.mne[j]) * e;
   const float unit = G.za[j] + t;
@@ -149,20 +145,33 @@ __device__ __forceinline__ float code_value(const uint8_t* smem, uint32_t q, con
   return u + G.mn[j];
 }
 
-// The 4 B operands (N-tiles jt = 0..3) of one step from the lane's 8 code
-// words: w[j] = the dword of row j of the step (byte jt = the code of
-// column jt), two rows per B register.
+// Half h of the 4 B operands (N-tiles jt = 0..3) of one step: registers
+// 2h, 2h + 1 of each, from the code words w[j] of rows 4h + j (byte jt = the
+// code of column jt) and those rows' groups; two rows per B register.
 template <int IO>
-__device__ __forceinline__ void dequant_step(const uint8_t* smem, const uint32_t* w, const Groups8& G,
+__device__ __forceinline__ void dequant_half(const uint8_t* smem, const uint32_t* w, const Groups4& G, int h,
                                              u32x4 (&B)[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       const float x0 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i], 8 * jt, 8), G, 2 * i);
       const float x1 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i + 1], 8 * jt, 8), G, 2 * i + 1);
-      B[jt][i] = pack_io2<IO>(x0, x1);
+      B[jt][2 * h + i] = pack_io2<IO>(x0, x1);
     }
+}
+
+// The 4 B operands of one step whose 8 rows' groups start at `first` in the
+// word arrays and whose code words are w[0..7].
+template <int IO>
+__device__ __forceinline__ void dequant_step(const uint8_t* smem, const uint8_t* ps, int first, const uint32_t* w,
+                                             u32x4 (&B)[4]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    Groups4 G;
+    read_groups(ps, first + 4 * h, G);
+    dequant_half<IO>(smem, w + 4 * h, G, h, B);
+  }
 }
 
 // The expm1 rows of one alpha into LDS (bytes 0 .. ET_BYTES of the workgroup's array).
@@ -183,13 +192,6 @@ __device__ __forceinline__ float across_groups_sum(float v) {
   v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-template <int MW>
-__device__ __forceinline__ float2 meta2(const __amdgpu_buffer_rsrc_t& r, int voff, int soff, int dt) {
-  uint32_t w[MW];
-  load_meta<MW>(w, r, voff, soff);
-  return meta_cvt<MW>(w, dt);
 }
 
 // ---------------------------------------------------------------- pass 1
@@ -217,66 +219,85 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
   const bool owner = ((4 * g) % RS) == 0;
   const int h0 = (4 * g) / RS;
   const float scaling2 = a.scaling * kLog2e;
-  const int64_t total = (int64_t)a.batch * a.kv_heads * n_tiles;
   const int64_t ng = a.n_groups;
-  for (int64_t u = (int64_t)blockIdx.x * WAVES + wave; u < total; u += (int64_t)gridDim.x * WAVES) {
-    const int tile = (int)(u % n_tiles);
-    const int64_t bk = u / n_tiles;
-    const int kvh = (int)(bk % a.kv_heads);
-    const int b = (int)(bk / a.kv_heads);
-    // the query operand: row n = head hA's query when rA == 0, else zero
+  // flat tile u = (b*Hkv + kvh)*n_tiles + tile (the host keeps the count below 2^31)
+  const uint32_t total = (uint32_t)a.batch * (uint32_t)a.kv_heads * (uint32_t)n_tiles;
+  const uint32_t stride = gridDim.x * WAVES;
+  const uint32_t dq = stride / (uint32_t)n_tiles, dr = stride % (uint32_t)n_tiles;
+  uint32_t u = blockIdx.x * WAVES + wave;
+  uint32_t tile = u % (uint32_t)n_tiles, bk = u / (uint32_t)n_tiles;
+
+  // The words of a tile (loaded one tile ahead, into the other of two
+  // register sets): the query operand, and for a quantized tile its code
+  // words (KW[8kt + i] = the dword of tokens 4n..4n+3 of channel row
+  // 32kt + 8g + i) and this lane's two key groups' metadata (channels
+  // 2*lane, 2*lane + 1).
+  struct Words {
     u32x4 qa[4];
-    {
-      const bool qrow = rA == 0 && hA < a.n_rep;
-      const uint16_t* qp =
-          (const uint16_t*)a.query + b * a.q_sb + (int64_t)(kvh * a.n_rep + min(hA, a.n_rep - 1)) * a.q_sh;
+    uint32_t KW[32], MN[MW], SC[MW];
+  };
+  auto issue = [&](Words& W, uint32_t t, uint32_t bk_) __attribute__((always_inline)) {
+    const int kvh = (int)(bk_ % (uint32_t)a.kv_heads), b = (int)(bk_ / (uint32_t)a.kv_heads);
+    const bool qrow = rA == 0 && hA < a.n_rep;  // row n = head hA's query when rA == 0, else zero
+    const uint16_t* qp =
+        (const uint16_t*)a.query + b * a.q_sb + (int64_t)(kvh * a.n_rep + min(hA, a.n_rep - 1)) * a.q_sh;
 #pragma unroll
-      for (int kq = 0; kq < 4; ++kq) {
-        const u32x4 v = *(const u32x4*)(qp + 32 * kq + 8 * g);
-        qa[kq] = qrow ? v : u32x4{0u, 0u, 0u, 0u};
-      }
+    for (int kq = 0; kq < 4; ++kq) {
+      const u32x4 v = *(const u32x4*)(qp + 32 * kq + 8 * g);
+      W.qa[kq] = qrow ? v : u32x4{0u, 0u, 0u, 0u};
     }
-    f32x4 s[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int n_valid, pos0;
-    if (tile < a.n_groups) {
-      n_valid = TILE;
-      pos0 = TILE * tile;
+    if ((int)t < a.n_groups) {
       const __amdgpu_buffer_rsrc_t kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * QB);
       const int64_t km = b * a.km_sb + kvh * a.km_sh;
       const __amdgpu_buffer_rsrc_t kmn = make_buf((const uint8_t*)a.k_mn + km * ES, ng * D * ES);
       const __amdgpu_buffer_rsrc_t ksc = make_buf((const uint8_t*)a.k_scale + km * ES, ng * D * ES);
-      // KW[8kt + i] = the dword of tokens 4n..4n+3 of channel row 32kt + 8g + i
-      uint32_t KW[32];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          KW[8 * kt + i] =
-              __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + 4 * n, tile * D * QB + (32 * kt + i) * QB, 0);
-      // this lane's two key groups: channels 2*lane, 2*lane + 1
-      const float2 mn = meta2<MW>(kmn, 2 * lane * ES, tile * D * ES, a.meta_dtype);
-      const float2 sc = meta2<MW>(ksc, 2 * lane * ES, tile * D * ES, a.meta_dtype);
+          W.KW[8 * kt + i] = __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + 4 * n,
+                                                                  (int)t * D * QB + (32 * kt + i) * QB, 0);
+      load_meta<MW>(W.MN, kmn, 2 * lane * ES, (int)t * D * ES);
+      load_meta<MW>(W.SC, ksc, 2 * lane * ES, (int)t * D * ES);
+    }
+  };
+  // one tile from the words in C; the next tile's loads go into N first
+  auto step = [&](Words& C, Words& N) __attribute__((always_inline)) {
+    const int kvh = (int)(bk % (uint32_t)a.kv_heads);
+    const int b = (int)(bk / (uint32_t)a.kv_heads);
+    const bool quant = (int)tile < a.n_groups;
+    if (quant) {
+      const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
       uint32_t w0[PW], w1[PW];
       group_words(mn.x, sc.x, w0);
       group_words(mn.y, sc.y, w1);
 #pragma unroll
       for (int k = 0; k < PW; ++k) *(uint2*)(ps + k * PS_ROW + 8 * lane) = uint2{w0[k], w1[k]};
+    }
+    const uint32_t un = u + stride;
+    uint32_t tn = tile + dr, bkn = bk + dq;
+    if (tn >= (uint32_t)n_tiles) tn -= (uint32_t)n_tiles, ++bkn;
+    if (un < total) issue(N, tn, bkn);
+
+    f32x4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int n_valid, pos0;
+    if (quant) {
+      n_valid = TILE;
+      pos0 = TILE * (int)tile;
       wave_lds_sync();
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        Groups8 G;
-        read_groups(ps, 32 * kt + 8 * g, G);
         u32x4 B[4];
-        dequant_step<IO>(smem, KW + 8 * kt, G, B);
+        dequant_step<IO>(smem, ps, 32 * kt + 8 * g, C.KW + 8 * kt, B);
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], B[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(C.qa[kt], B[jt], s[jt]);
       }
       wave_lds_sync();  // the group words are read before the next tile's are written
     } else {
       // residual tile: dense keys; rows past the filled ones read 0 (masked below)
-      const int r0 = (tile - a.n_groups) * TILE;
+      const int r0 = ((int)tile - a.n_groups) * TILE;
       n_valid = min(TILE, a.n_residual - r0);
       pos0 = TILE * a.n_groups + r0;
       const int kst = (int)a.kr_st * 2;
@@ -290,7 +311,7 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
           kb[jt] = __builtin_bit_cast(u32x4,
                                       __builtin_amdgcn_raw_buffer_load_b128(krb, (4 * n + jt) * kst + 16 * g, 64 * kt, 0));
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], kb[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(C.qa[kt], kb[jt], s[jt]);
       }
     }
     // this lane's logits: head slot sl = MFMA output element sl*RS, tokens 4n + jt
@@ -312,6 +333,16 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
             f32x4{v[0], v[1], v[2], v[3]};
       }
     }
+    u = un;
+    tile = tn;
+    bk = bkn;
+  };
+  Words W0, W1;
+  if (u < total) issue(W0, tile, bk);
+  while (u < total) {
+    step(W0, W1);
+    if (u >= total) break;
+    step(W1, W0);
   }
 }
 
@@ -370,7 +401,31 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[vg][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int tile = t_begin; tile < t_end; ++tile) {
+  // The words of a tile (loaded one tile ahead, into the other of two
+  // register sets), for a quantized tile: its code words (VW[8(2kt + vg) +
+  // j] = the dword of channels 4n..4n+3 of token row 32kt + 8g + j, group
+  // vg) and this lane's two value groups' metadata (groups 0, 1 of token
+  // lane).  This lane's logits of the tile (x[8kt + j] = token 32kt + 8g +
+  // j) are read at its start.
+  struct Words {
+    uint32_t VW[32], MN[MW], SC[MW];
+  };
+  auto issue = [&](Words& W, int t) __attribute__((always_inline)) {
+    if (t < a.n_groups) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int vg = 0; vg < 2; ++vg)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            W.VW[8 * (2 * kt + vg) + j] = __builtin_amdgcn_raw_buffer_load_b32(
+                vp, 8 * g * (2 * QB) + 4 * n, t * TILE * 2 * QB + (32 * kt + j) * (2 * QB) + QB * vg, 0);
+      load_meta<MW>(W.MN, vmn, 2 * lane * ES, t * TILE * 2 * ES);
+      load_meta<MW>(W.SC, vsc, 2 * lane * ES, t * TILE * 2 * ES);
+    }
+  };
+  // one tile from the words in C; the next tile's loads go into N first
+  auto step = [&](const int tile, Words& C, Words& N) __attribute__((always_inline)) {
     const bool quant = tile < a.n_groups;
     float x[16];
 #pragma unroll
@@ -381,20 +436,9 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
 #pragma unroll
         for (int j = 0; j < 4; ++j) x[8 * kt + 4 * h4 + j] = v[j];
       }
-    // VW[8(2kt + vg) + j] = the dword of channels 4n..4n+3 of token row 32kt + 8g + j, group vg
-    uint32_t VW[32];
+    const uint32_t* const VC = C.VW;
     if (quant) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int vg = 0; vg < 2; ++vg)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            VW[8 * (2 * kt + vg) + j] = __builtin_amdgcn_raw_buffer_load_b32(
-                vp, 8 * g * (2 * QB) + 4 * n, tile * TILE * 2 * QB + (32 * kt + j) * (2 * QB) + QB * vg, 0);
-      // this lane's two value groups: groups 0, 1 of token lane
-      const float2 mn = meta2<MW>(vmn, 2 * lane * ES, tile * TILE * 2 * ES, a.meta_dtype);
-      const float2 sc = meta2<MW>(vsc, 2 * lane * ES, tile * TILE * 2 * ES, a.meta_dtype);
+      const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
       uint32_t w0[PW], w1[PW];
       group_words(mn.x, sc.x, w0);
       group_words(mn.y, sc.y, w1);
@@ -404,29 +448,35 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
         *(uint32_t*)(ps + k * PS_ROW + 4 * lane) = w0[k];
         *(uint32_t*)(ps + k * PS_ROW + 4 * (TILE + lane)) = w1[k];
       }
-      wave_lds_sync();
     }
+    // the next tile's loads go out before this tile's work
+    if (tile + 1 < t_end) issue(N, tile + 1);
+    if (quant) wave_lds_sync();
 
     // ---------- online softmax: the tile's maximum of each head
     float tmax = x[0];
 #pragma unroll
     for (int j = 1; j < 16; ++j) tmax = fmaxf(tmax, x[j]);
     tmax = across_groups_max(tmax);
-    float corr[NREP], muse[NREP];
+    // mu / cu: the shift and correction of this lane's head hA; cs[sl]: the
+    // correction of head slot sl's rows
+    float mu = 0.f, cu = 1.f, cs[HS];
+#pragma unroll
+    for (int sl = 0; sl < HS; ++sl) cs[sl] = 1.f;
 #pragma unroll
     for (int h = 0; h < NREP; ++h) {
       const float th = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tmax), RS * h));
       const float m_new = fmaxf(m_run[h], th);
       // while a row is fully masked its maximum stays -inf; 0 stands in for
       // it, so exp2(-inf - 0) gives zero weights and a zero correction
-      muse[h] = m_new == -INFINITY ? 0.f : m_new;
-      corr[h] = __builtin_amdgcn_exp2f(m_run[h] - muse[h]);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float corr = __builtin_amdgcn_exp2f(m_run[h] - m_use);
       m_run[h] = m_new;
-    }
-    float mu = muse[0], cu = corr[0];
+      if (hA == h) mu = m_use, cu = corr;
 #pragma unroll
-    for (int h = 1; h < NREP; ++h)
-      if (hA == h) mu = muse[h], cu = corr[h];
+      for (int sl = 0; sl < HS; ++sl)
+        if (h0 + sl == h) cs[sl] = corr;
+    }
     float p[16];
     float psum = 0.f;
 #pragma unroll
@@ -447,10 +497,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
     // rescale the accumulators (rows sl*RS, sl*RS + 1 of each head slot)
 #pragma unroll
     for (int sl = 0; sl < HS; ++sl) {
-      float c = corr[0];
-#pragma unroll
-      for (int h = 1; h < NREP; ++h)
-        if (h0 + sl == h) c = corr[h];
+      const float c = cs[sl];
       const int i = sl * RS;
 #pragma unroll
       for (int vg = 0; vg < 2; ++vg)
@@ -463,10 +510,8 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int vg = 0; vg < 2; ++vg) {
-          Groups8 G;
-          read_groups(ps, 64 * vg + 32 * kt + 8 * g, G);
           u32x4 B[4];
-          dequant_step<IO>(smem, VW + 8 * (2 * kt + vg), G, B);
+          dequant_step<IO>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
         }
@@ -501,6 +546,13 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
         }
     }
+    };
+  Words W0, W1;
+  if (t_begin < t_end) issue(W0, t_begin);
+  for (int tile = t_begin; tile < t_end; tile += 2) {
+    step(tile, W0, W1);
+    if (tile + 1 >= t_end) break;
+    step(tile + 1, W1, W0);
   }
 
   // ---------------- this split's records: (acc[D], m in natural-log units, l)
