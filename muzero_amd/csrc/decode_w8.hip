@@ -36,7 +36,8 @@
 // them as 7 words (zl, the byte bases of the up and down rows, pe, za, s, mn)
 // in the wave's LDS area, structure of arrays; the lanes of a lane group then
 // read the 8 groups of a step with 16-byte broadcast reads.  A code costs a
-// bit-field extract, a compare, three address / select operations, one
+// byte extract shifted to a byte offset, a compare, a select of the row and
+// one v_sad_u16 for the table address, a select of the coefficient, one
 // 32-bit LDS read and the four fp32 steps.
 #include "decode_tile.hpp"
 
@@ -174,9 +175,12 @@ __device__ __forceinline__ void dequant_step(const uint8_t* smem, const uint8_t*
   }
 }
 
-// The expm1 rows of one alpha into LDS (bytes 0 .. ET_BYTES of the workgroup's array).
+// The expm1 rows of one alpha into LDS (bytes 0 .. 4 ET_N of the
+// workgroup's array): 16 bytes per load, the last ET_N % 4 entries one each.
 __device__ __forceinline__ void load_table(uint8_t* smem, const float* E) {
-  for (int i = threadIdx.x; i < ET_N; i += NT) ((float*)smem)[i] = E[i];
+  constexpr int V = ET_N / 4;
+  for (int i = threadIdx.x; i < V; i += NT) *(u32x4*)(smem + 16 * i) = *(const u32x4*)(E + 4 * i);
+  if (threadIdx.x < ET_N - 4 * V) ((float*)smem)[4 * V + threadIdx.x] = E[4 * V + threadIdx.x];
   __syncthreads();
 }
 
@@ -600,8 +604,12 @@ bool w8_supported(const mz_decode_args* a) {
   const bool fits = (int64_t)a->n_groups * w8::TILE * 2 * w8::QB < ((int64_t)1 << 31) &&
                     (int64_t)a->n_groups * w8::TILE * 2 * es < ((int64_t)1 << 31);
   const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * w8::TILE;
-  return a->bits == 8 && a->head_dim == w8::D && a->n_groups > 0 && fits && aligned && a->n_rep >= 1 &&
-         a->n_rep <= 8 && a->e_key && a->e_value && ((uintptr_t)a->k_packed % 4) == 0 &&
+  // pass 1 counts the flat tiles of all (batch, kv-head) in 32 bits
+  const bool count = (int64_t)a->batch * a->kv_heads * (a->n_groups + (a->n_residual + w8::TILE - 1) / w8::TILE) <
+                     ((int64_t)1 << 31);
+  return a->bits == 8 && a->head_dim == w8::D && a->n_groups > 0 && fits && count && aligned && a->n_rep >= 1 &&
+         a->n_rep <= 8 && a->e_key && a->e_value && ((uintptr_t)a->e_key % 16) == 0 &&
+         ((uintptr_t)a->e_value % 16) == 0 && ((uintptr_t)a->k_packed % 4) == 0 &&
          ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 && a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 &&
          a->vp_sh % 4 == 0 && w8_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
          w8_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
