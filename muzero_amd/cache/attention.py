@@ -23,8 +23,8 @@ when there is a quantized value prefix, and ``fused_prefix_decode_success`` /
 prefix decode with the residual merged in); plus ``hip_fused_decode`` for
 every call the kernel serves, split into ``hip_fold_kernel`` (the fold
 kernel's fp32 values) and ``hip_exact_kernel`` (the layer-dtype values: the
-codebook or the general kernel), and ``hip_{codebook,fold,general}_kernel_calls``
-by the kernel that ran.  When the launch raises, the matching
+codebook, two-pass or general kernel), and
+``hip_{codebook,fold,twopass,general}_kernel_calls`` by the kernel that ran.  When the launch raises, the matching
 ``*_fallback`` counters are incremented as in the reference, and the error
 propagates: this build has no dequantize-then-attend fallback to run instead.
 
@@ -37,11 +37,13 @@ Kernel choice, in the reference's environment-switch style (``attention.py:92``,
 ``:110``, ``:128``), ``MUZERO_DECODE_KERNEL``:
 
 * unset or ``auto``: the codebook kernel where it applies (1-5 bits,
-  head_dim 128), else the fold kernel (1-7 bits), else the general kernel;
+  head_dim 128), else the fold kernel (1-7 bits), else the two-pass kernel
+  (8 bits, head_dim 128), else the general kernel;
 * ``exact``: dequantized values rounded to the layer dtype like the
   reference's dequantize-then-attend path (``attention.py:213-226``,
   ``:274-283``, ``layer.py:263``) on every call: the codebook kernel where it
-  applies (1-5 bits), the general kernel elsewhere;
+  applies (1-5 bits), the two-pass kernel at 8 bits, the general kernel
+  elsewhere;
 * ``fold``: the fold kernel, whose full-precision values are those of the
   reference's fused CUDA kernels (``loader.py:197-263``); raises where it
   does not apply;
@@ -139,7 +141,7 @@ def mu_zero_decode_attention_forward(
         raise
     _count(key_prefix_length, value_prefix_length, "success")
     _MU_ZERO_DECODE_STATS["hip_fused_decode"] += 1
-    # hip_exact_kernel: calls whose values are the layer-dtype dequantized values (codebook or general kernel)
+    # hip_exact_kernel: calls whose values are the layer-dtype dequantized values (codebook, two-pass, general)
     _MU_ZERO_DECODE_STATS["hip_fold_kernel" if kernel == "fold" else "hip_exact_kernel"] += 1
     _MU_ZERO_DECODE_STATS[f"hip_{kernel}_kernel_calls"] += 1
     _MU_ZERO_DECODE_STATS["returns"] += 1

@@ -530,6 +530,44 @@ def test_three_paths_against_the_layer_dtype_path(bits, case):
     assert f.mean().item() <= dflt.mean().item(), (f.mean().item(), dflt.mean().item())
 
 
+@pytest.mark.parametrize("alphas", [(2.0, 2.0), (4.0, 2.0)])
+@pytest.mark.parametrize("case", ["cfg1", "offset", "peaked"])
+def test_twopass_against_the_layer_dtype_path(case, alphas):
+    """8 bits at config 1's row shape: the library's kernel there (the two-pass kernel) and the
+    general kernel meet the attention tolerance against the layer-dtype dequantize-then-attend
+    path, with one alpha and with the two the alpha rules give 8-bit keys with outlier channels
+    and their values (4 and 2); the reference's default GPU decode's distance is reported."""
+    from muzero_amd.kernels import loader as L
+    ak, av = alphas
+    hkv, n_rep, d, length, seed = 8, 4, 128, 4096, 1234
+    offsets = {"cfg1": {}, "offset": dict(k_offset=20.0, v_offset=5.0),
+               "peaked": dict(k_offset=20.0, v_offset=5.0, q_scale=4.0)}[case]
+    k, v, q, _ = ref.synthetic_kv(1, hkv, length, d, hkv * n_rep, seed=seed)
+    k, v, q = _offset_inputs(k, v, q, seed=seed, **offsets)
+    layer, st = ref.reference_decode(q, k, v, bits=8, alpha_k=ak, alpha_v=av, group_size=64, residual=128)
+    dev = lambda t: t.to(DEV)
+    kw = dict(bits=8, n_groups=st["lq"] // 64, k_packed=dev(st["packed_k"]), k_mn=dev(st["k_mn"]),
+              k_scale=dev(st["k_scale"]), v_packed=dev(st["packed_v"]), v_mn=dev(st["v_mn"]),
+              v_scale=dev(st["v_scale"]), k_res=dev(st["res_k"]), v_res=dev(st["res_v"]), alpha_key=ak,
+              alpha_value=av, scaling=d ** -0.5)
+    plan = L.DecodePlan(dev(q), **kw)
+    assert plan.kernel == "twopass"
+    outs = {"twopass": plan.run(), "general": L.DecodePlan(dev(q), kernel_path="general", **kw).run()}
+    torch.cuda.synchronize()
+    layer = layer[:, 0]
+    dist = {name: (o.cpu()[:, 0].double() - layer).abs() for name, o in outs.items()}
+    default = ref.default_path_decode(q, st, 8, ak, av, n_rep, d ** -0.5)
+    dist["default"] = (default.double() - layer).abs()
+    line = " ".join(f"{n} max {e.max().item():.2e} mean {e.mean().item():.2e};" for n, e in dist.items())
+    print(f"8 bits {case} alphas {alphas}: distance to the layer-dtype path: {line}", flush=True)
+    half_ulp = _half_ulp_bf16(layer)
+    rounding = (layer.to(torch.bfloat16).double() - layer).abs().mean().item()
+    for name in ("twopass", "general"):
+        ex = dist[name]
+        assert bool((ex <= MAX_ABS + half_ulp).all()), (name, (ex - MAX_ABS - half_ulp).max().item())
+        assert ex.mean().item() < MEAN_ABS + rounding, (name, ex.mean().item(), rounding)
+
+
 # ---------------------------------------------------------------- codebook kernel
 # The codebook kernel attends with the layer-dtype dequantized values themselves (each group's
 # values formed with the reference's fp32 operation order and rounded to the layer dtype), so
