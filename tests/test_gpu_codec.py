@@ -64,6 +64,39 @@ def test_quantize_rows_meta_dtypes(qgold, dname, mname):
     np.testing.assert_array_equal(bits_of(sc), bits_of(qgold[f"scale_{key}_m{mname}"]))
 
 
+@pytest.mark.parametrize("bits", [5, 8])
+def test_fp32_code_offset_fallback(bits):
+    """From 5 bits the fp32 path estimates each code's offset from the alpha that the table's
+    bins-1 threshold (its entry 0) implies, checks it against the thresholds around it and runs the
+    binary search where the check fails.  With that entry changed so that the estimate is useless
+    (the implied alpha is negative: every window starts at 0), every value above its row's third
+    threshold takes the binary search; no group here has a side of one bin, so no code reads the
+    entry itself, and the codes and metadata still equal the oracle's."""
+    import ctypes
+    from muzero_amd import _lib, tables
+    g = torch.Generator().manual_seed(77 + bits)
+    x = torch.randn(2048, 64, generator=g)
+    pq_ref, mn_ref, sc_ref = ref.quantize_rows(x, bits, 2.0)
+    # every group straddles zero well inside its range: both sides have more than one bin
+    za = (-mn_ref.float() / sc_ref.float()).clamp(0, 1)
+    zl = torch.round(za * ((1 << bits) - 1))
+    assert bool(((zl >= 2) & (zl <= (1 << bits) - 3)).all())
+    table = tables.device_table("thresholds", 2.0, torch.device(DEV)).clone()
+    table[0] = 0.9
+    xd = x.to(DEV)
+    pq = torch.empty(2048, 8 * bits, dtype=torch.uint8, device=DEV)
+    mn = torch.empty(2048, 1, dtype=torch.float16, device=DEV)
+    sc = torch.empty_like(mn)
+    st = _lib.load().muzero_quantize_rows(xd.data_ptr(), _lib.MZ_F32, 2048, 64, pq.data_ptr(), 8 * bits,
+                                          mn.data_ptr(), sc.data_ptr(), _lib.MZ_F16, 1, bits, ctypes.c_float(1e-8),
+                                          table.data_ptr(), _lib.stream_ptr(torch.device(DEV)))
+    torch.cuda.synchronize()
+    assert st == 0, st
+    assert torch.equal(pq.cpu(), pq_ref)
+    assert torch.equal(mn.cpu().view(torch.int16), mn_ref.view(torch.int16))
+    assert torch.equal(sc.cpu().view(torch.int16), sc_ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("dname", list(DT))
 @pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_quantize_rows_random_vs_oracle(dname, bits):
