@@ -230,9 +230,9 @@ typedef struct mz_decode_args {
  *    up to the fp16 rounding of its shifted (P, N) table entries); bits 1 to
  *    7, head_dim 64 or 128, aligned prefixes, n_rep 1 to 8, fold tables
  *    given, at 7 bits one table for keys and values;
- *  - two-pass: the dequantize-then-attend values for 8-bit codes (keys'
- *    logits with the key table in LDS, then softmax and values with the
- *    value table); head_dim 128, aligned prefixes, n_rep 1 to 8; its
+ *  - two-pass: the dequantize-then-attend values for 5- to 8-bit codes
+ *    (keys' logits with the key table in LDS, then softmax and values with
+ *    the value table); head_dim 128, aligned prefixes, n_rep 1 to 8; its
  *    logits (4 bytes per query head and token) live in the workspace after
  *    the split records, so it always runs split kernels + combine;
  *  - general: the dequantize-then-attend values, every width and layout.

@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libmuzero_hip.so")
-SOURCES = ["quantize.hip", "decode.hip", "decode_fold.hip", "decode_cb.hip", "decode_w8.hip", "prologue.hip", "qk_av.hip", "stream.hip"]
+SOURCES = ["quantize.hip", "decode.hip", "decode_fold.hip", "decode_cb.hip", "decode_twopass.hip", "prologue.hip", "qk_av.hip", "stream.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

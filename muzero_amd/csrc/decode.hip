@@ -716,10 +716,10 @@ int fold_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
 bool cb_supported(const mz_decode_args* a);
 int cb_choose_split(const mz_decode_args* a, int* tiles_per_split);
 int cb_launch_partials(const mz_decode_args* a, hipStream_t s, bool direct);
-bool w8_supported(const mz_decode_args* a);
-int w8_choose_split(const mz_decode_args* a, int* tiles_per_split);
-int64_t w8_workspace_bytes(const mz_decode_args* a, int ns);
-int w8_launch_partials(const mz_decode_args* a, hipStream_t s);
+bool tp_supported(const mz_decode_args* a);
+int tp_choose_split(const mz_decode_args* a, int* tiles_per_split);
+int64_t tp_workspace_bytes(const mz_decode_args* a, int ns);
+int tp_launch_partials(const mz_decode_args* a, hipStream_t s);
 
 
 static int choose_split(const mz_decode_args* a, int* tiles_per_split) {
@@ -784,17 +784,18 @@ enum Kernel { K_GENERAL = 0, K_FOLD = 1, K_CODEBOOK = 2, K_TWOPASS = 3 };
 // values: at 1-4 bits at the fold kernel's speed or better, at 5 bits ~13 %
 // slower, kept for the values), else the fold kernel (6-7 bits, head_dim
 // 64, 5 bits with two alphas or more query heads), else the two-pass kernel
-// (8 bits, the layer-dtype values), else the general one.
-// EXACT: the codebook kernel where it applies, else the two-pass kernel,
-// else the general kernel.
+// (8 bits, 7 bits with two alphas: the layer-dtype values), else the general
+// one.
+// EXACT: the codebook kernel where it applies, else the two-pass kernel
+// (5-8 bits), else the general kernel.
 static Kernel which_kernel(const mz_decode_args* a) {
   switch (a->kernel_path) {
     case MZ_PATH_GENERAL: return K_GENERAL;
     case MZ_PATH_FOLD: return fold_supported(a) ? K_FOLD : K_GENERAL;
     case MZ_PATH_CODEBOOK: return cb_supported(a) ? K_CODEBOOK : K_GENERAL;
-    case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : w8_supported(a) ? K_TWOPASS : K_GENERAL;
+    case MZ_PATH_EXACT: return cb_supported(a) ? K_CODEBOOK : tp_supported(a) ? K_TWOPASS : K_GENERAL;
     default:
-      return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : w8_supported(a) ? K_TWOPASS : K_GENERAL;
+      return cb_supported(a) ? K_CODEBOOK : fold_supported(a) ? K_FOLD : tp_supported(a) ? K_TWOPASS : K_GENERAL;
   }
 }
 
@@ -808,7 +809,7 @@ static int plan_split(const mz_decode_args* a, int* tps) {
   switch (which_kernel(a)) {
     case K_FOLD: return fold_choose_split(a, tps);
     case K_CODEBOOK: return cb_choose_split(a, tps);
-    case K_TWOPASS: return w8_choose_split(a, tps);
+    case K_TWOPASS: return tp_choose_split(a, tps);
     default: return choose_split(a, tps);
   }
 }
@@ -816,7 +817,7 @@ static int plan_split(const mz_decode_args* a, int* tps) {
 // Workspace bytes of a planned call: the split records, and for the
 // two-pass kernel its logits after them.
 static int64_t plan_workspace(const mz_decode_args* a, int ns) {
-  if (which_kernel(a) == K_TWOPASS) return w8_workspace_bytes(a, ns);
+  if (which_kernel(a) == K_TWOPASS) return tp_workspace_bytes(a, ns);
   return (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (a->head_dim + 2) * (int64_t)sizeof(float);
 }
 
@@ -825,7 +826,7 @@ static int64_t plan_workspace(const mz_decode_args* a, int ns) {
 static int launch_fast(const mz_decode_args* a, hipStream_t s, bool direct) {
   switch (which_kernel(a)) {
     case K_FOLD: return fold_launch_partials(a, s, direct);
-    case K_TWOPASS: return w8_launch_partials(a, s);
+    case K_TWOPASS: return tp_launch_partials(a, s);
     default: return cb_launch_partials(a, s, direct);
   }
 }

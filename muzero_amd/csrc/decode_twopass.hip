@@ -1,5 +1,5 @@
-// Packed-KV decode attention over 8-bit codes in two passes, attending with
-// the reference's dequantize-then-attend values (gfx950, wave64, MFMA
+// Packed-KV decode attention over 5- to 8-bit codes in two passes, attending
+// with the reference's dequantize-then-attend values (gfx950, wave64, MFMA
 // 16x16x32 in the layer dtype).
 //
 // An 8-bit group has 256 possible values for its 64 codes, so per-group
@@ -7,11 +7,11 @@
 // reference's fp32 operation sequence (muzero/quantizer.py:241-255: t = pe*E
 // above the zero level or -ne*E below it, unit = za + t, x = unit*s + mn)
 // rounded to the layer dtype (muzero/cache/layer.py:263), with E read from the
-// expm1 rows of bins 1..255 (the host-built table, 32,895 fp32 entries =
-// 128.5 KB) held in LDS.  One such table per alpha: keys and values usually
-// have different alphas at 8 bits (quantizer.py:72-77), and two tables do not
-// fit one CU's 160 KB.  Hence two launches, each with its one table in LDS
-// and one workgroup of 8 waves per CU (two per SIMD):
+// expm1 rows of bins 1..2^bits - 1 (the host-built table; 32,895 fp32 entries
+// = 128.5 KB at 8 bits) held in LDS.  One such table per alpha: keys and
+// values usually have different alphas at 8 bits (quantizer.py:72-77), and
+// two 8-bit tables do not fit one CU's 160 KB.  Hence two launches, each with
+// its one table in LDS and one workgroup of 8 waves per CU (two per SIMD):
 //   pass 1 (keys):   S = Q K^T per 64-token tile, written as fp32 logits in
 //                    base-2 units (scaled, masked) to the workspace;
 //   pass 2 (values): the logits back, an online softmax, P V per tile; each
@@ -21,16 +21,19 @@
 // The logits' round trip through HBM is 4 bytes per (query head, token), an
 // eighth of the 32 code bytes per token and kv-head at n_rep 4.
 //
+// The same kernels serve 5-7 bits (the exact path where the codebook kernel
+// does not apply, and 7 bits with two alphas), with the smaller tables.
+//
 // Layout of a tile on the MFMA (as the codebook kernel, decode_cb.hip):
 //   QK: rows = query heads (row RS*h; the others zero), columns = tokens
 //   4n+jt of N-tiles jt = 0..3; lane (n, g) of k-step kt holds channels
 //   32kt+8g+{0..7}.  A lane loads, for each of its 8 channel rows of a
-//   k-step, the dword of its tokens 4n..4n+3 (byte jt = the code of token
-//   4n+jt): every code byte of the tile is loaded once.
+//   k-step, the dword holding its tokens 4n..4n+3 (at 8 bits byte jt = the
+//   code of token 4n+jt): every code of the tile is loaded once.
 //   PV: rows RS*h / RS*h+1 = the high / low parts of the head's weights in
 //   the layer dtype; columns = channels 64vg+4n+jt; lane (n, g) of step
-//   (kt, vg) holds tokens 32kt+8g+{0..7} and loads, for each, the dword of
-//   its channels 4n..4n+3 of value group vg.
+//   (kt, vg) holds tokens 32kt+8g+{0..7} and loads, for each, the dword
+//   holding its channels 4n..4n+3 of value group vg.
 // Group quantities: a lane forms those of two groups of the tile (key
 // channels 2*lane, 2*lane+1; value groups 0, 1 of token lane) and stores
 // them as 7 words (zl, the byte bases of the up and down rows, pe, za, s, mn)
@@ -43,21 +46,32 @@
 
 namespace mz {
 
-namespace w8 {
+namespace tp {
 
 constexpr int D = 128;
 constexpr int TILE = 64;
 constexpr int WAVES = 8;
 constexpr int NT = 64 * WAVES;
-constexpr int QMAX = 255;
-constexpr int QB = 64;                              // bytes per packed 64-code row
-constexpr int ET_N = 32895;                         // expm1 entries of bins 1..255: sum of (bins + 1)
-constexpr int ET_BYTES = (ET_N * 4 + 15) / 16 * 16;
 constexpr int PW = 7;                               // words per group
 constexpr int PS_ROW = 128 * 4;                     // bytes per word row (128 groups)
 constexpr int PS_BYTES = PW * PS_ROW;               // per wave
-constexpr int LDS_BYTES = ET_BYTES + WAVES * PS_BYTES;
-static_assert(LDS_BYTES <= 160 * 1024, "one workgroup per CU");
+
+// Code width BITS (5 to 8).
+template <int BITS>
+struct Fmt {
+  static constexpr int QMAX = (1 << BITS) - 1;
+  static constexpr int QB = 8 * BITS;                         // bytes per packed 64-code row
+  static constexpr int ET_N = QMAX * (QMAX + 3) / 2;           // expm1 entries of bins 1..QMAX: sum of (bins + 1)
+  static constexpr int ET_BYTES = (ET_N * 4 + 15) / 16 * 16;
+  static constexpr int LDS_BYTES = ET_BYTES + WAVES * PS_BYTES;
+  static_assert(LDS_BYTES <= 160 * 1024, "one workgroup per CU");
+  // a lane's 4 codes of a row (tokens or channels 4n..4n+3) are 4*BITS bits
+  // from bit 4*BITS*n: the dword at byte word_byte(n) holds them from bit
+  // word_shift(n) (read unaligned; the last lane's dword moved back inside
+  // the row)
+  static __device__ __forceinline__ int word_byte(int n) { return min((4 * BITS * n) >> 3, QB - 4); }
+  static __device__ __forceinline__ uint32_t word_shift(int n) { return (uint32_t)(4 * BITS * n - 8 * word_byte(n)); }
+};
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr float kLn2 = 0.693147180559945309f;
 constexpr float kEps = 1e-8f;
@@ -88,6 +102,7 @@ __device__ __forceinline__ float io_to_f32(uint16_t h) {
 // all-zero group (stored scale 0) gives x = mn.  zl4 = 4 zl; up / down: the
 // byte address of expm1 entry 0 of the row for codes above / below the zero
 // level, so that code q's entry lies at 4|q - zl| past the side's row start.
+template <int QMAX>
 __device__ __forceinline__ void group_words(float mn, float s, uint32_t (&w)[PW]) {
   const float sg = s >= kEps ? s : kEps;  // NaN -> eps, as deq_row
   const float za = clamp01((0.f - mn) / sg);  // IEEE division: the zero level must match
@@ -149,34 +164,36 @@ __device__ __forceinline__ float code_value(const uint8_t* smem, uint32_t q, con
 // Half h of the 4 B operands (N-tiles jt = 0..3) of one step: registers
 // 2h, 2h + 1 of each, from the code words w[j] of rows 4h + j (byte jt = the
 // code of column jt) and those rows' groups; two rows per B register.
-template <int IO>
-__device__ __forceinline__ void dequant_half(const uint8_t* smem, const uint32_t* w, const Groups4& G, int h,
-                                             u32x4 (&B)[4]) {
+template <int IO, int BITS>
+__device__ __forceinline__ void dequant_half(const uint8_t* smem, const uint32_t* w, uint32_t sh, const Groups4& G,
+                                             int h, u32x4 (&B)[4]) {
 #pragma unroll
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const float x0 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i], 8 * jt, 8), G, 2 * i);
-      const float x1 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i + 1], 8 * jt, 8), G, 2 * i + 1);
+      const float x0 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i], sh + BITS * jt, BITS), G, 2 * i);
+      const float x1 = code_value(smem, __builtin_amdgcn_ubfe(w[2 * i + 1], sh + BITS * jt, BITS), G, 2 * i + 1);
       B[jt][2 * h + i] = pack_io2<IO>(x0, x1);
     }
 }
 
 // The 4 B operands of one step whose 8 rows' groups start at `first` in the
-// word arrays and whose code words are w[0..7].
-template <int IO>
+// word arrays and whose code words are w[0..7] (this lane's codes from bit sh).
+template <int IO, int BITS>
 __device__ __forceinline__ void dequant_step(const uint8_t* smem, const uint8_t* ps, int first, const uint32_t* w,
-                                             u32x4 (&B)[4]) {
+                                             uint32_t sh, u32x4 (&B)[4]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     Groups4 G;
     read_groups(ps, first + 4 * h, G);
-    dequant_half<IO>(smem, w + 4 * h, G, h, B);
+    dequant_half<IO, BITS>(smem, w + 4 * h, sh, G, h, B);
   }
 }
 
-// The expm1 rows of one alpha into LDS (bytes 0 .. 4 ET_N of the
-// workgroup's array): 16 bytes per load, the last ET_N % 4 entries one each.
+// The expm1 rows of bins 1..QMAX of one alpha (the table's first ET_N
+// entries) into LDS (bytes 0 .. 4 ET_N of the workgroup's array): 16 bytes
+// per load, the last ET_N % 4 entries one each.
+template <int ET_N>
 __device__ __forceinline__ void load_table(uint8_t* smem, const float* E) {
   constexpr int V = ET_N / 4;
   for (int i = threadIdx.x; i < V; i += NT) *(u32x4*)(smem + 16 * i) = *(const u32x4*)(E + 4 * i);
@@ -203,20 +220,24 @@ __device__ __forceinline__ float across_groups_sum(float v) {
 // (one workgroup per CU); wave u of the grid takes flat tiles u, u + 8*grid, ...
 // logits[(b*Hq + q-head)*lt + token] = (q . k) * scaling * log2(e), plus the
 // additive mask times log2(e); -inf past the filled residual rows.
-template <int IO, int NREP, int MW>
+template <int IO, int NREP, int MW, int BITS>
 __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, float* __restrict__ logits, int n_tiles,
                                                     int64_t lt) {
   using M = Mfma<IO>;
   constexpr int RS = 16 / NREP;
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;
   constexpr int ES = 2 * MW;  // metadata bytes per entry
-  __shared__ __align__(16) uint8_t smem[LDS_BYTES];
+  using F = Fmt<BITS>;
+  constexpr int QB = F::QB;
+  __shared__ __align__(16) uint8_t smem[F::LDS_BYTES];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  load_table(smem, a.e_key);
-  uint8_t* const ps = smem + ET_BYTES + wave * PS_BYTES;
+  load_table<F::ET_N>(smem, a.e_key);
+  uint8_t* const ps = smem + F::ET_BYTES + wave * PS_BYTES;
+  const int wbyte = F::word_byte(n);      // this lane's code dword of a row, and its codes' first bit
+  const uint32_t wsh = F::word_shift(n);
 
   const int Hq = a.kv_heads * a.n_rep;
   const int hA = n / RS, rA = n % RS;
@@ -259,7 +280,7 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          W.KW[8 * kt + i] = __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + 4 * n,
+          W.KW[8 * kt + i] = __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + wbyte,
                                                                   (int)t * D * QB + (32 * kt + i) * QB, 0);
       load_meta<MW>(W.MN, kmn, 2 * lane * ES, (int)t * D * ES);
       load_meta<MW>(W.SC, ksc, 2 * lane * ES, (int)t * D * ES);
@@ -273,8 +294,8 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
     if (quant) {
       const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
       uint32_t w0[PW], w1[PW];
-      group_words(mn.x, sc.x, w0);
-      group_words(mn.y, sc.y, w1);
+      group_words<F::QMAX>(mn.x, sc.x, w0);
+      group_words<F::QMAX>(mn.y, sc.y, w1);
 #pragma unroll
       for (int k = 0; k < PW; ++k) *(uint2*)(ps + k * PS_ROW + 8 * lane) = uint2{w0[k], w1[k]};
     }
@@ -294,7 +315,7 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         u32x4 B[4];
-        dequant_step<IO>(smem, ps, 32 * kt + 8 * g, C.KW + 8 * kt, B);
+        dequant_step<IO, BITS>(smem, ps, 32 * kt + 8 * g, C.KW + 8 * kt, wsh, B);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(C.qa[kt], B[jt], s[jt]);
       }
@@ -353,7 +374,7 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
 // ---------------------------------------------------------------- pass 2
 // One wave per split (a run of tps tiles of one (batch, kv-head)): unit u =
 // (b*Hkv + kvh)*ns + split is wave u % 8 of workgroup u / 8.
-template <int IO, int NREP, int MW>
+template <int IO, int NREP, int MW, int BITS>
 __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, const float* __restrict__ logits,
                                                     int n_tiles, int64_t lt, int tps, int ns) {
   using M = Mfma<IO>;
@@ -361,13 +382,17 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
   static_assert(RS >= 2, "P.V needs a second row per head for the weights' low part");
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;
   constexpr int ES = 2 * MW;
-  __shared__ __align__(16) uint8_t smem[LDS_BYTES];
+  using F = Fmt<BITS>;
+  constexpr int QB = F::QB;
+  __shared__ __align__(16) uint8_t smem[F::LDS_BYTES];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  load_table(smem, a.e_value);
-  uint8_t* const ps = smem + ET_BYTES + wave * PS_BYTES;
+  load_table<F::ET_N>(smem, a.e_value);
+  uint8_t* const ps = smem + F::ET_BYTES + wave * PS_BYTES;
+  const int wbyte = F::word_byte(n);      // this lane's code dword of a row, and its codes' first bit
+  const uint32_t wsh = F::word_shift(n);
 
   const int64_t unit = (int64_t)blockIdx.x * WAVES + wave;
   if (unit >= (int64_t)a.batch * a.kv_heads * ns) return;
@@ -423,7 +448,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
 #pragma unroll
           for (int j = 0; j < 8; ++j)
             W.VW[8 * (2 * kt + vg) + j] = __builtin_amdgcn_raw_buffer_load_b32(
-                vp, 8 * g * (2 * QB) + 4 * n, t * TILE * 2 * QB + (32 * kt + j) * (2 * QB) + QB * vg, 0);
+                vp, 8 * g * (2 * QB) + wbyte, t * TILE * 2 * QB + (32 * kt + j) * (2 * QB) + QB * vg, 0);
       load_meta<MW>(W.MN, vmn, 2 * lane * ES, t * TILE * 2 * ES);
       load_meta<MW>(W.SC, vsc, 2 * lane * ES, t * TILE * 2 * ES);
     }
@@ -444,8 +469,8 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
     if (quant) {
       const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
       uint32_t w0[PW], w1[PW];
-      group_words(mn.x, sc.x, w0);
-      group_words(mn.y, sc.y, w1);
+      group_words<F::QMAX>(mn.x, sc.x, w0);
+      group_words<F::QMAX>(mn.y, sc.y, w1);
       // group (token t, vg) at index 64*vg + t
 #pragma unroll
       for (int k = 0; k < PW; ++k) {
@@ -515,7 +540,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
 #pragma unroll
         for (int vg = 0; vg < 2; ++vg) {
           u32x4 B[4];
-          dequant_step<IO>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), B);
+          dequant_step<IO, BITS>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), wsh, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
         }
@@ -589,43 +614,44 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
   }
 }
 
-}  // namespace w8
+}  // namespace tp
 
 // ------------------------------------------------------------------ host side
 
-static bool w8_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
+static bool tp_meta_aligned(const void* p, int64_t sb, int64_t sh, int dt) {
   const int pair = dt == MZ_F32 ? 8 : 4;  // two adjacent entries are read at once
   return ((uintptr_t)p % pair) == 0 && sb % 2 == 0 && sh % 2 == 0;
 }
 
-bool w8_supported(const mz_decode_args* a) {
+bool tp_supported(const mz_decode_args* a) {
   const int64_t es = a->meta_dtype == MZ_F32 ? 4 : 2;
   // buffer-resource ranges are 32-bit
-  const bool fits = (int64_t)a->n_groups * w8::TILE * 2 * w8::QB < ((int64_t)1 << 31) &&
-                    (int64_t)a->n_groups * w8::TILE * 2 * es < ((int64_t)1 << 31);
-  const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * w8::TILE;
+  const bool fits = (int64_t)a->n_groups * tp::TILE * 2 * (8 * a->bits) < ((int64_t)1 << 31) &&
+                    (int64_t)a->n_groups * tp::TILE * 2 * es < ((int64_t)1 << 31);
+  const bool aligned = a->v_prefix == 0 || a->v_prefix == a->n_groups * tp::TILE;
   // pass 1 counts the flat tiles of all (batch, kv-head) in 32 bits
-  const bool count = (int64_t)a->batch * a->kv_heads * (a->n_groups + (a->n_residual + w8::TILE - 1) / w8::TILE) <
+  const bool count = (int64_t)a->batch * a->kv_heads * (a->n_groups + (a->n_residual + tp::TILE - 1) / tp::TILE) <
                      ((int64_t)1 << 31);
-  return a->bits == 8 && a->head_dim == w8::D && a->n_groups > 0 && fits && count && aligned && a->n_rep >= 1 &&
+  return a->bits >= 5 && a->bits <= 8 && a->head_dim == tp::D && a->n_groups > 0 && fits && count && aligned &&
+         a->n_rep >= 1 &&
          a->n_rep <= 8 && a->e_key && a->e_value && ((uintptr_t)a->e_key % 16) == 0 &&
          ((uintptr_t)a->e_value % 16) == 0 && ((uintptr_t)a->k_packed % 4) == 0 &&
          ((uintptr_t)a->v_packed % 4) == 0 && a->kp_sb % 4 == 0 && a->kp_sh % 4 == 0 && a->vp_sb % 4 == 0 &&
-         a->vp_sh % 4 == 0 && w8_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
-         w8_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
-         w8_meta_aligned(a->v_mn, a->vm_sb, a->vm_sh, a->meta_dtype) &&
-         w8_meta_aligned(a->v_scale, a->vm_sb, a->vm_sh, a->meta_dtype);
+         a->vp_sh % 4 == 0 && tp_meta_aligned(a->k_mn, a->km_sb, a->km_sh, a->meta_dtype) &&
+         tp_meta_aligned(a->k_scale, a->km_sb, a->km_sh, a->meta_dtype) &&
+         tp_meta_aligned(a->v_mn, a->vm_sb, a->vm_sh, a->meta_dtype) &&
+         tp_meta_aligned(a->v_scale, a->vm_sb, a->vm_sh, a->meta_dtype);
 }
 
-static int w8_tiles(const mz_decode_args* a) { return a->n_groups + (a->n_residual + w8::TILE - 1) / w8::TILE; }
+static int tp_tiles(const mz_decode_args* a) { return a->n_groups + (a->n_residual + tp::TILE - 1) / tp::TILE; }
 
-int w8_choose_split(const mz_decode_args* a, int* tiles_per_split) {
-  const int n_tiles = w8_tiles(a);
+int tp_choose_split(const mz_decode_args* a, int* tiles_per_split) {
+  const int n_tiles = tp_tiles(a);
   int ns = a->n_split;
   if (ns <= 0) {
     // one wave per split: fill the CUs' 8 resident waves once
     const int64_t units = std::max<int64_t>(1, (int64_t)a->batch * a->kv_heads);
-    const int64_t slots = (int64_t)w8::WAVES * device_cu_count();
+    const int64_t slots = (int64_t)tp::WAVES * device_cu_count();
     ns = (int)((slots + units - 1) / units);
     ns = max(1, min(ns, (n_tiles + 1) / 2));  // at least 2 tiles per split
   }
@@ -636,57 +662,68 @@ int w8_choose_split(const mz_decode_args* a, int* tiles_per_split) {
 }
 
 // Bytes of the split records, then the logits (256-byte aligned).
-static int64_t w8_records_bytes(const mz_decode_args* a, int ns) {
-  const int64_t r = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (w8::D + 2) * (int64_t)sizeof(float);
+static int64_t tp_records_bytes(const mz_decode_args* a, int ns) {
+  const int64_t r = (int64_t)a->batch * a->kv_heads * a->n_rep * ns * (tp::D + 2) * (int64_t)sizeof(float);
   return (r + 255) / 256 * 256;
 }
 
-int64_t w8_workspace_bytes(const mz_decode_args* a, int ns) {
-  return w8_records_bytes(a, ns) +
-         (int64_t)a->batch * a->kv_heads * a->n_rep * w8_tiles(a) * w8::TILE * (int64_t)sizeof(float);
+int64_t tp_workspace_bytes(const mz_decode_args* a, int ns) {
+  return tp_records_bytes(a, ns) +
+         (int64_t)a->batch * a->kv_heads * a->n_rep * tp_tiles(a) * tp::TILE * (int64_t)sizeof(float);
+}
+
+template <int IO, int NR, int MW, int BB>
+static void tp_launch_one(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
+  const int64_t lt = (int64_t)n_tiles * tp::TILE;
+  const int64_t total = (int64_t)a->batch * a->kv_heads * n_tiles;
+  const int64_t g1 = std::min<int64_t>(device_cu_count(), (total + tp::WAVES - 1) / tp::WAVES);
+  hipLaunchKernelGGL((tp::logits_kernel<IO, NR, MW, BB>), dim3((unsigned)g1), dim3(tp::NT), 0, s, *a, logits,
+                     n_tiles, lt);
+  const int64_t units = (int64_t)a->batch * a->kv_heads * ns;
+  hipLaunchKernelGGL((tp::attend_kernel<IO, NR, MW, BB>), dim3((unsigned)((units + tp::WAVES - 1) / tp::WAVES)),
+                     dim3(tp::NT), 0, s, *a, (const float*)logits, n_tiles, lt, tps, ns);
 }
 
 template <int IO, int NR, int MW>
-static void w8_launch_one(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
-  const int64_t lt = (int64_t)n_tiles * w8::TILE;
-  const int64_t total = (int64_t)a->batch * a->kv_heads * n_tiles;
-  const int64_t g1 = std::min<int64_t>(device_cu_count(), (total + w8::WAVES - 1) / w8::WAVES);
-  hipLaunchKernelGGL((w8::logits_kernel<IO, NR, MW>), dim3((unsigned)g1), dim3(w8::NT), 0, s, *a, logits, n_tiles,
-                     lt);
-  const int64_t units = (int64_t)a->batch * a->kv_heads * ns;
-  hipLaunchKernelGGL((w8::attend_kernel<IO, NR, MW>), dim3((unsigned)((units + w8::WAVES - 1) / w8::WAVES)),
-                     dim3(w8::NT), 0, s, *a, (const float*)logits, n_tiles, lt, tps, ns);
-}
-
-template <int IO, int NR>
-static void w8_launch_nr(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
-  if (a->meta_dtype == MZ_F32) w8_launch_one<IO, NR, 2>(a, s, logits, n_tiles, tps, ns);
-  else w8_launch_one<IO, NR, 1>(a, s, logits, n_tiles, tps, ns);
-}
-
-template <int IO>
-static int w8_launch_io(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
-  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
-  switch (a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0) {
-    case 1: w8_launch_nr<IO, 1>(a, s, logits, n_tiles, tps, ns); break;
-    case 2: w8_launch_nr<IO, 2>(a, s, logits, n_tiles, tps, ns); break;
-    case 4: w8_launch_nr<IO, 4>(a, s, logits, n_tiles, tps, ns); break;
-    case 8: w8_launch_nr<IO, 8>(a, s, logits, n_tiles, tps, ns); break;
+static int tp_launch_bits(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
+  switch (a->bits) {
+    case 5: tp_launch_one<IO, NR, MW, 5>(a, s, logits, n_tiles, tps, ns); break;
+    case 6: tp_launch_one<IO, NR, MW, 6>(a, s, logits, n_tiles, tps, ns); break;
+    case 7: tp_launch_one<IO, NR, MW, 7>(a, s, logits, n_tiles, tps, ns); break;
+    case 8: tp_launch_one<IO, NR, MW, 8>(a, s, logits, n_tiles, tps, ns); break;
     default: return MZ_EUNSUPPORTED;
   }
   return MZ_OK;
 }
 
+template <int IO, int NR>
+static int tp_launch_nr(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
+  return a->meta_dtype == MZ_F32 ? tp_launch_bits<IO, NR, 2>(a, s, logits, n_tiles, tps, ns)
+                                 : tp_launch_bits<IO, NR, 1>(a, s, logits, n_tiles, tps, ns);
+}
+
+template <int IO>
+static int tp_launch_io(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
+  // query heads per kv-head of the kernel that runs: n_rep rounded up to a power of two
+  switch (a->n_rep <= 1 ? 1 : a->n_rep <= 2 ? 2 : a->n_rep <= 4 ? 4 : a->n_rep <= 8 ? 8 : 0) {
+    case 1: return tp_launch_nr<IO, 1>(a, s, logits, n_tiles, tps, ns);
+    case 2: return tp_launch_nr<IO, 2>(a, s, logits, n_tiles, tps, ns);
+    case 4: return tp_launch_nr<IO, 4>(a, s, logits, n_tiles, tps, ns);
+    case 8: return tp_launch_nr<IO, 8>(a, s, logits, n_tiles, tps, ns);
+    default: return MZ_EUNSUPPORTED;
+  }
+}
+
 // Both passes; the records go to the start of the workspace (the combine
 // kernel's layout), the logits after them.
-int w8_launch_partials(const mz_decode_args* a, hipStream_t s) {
+int tp_launch_partials(const mz_decode_args* a, hipStream_t s) {
   int tps;
-  const int ns = w8_choose_split(a, &tps);
-  if (!a->workspace || a->workspace_bytes < w8_workspace_bytes(a, ns)) return MZ_EWORKSPACE;
-  float* logits = (float*)((uint8_t*)a->workspace + w8_records_bytes(a, ns));
-  const int n_tiles = w8_tiles(a);
-  const int st = a->io_dtype == MZ_BF16 ? w8_launch_io<MZ_BF16>(a, s, logits, n_tiles, tps, ns)
-                                        : w8_launch_io<MZ_F16>(a, s, logits, n_tiles, tps, ns);
+  const int ns = tp_choose_split(a, &tps);
+  if (!a->workspace || a->workspace_bytes < tp_workspace_bytes(a, ns)) return MZ_EWORKSPACE;
+  float* logits = (float*)((uint8_t*)a->workspace + tp_records_bytes(a, ns));
+  const int n_tiles = tp_tiles(a);
+  const int st = a->io_dtype == MZ_BF16 ? tp_launch_io<MZ_BF16>(a, s, logits, n_tiles, tps, ns)
+                                        : tp_launch_io<MZ_F16>(a, s, logits, n_tiles, tps, ns);
   if (st != MZ_OK) return st;
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MZ_OK : (int)e;

@@ -66,7 +66,7 @@ def expected_kernel(kernel_path, bits, d, n_rep, lq, alpha_k=2.0, alpha_v=2.0):
     if kernel_path in ("fold", "codebook", "general"):
         return kernel_path
     cb = codebook_takes(bits, d, n_rep, lq, alpha_k, alpha_v)
-    twopass = bits == 8 and d == 128 and lq > 0 and 1 <= n_rep <= 8
+    twopass = 5 <= bits <= 8 and d == 128 and lq > 0 and 1 <= n_rep <= 8
     if kernel_path == "exact":
         return "codebook" if cb else "twopass" if twopass else "general"
     fold = d in (64, 128) and lq > 0 and 1 <= n_rep <= 8 and (1 <= bits <= 6 or (bits == 7 and alpha_k == alpha_v))

@@ -670,44 +670,65 @@ def test_codebook_kernel_single_split_direct_output_matches_two_kernel_path(bits
     assert torch.equal(direct.view(torch.int16), two.view(torch.int16))
 
 
-# 8 bits: the two-pass kernel (AUTO and EXACT run it), the layer-dtype values like the codebook
+# 5- to 8-bit codes: the two-pass kernel (AUTO runs it at 8 bits and at 7 bits with two alphas,
+# EXACT wherever the codebook kernel does not apply), the layer-dtype values like the codebook
 # kernel, so held to the same bounds against the fp64 oracle over those values.
+TP_BITS = [8, 7, 6, 5]
+
+
+@pytest.mark.parametrize("bits", TP_BITS)
 @pytest.mark.parametrize("shape", CB_SHAPES, ids=lambda c: "B{}_kv{}_r{}_d{}_L{}_R{}".format(*c))
-def test_twopass_kernel(shape):
+def test_twopass_kernel(shape, bits):
     B, hkv, n_rep, d, length, residual = shape
-    mx, mean, _, _ = _run_case(B, hkv, n_rep, d, length, 8, residual, kernel_path="exact", expect_kernel="twopass")
-    print(f"{shape}: max {mx:.2e} mean {mean:.2e}", flush=True)
+    # at 5 bits with up to 4 query heads and one alpha EXACT runs the codebook kernel: two alphas here
+    mx, mean, _, _ = _run_case(B, hkv, n_rep, d, length, bits, residual, kernel_path="exact", expect_kernel="twopass",
+                               alpha_k=4.0, alpha_v=2.0)
+    print(f"{shape} bits={bits}: max {mx:.2e} mean {mean:.2e}", flush=True)
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", TP_BITS)
 @pytest.mark.parametrize("dtype,meta", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
                                         (torch.bfloat16, torch.float32), (torch.float16, torch.float32)])
-def test_twopass_kernel_dtypes(dtype, meta):
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, 8, 128, dtype=dtype, meta=meta, expect_kernel="twopass")
+def test_twopass_kernel_dtypes(dtype, meta, bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 900, bits, 128, dtype=dtype, meta=meta, kernel_path="exact",
+                               expect_kernel="twopass", alpha_k=4.0, alpha_v=2.0)
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", [8, 7])
 @pytest.mark.parametrize("alphas", [(4.0, 2.0), (16.0, 16.0)])
 @pytest.mark.parametrize("mask", ["float", "bool"])
 @pytest.mark.parametrize("n_split", [0, 1, 3, 64])
-def test_twopass_kernel_split_and_mask(n_split, mask, alphas):
-    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, 8, 128, mask=mask, n_split=n_split, expect_kernel="twopass",
-                               alpha_k=alphas[0], alpha_v=alphas[1])
+def test_twopass_kernel_split_and_mask(n_split, mask, alphas, bits):
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 2000, bits, 128, mask=mask, n_split=n_split, kernel_path="exact",
+                               expect_kernel="twopass", alpha_k=alphas[0], alpha_v=alphas[1])
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", TP_BITS)
 @pytest.mark.parametrize("q_scale", [1.0, 4.0])
-def test_twopass_kernel_offset_and_peaked(q_scale):
+def test_twopass_kernel_offset_and_peaked(q_scale, bits):
     """One-signed key and value groups (|mn| >> scale) and, with the query x4, peaked rows."""
-    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, 8, 128, seed=11, k_offset=20.0, v_offset=5.0,
-                                   q_scale=q_scale, expect_kernel="twopass")
+    mx, mean, _, exact = _run_case(2, 2, 4, 128, 1500, bits, 128, seed=11, k_offset=20.0, v_offset=5.0,
+                                   q_scale=q_scale, kernel_path="exact", expect_kernel="twopass", alpha_k=4.0,
+                                   alpha_v=2.0)
     scale = max(1.0, exact.abs().max().item())
     assert mx < CB_MAX_ABS * scale and mean < CB_MEAN_ABS * scale, (mx, mean)
 
 
+@pytest.mark.parametrize("bits", [8, 6])
 @pytest.mark.parametrize("length", [8192, 32768])
-def test_twopass_kernel_long_context(length):
-    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, 8, 128, seed=length, expect_kernel="twopass")
+def test_twopass_kernel_long_context(length, bits):
+    mx, mean, _, _ = _run_case(1, 2, 4, 128, length, bits, 128, seed=length, kernel_path="exact",
+                               expect_kernel="twopass", alpha_k=4.0, alpha_v=2.0)
+    assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
+
+
+def test_seven_bits_two_alphas_run_the_twopass_kernel():
+    """AUTO at 7 bits: the fold kernel needs one table for keys and values; with two alphas the
+    call runs the two-pass kernel (it ran the general kernel before)."""
+    mx, mean, _, _ = _run_case(2, 2, 4, 128, 1500, 7, 128, alpha_k=4.0, alpha_v=2.0, expect_kernel="twopass")
     assert mx < CB_MAX_ABS and mean < CB_MEAN_ABS, (mx, mean)
 
 
