@@ -38,11 +38,11 @@ Kernel choice, in the reference's environment-switch style (``attention.py:92``,
 
 * unset or ``auto``: the codebook kernel where it applies (1-5 bits,
   head_dim 128), else the fold kernel (1-7 bits), else the two-pass kernel
-  (8 bits, head_dim 128), else the general kernel;
+  (8 bits and 7 bits with two alphas, head_dim 128), else the general kernel;
 * ``exact``: dequantized values rounded to the layer dtype like the
   reference's dequantize-then-attend path (``attention.py:213-226``,
   ``:274-283``, ``layer.py:263``) on every call: the codebook kernel where it
-  applies (1-5 bits), the two-pass kernel at 8 bits, the general kernel
+  applies (1-5 bits), the two-pass kernel at 5-8 bits, the general kernel
   elsewhere;
 * ``fold``: the fold kernel, whose full-precision values are those of the
   reference's fused CUDA kernels (``loader.py:197-263``); raises where it
