@@ -592,7 +592,8 @@ def main():
     else:
         ms_split = time_region(lambda i: plans[i % len(plans)].partials(), args.steps, stream)
         ms_combine = time_region(lambda i: plans[i % len(plans)].combine(), args.steps, stream)
-        kernels_ms = {"decode_split": round(ms_split, 5), "decode_combine": round(ms_combine, 5)}
+        split_name = "decode_twopass_logits_and_attend" if plans[0].kernel == "twopass" else "decode_split"
+        kernels_ms = {split_name: round(ms_split, 5), "decode_combine": round(ms_combine, 5)}
         ms_kernel = ms_split
 
     nbytes = algorithmic_bytes(B, hkv, hq, d, lq, r, bits)
