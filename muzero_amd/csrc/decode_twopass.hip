@@ -18,8 +18,9 @@
 //                    wave owns one contiguous run of tiles (a split) and
 //                    writes its (acc, m, l) record, merged by the combine
 //                    kernel of decode.hip.
-// The logits' round trip through HBM is 4 bytes per (query head, token), an
-// eighth of the 32 code bytes per token and kv-head at n_rep 4.
+// The logits' round trip through HBM is 4 bytes per (query head, token),
+// written once and read once: at n_rep 4 and 8 bits, 32 bytes per token and
+// kv-head against its 256 code bytes.
 //
 // The same kernels serve 5-7 bits (the exact path where the codebook kernel
 // does not apply, and 7 bits with two alphas), with the smaller tables.
@@ -38,10 +39,11 @@
 // channels 2*lane, 2*lane+1; value groups 0, 1 of token lane) and stores
 // them as 7 words (zl, the byte bases of the up and down rows, pe, za, s, mn)
 // in the wave's LDS area, structure of arrays; the lanes of a lane group then
-// read the 8 groups of a step with 16-byte broadcast reads.  A code costs a
-// byte extract shifted to a byte offset, a compare, a select of the row and
-// one v_sad_u16 for the table address, a select of the coefficient, one
-// 32-bit LDS read and the four fp32 steps.
+// read the 4 groups of a half step with one 16-byte broadcast read per word.
+// A code costs its extract scaled to a byte offset (one SDWA shift at 8
+// bits), a compare, a select of the row and one v_sad_u16 for the table
+// address, a select of the coefficient, one 32-bit LDS read and the four
+// fp32 steps.
 #include "decode_tile.hpp"
 
 namespace mz {
@@ -76,8 +78,6 @@ constexpr float kLog2e = 1.44269504088896341f;
 constexpr float kLn2 = 0.693147180559945309f;
 constexpr float kEps = 1e-8f;
 enum { P_ZL = 0, P_UP, P_DN, P_PE, P_ZA, P_S, P_MN };
-
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // Two fp32 values rounded to the io dtype (round to nearest even), packed low / high.
 template <int IO>
