@@ -11,11 +11,13 @@
 // = 128.5 KB at 8 bits) held in LDS.  One such table per alpha: keys and
 // values usually have different alphas at 8 bits (quantizer.py:72-77), and
 // two 8-bit tables do not fit one CU's 160 KB.  Hence two launches, each with
-// its one table in LDS and one workgroup of 8 waves per CU (two per SIMD):
-//   pass 1 (keys):   S = Q K^T per 64-token tile, written as fp32 logits in
-//                    base-2 units (scaled, masked) to the workspace;
-//   pass 2 (values): the logits back, an online softmax, P V per tile; each
-//                    wave owns one contiguous run of tiles (a split) and
+// its one table in LDS and one workgroup per CU:
+//   pass 1 (keys):   12 waves (three per SIMD); S = Q K^T per 64-token tile,
+//                    written as fp32 logits in base-2 units (scaled, masked)
+//                    to the workspace;
+//   pass 2 (values): 8 waves (two per SIMD); the logits back, an online
+//                    softmax, P V per tile; each wave owns one contiguous
+//                    run of tiles (a split) and
 //                    writes its (acc, m, l) record, merged by the combine
 //                    kernel of decode.hip.
 // The logits' round trip through HBM is 4 bytes per (query head, token),
@@ -40,6 +42,8 @@
 // them as 7 words (zl, the byte bases of the up and down rows, pe, za, s, mn)
 // in the wave's LDS area, structure of arrays; the lanes of a lane group then
 // read the 4 groups of a half step with one 16-byte broadcast read per word.
+// Pass 1 keeps the words of 64 key groups at a time (channels 0-63, then
+// 64-127: half the area, so that 12 waves' areas fit beside the table).
 // A code costs its extract scaled to a byte offset (one SDWA shift at 8
 // bits), a compare, a select of the row and one v_sad_u16 for the table
 // address, a select of the coefficient, one 32-bit LDS read and the four
@@ -52,11 +56,15 @@ namespace tp {
 
 constexpr int D = 128;
 constexpr int TILE = 64;
-constexpr int WAVES = 8;
+constexpr int WAVES = 8;                            // pass 2
 constexpr int NT = 64 * WAVES;
+constexpr int WAVES_1 = 12;                         // pass 1
+constexpr int NT_1 = 64 * WAVES_1;
 constexpr int PW = 7;                               // words per group
-constexpr int PS_ROW = 128 * 4;                     // bytes per word row (128 groups)
+constexpr int PS_ROW = 128 * 4;                     // bytes per word row (128 groups), pass 2
 constexpr int PS_BYTES = PW * PS_ROW;               // per wave
+constexpr int PS_ROW_1 = 64 * 4;                    // pass 1: 64 groups
+constexpr int PS_BYTES_1 = PW * PS_ROW_1;
 
 // Code width BITS (5 to 8).
 template <int BITS>
@@ -66,7 +74,8 @@ struct Fmt {
   static constexpr int ET_N = QMAX * (QMAX + 3) / 2;           // expm1 entries of bins 1..QMAX: sum of (bins + 1)
   static constexpr int ET_BYTES = (ET_N * 4 + 15) / 16 * 16;
   static constexpr int LDS_BYTES = ET_BYTES + WAVES * PS_BYTES;
-  static_assert(LDS_BYTES <= 160 * 1024, "one workgroup per CU");
+  static constexpr int LDS_BYTES_1 = ET_BYTES + WAVES_1 * PS_BYTES_1;
+  static_assert(LDS_BYTES <= 160 * 1024 && LDS_BYTES_1 <= 160 * 1024, "one workgroup per CU");
   // a lane's 4 codes of a row (tokens or channels 4n..4n+3) are 4*BITS bits
   // from bit 4*BITS*n: the dword at byte word_byte(n) holds them from bit
   // word_shift(n) (read unaligned; the last lane's dword moved back inside
@@ -125,10 +134,12 @@ struct Groups4 {
   float pe[4], mne[4], za[4], s[4], mn[4];
 };
 
-// Groups first .. first + 3 of the wave's word arrays (one 16-byte read per
-// word; the lanes of a lane group read the same groups: a broadcast).
+// Groups first .. first + 3 of the wave's word arrays, rows of ROW bytes (one
+// 16-byte read per word; the lanes of a lane group read the same groups: a
+// broadcast).
+template <int ROW>
 __device__ __forceinline__ void read_groups(const uint8_t* ps, int first, Groups4& G) {
-  auto rd = [&](int k) __attribute__((always_inline)) { return *(const u32x4*)(ps + k * PS_ROW + 4 * first); };
+  auto rd = [&](int k) __attribute__((always_inline)) { return *(const u32x4*)(ps + k * ROW + 4 * first); };
   const u32x4 zl = rd(P_ZL), up = rd(P_UP), dn = rd(P_DN), pe = rd(P_PE), za = rd(P_ZA), sc = rd(P_S),
               mn = rd(P_MN);
 #pragma unroll
@@ -178,25 +189,27 @@ __device__ __forceinline__ void dequant_half(const uint8_t* smem, const uint32_t
 }
 
 // The 4 B operands of one step whose 8 rows' groups start at `first` in the
-// word arrays and whose code words are w[0..7] (this lane's codes from bit sh).
-template <int IO, int BITS>
+// word arrays (rows of ROW bytes) and whose code words are w[0..7] (this
+// lane's codes from bit sh).
+template <int IO, int BITS, int ROW>
 __device__ __forceinline__ void dequant_step(const uint8_t* smem, const uint8_t* ps, int first, const uint32_t* w,
                                              uint32_t sh, u32x4 (&B)[4]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     Groups4 G;
-    read_groups(ps, first + 4 * h, G);
+    read_groups<ROW>(ps, first + 4 * h, G);
     dequant_half<IO, BITS>(smem, w + 4 * h, sh, G, h, B);
   }
 }
 
 // The expm1 rows of bins 1..QMAX of one alpha (the table's first ET_N
-// entries) into LDS (bytes 0 .. 4 ET_N of the workgroup's array): 16 bytes
-// per load, the last ET_N % 4 entries one each.
-template <int ET_N>
+// entries) into LDS (bytes 0 .. 4 ET_N of the workgroup's array) by the NTH
+// threads of the workgroup: 16 bytes per load, the last ET_N % 4 entries one
+// each.
+template <int ET_N, int NTH>
 __device__ __forceinline__ void load_table(uint8_t* smem, const float* E) {
   constexpr int V = ET_N / 4;
-  for (int i = threadIdx.x; i < V; i += NT) *(u32x4*)(smem + 16 * i) = *(const u32x4*)(E + 4 * i);
+  for (int i = threadIdx.x; i < V; i += NTH) *(u32x4*)(smem + 16 * i) = *(const u32x4*)(E + 4 * i);
   if (threadIdx.x < ET_N - 4 * V) ((float*)smem)[4 * V + threadIdx.x] = E[4 * V + threadIdx.x];
   __syncthreads();
 }
@@ -217,28 +230,31 @@ __device__ __forceinline__ float across_groups_sum(float v) {
 
 // ---------------------------------------------------------------- pass 1
 // Logits of every tile of every (batch, kv-head): the grid is persistent
-// (one workgroup per CU); wave u of the grid takes flat tiles u, u + 8*grid, ...
+// (one workgroup of 12 waves per CU); wave u of the grid takes flat tiles
+// u, u + 12*grid, ...
 // logits[(b*Hq + q-head)*lt + token] = (q . k) * scaling * log2(e), plus the
 // additive mask times log2(e); -inf past the filled residual rows.
+// Three waves per SIMD hide the table reads' latency with no prefetch of the
+// next tile's words: each wave loads a tile's codes and metadata and uses
+// them at once (163 VGPRs at 8 bits, none spilled).
 template <int IO, int NREP, int MW, int BITS>
-__global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, float* __restrict__ logits, int n_tiles,
-                                                    int64_t lt) {
+__global__ __launch_bounds__(NT_1) void logits_kernel(const mz_decode_args a, float* __restrict__ logits, int n_tiles,
+                                                      int64_t lt) {
   using M = Mfma<IO>;
   constexpr int RS = 16 / NREP;
   constexpr int HS = NREP > 4 ? NREP / 4 : 1;
   constexpr int ES = 2 * MW;  // metadata bytes per entry
   using F = Fmt<BITS>;
   constexpr int QB = F::QB;
-  __shared__ __align__(16) uint8_t smem[F::LDS_BYTES];
+  __shared__ __align__(16) uint8_t smem[F::LDS_BYTES_1];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  load_table<F::ET_N>(smem, a.e_key);
-  uint8_t* const ps = smem + F::ET_BYTES + wave * PS_BYTES;
+  load_table<F::ET_N, NT_1>(smem, a.e_key);
+  uint8_t* const ps = smem + F::ET_BYTES + wave * PS_BYTES_1;
   const int wbyte = F::word_byte(n);      // this lane's code dword of a row, and its codes' first bit
   const uint32_t wsh = F::word_shift(n);
-
   const int Hq = a.kv_heads * a.n_rep;
   const int hA = n / RS, rA = n % RS;
   const bool owner = ((4 * g) % RS) == 0;
@@ -247,79 +263,68 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
   const int64_t ng = a.n_groups;
   // flat tile u = (b*Hkv + kvh)*n_tiles + tile (the host keeps the count below 2^31)
   const uint32_t total = (uint32_t)a.batch * (uint32_t)a.kv_heads * (uint32_t)n_tiles;
-  const uint32_t stride = gridDim.x * WAVES;
-  const uint32_t dq = stride / (uint32_t)n_tiles, dr = stride % (uint32_t)n_tiles;
-  uint32_t u = blockIdx.x * WAVES + wave;
-  uint32_t tile = u % (uint32_t)n_tiles, bk = u / (uint32_t)n_tiles;
-
-  // The words of a tile (loaded one tile ahead, into the other of two
-  // register sets): the query operand, and for a quantized tile its code
-  // words (KW[8kt + i] = the dword of tokens 4n..4n+3 of channel row
-  // 32kt + 8g + i) and this lane's two key groups' metadata (channels
-  // 2*lane, 2*lane + 1).
-  struct Words {
+  const uint32_t stride = gridDim.x * WAVES_1;
+  for (uint32_t u = blockIdx.x * WAVES_1 + wave; u < total; u += stride) {
+    const uint32_t tile = u % (uint32_t)n_tiles, bk = u / (uint32_t)n_tiles;
+    const int kvh = (int)(bk % (uint32_t)a.kv_heads), b = (int)(bk / (uint32_t)a.kv_heads);
+    // the query operand: row n = head hA's query when rA == 0, else zero
     u32x4 qa[4];
-    uint32_t KW[32], MN[MW], SC[MW];
-  };
-  auto issue = [&](Words& W, uint32_t t, uint32_t bk_) __attribute__((always_inline)) {
-    const int kvh = (int)(bk_ % (uint32_t)a.kv_heads), b = (int)(bk_ / (uint32_t)a.kv_heads);
-    const bool qrow = rA == 0 && hA < a.n_rep;  // row n = head hA's query when rA == 0, else zero
-    const uint16_t* qp =
-        (const uint16_t*)a.query + b * a.q_sb + (int64_t)(kvh * a.n_rep + min(hA, a.n_rep - 1)) * a.q_sh;
+    {
+      const bool qrow = rA == 0 && hA < a.n_rep;
+      const uint16_t* qp =
+          (const uint16_t*)a.query + b * a.q_sb + (int64_t)(kvh * a.n_rep + min(hA, a.n_rep - 1)) * a.q_sh;
 #pragma unroll
-    for (int kq = 0; kq < 4; ++kq) {
-      const u32x4 v = *(const u32x4*)(qp + 32 * kq + 8 * g);
-      W.qa[kq] = qrow ? v : u32x4{0u, 0u, 0u, 0u};
+      for (int kq = 0; kq < 4; ++kq) {
+        const u32x4 v = *(const u32x4*)(qp + 32 * kq + 8 * g);
+        qa[kq] = qrow ? v : u32x4{0u, 0u, 0u, 0u};
+      }
     }
-    if ((int)t < a.n_groups) {
-      const __amdgpu_buffer_rsrc_t kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * QB);
-      const int64_t km = b * a.km_sb + kvh * a.km_sh;
-      const __amdgpu_buffer_rsrc_t kmn = make_buf((const uint8_t*)a.k_mn + km * ES, ng * D * ES);
-      const __amdgpu_buffer_rsrc_t ksc = make_buf((const uint8_t*)a.k_scale + km * ES, ng * D * ES);
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          W.KW[8 * kt + i] = __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + wbyte,
-                                                                  (int)t * D * QB + (32 * kt + i) * QB, 0);
-      load_meta<MW>(W.MN, kmn, 2 * lane * ES, (int)t * D * ES);
-      load_meta<MW>(W.SC, ksc, 2 * lane * ES, (int)t * D * ES);
-    }
-  };
-  // one tile from the words in C; the next tile's loads go into N first
-  auto step = [&](Words& C, Words& N) __attribute__((always_inline)) {
-    const int kvh = (int)(bk % (uint32_t)a.kv_heads);
-    const int b = (int)(bk / (uint32_t)a.kv_heads);
-    const bool quant = (int)tile < a.n_groups;
-    if (quant) {
-      const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
-      uint32_t w0[PW], w1[PW];
-      group_words<F::QMAX>(mn.x, sc.x, w0);
-      group_words<F::QMAX>(mn.y, sc.y, w1);
-#pragma unroll
-      for (int k = 0; k < PW; ++k) *(uint2*)(ps + k * PS_ROW + 8 * lane) = uint2{w0[k], w1[k]};
-    }
-    const uint32_t un = u + stride;
-    uint32_t tn = tile + dr, bkn = bk + dq;
-    if (tn >= (uint32_t)n_tiles) tn -= (uint32_t)n_tiles, ++bkn;
-    if (un < total) issue(N, tn, bkn);
-
     f32x4 s[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
     int n_valid, pos0;
-    if (quant) {
+    if ((int)tile < a.n_groups) {
       n_valid = TILE;
       pos0 = TILE * (int)tile;
-      wave_lds_sync();
+      const __amdgpu_buffer_rsrc_t kp = make_buf(a.k_packed + b * a.kp_sb + kvh * a.kp_sh, ng * D * QB);
+      const int64_t km = b * a.km_sb + kvh * a.km_sh;
+      const __amdgpu_buffer_rsrc_t kmn = make_buf((const uint8_t*)a.k_mn + km * ES, ng * D * ES);
+      const __amdgpu_buffer_rsrc_t ksc = make_buf((const uint8_t*)a.k_scale + km * ES, ng * D * ES);
+      // this lane's code words (KW[8kt + i] = the dword of tokens 4n..4n+3
+      // of channel row 32kt + 8g + i) and its two key groups' metadata
+      // (channels 2*lane, 2*lane + 1)
+      uint32_t KW[32], MN[MW], SC[MW];
+      load_meta<MW>(MN, kmn, 2 * lane * ES, (int)tile * D * ES);
+      load_meta<MW>(SC, ksc, 2 * lane * ES, (int)tile * D * ES);
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        u32x4 B[4];
-        dequant_step<IO, BITS>(smem, ps, 32 * kt + 8 * g, C.KW + 8 * kt, wsh, B);
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(C.qa[kt], B[jt], s[jt]);
+        for (int i = 0; i < 8; ++i)
+          KW[8 * kt + i] = __builtin_amdgcn_raw_buffer_load_b32(kp, 8 * g * QB + wbyte,
+                                                                (int)tile * D * QB + (32 * kt + i) * QB, 0);
+      const float2 mn = meta_cvt<MW>(MN, a.meta_dtype), sc = meta_cvt<MW>(SC, a.meta_dtype);
+      uint32_t w0[PW], w1[PW];
+      group_words<F::QMAX>(mn.x, sc.x, w0);
+      group_words<F::QMAX>(mn.y, sc.y, w1);
+      // channel half hh (k-steps 2hh, 2hh + 1): the words of its 64 groups,
+      // stored by lanes 32hh .. 32hh + 31, at group index channel - 64hh
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        if ((lane >> 5) == hh) {
+#pragma unroll
+          for (int k = 0; k < PW; ++k) *(uint2*)(ps + k * PS_ROW_1 + 8 * (lane - 32 * hh)) = uint2{w0[k], w1[k]};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const int kt = 2 * hh + k2;
+          u32x4 B[4];
+          dequant_step<IO, BITS, PS_ROW_1>(smem, ps, 32 * k2 + 8 * g, KW + 8 * kt, wsh, B);
+#pragma unroll
+          for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], B[jt], s[jt]);
+        }
+        wave_lds_sync();  // the group words are read before the next ones are written
       }
-      wave_lds_sync();  // the group words are read before the next tile's are written
     } else {
       // residual tile: dense keys; rows past the filled ones read 0 (masked below)
       const int r0 = ((int)tile - a.n_groups) * TILE;
@@ -336,7 +341,7 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
           kb[jt] = __builtin_bit_cast(u32x4,
                                       __builtin_amdgcn_raw_buffer_load_b128(krb, (4 * n + jt) * kst + 16 * g, 64 * kt, 0));
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(C.qa[kt], kb[jt], s[jt]);
+        for (int jt = 0; jt < 4; ++jt) s[jt] = M::run(qa[kt], kb[jt], s[jt]);
       }
     }
     // this lane's logits: head slot sl = MFMA output element sl*RS, tokens 4n + jt
@@ -358,16 +363,6 @@ __global__ __launch_bounds__(NT) void logits_kernel(const mz_decode_args a, floa
             f32x4{v[0], v[1], v[2], v[3]};
       }
     }
-    u = un;
-    tile = tn;
-    bk = bkn;
-  };
-  Words W0, W1;
-  if (u < total) issue(W0, tile, bk);
-  while (u < total) {
-    step(W0, W1);
-    if (u >= total) break;
-    step(W1, W0);
   }
 }
 
@@ -389,7 +384,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15;
   const int g = lane >> 4;
-  load_table<F::ET_N>(smem, a.e_value);
+  load_table<F::ET_N, NT>(smem, a.e_value);
   uint8_t* const ps = smem + F::ET_BYTES + wave * PS_BYTES;
   const int wbyte = F::word_byte(n);      // this lane's code dword of a row, and its codes' first bit
   const uint32_t wsh = F::word_shift(n);
@@ -540,7 +535,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
 #pragma unroll
         for (int vg = 0; vg < 2; ++vg) {
           u32x4 B[4];
-          dequant_step<IO, BITS>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), wsh, B);
+          dequant_step<IO, BITS, PS_ROW>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), wsh, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
         }
@@ -676,8 +671,8 @@ template <int IO, int NR, int MW, int BB>
 static void tp_launch_one(const mz_decode_args* a, hipStream_t s, float* logits, int n_tiles, int tps, int ns) {
   const int64_t lt = (int64_t)n_tiles * tp::TILE;
   const int64_t total = (int64_t)a->batch * a->kv_heads * n_tiles;
-  const int64_t g1 = std::min<int64_t>(device_cu_count(), (total + tp::WAVES - 1) / tp::WAVES);
-  hipLaunchKernelGGL((tp::logits_kernel<IO, NR, MW, BB>), dim3((unsigned)g1), dim3(tp::NT), 0, s, *a, logits,
+  const int64_t g1 = std::min<int64_t>(device_cu_count(), (total + tp::WAVES_1 - 1) / tp::WAVES_1);
+  hipLaunchKernelGGL((tp::logits_kernel<IO, NR, MW, BB>), dim3((unsigned)g1), dim3(tp::NT_1), 0, s, *a, logits,
                      n_tiles, lt);
   const int64_t units = (int64_t)a->batch * a->kv_heads * ns;
   hipLaunchKernelGGL((tp::attend_kernel<IO, NR, MW, BB>), dim3((unsigned)((units + tp::WAVES - 1) / tp::WAVES)),
