@@ -429,8 +429,9 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
   // register sets), for a quantized tile: its code words (VW[8(2kt + vg) +
   // j] = the dword of channels 4n..4n+3 of token row 32kt + 8g + j, group
   // vg) and this lane's two value groups' metadata (groups 0, 1 of token
-  // lane).  This lane's logits of the tile (x[8kt + j] = token 32kt + 8g +
-  // j) are read at its start.
+  // lane).  This lane's logits of a tile (xn[8kt + j] = token 32kt + 8g + j)
+  // are loaded halfway through the tile before it, once the first k-step's
+  // registers are free.
   struct Words {
     uint32_t VW[32], MN[MW], SC[MW];
   };
@@ -448,18 +449,23 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
       load_meta<MW>(W.SC, vsc, 2 * lane * ES, t * TILE * 2 * ES);
     }
   };
+  float xn[16];
+  auto load_x = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int h4 = 0; h4 < 2; ++h4) {
+        const f32x4 v = *(const f32x4*)(lrow + (int64_t)t * TILE + 32 * kt + 8 * g + 4 * h4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xn[8 * kt + 4 * h4 + j] = v[j];
+      }
+  };
   // one tile from the words in C; the next tile's loads go into N first
   auto step = [&](const int tile, Words& C, Words& N) __attribute__((always_inline)) {
     const bool quant = tile < a.n_groups;
     float x[16];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int h4 = 0; h4 < 2; ++h4) {
-        const f32x4 v = *(const f32x4*)(lrow + (int64_t)tile * TILE + 32 * kt + 8 * g + 4 * h4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) x[8 * kt + 4 * h4 + j] = v[j];
-      }
+    for (int j = 0; j < 16; ++j) x[j] = xn[j];
     const uint32_t* const VC = C.VW;
     if (quant) {
       const float2 mn = meta_cvt<MW>(C.MN, a.meta_dtype), sc = meta_cvt<MW>(C.SC, a.meta_dtype);
@@ -538,6 +544,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
           dequant_step<IO, BITS, PS_ROW>(smem, ps, 64 * vg + 32 * kt + 8 * g, VC + 8 * (2 * kt + vg), wsh, B);
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
+          if (kt == 0 && vg == 1 && tile + 1 < t_end) load_x(tile + 1);
         }
       wave_lds_sync();  // the group words are read before the next tile's are written
     } else {
@@ -552,11 +559,16 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int vg = 0; vg < 2; ++vg) {
+          // the lane's row offset is formed here, opaque to the compiler: hoisted
+          // out of the tile loop, the 16 offsets of a residual tile would hold
+          // (or spill) 16 VGPRs through every quantized tile
+          int rb = 8 * g * vst + 8 * n;
+          asm volatile("" : "+v"(rb));
           uint2 w[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j)
             w[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                 vrb, (32 * kt + 8 * g + j) * vst + (64 * vg + 4 * n) * 2, 0, 0));
+                                                 vrb, rb + (32 * kt + j) * vst + 128 * vg, 0, 0));
           u32x4 B[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
@@ -568,11 +580,12 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
           }
 #pragma unroll
           for (int jt = 0; jt < 4; ++jt) acc[vg][jt] = M::run(pa[kt], B[jt], acc[vg][jt]);
+          if (kt == 0 && vg == 1 && tile + 1 < t_end) load_x(tile + 1);
         }
     }
     };
   Words W0, W1;
-  if (t_begin < t_end) issue(W0, t_begin);
+  if (t_begin < t_end) issue(W0, t_begin), load_x(t_begin);
   for (int tile = t_begin; tile < t_end; tile += 2) {
     step(tile, W0, W1);
     if (tile + 1 >= t_end) break;
