@@ -587,6 +587,8 @@ CB_SHAPES = [
     (1, 2, 2, 128, 700, 128),
     (1, 2, 3, 128, 700, 128),    # the 4-head kernel, one head idle
     (1, 1, 8, 128, 700, 128),
+    (1, 2, 5, 128, 700, 128),    # the 8-head kernel, three heads idle
+    (2, 1, 6, 128, 1024, 64),
     (2, 2, 7, 128, 1024, 128),
     (1, 2, 4, 128, 4096, 128),   # many tiles per wave
     (2, 1, 4, 128, 300, 0),      # no residual
