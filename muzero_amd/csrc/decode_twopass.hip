@@ -431,7 +431,7 @@ __global__ __launch_bounds__(NT) void attend_kernel(const mz_decode_args a, cons
   // vg) and this lane's two value groups' metadata (groups 0, 1 of token
   // lane).  This lane's logits of a tile (xn[8kt + j] = token 32kt + 8g + j)
   // are loaded halfway through the tile before it, once the first k-step's
-  // registers are free.
+  // registers are free (the split's first tile's before the loop).
   struct Words {
     uint32_t VW[32], MN[MW], SC[MW];
   };
